@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE feed-forward block (HunyuanImage-3 shape).
+
+Default workload (what the one JSON line reports): one MoE layer, hidden 4096,
+64 routed experts + 1 shared, FFN width 3072, top-8, GGUF Q8_0 weights, T=512
+tokens per step (prefill batch), inputs resident in HBM.  A step is one full
+layer forward: Q8_0 activation quantization, router + top-8, dispatch, gate_up +
+SwiGLU, down + combine.  Weights are random-init N(0, 0.02) (synthetic, generated
+on the device), activations N(0, 1).
+
+Other workloads (--config): c1 F32 T=16, c3 Q4_0 decode (--tokens 1/2/4/8),
+c4 Q4_0 T=4096 Zipf-skewed routing, c5 32-layer Q8_0 stack T=4096.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+H, I, E, K = 4096, 3072, 64, 8
+PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
+PEAK_INT8 = 5.0e15         # ops/s, dense int8 MFMA
+PARAMS_PER_EXPERT = 3 * H * I
+BYTES = {0: 4.0, 8: 34.0 / 32.0, 2: 18.0 / 32.0}   # bytes per weight element
+
+
+def load_pkg():
+    import importlib.util
+    pkg = os.path.join(ROOT, "hunyuan-image-3-80b.cpp_amd")
+    spec = importlib.util.spec_from_file_location("hy3moe", os.path.join(pkg, "__init__.py"),
+                                                  submodule_search_locations=[pkg])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["hy3moe"] = mod
+    spec.loader.exec_module(mod)
+    return mod.hy_moe
+
+
+WORKLOADS = {
+    "c1": dict(name="moe_layer_f32_t16", wtype=0, T=16, layers=1, rot=1),
+    "c2": dict(name="moe_layer_q8_0_t512", wtype=8, T=512, layers=1, rot=2),
+    "c3": dict(name="moe_layer_q4_0_decode", wtype=2, T=1, layers=1, rot=8),
+    "c4": dict(name="moe_layer_q4_0_t4096_zipf", wtype=2, T=4096, layers=1, rot=1, zipf=True),
+    "c5": dict(name="moe_stack32_q8_0_t4096", wtype=8, T=4096, layers=32, rot=1, stack=True),
+}
+
+
+def zipf_bias(seed=42, s=1.1, beta=1.0):
+    """Per-expert additive router bias b_e = beta * ln p_e, p_e ~ rank^-s under a seeded
+    rank permutation (folded into input feature 0, which is set to 1)."""
+    rng = np.random.default_rng(seed)
+    ranks = rng.permutation(E) + 1
+    p = ranks.astype(np.float64) ** -s
+    p /= p.sum()
+    return (beta * np.log(p)).astype(np.float32)
+
+
+def expert_bytes(wtype):
+    return PARAMS_PER_EXPERT * BYTES[wtype]
+
+
+def kernel_traffic(kname, wtype, T, D, shared=True):
+    """Algorithmic HBM bytes of one launch of a kernel of the layer forward."""
+    wb = BYTES[wtype]
+    n_exp = D + (1 if shared else 0)
+    act_b = 1.0 + 8.0 / 32.0 if wtype != 0 else 4.0   # int8 + scale + sum per element
+    if kname == "ffn_up":
+        return n_exp * 2 * I * H * wb + T * H * act_b + (T * K + T) * I * act_b
+    if kname == "ffn_down":
+        return D * H * I * wb + T * K * I * act_b + T * K * H * 4
+    if kname == "ffn_down_shared_combine":
+        return H * I * wb + T * I * act_b + T * K * H * 4 + T * H * 4
+    return 0.0
+
+
+def kernel_ops(kname, T):
+    if kname == "ffn_up":
+        return 2.0 * T * (K + 1) * 2 * I * H
+    if kname in ("ffn_down",):
+        return 2.0 * T * K * H * I
+    if kname == "ffn_down_shared_combine":
+        return 2.0 * T * H * I
+    return 0.0
+
+
+def cpu_baseline(wl, seed, budget_s=15.0):
+    """The oracle's q-semantics layer (int8 block dots, OpenMP over all host
+    threads) on a bounded token sample of the same workload."""
+    import hy_oracle as O
+    nthreads = os.cpu_count() or 1
+    wtype = wl["wtype"]
+    layer = O.synth_layer(H, I, E, K, wtype, seed=seed, layer=0, std=0.02)
+    T = wl["T"]
+    x = O.synth(seed + 1000, 0, O.T_X, 0, (T, H), 1.0)
+    n = min(T, max(8, nthreads))
+    rows = np.arange(n) % T
+    t0 = time.perf_counter()
+    O.moe_forward_q_rows(layer, x, rows, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    n2 = int(min(T * 4, max(n, n * budget_s / max(dt, 1e-6))))
+    rows = np.arange(n2) % T
+    t0 = time.perf_counter()
+    O.moe_forward_q_rows(layer, x, rows, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    return {"value": n2 / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"{n2} tokens of the {wl['name']} workload through the oracle's int8 (ggml-semantics) "
+                      f"layer, {nthreads} OpenMP threads, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--tokens", type=int, default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--verbose", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): this build has no multi-GPU path; "
+              f"expert-parallel sharding is a design note, not code.", file=sys.stderr)
+        sys.exit(2)
+
+    hy = load_pkg()
+    if hy.device_count() < 1:
+        sys.exit("no HIP device visible")
+    wl = dict(WORKLOADS[a.config])
+    if a.tokens:
+        wl["T"] = a.tokens
+    T, wtype, nl = wl["T"], wl["wtype"], wl["layers"]
+    rot = wl["rot"] if not wl.get("stack") else 1
+    n_layers = nl * rot
+    bias = zipf_bias(a.seed) if wl.get("zipf") else None
+
+    m = hy.Moe(H, I, E, K, wtype, num_layers=n_layers, max_tokens=T)
+    for l in range(n_layers):
+        m.synth(l, seed=a.seed, std=0.02, router_bias=bias)
+    x = hy.Buf.empty((T, H))
+    hy.check(hy.lib().hy_synth_fill(x.ptr, T * H, a.seed + 1000, 0, 0, 0, 1.0, None))
+    if bias is not None:   # feature 0 carries the per-expert bias
+        xh = x.numpy()
+        xh[:, 0] = 1.0
+        x = hy.Buf.from_array(xh)
+    out = hy.Buf.empty((T, H))
+    stream = None
+
+    def step(i):
+        if wl.get("stack"):
+            m.stack_forward(0, nl, x, T, 1e-5, out, stream)
+        else:
+            m.forward(i % rot, x, T, out, stream)
+
+    for i in range(a.warmup):
+        step(i)
+    hy.sync()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    hy.sync()
+    t0 = time.perf_counter()
+    hy.check(hy.lib().hy_event_record(ev0, stream))
+    for i in range(a.steps):
+        step(i)
+    hy.check(hy.lib().hy_event_record(ev1, stream))
+    hy.sync()
+    wall = time.perf_counter() - t0
+    ms = hy.C.c_float()
+    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+    ms_per_step = ms.value / a.steps
+    tokens_per_s = T / (ms_per_step / 1e3)
+
+    D, counts = m.last_routing()
+    # per-kernel durations on the launch stream (separate, profiled pass)
+    m.prof_enable(True)
+    for i in range(a.steps):
+        step(i)
+    hy.sync()
+    prof = m.prof_read()
+    m.prof_enable(False)
+    kern = {k: (n, t) for k, (n, t) in prof.items() if n > 0}
+    dom = max(kern, key=lambda k: kern[k][1])
+    n_l, t_l = kern[dom]
+    avg_s = t_l / n_l / 1e3
+    n_layer_launch = nl if wl.get("stack") else 1
+    traffic = kernel_traffic(dom, wtype, T, D)
+    ops = kernel_ops(dom, T)
+    layer_bytes = (D + 1) * expert_bytes(wtype) + E * H * 4 + 2 * T * H * 4
+    layer_ops = 2.0 * T * (K + 1) * PARAMS_PER_EXPERT
+    t_layer = ms_per_step / 1e3 / n_layer_launch
+    # bound: HBM when the layer's bytes take longer at peak than its ops at int8 peak
+    bound = "hbm" if layer_bytes / PEAK_HBM >= layer_ops / PEAK_INT8 else "mfma"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "kernel": dom, "achieved": traffic / avg_s / 1e9, "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": traffic / avg_s / PEAK_HBM, "traffic": None,
+                "algorithmic_bytes_per_launch": traffic, "avg_launch_ms": avg_s * 1e3}
+    else:
+        roof = {"bound": "mfma", "kernel": dom, "achieved": ops / avg_s / 1e12, "peak": PEAK_INT8 / 1e12,
+                "unit": "TFLOP/s", "frac": ops / avg_s / PEAK_INT8, "traffic": None,
+                "algorithmic_ops_per_launch": ops, "avg_launch_ms": avg_s * 1e3}
+
+    res = {
+        "metric": "MoE-layer tokens/sec + achieved HBM GB/s / int8 MFMA util, 1 MI355X",
+        "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8" if wtype != 0 else "f32", "data": "synthetic",
+        "config": {"workload": wl["name"], "hidden": H, "intermediate": I, "experts": E, "shared_experts": 1,
+                   "topk": K, "tokens": T, "weights": {0: "F32", 2: "Q4_0", 8: "Q8_0"}[wtype],
+                   "layers": nl, "resident_weight_sets": n_layers, "distinct_experts_last_step": int(D)},
+        "layer_hbm_gbps": layer_bytes / t_layer / 1e9,
+        "layer_hbm_frac": layer_bytes / t_layer / PEAK_HBM,
+        "layer_int8_util": layer_ops / t_layer / PEAK_INT8,
+        "roofline": roof,
+        "kernels_ms": {k: round(t / n, 5) for k, (n, t) in kern.items()},
+        "wall_s": wall,
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(wl, a.seed)
+    print(json.dumps(res), flush=True)
+    m.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,615 @@
+// hy_capi.hip -- the C ABI (include/hy_moe.h): context, resident weights, work
+// arena, forward orchestration, timing.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hy_moe.h"
+#include "hy_device.hpp"
+#include "hy_launch.hpp"
+#include "hy_layout.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                                    \
+    do {                                                                                                 \
+        hipError_t e_ = (expr);                                                                          \
+        if (e_ != hipSuccess) return fail(HY_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_),   \
+                                          __FILE__, __LINE__);                                           \
+    } while (0)
+
+#define HY_TRY(expr)              \
+    do {                          \
+        int r_ = (expr);          \
+        if (r_ != HY_OK) return r_; \
+    } while (0)
+
+size_t row_bytes(int wtype, int cols) {
+    switch (wtype) {
+    case HY_TYPE_F32: return (size_t)cols * 4;
+    case HY_TYPE_Q8_0: return (size_t)cols;       // resident int8 plane
+    case HY_TYPE_Q4_0: return (size_t)cols / 2;   // resident nibble plane
+    default: return 0;
+    }
+}
+size_t gguf_row_bytes(int wtype, int cols) {
+    switch (wtype) {
+    case HY_TYPE_F32: return (size_t)cols * 4;
+    case HY_TYPE_Q8_0: return (size_t)cols / 32 * 34;
+    case HY_TYPE_Q4_0: return (size_t)cols / 32 * 18;
+    default: return 0;
+    }
+}
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct LayerW {
+    uint8_t* base = nullptr;
+    float* router = nullptr;
+    uint8_t* gu_qs = nullptr;
+    uint16_t* gu_sc = nullptr;
+    uint8_t* dn_qs = nullptr;
+    uint16_t* dn_sc = nullptr;
+    bool loaded = false;
+};
+
+struct ProfRec {
+    int kid;
+    hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct hy_moe_ctx {
+    hy_moe_config cfg{};
+    int H = 0, I = 0, E = 0, K = 0, X = 0;  // X = experts incl. shared slot
+    size_t gu_qs_stride = 0, gu_sc_stride = 0, dn_qs_stride = 0, dn_sc_stride = 0;
+    size_t layer_bytes = 0;
+    std::vector<LayerW> layers;
+
+    // arena
+    void* arena = nullptr;
+    int8_t* xq = nullptr;
+    float* xd = nullptr;
+    int* xs = nullptr;
+    float* logits = nullptr;
+    float* topw = nullptr;
+    int* topi = nullptr;
+    int *cnt = nullptr, *off = nullptr, *srt_tok = nullptr, *pair_pos = nullptr, *comb_pos = nullptr;
+    float* comb_w = nullptr;
+    int *tile_e = nullptr, *tile_start = nullptr, *tile_n = nullptr, *meta = nullptr;
+    int8_t* hq = nullptr;
+    float* hd = nullptr;
+    int* hs = nullptr;
+    float* hf = nullptr;
+    float* y = nullptr;
+    float* xn = nullptr;
+    float* cur = nullptr;
+    int max_tiles = 0;
+
+    // timing
+    bool prof = false;
+    std::vector<ProfRec> pending;
+    std::vector<hipEvent_t> pool;
+    uint64_t prof_n[hy::KID_COUNT] = {};
+    double prof_ms[hy::KID_COUNT] = {};
+
+    hipStream_t last_stream = nullptr;
+};
+
+namespace {
+
+const char* kKernelNames[hy::KID_COUNT] = {"quant_q8_0", "router", "dispatch", "ffn_up",
+                                           "ffn_down",   "ffn_down_shared_combine", "combine", "rms_norm"};
+
+int get_event(hy_moe_ctx* c, hipEvent_t* ev) {
+    if (!c->pool.empty()) {
+        *ev = c->pool.back();
+        c->pool.pop_back();
+        return HY_OK;
+    }
+    HIP_TRY(hipEventCreate(ev));
+    return HY_OK;
+}
+
+int drain_prof(hy_moe_ctx* c) {
+    for (auto& r : c->pending) {
+        HIP_TRY(hipEventSynchronize(r.b));
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, r.a, r.b));
+        c->prof_n[r.kid]++;
+        c->prof_ms[r.kid] += ms;
+        c->pool.push_back(r.a);
+        c->pool.push_back(r.b);
+    }
+    c->pending.clear();
+    return HY_OK;
+}
+
+// Launch wrapper: brackets a launch with events when timing is on.
+template <typename F>
+int timed(hy_moe_ctx* c, int kid, hipStream_t s, F&& launch) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (c->prof) {
+        HY_TRY(get_event(c, &a));
+        HY_TRY(get_event(c, &b));
+        HIP_TRY(hipEventRecord(a, s));
+    }
+    hipError_t e = launch();
+    if (e != hipSuccess)
+        return fail(HY_ERR_HIP, "launch of %s failed: %s", kKernelNames[kid], hipGetErrorString(e));
+    if (c->prof) {
+        HIP_TRY(hipEventRecord(b, s));
+        c->pending.push_back({kid, a, b});
+        if (c->pending.size() > 4096) HY_TRY(drain_prof(c));
+    }
+    return HY_OK;
+}
+
+int tile_bound_routed(int T, int K, int E, int NT) { return (T * K + E * (NT - 1)) / NT; }
+
+int check_cfg(const hy_moe_config* c) {
+    if (!c) return fail(HY_ERR_INVALID, "null config");
+    if (c->hidden == 0 || c->hidden % 64)
+        return fail(HY_ERR_INVALID, "hidden=%u must be a positive multiple of 64", c->hidden);
+    if (c->intermediate == 0 || c->intermediate % 32)
+        return fail(HY_ERR_INVALID, "intermediate=%u must be a positive multiple of 32", c->intermediate);
+    if (c->num_experts == 0 || c->num_experts > hy::MAX_E)
+        return fail(HY_ERR_INVALID, "num_experts=%u must be in 1..%d", c->num_experts, hy::MAX_E);
+    if (c->topk == 0 || c->topk > c->num_experts || c->topk > (uint32_t)hy::MAX_K)
+        return fail(HY_ERR_INVALID, "topk=%u must be in 1..min(num_experts, %d)", c->topk, hy::MAX_K);
+    if (c->num_layers == 0) return fail(HY_ERR_INVALID, "num_layers must be >= 1");
+    if (c->max_tokens == 0 || c->max_tokens > 16384)
+        return fail(HY_ERR_INVALID, "max_tokens=%u must be in 1..16384", c->max_tokens);
+    if (c->wtype != HY_TYPE_F32 && c->wtype != HY_TYPE_Q8_0 && c->wtype != HY_TYPE_Q4_0)
+        return fail(HY_ERR_UNSUPPORTED, "weight type %d not supported (F32=0, Q4_0=2, Q8_0=8)", c->wtype);
+    if (c->group_limited_greedy || c->drop_tokens || c->compute_aux_loss)
+        return fail(HY_ERR_UNSUPPORTED,
+                    "group-limited greedy, token dropping and the aux loss are not run on the GPU path");
+    return HY_OK;
+}
+
+hy::MatView gu_view(const hy_moe_ctx* c, const LayerW& L) {
+    return {L.gu_qs, L.gu_sc, c->gu_qs_stride, c->gu_sc_stride, 2 * c->I, c->H};
+}
+hy::MatView dn_view(const hy_moe_ctx* c, const LayerW& L) {
+    return {L.dn_qs, L.dn_sc, c->dn_qs_stride, c->dn_sc_stride, c->H, c->I};
+}
+hy::Routing routing(const hy_moe_ctx* c) {
+    return {c->topi, c->topw, c->cnt, c->off, c->srt_tok, c->comb_pos, c->comb_w, c->tile_e, c->tile_start,
+            c->tile_n, c->meta};
+}
+
+int alloc_layer(hy_moe_ctx* c, LayerW& L) {
+    if (L.base) return HY_OK;
+    void* p = nullptr;
+    if (hipMalloc(&p, c->layer_bytes) != hipSuccess)
+        return fail(HY_ERR_NOMEM, "hipMalloc of %zu bytes for a layer failed", c->layer_bytes);
+    uint8_t* b = static_cast<uint8_t*>(p);
+    size_t o = 0;
+    L.base = b;
+    L.router = reinterpret_cast<float*>(b + o);
+    o += align256((size_t)c->E * c->H * 4);
+    L.gu_qs = b + o;
+    o += align256(c->gu_qs_stride * c->X);
+    L.gu_sc = reinterpret_cast<uint16_t*>(b + o);
+    o += align256(c->gu_sc_stride * 2 * c->X);
+    L.dn_qs = b + o;
+    o += align256(c->dn_qs_stride * c->X);
+    L.dn_sc = reinterpret_cast<uint16_t*>(b + o);
+    return HY_OK;
+}
+
+// forward of one layer; resid may be null.
+int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, float* out, const float* resid,
+                 hipStream_t s) {
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    const LayerW& L = c->layers[layer];
+    if (!L.loaded) return fail(HY_ERR_STATE, "layer %u has no weights", layer);
+    if (T == 0 || T > c->cfg.max_tokens)
+        return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%u", T, c->cfg.max_tokens);
+    if (!x || !out) return fail(HY_ERR_INVALID, "null x/out");
+    c->last_stream = s;
+    const int H = c->H, I = c->I, E = c->E, K = c->K, wt = c->cfg.wtype;
+    const int iT = (int)T;
+    const int has_shared = c->cfg.has_shared ? 1 : 0;
+    if (wt != HY_TYPE_F32)
+        HY_TRY(timed(c, hy::KID_QUANT, s, [&] {
+            return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
+        }));
+    HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
+        return hy::launch_router(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob, c->cfg.routed_scaling_factor,
+                                 c->logits, c->topw, c->topi, s);
+    }));
+    const int NT = T <= 64 ? 8 : 16;
+    HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
+        return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
+                                   c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
+                                   c->meta, s);
+    }));
+    const hy::Routing R = routing(c);
+    const hy::ActQ X{c->xq, c->xd, c->xs, H};
+    const int routed_bound = tile_bound_routed(iT, K, E, NT);
+    const int shared_tiles = has_shared ? (iT + NT - 1) / NT : 0;
+    HY_TRY(timed(c, hy::KID_UP, s, [&] {
+        return hy::launch_ffn_up_valu(wt, NT, routed_bound + shared_tiles, gu_view(c, L), R, X, x, iT, H, I, E, K,
+                                      c->hq, c->hd, c->hs, c->hf, s);
+    }));
+    HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
+        return hy::launch_ffn_down_valu(wt, NT, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT,
+                                        H, I, E, K, c->y, nullptr, nullptr, s);
+    }));
+    if (has_shared) {
+        HY_TRY(timed(c, hy::KID_DOWN_SHARED, s, [&] {
+            return hy::launch_ffn_down_valu(wt, NT, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf,
+                                            iT, H, I, E, K, c->y, resid, out, s);
+        }));
+    } else {
+        HY_TRY(timed(c, hy::KID_COMBINE, s, [&] { return hy::launch_combine(R, c->y, iT, H, K, resid, out, s); }));
+    }
+    return HY_OK;
+}
+
+}  // namespace
+
+// =====================================================================================
+extern "C" {
+
+const char* hy_last_error(void) { return g_last_error.c_str(); }
+
+int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
+    if (!out) return fail(HY_ERR_INVALID, "null out");
+    *out = nullptr;
+    HY_TRY(check_cfg(cfg));
+    HIP_TRY(hipSetDevice(cfg->device));
+    hy_moe_ctx* c = new hy_moe_ctx();
+    c->cfg = *cfg;
+    c->H = (int)cfg->hidden;
+    c->I = (int)cfg->intermediate;
+    c->E = (int)cfg->num_experts;
+    c->K = (int)cfg->topk;
+    c->X = c->E + (cfg->has_shared ? 1 : 0);
+    const int wt = cfg->wtype;
+    c->gu_qs_stride = align256(row_bytes(wt, c->H) * 2 * c->I);
+    c->gu_sc_stride = wt == HY_TYPE_F32 ? 0 : (size_t)2 * c->I * (c->H / 32);
+    c->dn_qs_stride = align256(row_bytes(wt, c->I) * c->H);
+    c->dn_sc_stride = wt == HY_TYPE_F32 ? 0 : (size_t)c->H * (c->I / 32);
+    c->layer_bytes = align256((size_t)c->E * c->H * 4) + align256(c->gu_qs_stride * c->X) +
+                     align256(c->gu_sc_stride * 2 * c->X) + align256(c->dn_qs_stride * c->X) +
+                     align256(c->dn_sc_stride * 2 * c->X);
+    c->layers.resize(cfg->num_layers);
+
+    // work arena
+    const size_t Tm = cfg->max_tokens, H = c->H, I = c->I, E = c->E, K = c->K;
+    const size_t pairs = Tm * K, slots = Tm * (K + 1);
+    c->max_tiles = tile_bound_routed((int)Tm, (int)K, (int)E, 8) + (int)((Tm + 7) / 8) + 1;
+    struct Part {
+        void** p;
+        size_t bytes;
+    };
+    std::vector<Part> parts = {
+        {(void**)&c->xq, Tm * H},          {(void**)&c->xd, Tm * (H / 32) * 4},
+        {(void**)&c->xs, Tm * (H / 32) * 4}, {(void**)&c->logits, Tm * E * 4},
+        {(void**)&c->topw, pairs * 4},     {(void**)&c->topi, pairs * 4},
+        {(void**)&c->cnt, E * 4},          {(void**)&c->off, (E + 1) * 4},
+        {(void**)&c->srt_tok, pairs * 4},  {(void**)&c->pair_pos, pairs * 4},
+        {(void**)&c->comb_pos, pairs * 4}, {(void**)&c->comb_w, pairs * 4},
+        {(void**)&c->tile_e, (size_t)c->max_tiles * 4}, {(void**)&c->tile_start, (size_t)c->max_tiles * 4},
+        {(void**)&c->tile_n, (size_t)c->max_tiles * 4}, {(void**)&c->meta, 16},
+        {(void**)&c->hq, slots * I},       {(void**)&c->hd, slots * (I / 32) * 4},
+        {(void**)&c->hs, slots * (I / 32) * 4},
+        {(void**)&c->hf, wt == HY_TYPE_F32 ? slots * I * 4 : 16},
+        {(void**)&c->y, pairs * H * 4},    {(void**)&c->xn, Tm * H * 4},
+        {(void**)&c->cur, Tm * H * 4},
+    };
+    size_t total = 0;
+    for (auto& p : parts) total += align256(p.bytes);
+    if (hipMalloc(&c->arena, total) != hipSuccess) {
+        delete c;
+        return fail(HY_ERR_NOMEM, "hipMalloc of a %zu-byte work arena failed", total);
+    }
+    size_t o = 0;
+    for (auto& p : parts) {
+        *p.p = static_cast<uint8_t*>(c->arena) + o;
+        o += align256(p.bytes);
+    }
+    if (hipMemset(c->arena, 0, total) != hipSuccess) {
+        (void)hipFree(c->arena);
+        delete c;
+        return fail(HY_ERR_HIP, "hipMemset of the work arena failed");
+    }
+    *out = c;
+    return HY_OK;
+}
+
+int hy_moe_destroy(hy_moe_ctx* c) {
+    if (!c) return HY_OK;
+    (void)hipDeviceSynchronize();
+    for (auto& L : c->layers)
+        if (L.base) (void)hipFree(L.base);
+    if (c->arena) (void)hipFree(c->arena);
+    for (auto& r : c->pending) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    for (auto e : c->pool) (void)hipEventDestroy(e);
+    delete c;
+    return HY_OK;
+}
+
+size_t hy_moe_layer_bytes(const hy_moe_ctx* c) { return c ? c->layer_bytes : 0; }
+
+int hy_moe_upload_layer(hy_moe_ctx* c, uint32_t layer, const float* router, const void* sgu, const void* sdn,
+                        const void* gu, const void* dn) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    if (!router || !gu || !dn) return fail(HY_ERR_INVALID, "null router/gu/dn");
+    if (c->cfg.has_shared && (!sgu || !sdn)) return fail(HY_ERR_INVALID, "config has a shared expert: pass it");
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    LayerW& L = c->layers[layer];
+    HY_TRY(alloc_layer(c, L));
+    const int wt = c->cfg.wtype, H = c->H, I = c->I, E = c->E;
+    const size_t gu_b = gguf_row_bytes(wt, H) * 2 * I, dn_b = gguf_row_bytes(wt, I) * H;
+    void* staging = nullptr;
+    if (hipMalloc(&staging, gu_b > dn_b ? gu_b : dn_b) != hipSuccess)
+        return fail(HY_ERR_NOMEM, "staging allocation failed");
+    int rc = HY_OK;
+    auto up = [&](const void* src, size_t bytes, int rows, int cols, int guI, uint8_t* qs, uint16_t* sc) -> int {
+        HIP_TRY(hipMemcpy(staging, src, bytes, hipMemcpyHostToDevice));
+        HIP_TRY(hy::launch_repack(wt, static_cast<uint8_t*>(staging), rows, cols, guI, qs, sc, nullptr));
+        return HY_OK;
+    };
+    for (int e = 0; e < c->X && rc == HY_OK; e++) {
+        const uint8_t* gsrc = e < E ? static_cast<const uint8_t*>(gu) + (size_t)e * gu_b
+                                    : static_cast<const uint8_t*>(sgu);
+        const uint8_t* dsrc = e < E ? static_cast<const uint8_t*>(dn) + (size_t)e * dn_b
+                                    : static_cast<const uint8_t*>(sdn);
+        rc = up(gsrc, gu_b, 2 * I, H, I, L.gu_qs + (size_t)e * c->gu_qs_stride,
+                L.gu_sc ? L.gu_sc + (size_t)e * c->gu_sc_stride : nullptr);
+        if (rc == HY_OK)
+            rc = up(dsrc, dn_b, H, I, 0, L.dn_qs + (size_t)e * c->dn_qs_stride,
+                    L.dn_sc ? L.dn_sc + (size_t)e * c->dn_sc_stride : nullptr);
+    }
+    if (rc == HY_OK && hipMemcpy(L.router, router, (size_t)E * H * 4, hipMemcpyHostToDevice) != hipSuccess)
+        rc = fail(HY_ERR_HIP, "router upload failed");
+    if (rc == HY_OK && hipDeviceSynchronize() != hipSuccess) rc = fail(HY_ERR_HIP, "repack failed");
+    (void)hipFree(staging);
+    if (rc == HY_OK) L.loaded = true;
+    return rc;
+}
+
+int hy_moe_synth_layer(hy_moe_ctx* c, uint32_t layer, uint64_t seed, float std, const float* bias) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    LayerW& L = c->layers[layer];
+    HY_TRY(alloc_layer(c, L));
+    const int wt = c->cfg.wtype, H = c->H, I = c->I, E = c->E;
+    const float scale = std * hy::NORM_SCALE;
+    HIP_TRY(hy::launch_synth_fill(L.router, (size_t)E * H, hy::stream_key(seed, layer, hy::TENSOR_ROUTER, 0), scale,
+                                  nullptr));
+    if (bias) HIP_TRY(hipMemcpy2D(L.router, (size_t)H * 4, bias, 4, 4, E, hipMemcpyHostToDevice));
+    for (int e = 0; e < c->X; e++) {
+        HIP_TRY(hy::launch_synth_matrix(wt, hy::stream_key(seed, layer, hy::TENSOR_GU, e), scale, 2 * I, H, I,
+                                        L.gu_qs + (size_t)e * c->gu_qs_stride,
+                                        L.gu_sc ? L.gu_sc + (size_t)e * c->gu_sc_stride : nullptr, nullptr));
+        HIP_TRY(hy::launch_synth_matrix(wt, hy::stream_key(seed, layer, hy::TENSOR_DN, e), scale, H, I, 0,
+                                        L.dn_qs + (size_t)e * c->dn_qs_stride,
+                                        L.dn_sc ? L.dn_sc + (size_t)e * c->dn_sc_stride : nullptr, nullptr));
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    L.loaded = true;
+    return HY_OK;
+}
+
+int hy_moe_forward(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, float* out, void* stream) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    return forward_impl(c, layer, x, T, out, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int hy_moe_forward_debug(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, float* out, float* lg, float* w,
+                         int32_t* idx, void* stream) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    HY_TRY(forward_impl(c, layer, x, T, out, nullptr, s));
+    if (lg) HIP_TRY(hipMemcpyAsync(lg, c->logits, (size_t)T * c->E * 4, hipMemcpyDeviceToDevice, s));
+    if (w) HIP_TRY(hipMemcpyAsync(w, c->topw, (size_t)T * c->K * 4, hipMemcpyDeviceToDevice, s));
+    if (idx) HIP_TRY(hipMemcpyAsync(idx, c->topi, (size_t)T * c->K * 4, hipMemcpyDeviceToDevice, s));
+    return HY_OK;
+}
+
+int hy_moe_stack_forward(hy_moe_ctx* c, uint32_t first, uint32_t n, const float* x, uint32_t T, float eps,
+                         float* out, void* stream) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (n == 0 || first + n > c->layers.size()) return fail(HY_ERR_INVALID, "layer range out of bounds");
+    if (T == 0 || T > c->cfg.max_tokens) return fail(HY_ERR_INVALID, "T out of range");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t bytes = (size_t)T * c->H * 4;
+    HIP_TRY(hipMemcpyAsync(c->cur, x, bytes, hipMemcpyDeviceToDevice, s));
+    for (uint32_t l = 0; l < n; l++) {
+        HY_TRY(timed(c, hy::KID_RMSNORM, s, [&] { return hy::launch_rms_norm(c->cur, (int)T, c->H, eps, c->xn, s); }));
+        // residual fused into the combine; in place on cur (each element read then written by one thread)
+        HY_TRY(forward_impl(c, first + l, c->xn, T, c->cur, c->cur, s));
+    }
+    HIP_TRY(hipMemcpyAsync(out, c->cur, bytes, hipMemcpyDeviceToDevice, s));
+    return HY_OK;
+}
+
+// ---------------------------------------------------------------- stateless kernels
+int hy_router_topk(const float* x, const float* wr, uint32_t T, uint32_t H, uint32_t E, uint32_t K, int32_t norm,
+                   float scale, float* lg, float* w, int32_t* idx, void* stream) {
+    if (!x || !wr || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || H == 0 || H % 4 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
+        return fail(HY_ERR_INVALID, "bad router shape T=%u H=%u E=%u K=%u", T, H, E, K);
+    HIP_TRY(hy::launch_router(x, wr, (int)T, (int)H, (int)E, (int)K, norm, scale, lg, w, idx,
+                              static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_topkgating_easy(const float* lg, uint32_t T, uint32_t E, uint32_t K, float* w, int32_t* idx, void* stream) {
+    if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
+        return fail(HY_ERR_INVALID, "bad gating shape");
+    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, w, idx, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_softmax_rows(float* x, uint32_t rows, uint32_t n, void* stream) {
+    if (!x || rows == 0 || n == 0 || n > 1024) return fail(HY_ERR_INVALID, "bad softmax shape");
+    HIP_TRY(hy::launch_softmax_rows(x, (int)rows, (int)n, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_quantize_q8_0(const float* x, uint32_t rows, uint32_t n, void* blocks, void* stream) {
+    if (!x || !blocks || n % 32) return fail(HY_ERR_INVALID, "bad quantize arguments (n %% 32 == 0)");
+    HIP_TRY(hy::launch_quant_q8_0(x, (size_t)rows * n, nullptr, nullptr, nullptr, static_cast<uint8_t*>(blocks),
+                                  static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_dequantize(int32_t type, const void* blocks, size_t n, float* out, void* stream) {
+    if (!blocks || !out || n % 32) return fail(HY_ERR_INVALID, "bad dequantize arguments");
+    if (type != HY_TYPE_Q8_0 && type != HY_TYPE_Q4_0 && type != HY_TYPE_F32)
+        return fail(HY_ERR_UNSUPPORTED, "type %d", type);
+    HIP_TRY(hy::launch_dequant(type, static_cast<const uint8_t*>(blocks), n, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_block_dots(int32_t wtype, const void* w, const void* x, uint32_t rows, uint32_t n, int32_t path, int32_t* out,
+                  void* stream) {
+    if (!w || !x || !out || n % 32 || rows == 0 || rows > 4096) return fail(HY_ERR_INVALID, "bad block-dot args");
+    if (wtype != HY_TYPE_Q8_0 && wtype != HY_TYPE_Q4_0) return fail(HY_ERR_UNSUPPORTED, "wtype %d", wtype);
+    if (path != 0) return fail(HY_ERR_UNSUPPORTED, "path %d not built", path);
+    HIP_TRY(hy::launch_block_dots_valu(wtype, static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(x),
+                                       (int)rows, (int)(n / 32), out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_rms_norm(const float* x, uint32_t T, uint32_t H, float eps, float* out, void* stream) {
+    if (!x || !out || T == 0 || H == 0 || H % 4) return fail(HY_ERR_INVALID, "bad rms_norm args");
+    HIP_TRY(hy::launch_rms_norm(x, (int)T, (int)H, eps, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+// ---------------------------------------------------------------- memory / streams
+int hy_device_count(int* n) {
+    HIP_TRY(hipGetDeviceCount(n));
+    return HY_OK;
+}
+int hy_set_device(int d) {
+    HIP_TRY(hipSetDevice(d));
+    return HY_OK;
+}
+int hy_malloc(void** p, size_t bytes) {
+    if (hipMalloc(p, bytes) != hipSuccess) return fail(HY_ERR_NOMEM, "hipMalloc(%zu) failed", bytes);
+    return HY_OK;
+}
+int hy_free(void* p) {
+    HIP_TRY(hipFree(p));
+    return HY_OK;
+}
+int hy_memcpy_h2d(void* d, const void* s, size_t b) {
+    HIP_TRY(hipMemcpy(d, s, b, hipMemcpyHostToDevice));
+    return HY_OK;
+}
+int hy_memcpy_d2h(void* d, const void* s, size_t b) {
+    HIP_TRY(hipMemcpy(d, s, b, hipMemcpyDeviceToHost));
+    return HY_OK;
+}
+int hy_memset(void* d, int v, size_t b) {
+    HIP_TRY(hipMemset(d, v, b));
+    return HY_OK;
+}
+int hy_device_synchronize(void) {
+    HIP_TRY(hipDeviceSynchronize());
+    return HY_OK;
+}
+int hy_stream_create(void** s) {
+    hipStream_t st;
+    HIP_TRY(hipStreamCreate(&st));
+    *s = st;
+    return HY_OK;
+}
+int hy_stream_destroy(void* s) {
+    HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(s)));
+    return HY_OK;
+}
+int hy_stream_synchronize(void* s) {
+    HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(s)));
+    return HY_OK;
+}
+int hy_event_create(void** ev) {
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e));
+    *ev = e;
+    return HY_OK;
+}
+int hy_event_destroy(void* ev) {
+    HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+    return HY_OK;
+}
+int hy_event_record(void* ev, void* s) {
+    HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(s)));
+    return HY_OK;
+}
+int hy_event_elapsed_ms(void* a, void* b, float* ms) {
+    HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(b)));
+    HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)));
+    return HY_OK;
+}
+int hy_synth_fill(float* dev, size_t n, uint64_t seed, uint32_t layer, uint32_t tensor, uint32_t expert, float std,
+                  void* stream) {
+    if (!dev) return fail(HY_ERR_INVALID, "null pointer");
+    HIP_TRY(hy::launch_synth_fill(dev, n, hy::stream_key(seed, layer, tensor, expert), std * hy::NORM_SCALE,
+                                  static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+// ---------------------------------------------------------------- timing
+int hy_moe_prof_enable(hy_moe_ctx* c, int32_t on) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    HY_TRY(drain_prof(c));
+    c->prof = on != 0;
+    for (int i = 0; i < hy::KID_COUNT; i++) {
+        c->prof_n[i] = 0;
+        c->prof_ms[i] = 0.0;
+    }
+    return HY_OK;
+}
+int hy_moe_prof_read(hy_moe_ctx* c, int32_t kid, uint64_t* n, double* ms) {
+    if (!c || kid < 0 || kid >= hy::KID_COUNT) return fail(HY_ERR_INVALID, "bad kernel id");
+    HY_TRY(drain_prof(c));
+    if (n) *n = c->prof_n[kid];
+    if (ms) *ms = c->prof_ms[kid];
+    return HY_OK;
+}
+const char* hy_moe_prof_name(int32_t kid) { return (kid >= 0 && kid < hy::KID_COUNT) ? kKernelNames[kid] : ""; }
+int32_t hy_moe_prof_count(void) { return hy::KID_COUNT; }
+
+int hy_moe_last_routing(hy_moe_ctx* c, uint32_t* distinct, int32_t* counts) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    HIP_TRY(hipStreamSynchronize(c->last_stream));
+    int meta[4];
+    HIP_TRY(hipMemcpy(meta, c->meta, sizeof(meta), hipMemcpyDeviceToHost));
+    if (distinct) *distinct = (uint32_t)meta[2];
+    if (counts) HIP_TRY(hipMemcpy(counts, c->cnt, (size_t)c->E * 4, hipMemcpyDeviceToHost));
+    return HY_OK;
+}
+
+}  // extern "C"

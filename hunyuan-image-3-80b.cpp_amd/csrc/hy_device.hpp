@@ -1,0 +1,110 @@
+// hy_device.hpp -- device helpers shared by the gfx950 kernels of the MoE block.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hy {
+
+constexpr int QK = 32;       // GGUF block length (Q8_0 and Q4_0)
+constexpr int WAVE = 64;     // CDNA wavefront
+constexpr int MAX_E = 64;    // experts per layer handled by the routing kernels
+constexpr int MAX_K = 16;    // top-k bound
+
+// ---------------------------------------------------------------- fp16
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+// round to nearest even (v_cvt_f16_f32 in the default rounding mode)
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// ---------------------------------------------------------------- synthetic data
+// Counter-based generator: splitmix64 finaliser, normal approximated by the centred
+// sum of four 16-bit uniforms.  Integer ops plus one int->float conversion and one
+// float multiply, identical to the CPU definition.
+
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__host__ __device__ __forceinline__ uint64_t stream_key(uint64_t seed, uint32_t layer, uint32_t tensor,
+                                                        uint32_t expert) {
+    return mix64(mix64(seed) ^ (((uint64_t)layer << 40) | ((uint64_t)tensor << 24) | (uint64_t)expert));
+}
+
+constexpr float NORM_SCALE = 2.6428990e-05f;  // 1 / sqrt((65536^2 - 1) / 3)
+
+__device__ __forceinline__ float synth_normal(uint64_t key, uint64_t idx, float scale) {
+    uint64_t r = mix64(key ^ (idx * 0xD1B54A32D192ED03ull));
+    int32_t s = (int32_t)(r & 0xffffu) + (int32_t)((r >> 16) & 0xffffu) + (int32_t)((r >> 32) & 0xffffu) +
+                (int32_t)(r >> 48) - 131070;
+    return (float)s * scale;  // scale = stddev * NORM_SCALE, rounded once on the host
+}
+
+// tensor ids of the generator streams
+enum { TENSOR_X = 0, TENSOR_ROUTER = 1, TENSOR_GU = 2, TENSOR_DN = 3 };
+
+// ---------------------------------------------------------------- wave helpers
+
+template <typename T>
+__device__ __forceinline__ T shfl_down(T v, int d) { return __shfl_down(v, d, WAVE); }
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int m, int width = WAVE) { return __shfl_xor(v, m, width); }
+
+// Fold 64 lane partials in the fixed tree p[l] += p[l+s], s = 32..1; lane 0 holds
+// the result.  This is the reduction order the oracle restates.
+__device__ __forceinline__ float tree_sum64(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += shfl_down(v, s);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, shfl_xor(v, s));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += shfl_xor(v, s);
+    return v;
+}
+
+// ---------------------------------------------------------------- Q8_0 quantizer
+// ggml's scalar quantize_row_q8_0: d = amax/127, q = roundf(x * (1/d)), d stored as
+// fp16.  Called by the 32 lanes of a half-wave, one element each (xor width 32).
+struct Q8Result {
+    int8_t q;
+    uint16_t dh;
+};
+
+__device__ __forceinline__ Q8Result quant_q8_0_lane32(float x) {
+    float amax = fabsf(x);
+#pragma unroll
+    for (int s = 16; s >= 1; s >>= 1) amax = fmaxf(amax, shfl_xor(amax, s, 32));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    Q8Result r;
+    r.q = (int8_t)__builtin_roundf(x * id);
+    r.dh = f2h(d);
+    return r;
+}
+
+// ---------------------------------------------------------------- int8 dots
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// silu(g) * u exactly as the reference spells it (src/hunyuan_moe_full.cpp:484)
+__device__ __forceinline__ float swiglu(float g, float u) {
+    return g * (1.0f / (1.0f + expf(-g))) * u;
+}
+
+}  // namespace hy

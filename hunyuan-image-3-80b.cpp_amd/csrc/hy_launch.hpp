@@ -1,0 +1,60 @@
+// hy_launch.hpp -- host-side launchers of the MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/hy_moe.h"
+#include "hy_layout.hpp"
+
+namespace hy {
+
+// routing side (hy_route.hip)
+hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
+                         float* logits, float* topw, int* topi, hipStream_t s);
+hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, float* topw, int* topi, hipStream_t s);
+hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s);
+hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
+                             hipStream_t s);
+hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared, int* cnt,
+                           int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w, int* tile_e,
+                           int* tile_start, int* tile_n, int* meta, hipStream_t s);
+hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s);
+
+// expert products, VALU path (hy_ffn.hip)
+size_t ffn_up_smem(int wtype, int NT, int H);
+size_t ffn_down_smem(int wtype, int NT, int I);
+hipError_t launch_ffn_up_valu(int wtype, int NT, int max_tiles, const MatView& W, const Routing& R, const ActQ& X,
+                              const float* xf, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
+                              float* hf, hipStream_t s);
+hipError_t launch_ffn_down_valu(int wtype, int NT, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
+                                const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H,
+                                int I, int E, int K, float* y, const float* resid, float* out, hipStream_t s);
+hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, const float* resid, float* out,
+                          hipStream_t s);
+hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
+                                  hipStream_t s);
+
+// residency (hy_data.hip)
+hipError_t launch_synth_matrix(int wtype, uint64_t key, float scale, int rows, int cols, int gu_I, uint8_t* qs,
+                               uint16_t* sc, hipStream_t s);
+hipError_t launch_synth_fill(float* out, size_t n, uint64_t key, float scale, hipStream_t s);
+hipError_t launch_repack(int wtype, const uint8_t* src, int rows, int cols, int gu_I, uint8_t* qs, uint16_t* sc,
+                         hipStream_t s);
+hipError_t launch_dequant(int wtype, const uint8_t* src, size_t n, float* out, hipStream_t s);
+
+// kernel ids for per-kernel timing
+enum KernelId {
+    KID_QUANT = 0,
+    KID_ROUTER,
+    KID_DISPATCH,
+    KID_UP,
+    KID_DOWN,
+    KID_DOWN_SHARED,
+    KID_COMBINE,
+    KID_RMSNORM,
+    KID_COUNT
+};
+
+}  // namespace hy

@@ -1,0 +1,383 @@
+// hy_route.hip -- routing-side kernels: router GEMV + top-k, activation Q8_0
+// quantizer, token->expert dispatch, RMSNorm, softmax.
+#include "hy_device.hpp"
+#include "hy_launch.hpp"
+#include "hy_layout.hpp"
+
+namespace hy {
+
+// ----------------------------------------------------------------------------
+// Router.  Reference: src/hunyuan_moe_full.cpp:414-423 (GEMV), :41-50 (softmax),
+// :56-82 (top-k), :104-108 / :230-243 (renormalisation).
+//
+// logits[t][e]: lane l of a wave owns x/Wr elements h = 4l + 256i (+0..3) and
+// accumulates them with fmaf in increasing h; the 64 partials fold in the tree
+// p[l] += p[l+s], s = 32..1.  Top-k on the logits: K rounds of a wave max, lowest
+// lane among equal maxima (lower expert index wins ties), then weights
+// p_k = exp(l_k - m) / sum_e exp(l_e - m) renormalised by max(sum_k p_k, 1e-8).
+// One wave handles TPW tokens; experts are processed 8 at a time so each Wr
+// float4 feeds TPW tokens.
+// ----------------------------------------------------------------------------
+constexpr int ROUTER_TPW = 4;
+constexpr int ROUTER_WAVES = 4;
+
+__device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, float scale, int lane,
+                                          float* w_out, int* i_out) {
+    float v = lane < E ? v_in : -INFINITY;
+    const float orig = v;
+    float m0 = 0.0f;
+    float selv = 0.0f;
+    int seli = 0;
+    for (int k = 0; k < K; k++) {
+        const float m = wave_max(v);
+        const unsigned long long bal = __ballot(v == m);
+        const int sel = (int)__builtin_ctzll(bal);
+        if (k == 0) m0 = m;
+        if (lane == k) { selv = m; seli = sel; }
+        if (lane == sel) v = -INFINITY;
+    }
+    const float s = wave_sum(lane < E ? expf(orig - m0) : 0.0f);
+    // p_k for the lane's own rank k = lane (lanes >= K carry 0)
+    const float p = lane < K ? expf(selv - m0) / s : 0.0f;
+    // sum_k p_k in rank order (every lane computes the same value)
+    float ps = 0.0f;
+    for (int k = 0; k < K; k++) ps += __shfl(p, k, WAVE);
+    if (ps < 1e-8f) ps = 1e-8f;
+    if (lane < K) {
+        w_out[lane] = norm ? p / ps : p * scale;
+        i_out[lane] = seli;
+    }
+}
+
+__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_kernel(
+    const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, int K, int norm,
+    float scale, float* __restrict__ logits, float* __restrict__ topw, int* __restrict__ topi) {
+    __shared__ float lg[ROUTER_WAVES][ROUTER_TPW][MAX_E];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int t0 = (blockIdx.x * ROUTER_WAVES + wave) * ROUTER_TPW;
+
+    for (int eg = 0; eg < E; eg += 8) {
+        float acc[ROUTER_TPW][8];
+#pragma unroll
+        for (int t = 0; t < ROUTER_TPW; t++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[t][e] = 0.0f;
+        for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
+            float4 xv[ROUTER_TPW], wv[8];
+#pragma unroll
+            for (int t = 0; t < ROUTER_TPW; t++)
+                xv[t] = (t0 + t < T) ? *reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * H + h0)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                wv[e] = (eg + e < E) ? *reinterpret_cast<const float4*>(wr + (size_t)(eg + e) * H + h0)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int t = 0; t < ROUTER_TPW; t++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float a = acc[t][e];
+                    a = fmaf(xv[t].x, wv[e].x, a);
+                    a = fmaf(xv[t].y, wv[e].y, a);
+                    a = fmaf(xv[t].z, wv[e].z, a);
+                    a = fmaf(xv[t].w, wv[e].w, a);
+                    acc[t][e] = a;
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < ROUTER_TPW; t++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = tree_sum64(acc[t][e]);
+                if (lane == 0 && eg + e < E) lg[wave][t][eg + e] = v;
+            }
+    }
+    __syncthreads();
+    for (int t = 0; t < ROUTER_TPW; t++) {
+        const int tok = t0 + t;
+        if (tok >= T) break;
+        const float v = lane < E ? lg[wave][t][lane] : 0.0f;
+        if (logits && lane < E) logits[(size_t)tok * E + lane] = v;
+        topk_wave(v, E, K, norm, scale, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
+    }
+}
+
+hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
+                         float* logits, float* topw, int* topi, hipStream_t s) {
+    const int per_block = ROUTER_WAVES * ROUTER_TPW;
+    dim3 grid((T + per_block - 1) / per_block);
+    hipLaunchKernelGGL(router_kernel, grid, dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, K, norm, scale,
+                       logits, topw, topi);
+    return hipGetLastError();
+}
+
+// top-k gating from given logits (topkgating_easy, src/hunyuan_moe_full.cpp:88-113):
+// one wave per token.
+__global__ __launch_bounds__(256) void topk_from_logits_kernel(const float* __restrict__ logits, int T, int E,
+                                                               int K, float* topw, int* topi) {
+    const int tok = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (tok >= T) return;
+    const float v = lane < E ? logits[(size_t)tok * E + lane] : 0.0f;
+    topk_wave(v, E, K, 1, 1.0f, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
+}
+
+hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, float* topw, int* topi,
+                                   hipStream_t s) {
+    hipLaunchKernelGGL(topk_from_logits_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, topw, topi);
+    return hipGetLastError();
+}
+
+// softmax_f32 (src/hunyuan_moe_full.cpp:41-50) per row: max, exp, sum, divide.
+__global__ __launch_bounds__(256) void softmax_rows_kernel(float* x, int rows, int n) {
+    const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (row >= rows) return;
+    float* r = x + (size_t)row * n;
+    float m = -INFINITY;
+    for (int i = lane; i < n; i += WAVE) m = fmaxf(m, r[i]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int i = lane; i < n; i += WAVE) {
+        const float e = expf(r[i] - m);
+        r[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    for (int i = lane; i < n; i += WAVE) r[i] = r[i] / s;
+}
+
+hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s) {
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, rows, n);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------
+// Activation quantizer (ggml quantize_row_q8_0 definition).  One element per lane,
+// a half-wave per 32-block.  Writes the int8 plane, the scale as f32 (the exact
+// value of the fp16 scale), the block's int sum, and optionally GGUF blocks.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_q8_0_kernel(const float* __restrict__ x, size_t n,
+                                                         int8_t* __restrict__ q, float* __restrict__ d,
+                                                         int* __restrict__ qsum, uint8_t* __restrict__ blocks) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = idx < n;  // n is a multiple of 32: a half-wave is all live or all dead
+    const float v = live ? x[idx] : 0.0f;
+    const Q8Result r = quant_q8_0_lane32(v);
+    int s = r.q;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
+    if (!live) return;
+    const size_t b = idx / QK;
+    const int j = (int)(idx % QK);
+    if (q) q[idx] = r.q;
+    if (j == 0) {
+        if (d) d[b] = h2f(r.dh);
+        if (qsum) qsum[b] = s;
+    }
+    if (blocks) {
+        uint8_t* blk = blocks + b * 34;
+        blk[2 + j] = (uint8_t)r.q;
+        if (j == 0) {
+            blk[0] = (uint8_t)(r.dh & 0xff);
+            blk[1] = (uint8_t)(r.dh >> 8);
+        }
+    }
+}
+
+hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
+                             hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(quant_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, q, d, qsum,
+                       blocks);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------
+// Dispatch: counting sort of the T*K (token, expert) pairs by expert.  Within an
+// expert the order is the reference's capacity-slot priority
+// (src/hunyuan_moe_full.cpp:245-304): flat slot i = k*T + t ascending, i.e. all
+// rank-0 choices by token, then rank-1, ...  A pair's position inside its expert's
+// list is therefore the reference's dispatch_mask slot c.  Also builds the per-token
+// combine lists (pairs in ascending expert order, the einsum_combine summation
+// order of :387-397) and a list of tiles of at most NT pairs.
+// Single workgroup of 1024 threads; one token bitmap per expert in LDS per rank k
+// (T <= 16384).  Deterministic: no atomics except the bitmap ORs.
+// ----------------------------------------------------------------------------
+constexpr int DSP_THREADS = 1024;
+constexpr int DSP_MAX_WORDS = 512;  // 16384 tokens
+
+struct DispatchOut {
+    int* cnt;
+    int* off;
+    int* srt_tok;
+    int* pair_pos;
+    int* comb_pos;
+    float* comb_w;
+    int* tile_e;
+    int* tile_start;
+    int* tile_n;
+    int* meta;
+};
+
+__global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __restrict__ topi,
+                                                               const float* __restrict__ topw, int T, int K,
+                                                               int E, int NT, int has_shared, DispatchOut o) {
+    __shared__ uint32_t mask[MAX_E][DSP_MAX_WORDS];
+    __shared__ int part[MAX_E][16];
+    __shared__ int run_s[MAX_E];
+    __shared__ int off_s[MAX_E + 1];
+    __shared__ int toff_s[MAX_E + 1];
+    const int tid = threadIdx.x;
+    const int nwords = (T + 31) / 32;
+    const int e = tid / 16, c = tid % 16;  // 16 threads per expert, each a run of words
+    const int wpc = (nwords + 15) / 16;
+    const int w0 = c * wpc, w1 = min(nwords, w0 + wpc);
+    if (tid < MAX_E) run_s[tid] = 0;
+    for (int k = 0; k < K; k++) {
+        for (int i = tid; i < MAX_E * nwords; i += DSP_THREADS) mask[i / nwords][i % nwords] = 0u;
+        __syncthreads();
+        for (int t = tid; t < T; t += DSP_THREADS) {
+            const int ee = topi[t * K + k];
+            atomicOr(&mask[ee][t / 32], 1u << (t % 32));
+        }
+        __syncthreads();
+        int local = 0;
+        if (e < E)
+            for (int w = w0; w < w1; w++) local += __popc(mask[e][w]);
+        part[e][c] = local;
+        __syncthreads();
+        if (e < E) {
+            int rank = run_s[e];
+            for (int cc = 0; cc < c; cc++) rank += part[e][cc];
+            // relative position of each pair inside its expert, parked in pair_pos
+            for (int w = w0; w < w1; w++) {
+                uint32_t bits = mask[e][w];
+                while (bits) {
+                    const int bit = __builtin_ctz(bits);
+                    bits &= bits - 1;
+                    o.pair_pos[(w * 32 + bit) * K + k] = rank++;
+                }
+            }
+        }
+        __syncthreads();
+        if (c == 0 && e < E) {
+            int tot = 0;
+            for (int cc = 0; cc < 16; cc++) tot += part[e][cc];
+            run_s[e] += tot;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        int acc = 0, tacc = 0, distinct = 0;
+        for (int ee = 0; ee < E; ee++) {
+            off_s[ee] = acc;
+            toff_s[ee] = tacc;
+            acc += run_s[ee];
+            tacc += (run_s[ee] + NT - 1) / NT;
+            distinct += run_s[ee] > 0;
+        }
+        off_s[E] = acc;
+        toff_s[E] = tacc;
+        o.meta[0] = tacc;
+        o.meta[1] = tacc + (has_shared ? (T + NT - 1) / NT : 0);
+        o.meta[2] = distinct;
+    }
+    __syncthreads();
+    if (tid < E) {
+        o.cnt[tid] = run_s[tid];
+        o.off[tid] = off_s[tid];
+        const int nt = (run_s[tid] + NT - 1) / NT;
+        for (int j = 0; j < nt; j++) {
+            const int ti = toff_s[tid] + j;
+            o.tile_e[ti] = tid;
+            o.tile_start[ti] = j * NT;
+            o.tile_n[ti] = min(NT, run_s[tid] - j * NT);
+        }
+    }
+    if (tid == E) o.off[E] = off_s[E];
+    if (has_shared) {
+        const int ns = (T + NT - 1) / NT;
+        for (int j = tid; j < ns; j += DSP_THREADS) {
+            const int ti = toff_s[E] + j;
+            o.tile_e[ti] = E;
+            o.tile_start[ti] = j * NT;
+            o.tile_n[ti] = min(NT, T - j * NT);
+        }
+    }
+    // absolute positions and the sorted token list (each thread rewrites only the
+    // pairs it reads, so no barrier is needed between the read and the write)
+    for (int p = tid; p < T * K; p += DSP_THREADS) {
+        const int pos = off_s[topi[p]] + o.pair_pos[p];
+        o.pair_pos[p] = pos;
+        o.srt_tok[pos] = p / K;
+    }
+    __syncthreads();
+    // combine lists: each token's pairs sorted by expert id
+    for (int t = tid; t < T; t += DSP_THREADS) {
+        int ek[MAX_K], pk[MAX_K];
+        float wk[MAX_K];
+        for (int k = 0; k < K; k++) {
+            ek[k] = topi[t * K + k];
+            pk[k] = o.pair_pos[t * K + k];
+            wk[k] = topw[t * K + k];
+        }
+        for (int a = 1; a < K; a++) {
+            const int ea = ek[a], pa = pk[a];
+            const float wa = wk[a];
+            int b = a - 1;
+            while (b >= 0 && ek[b] > ea) {
+                ek[b + 1] = ek[b];
+                pk[b + 1] = pk[b];
+                wk[b + 1] = wk[b];
+                b--;
+            }
+            ek[b + 1] = ea;
+            pk[b + 1] = pa;
+            wk[b + 1] = wa;
+        }
+        for (int k = 0; k < K; k++) {
+            o.comb_pos[t * K + k] = pk[k];
+            o.comb_w[t * K + k] = wk[k];
+        }
+    }
+}
+
+hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared,
+                           int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w,
+                           int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s) {
+    DispatchOut o{cnt, off, srt_tok, pair_pos, comb_pos, comb_w, tile_e, tile_start, tile_n, meta};
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), 0, s, topi, topw, T, K, E, NT, has_shared, o);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------
+// RMSNorm with unit weight (src/rms_norm.cpp:9-33): sum of squares in the router's
+// blocked fmaf order, then x * (1 / sqrtf(ss / H + eps)).  One wave per row.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, int T, int H, float eps,
+                                                       float* __restrict__ out) {
+    const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (row >= T) return;
+    const float* xr = x + (size_t)row * H;
+    float a = 0.0f;
+    for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + h0);
+        a = fmaf(v.x, v.x, a);
+        a = fmaf(v.y, v.y, a);
+        a = fmaf(v.z, v.z, a);
+        a = fmaf(v.w, v.w, a);
+    }
+    const float ss = __shfl(tree_sum64(a), 0, WAVE);
+    const float rms = 1.0f / sqrtf(ss / (float)H + eps);
+    float* o = out + (size_t)row * H;
+    for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + h0);
+        *reinterpret_cast<float4*>(o + h0) = make_float4(v.x * rms, v.y * rms, v.z * rms, v.w * rms);
+    }
+}
+
+hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, T, H, eps, out);
+    return hipGetLastError();
+}
+
+}  // namespace hy

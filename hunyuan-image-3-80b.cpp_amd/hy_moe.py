@@ -1,0 +1,331 @@
+"""Python binding of libhy_moe.so (the C ABI in include/hy_moe.h), for the tests
+and the benchmark.  Device memory is handled through the library's own helpers
+(hy_malloc / hy_memcpy_*), host arrays are numpy.
+
+The GPU path has no fallback: if libhy_moe.so is missing or no GPU is present the
+calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhy_moe.so")
+ROOT = os.path.dirname(HERE)
+HEADER = os.path.join(ROOT, "include", "hy_moe.h")
+
+F32, Q4_0, Q8_0 = 0, 2, 8
+TENSOR_X, TENSOR_ROUTER, TENSOR_GU, TENSOR_DN = 0, 1, 2, 3
+
+
+class HyError(RuntimeError):
+    pass
+
+
+class Config(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32), ("intermediate", C.c_uint32), ("num_experts", C.c_uint32),
+        ("topk", C.c_uint32), ("num_layers", C.c_uint32), ("max_tokens", C.c_uint32),
+        ("wtype", C.c_int32), ("has_shared", C.c_int32), ("norm_topk_prob", C.c_int32),
+        ("routed_scaling_factor", C.c_float), ("group_limited_greedy", C.c_int32),
+        ("drop_tokens", C.c_int32), ("compute_aux_loss", C.c_int32), ("device", C.c_int32),
+    ]
+
+
+_vp = C.c_void_p
+_u32, _i32, _u64, _f = C.c_uint32, C.c_int32, C.c_uint64, C.c_float
+_SIGS = {
+    "hy_last_error": (C.c_char_p, []),
+    "hy_moe_create": (C.c_int, [C.POINTER(Config), C.POINTER(_vp)]),
+    "hy_moe_destroy": (C.c_int, [_vp]),
+    "hy_moe_layer_bytes": (C.c_size_t, [_vp]),
+    "hy_moe_upload_layer": (C.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp]),
+    "hy_moe_synth_layer": (C.c_int, [_vp, _u32, _u64, _f, _vp]),
+    "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
+    "hy_moe_forward_debug": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
+    "hy_moe_stack_forward": (C.c_int, [_vp, _u32, _u32, _vp, _u32, _f, _vp, _vp]),
+    "hy_router_topk": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _i32, _f, _vp, _vp, _vp, _vp]),
+    "hy_topkgating_easy": (C.c_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "hy_softmax_rows": (C.c_int, [_vp, _u32, _u32, _vp]),
+    "hy_quantize_q8_0": (C.c_int, [_vp, _u32, _u32, _vp, _vp]),
+    "hy_dequantize": (C.c_int, [_i32, _vp, C.c_size_t, _vp, _vp]),
+    "hy_block_dots": (C.c_int, [_i32, _vp, _vp, _u32, _u32, _i32, _vp, _vp]),
+    "hy_rms_norm": (C.c_int, [_vp, _u32, _u32, _f, _vp, _vp]),
+    "hy_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "hy_set_device": (C.c_int, [C.c_int]),
+    "hy_malloc": (C.c_int, [C.POINTER(_vp), C.c_size_t]),
+    "hy_free": (C.c_int, [_vp]),
+    "hy_memcpy_h2d": (C.c_int, [_vp, _vp, C.c_size_t]),
+    "hy_memcpy_d2h": (C.c_int, [_vp, _vp, C.c_size_t]),
+    "hy_memset": (C.c_int, [_vp, C.c_int, C.c_size_t]),
+    "hy_device_synchronize": (C.c_int, []),
+    "hy_stream_create": (C.c_int, [C.POINTER(_vp)]),
+    "hy_stream_destroy": (C.c_int, [_vp]),
+    "hy_stream_synchronize": (C.c_int, [_vp]),
+    "hy_event_create": (C.c_int, [C.POINTER(_vp)]),
+    "hy_event_destroy": (C.c_int, [_vp]),
+    "hy_event_record": (C.c_int, [_vp, _vp]),
+    "hy_event_elapsed_ms": (C.c_int, [_vp, _vp, C.POINTER(C.c_float)]),
+    "hy_synth_fill": (C.c_int, [_vp, C.c_size_t, _u64, _u32, _u32, _u32, _f, _vp]),
+    "hy_moe_prof_enable": (C.c_int, [_vp, _i32]),
+    "hy_moe_prof_read": (C.c_int, [_vp, _i32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]),
+    "hy_moe_prof_name": (C.c_char_p, [_i32]),
+    "hy_moe_prof_count": (_i32, []),
+    "hy_moe_last_routing": (C.c_int, [_vp, C.POINTER(_u32), _vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libhy_moe.so; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HyError(f"{LIB_PATH} is not built: run python hunyuan-image-3-80b.cpp_amd/build.py")
+        L = C.CDLL(LIB_PATH, mode=os.RTLD_LAZY | os.RTLD_LOCAL)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise HyError(f"hy error {rc}: {lib().hy_last_error().decode()}")
+
+
+def device_count():
+    n = C.c_int(0)
+    rc = lib().hy_device_count(C.byref(n))
+    return n.value if rc == 0 else 0
+
+
+# ------------------------------------------------------------------ device buffers
+
+class Buf:
+    """Device allocation of `nbytes`, freed with the object."""
+
+    def __init__(self, nbytes, dtype=np.float32, shape=None):
+        self.nbytes = int(max(nbytes, 1))
+        self.dtype = np.dtype(dtype)
+        self.shape = shape
+        p = _vp()
+        check(lib().hy_malloc(C.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes, a.dtype, a.shape)
+        check(lib().hy_memcpy_h2d(b.ptr, a.ctypes.data, a.nbytes))
+        return b
+
+    @classmethod
+    def empty(cls, shape, dtype=np.float32):
+        dt = np.dtype(dtype)
+        return cls(int(np.prod(shape)) * dt.itemsize, dt, tuple(shape))
+
+    def zero(self):
+        check(lib().hy_memset(self.ptr, 0, self.nbytes))
+        return self
+
+    def numpy(self, shape=None, dtype=None):
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        shp = shape if shape is not None else (self.shape if self.shape is not None else (self.nbytes // dt.itemsize,))
+        out = np.empty(shp, dtype=dt)
+        check(lib().hy_device_synchronize())
+        check(lib().hy_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().hy_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def sync():
+    check(lib().hy_device_synchronize())
+
+
+# ------------------------------------------------------------------ context
+
+class Moe:
+    """A resident MoE stack (hy_moe_ctx)."""
+
+    def __init__(self, H, I, E, K, wtype, num_layers=1, max_tokens=64, has_shared=True, norm_topk_prob=True,
+                 routed_scaling_factor=1.0, device=0, **unsupported):
+        c = Config()
+        c.hidden, c.intermediate, c.num_experts, c.topk = H, I, E, K
+        c.num_layers, c.max_tokens, c.wtype = num_layers, max_tokens, wtype
+        c.has_shared, c.norm_topk_prob = int(has_shared), int(norm_topk_prob)
+        c.routed_scaling_factor = routed_scaling_factor
+        c.group_limited_greedy = int(unsupported.get("group_limited_greedy", 0))
+        c.drop_tokens = int(unsupported.get("drop_tokens", 0))
+        c.compute_aux_loss = int(unsupported.get("compute_aux_loss", 0))
+        c.device = device
+        self.cfg = c
+        self.H, self.I, self.E, self.K, self.wtype = H, I, E, K, wtype
+        self.max_tokens = max_tokens
+        h = _vp()
+        check(lib().hy_moe_create(C.byref(c), C.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hy_moe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def layer_bytes(self):
+        return lib().hy_moe_layer_bytes(self.h)
+
+    def upload(self, layer_idx, layer):
+        """layer: an oracle Layer (GGUF-layout numpy arrays)."""
+        def p(a):
+            return None if a is None else np.ascontiguousarray(a).ctypes.data
+        keep = [np.ascontiguousarray(a) for a in (layer.router, layer.shared_gu, layer.shared_dn, layer.gu, layer.dn)
+                if a is not None]
+        check(lib().hy_moe_upload_layer(self.h, layer_idx, p(layer.router), p(layer.shared_gu), p(layer.shared_dn),
+                                        p(layer.gu), p(layer.dn)))
+        del keep
+
+    def synth(self, layer_idx, seed=42, std=0.02, router_bias=None):
+        b = None
+        if router_bias is not None:
+            b = np.ascontiguousarray(router_bias, dtype=np.float32)
+        check(lib().hy_moe_synth_layer(self.h, layer_idx, seed, std, None if b is None else b.ctypes.data))
+
+    def forward(self, layer_idx, x: Buf, T, out: Buf, stream=None):
+        check(lib().hy_moe_forward(self.h, layer_idx, x.ptr, T, out.ptr, stream))
+
+    def forward_debug(self, layer_idx, x: Buf, T, out: Buf, lg: Buf, w: Buf, idx: Buf, stream=None):
+        check(lib().hy_moe_forward_debug(self.h, layer_idx, x.ptr, T, out.ptr, lg.ptr if lg else None,
+                                         w.ptr if w else None, idx.ptr if idx else None, stream))
+
+    def stack_forward(self, first, n, x: Buf, T, eps, out: Buf, stream=None):
+        check(lib().hy_moe_stack_forward(self.h, first, n, x.ptr, T, eps, out.ptr, stream))
+
+    def prof_enable(self, on=True):
+        check(lib().hy_moe_prof_enable(self.h, int(on)))
+
+    def prof_read(self):
+        res = {}
+        for k in range(lib().hy_moe_prof_count()):
+            n = C.c_uint64()
+            ms = C.c_double()
+            check(lib().hy_moe_prof_read(self.h, k, C.byref(n), C.byref(ms)))
+            res[lib().hy_moe_prof_name(k).decode()] = (n.value, ms.value)
+        return res
+
+    def last_routing(self):
+        d = C.c_uint32()
+        counts = np.zeros(self.E, dtype=np.int32)
+        check(lib().hy_moe_last_routing(self.h, C.byref(d), counts.ctypes.data))
+        return d.value, counts
+
+    # convenience: host in, host out
+    def run(self, layer_idx, x, debug=False):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        xb = Buf.from_array(x)
+        ob = Buf.empty((T, self.H))
+        if not debug:
+            self.forward(layer_idx, xb, T, ob)
+            return ob.numpy()
+        lg = Buf.empty((T, self.E))
+        w = Buf.empty((T, self.K))
+        idx = Buf.empty((T, self.K), np.int32)
+        self.forward_debug(layer_idx, xb, T, ob, lg, w, idx)
+        return ob.numpy(), lg.numpy(), w.numpy(), idx.numpy()
+
+
+# ------------------------------------------------------------------ stateless kernels
+
+def router_topk(x, wr, K, norm=True, scale=1.0):
+    x = np.ascontiguousarray(x, np.float32)
+    wr = np.ascontiguousarray(wr, np.float32)
+    T, H = x.shape
+    E = wr.shape[0]
+    xb, wb = Buf.from_array(x), Buf.from_array(wr)
+    lg, w, idx = Buf.empty((T, E)), Buf.empty((T, K)), Buf.empty((T, K), np.int32)
+    check(lib().hy_router_topk(xb.ptr, wb.ptr, T, H, E, K, int(norm), scale, lg.ptr, w.ptr, idx.ptr, None))
+    return lg.numpy(), w.numpy(), idx.numpy()
+
+
+def topkgating_easy(logits, K):
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    lb = Buf.from_array(logits)
+    w, idx = Buf.empty((T, K)), Buf.empty((T, K), np.int32)
+    check(lib().hy_topkgating_easy(lb.ptr, T, E, K, w.ptr, idx.ptr, None))
+    return w.numpy(), idx.numpy()
+
+
+def softmax_rows(x):
+    x = np.ascontiguousarray(x, np.float32)
+    b = Buf.from_array(x)
+    check(lib().hy_softmax_rows(b.ptr, x.shape[0], x.shape[1], None))
+    return b.numpy()
+
+
+def quantize_q8_0(x):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    xb = Buf.from_array(x)
+    ob = Buf.empty((rows, n // 32 * 34), np.uint8)
+    check(lib().hy_quantize_q8_0(xb.ptr, rows, n, ob.ptr, None))
+    return ob.numpy()
+
+
+def dequantize(blocks, wtype, n):
+    bb = Buf.from_array(np.ascontiguousarray(blocks))
+    ob = Buf.empty((n,))
+    check(lib().hy_dequantize(wtype, bb.ptr, n, ob.ptr, None))
+    return ob.numpy()
+
+
+def block_dots(wtype, w_blocks, x_blocks, rows, n, path=0):
+    wb = Buf.from_array(np.ascontiguousarray(w_blocks))
+    xb = Buf.from_array(np.ascontiguousarray(x_blocks))
+    ob = Buf.empty((rows, n // 32), np.int32)
+    check(lib().hy_block_dots(wtype, wb.ptr, xb.ptr, rows, n, path, ob.ptr, None))
+    return ob.numpy()
+
+
+def rms_norm(x, eps=1e-5):
+    x = np.ascontiguousarray(x, np.float32)
+    xb = Buf.from_array(x)
+    ob = Buf.empty(x.shape)
+    check(lib().hy_rms_norm(xb.ptr, x.shape[0], x.shape[1], eps, ob.ptr, None))
+    return ob.numpy()
+
+
+def synth_fill(n, seed, layer, tensor, expert, std):
+    b = Buf.empty((n,))
+    check(lib().hy_synth_fill(b.ptr, n, seed, layer, tensor, expert, std, None))
+    return b.numpy()
+
+
+def header_symbols(path=HEADER):
+    """Function names declared in include/hy_moe.h."""
+    import re
+    txt = open(path).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(hy_[a-z_0-9]+)\s*\(", txt, flags=re.M)))

@@ -1,0 +1,189 @@
+/*
+ * hy_moe.h -- C ABI of the MI355X (gfx950) HunyuanImage-3 MoE feed-forward block.
+ *
+ * Plain pointers and sizes only.  "dev" pointers are device (HBM) addresses, "host"
+ * pointers are ordinary host memory; `stream` is a hipStream_t passed as void*
+ * (NULL = the default stream).  Every function returns HY_OK (0) or a negative
+ * hy_status; hy_last_error() gives a message for the calling thread's last failure.
+ * On failure nothing is written to caller-owned outputs.
+ *
+ * The reference's interface for this path is the C++ API of
+ * src/hunyuan_moe_full.h:76-155 plus moe_forward_cpu / swiglu_ffn_f32 /
+ * MoEWeights (src/hunyuan_model.h:118-156).  Each entry point below names the
+ * reference function it replaces.  include/hunyuan_moe_full.h re-exposes the
+ * reference's own names and signatures on top of this ABI.
+ */
+#ifndef HY_MOE_H
+#define HY_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    HY_OK = 0,
+    HY_ERR_INVALID = -1,     /* bad argument or shape */
+    HY_ERR_UNSUPPORTED = -2, /* routing feature or weight type the GPU path does not run */
+    HY_ERR_HIP = -3,         /* HIP runtime error */
+    HY_ERR_NOMEM = -4,       /* device allocation failed */
+    HY_ERR_STATE = -5        /* e.g. layer not loaded */
+} hy_status;
+
+/* ggml_type values accepted as weight formats (ggml.h numbering). */
+enum { HY_TYPE_F32 = 0, HY_TYPE_Q4_0 = 2, HY_TYPE_Q8_0 = 8 };
+
+/* Shapes and routing of one resident MoE stack.  The routing fields mirror
+ * MoERoutingConfig (src/hunyuan_moe_full.h:25-47); the GPU runs the default
+ * subset (softmax -> top-k -> renormalise or scale), and hy_moe_create rejects
+ * group-limited greedy, token dropping and the aux loss with HY_ERR_UNSUPPORTED. */
+typedef struct {
+    uint32_t hidden;        /* H, multiple of 32 */
+    uint32_t intermediate;  /* I, multiple of 32 */
+    uint32_t num_experts;   /* E, 1..64 */
+    uint32_t topk;          /* K, 1..min(E, 16) */
+    uint32_t num_layers;    /* resident layers */
+    uint32_t max_tokens;    /* largest T per call, 1..16384; sizes the work arena */
+    int32_t  wtype;         /* HY_TYPE_F32 / HY_TYPE_Q8_0 / HY_TYPE_Q4_0 */
+    int32_t  has_shared;    /* 1: one shared expert (num_shared_expert = 1) */
+    int32_t  norm_topk_prob;
+    float    routed_scaling_factor;
+    int32_t  group_limited_greedy; /* must be 0 */
+    int32_t  drop_tokens;          /* must be 0 */
+    int32_t  compute_aux_loss;     /* must be 0 */
+    int32_t  device;               /* HIP device ordinal */
+} hy_moe_config;
+
+typedef struct hy_moe_ctx hy_moe_ctx;
+
+const char* hy_last_error(void);
+
+/* ---- context and resident weights ---------------------------------------- */
+
+/* Replaces the per-call weight handling of moe_forward_full
+ * (src/hunyuan_moe_full.h:121-142) and the layer streaming of
+ * HunyuanFullModel::forward (src/hunyuan_full_model.cpp:193-207): every layer's
+ * router, shared expert and routed experts stay resident in HBM. */
+int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out);
+int hy_moe_destroy(hy_moe_ctx* ctx);
+/* bytes of HBM the resident weights of one layer take */
+size_t hy_moe_layer_bytes(const hy_moe_ctx* ctx);
+
+/* Upload one layer from host memory in ggml layout (ne0 = in-features, GGUF
+ * blocks of 32 along it).  Replaces StackedExpertWeights::build_from_experts
+ * (src/hunyuan_extended.cpp:8-26) and the tensors load_layer_weights reads
+ * (src/hunyuan_gguf_loader.cpp:229-280):
+ *   router    f32 [E][H]                         (blk.N.ffn_gate.weight)
+ *   shared_gu wtype rows [2I][H]                 (blk.N.ffn_shared_gate_up.weight)
+ *   shared_dn wtype rows [H][I]                  (blk.N.ffn_shared_down.weight)
+ *   gu        wtype rows [E][2I][H], expert-major (blk.N.ffn_expert_E_gate_up.weight)
+ *   dn        wtype rows [E][H][I]               (blk.N.ffn_expert_E_down.weight)
+ * Rows [0,I) of a gate_up matrix are the gate (SiLU) half, [I,2I) the up half, as
+ * src/hunyuan_moe_full.cpp:482-485 reads them. */
+int hy_moe_upload_layer(hy_moe_ctx* ctx, uint32_t layer, const float* router_host,
+                        const void* shared_gu_host, const void* shared_dn_host,
+                        const void* gu_host, const void* dn_host);
+
+/* Generate one layer on the device from the counter-based synthetic generator
+ * (weights ~ N(0,std) quantized to wtype; router ~ N(0,std), column 0 replaced
+ * by router_bias_host[E] when given).  Same values as the oracle's synth_layer. */
+int hy_moe_synth_layer(hy_moe_ctx* ctx, uint32_t layer, uint64_t seed, float std,
+                       const float* router_bias_host);
+
+/* ---- forward ------------------------------------------------------------- */
+
+/* One MoE layer: out = shared(x) + sum_k w_k expert_k(x).
+ * Replaces moe_forward_full (src/hunyuan_moe_full.h:121-142, .cpp:405-516) and its
+ * twin moe_forward_cpu (src/hunyuan_model.h:147-156, src/attention.cpp:191-313).
+ * x_dev, out_dev: f32 [T][H] device; 1 <= T <= max_tokens.  Stream-ordered. */
+int hy_moe_forward(hy_moe_ctx* ctx, uint32_t layer, const float* x_dev, uint32_t T,
+                   float* out_dev, void* stream);
+
+/* Same, also copying the routing into caller device buffers (any may be NULL):
+ * logits [T][E] f32, weights [T][K] f32, indices [T][K] i32 in rank order.
+ * Mirrors moe_forward_cpu's debug_router_* outputs (src/attention.cpp:278-280). */
+int hy_moe_forward_debug(hy_moe_ctx* ctx, uint32_t layer, const float* x_dev, uint32_t T,
+                         float* out_dev, float* logits_dev, float* weights_dev,
+                         int32_t* indices_dev, void* stream);
+
+/* n_layers x [ RMSNorm(eps, unit weight) -> MoE -> residual add ] over resident
+ * layers first..first+n_layers-1.  The decoder-layer MoE half of
+ * decoder_layer_forward_cpu (src/decoder_layer.cpp:33-42) with rms_norm_f32
+ * (src/rms_norm.cpp:9-33), stacked. */
+int hy_moe_stack_forward(hy_moe_ctx* ctx, uint32_t first_layer, uint32_t n_layers,
+                         const float* x_dev, uint32_t T, float eps, float* out_dev, void* stream);
+
+/* ---- stateless kernels (component parity) ----------------------------------- */
+
+/* Router: logits = x Wr^T (64-lane blocked fmaf order), top-k on logits with lower
+ * index winning ties, weights = softmax at the selection renormalised (or scaled).
+ * Replaces the router GEMV of src/hunyuan_moe_full.cpp:414-423 plus
+ * topkgating_easy (src/hunyuan_moe_full.h:83-89). */
+int hy_router_topk(const float* x_dev, const float* wr_dev, uint32_t T, uint32_t H, uint32_t E,
+                   uint32_t K, int32_t norm_topk_prob, float routed_scaling_factor,
+                   float* logits_dev, float* weights_dev, int32_t* indices_dev, void* stream);
+
+/* topkgating_easy (src/hunyuan_moe_full.h:83-89) from precomputed logits. */
+int hy_topkgating_easy(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K,
+                       float* weights_dev, int32_t* indices_dev, void* stream);
+
+/* softmax_f32 (src/hunyuan_moe_full.h:148) over each of `rows` rows of n (n <= 1024). */
+int hy_softmax_rows(float* x_dev, uint32_t rows, uint32_t n, void* stream);
+
+/* Activation quantizer: rows of n f32 -> GGUF Q8_0 blocks (34 B), ggml's scalar
+ * quantize_row_q8_0 definition.  The same device code feeds the expert GEMMs. */
+int hy_quantize_q8_0(const float* x_dev, uint32_t rows, uint32_t n, void* blocks_dev, void* stream);
+
+/* GGUF dequantization (src/hunyuan_gguf_loader.cpp:10-72 block formats; Q4_0 in the
+ * GGUF nibble order) of n elements of type `type` into f32. */
+int hy_dequantize(int32_t type, const void* blocks_dev, size_t n, float* out_dev, void* stream);
+
+/* Exact per-32-block int32 dots of weight blocks (Q8_0 or Q4_0 rows) with Q8_0
+ * activation blocks, computed by the device dot routines the expert kernels use:
+ * out[r][b] = sum_j w[r][b][j] * x[b][j].  `path` 0 = VALU dot4 routine, 1 = MFMA tile
+ * routine.  rows <= 4096. */
+int hy_block_dots(int32_t wtype, const void* w_blocks_dev, const void* x_blocks_dev, uint32_t rows,
+                  uint32_t n, int32_t path, int32_t* out_dev, void* stream);
+
+/* RMSNorm with unit weight (blocked sum of squares, eps) over T rows of H. */
+int hy_rms_norm(const float* x_dev, uint32_t T, uint32_t H, float eps, float* out_dev, void* stream);
+
+/* ---- device memory / streams / timing helpers ------------------------------ */
+int hy_device_count(int* n);
+int hy_set_device(int device);
+int hy_malloc(void** p, size_t bytes);
+int hy_free(void* p);
+int hy_memcpy_h2d(void* dst_dev, const void* src_host, size_t bytes);
+int hy_memcpy_d2h(void* dst_host, const void* src_dev, size_t bytes);
+int hy_memset(void* dst_dev, int value, size_t bytes);
+int hy_device_synchronize(void);
+int hy_stream_create(void** stream);
+int hy_stream_destroy(void* stream);
+int hy_stream_synchronize(void* stream);
+int hy_event_create(void** ev);
+int hy_event_destroy(void* ev);
+int hy_event_record(void* ev, void* stream);
+int hy_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Fill f32 [n] with the synthetic N(0,std) stream (seed, layer, tensor, expert). */
+int hy_synth_fill(float* dev, size_t n, uint64_t seed, uint32_t layer, uint32_t tensor,
+                  uint32_t expert, float std, void* stream);
+
+/* Per-kernel timing of the forward path, recorded with HIP events on the launch
+ * stream.  While enabled, every kernel launch of hy_moe_forward* is bracketed by
+ * events; hy_moe_prof_read returns, per kernel id, the launch count and total
+ * milliseconds since the last reset.  Names via hy_moe_prof_name. */
+int hy_moe_prof_enable(hy_moe_ctx* ctx, int32_t on);
+int hy_moe_prof_read(hy_moe_ctx* ctx, int32_t kernel_id, uint64_t* launches, double* total_ms);
+const char* hy_moe_prof_name(int32_t kernel_id);
+int32_t hy_moe_prof_count(void);
+
+/* Counters of the last forward (host copy after completion): distinct routed
+ * experts D, and tokens routed to each expert (counts [E]). */
+int hy_moe_last_routing(hy_moe_ctx* ctx, uint32_t* distinct, int32_t* counts_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

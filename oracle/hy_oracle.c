@@ -118,7 +118,10 @@ size_t hyo_type_row_bytes(int type, size_t n) {
  * computed as roundf(x * (1/d)); d stored as fp16 (round to nearest even). */
 void hyo_quantize_row_q8_0(const float* x, void* vy, size_t n) {
     hyo_block_q8_0* y = (hyo_block_q8_0*)vy;
-    for (size_t b = 0; b < n / HYO_QK; b++) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
+#endif
+    for (int64_t b = 0; b < (int64_t)(n / HYO_QK); b++) {
         const float* xb = x + b * HYO_QK;
         float amax = 0.0f;
         for (int j = 0; j < HYO_QK; j++) {
@@ -137,7 +140,10 @@ void hyo_quantize_row_q8_0(const float* x, void* vy, size_t n) {
  * byte j, element j+16 to the high nibble. */
 void hyo_quantize_row_q4_0(const float* x, void* vy, size_t n) {
     hyo_block_q4_0* y = (hyo_block_q4_0*)vy;
-    for (size_t b = 0; b < n / HYO_QK; b++) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
+#endif
+    for (int64_t b = 0; b < (int64_t)(n / HYO_QK); b++) {
         const float* xb = x + b * HYO_QK;
         float amax = 0.0f, max = 0.0f;
         for (int j = 0; j < HYO_QK; j++) {
@@ -302,7 +308,10 @@ float hyo_synth_normal(uint64_t key, uint64_t idx, float stddev) {
 }
 
 void hyo_synth_fill(uint64_t key, uint64_t idx0, size_t n, float stddev, float* out) {
-    for (size_t i = 0; i < n; i++) out[i] = hyo_synth_normal(key, idx0 + i, stddev);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
+#endif
+    for (int64_t i = 0; i < (int64_t)n; i++) out[i] = hyo_synth_normal(key, idx0 + (uint64_t)i, stddev);
 }
 
 /* ======================================================================

@@ -1,0 +1,231 @@
+"""GPU parity: every kernel of the MoE block through the C ABI against the oracle.
+
+Bars: bit-exact for integer/byte/index work (quantized blocks, int dots, expert
+indices, dispatch positions) and for the operations that share a defined order
+with the oracle (router logits, RMSNorm, synthetic weights); layer outputs within
+normwise max relative error 1e-3 and cosine >= 0.99999 of the oracle's q semantics.
+"""
+import numpy as np
+import pytest
+
+import hy_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+COS_TOL = 0.99999
+
+
+def rel_err(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def cosine(a, b):
+    a = a.astype(np.float64).ravel()
+    b = b.astype(np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def assert_close(got, ref, what=""):
+    e, c = rel_err(got, ref), cosine(got, ref)
+    assert e <= REL_TOL and c >= COS_TOL, f"{what}: rel_err={e:.3e} cos={c:.8f}"
+
+
+# ------------------------------------------------------------------ data kernels
+
+def test_synth_fill_bit_exact(gpu):
+    for (seed, layer, tensor, expert, std) in [(42, 0, 2, 5, 0.02), (7, 31, 3, 64, 1.0)]:
+        got = gpu.synth_fill(100_003, seed, layer, tensor, expert, std)
+        ref = O.synth(seed, layer, tensor, expert, (100_003,), std)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_quantize_q8_0_bytes(gpu):
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal((37, 4096)) * np.exp(rng.standard_normal((37, 1)) * 3)).astype(np.float32)
+    x[0, :32] = 0.0                      # all-zero block
+    x[1, :32] = np.linspace(-1, 1, 32)   # exact .5 ties after scaling
+    x[2, 32:64] = 1e-30                  # subnormal-range scale
+    got = gpu.quantize_q8_0(x)
+    ref = O.quantize(x, O.Q8_0)
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+def test_dequantize_bit_exact(gpu, wtype):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((8, 1024)).astype(np.float32)
+    q = O.quantize(x, wtype)
+    got = gpu.dequantize(q, wtype, x.size)
+    ref = O.dequantize(q, wtype, 1024).ravel()
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+def test_block_dots_exact(gpu, wtype):
+    rng = np.random.default_rng(2)
+    rows, n = 33, 4096
+    w = O.quantize(rng.standard_normal((rows, n)).astype(np.float32), wtype)
+    if wtype == O.Q8_0:   # full int8 range incl. -128
+        wq = w.reshape(rows, n // 32, 34)
+        wq[:, :, 2:] = rng.integers(0, 256, size=wq[:, :, 2:].shape, dtype=np.uint8)
+        w = wq.reshape(rows, -1)
+    x = O.quantize(rng.standard_normal((1, n)).astype(np.float32), O.Q8_0)
+    xb = x.reshape(n // 32, 34)
+    xb[0, 2:] = np.uint8(0x80)            # a block of -128
+    got = gpu.block_dots(wtype, w, x, rows, n, path=0)
+    f = O.lib().hyo_block_dots_q8_0_q8_0 if wtype == O.Q8_0 else O.lib().hyo_block_dots_q4_0_q8_0
+    for r in range(rows):
+        ref = np.zeros(n // 32, np.int32)
+        f(O.vp(np.ascontiguousarray(w[r])), O.vp(x), n, O.ip(ref))
+        np.testing.assert_array_equal(got[r], ref)
+
+
+# ------------------------------------------------------------------ routing
+
+@pytest.mark.parametrize("T,H,E,K", [(37, 4096, 64, 8), (5, 256, 16, 4), (1, 4096, 64, 8), (64, 512, 8, 2)])
+def test_router_logits_and_indices_bit_exact(gpu, T, H, E, K):
+    x = O.synth(3, 0, O.T_X, 0, (T, H), 1.0)
+    wr = O.synth(3, 0, O.T_ROUTER, 0, (E, H), 0.02)
+    wr[E // 2] = wr[1]            # identical experts: equal logits, lower index must win
+    lg, w, idx = gpu.router_topk(x, wr, K)
+    ref_lg = O.router_logits_blocked(x, wr)
+    np.testing.assert_array_equal(lg.view(np.uint32), ref_lg.view(np.uint32))
+    ref_w, ref_idx = O.route_topk(ref_lg, K)
+    np.testing.assert_array_equal(idx, ref_idx)
+    np.testing.assert_allclose(w, ref_w, rtol=2e-6, atol=1e-7)
+
+
+def test_router_scaling_without_norm(gpu):
+    T, H, E, K = 9, 256, 16, 4
+    x = O.synth(4, 0, O.T_X, 0, (T, H), 1.0)
+    wr = O.synth(4, 0, O.T_ROUTER, 0, (E, H), 0.1)
+    lg, w, idx = gpu.router_topk(x, wr, K, norm=False, scale=2.5)
+    ref_w, ref_idx = O.route_topk(O.router_logits_blocked(x, wr), K, norm=False, scale=2.5)
+    np.testing.assert_array_equal(idx, ref_idx)
+    np.testing.assert_allclose(w, ref_w, rtol=2e-6)
+
+
+def test_topkgating_easy_from_logits(gpu):
+    rng = np.random.default_rng(5)
+    T, E, K = 50, 64, 8
+    lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    w, idx = gpu.topkgating_easy(lg, K)
+    rw = np.zeros((T, K), np.float32)
+    ri = np.zeros((T, K), np.int32)
+    O.lib().hyo_topkgating_easy(O.fp(lg), T, E, K, O.fp(rw), O.ip(ri))
+    np.testing.assert_array_equal(idx, ri)
+    np.testing.assert_allclose(w, rw, rtol=2e-6)
+
+
+def test_softmax_rows(gpu):
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((7, 64)) * 3).astype(np.float32)
+    got = gpu.softmax_rows(x)
+    ref = x.copy()
+    for r in range(7):
+        O.lib().hyo_softmax_f32(O.fp(ref[r]), 64)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-9)
+
+
+def test_rms_norm_bit_exact(gpu):
+    T, H = 19, 4096
+    x = O.synth(8, 0, O.T_X, 0, (T, H), 1.5)
+    got = gpu.rms_norm(x, 1e-5)
+    ss = np.array([O.router_logits_blocked(x[t:t + 1], x[t:t + 1])[0, 0] for t in range(T)], np.float32)
+    rms = np.float32(1.0) / np.sqrt(ss / np.float32(H) + np.float32(1e-5))
+    ref = (x * rms[:, None]).astype(np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ whole layer
+
+SMALL = dict(H=256, I=128, E=16, K=4)
+
+
+@pytest.fixture(scope="module")
+def small_layers():
+    return {wt: O.synth_layer(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], wt, seed=11, std=0.05)
+            for wt in (O.Q8_0, O.Q4_0, O.F32)}
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+@pytest.mark.parametrize("T", [1, 3, 17, 64, 100])
+def test_layer_small(gpu, small_layers, wtype, T):
+    layer = small_layers[wtype]
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], wtype, max_tokens=128)
+    m.upload(0, layer)
+    x = O.synth(12 + T, 0, O.T_X, 0, (T, SMALL["H"]), 1.0)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+    np.testing.assert_array_equal(lg.view(np.uint32), rlg.view(np.uint32))
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=2e-6, atol=1e-7)
+    assert_close(out, ref, f"wtype={wtype} T={T}")
+    m.close()
+
+
+def test_layer_without_shared_expert(gpu, small_layers):
+    base = small_layers[O.Q8_0]
+    layer = O.Layer(base.H, base.I, base.E, base.K, O.Q8_0, base.router, None, None, base.gu, base.dn)
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q8_0, max_tokens=32, has_shared=False)
+    m.upload(0, layer)
+    x = O.synth(30, 0, O.T_X, 0, (20, SMALL["H"]), 1.0)
+    assert_close(m.run(0, x), O.moe_forward_q(layer, x), "no shared")
+    m.close()
+
+
+def test_device_synth_equals_host_upload(gpu):
+    H, I, E, K = 256, 128, 16, 4
+    for wt in (O.Q8_0, O.Q4_0):
+        host = O.synth_layer(H, I, E, K, wt, seed=77, layer=3, std=0.02)
+        a = gpu.Moe(H, I, E, K, wt, max_tokens=16, num_layers=4)
+        a.upload(3, host)
+        a.synth(2, seed=77, std=0.02)   # wrong layer index on purpose: different weights
+        b = gpu.Moe(H, I, E, K, wt, max_tokens=16, num_layers=4)
+        b.synth(3, seed=77, std=0.02)
+        x = O.synth(5, 0, O.T_X, 0, (16, H), 1.0)
+        ya, yb = a.run(3, x), b.run(3, x)
+        np.testing.assert_array_equal(ya.view(np.uint32), yb.view(np.uint32))
+        assert not np.array_equal(a.run(2, x), ya)
+        a.close()
+        b.close()
+
+
+def test_forward_is_deterministic(gpu, small_layers):
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q4_0, max_tokens=128)
+    m.upload(0, small_layers[O.Q4_0])
+    x = O.synth(40, 0, O.T_X, 0, (100, SMALL["H"]), 1.0)
+    a, b = m.run(0, x), m.run(0, x)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    m.close()
+
+
+def test_stack_matches_oracle(gpu):
+    H, I, E, K, L, T = 256, 128, 16, 4, 3, 24
+    layers = [O.synth_layer(H, I, E, K, O.Q8_0, seed=5, layer=l, std=0.05) for l in range(L)]
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=T, num_layers=L)
+    for l in range(L):
+        m.synth(l, seed=5, std=0.05)
+    x = O.synth(6, 0, O.T_X, 0, (T, H), 1.0)
+    xb = gpu.Buf.from_array(x)
+    ob = gpu.Buf.empty((T, H))
+    m.stack_forward(0, L, xb, T, 1e-5, ob)
+    got = ob.numpy()
+    ref = O.moe_stack_q(layers, x, eps=1e-5)
+    assert_close(got, ref, "stack")
+    m.close()
+
+
+def test_invalid_token_count_rejected(gpu, small_layers):
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q8_0, max_tokens=8)
+    xb = gpu.Buf.empty((16, SMALL["H"]))
+    ob = gpu.Buf.empty((16, SMALL["H"]))
+    with pytest.raises(gpu.HyError):
+        m.forward(0, xb, 4, ob)          # layer not loaded
+    m.upload(0, small_layers[O.Q8_0])
+    with pytest.raises(gpu.HyError):
+        m.forward(0, xb, 16, ob)         # T > max_tokens
+    with pytest.raises(gpu.HyError):
+        m.forward(0, xb, 0, ob)
+    m.close()
