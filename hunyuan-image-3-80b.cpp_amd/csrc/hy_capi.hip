@@ -111,6 +111,7 @@ struct hy_moe_ctx {
     double prof_ms[hy::KID_COUNT] = {};
 
     hipStream_t last_stream = nullptr;
+    int path = 0;  // HY_PATH_AUTO / _VALU / _MFMA
 };
 
 namespace {
@@ -163,6 +164,9 @@ int timed(hy_moe_ctx* c, int kid, hipStream_t s, F&& launch) {
 }
 
 int tile_bound_routed(int T, int K, int E, int NT) { return (T * K + E * (NT - 1)) / NT; }
+
+// largest batch the decode GEMV takes in AUTO mode; above it the MFMA grouped GEMM
+constexpr uint32_t kGemvMaxTokens = 16;
 
 int check_cfg(const hy_moe_config* c) {
     if (!c) return fail(HY_ERR_INVALID, "null config");
@@ -229,15 +233,21 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int H = c->H, I = c->I, E = c->E, K = c->K, wt = c->cfg.wtype;
     const int iT = (int)T;
     const int has_shared = c->cfg.has_shared ? 1 : 0;
-    if (wt != HY_TYPE_F32)
+    // small batches quantize the activations inside the selection pass, large ones in
+    // a bandwidth-shaped kernel of their own
+    const bool fuse_quant = wt != HY_TYPE_F32 && T <= 32;
+    if (wt != HY_TYPE_F32 && !fuse_quant)
         HY_TRY(timed(c, hy::KID_QUANT, s, [&] {
             return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
         }));
     HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
-        return hy::launch_router(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob, c->cfg.routed_scaling_factor,
-                                 c->logits, c->topw, c->topi, s);
+        return hy::launch_router_q(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob, c->cfg.routed_scaling_factor,
+                                   c->logits, c->topw, c->topi, fuse_quant ? c->xq : nullptr, c->xd, c->xs, s);
     }));
-    const int NT = T <= 64 ? 8 : 16;
+    // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode
+    const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) &&
+                      (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
+    const int NT = mfma ? hy::mfma_tile_tokens() : hy::gemv_tile_tokens();
     HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
         return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
                                    c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
@@ -247,18 +257,36 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const hy::ActQ X{c->xq, c->xd, c->xs, H};
     const int routed_bound = tile_bound_routed(iT, K, E, NT);
     const int shared_tiles = has_shared ? (iT + NT - 1) / NT : 0;
+    if (mfma) {
+        HY_TRY(timed(c, hy::KID_UP, s, [&] {
+            return hy::launch_ffn_up_mfma(wt, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
+                                          c->hd, c->hs, s);
+        }));
+        HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
+            return hy::launch_ffn_down_mfma(wt, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
+                                            c->y, nullptr, nullptr, s);
+        }));
+        if (has_shared)
+            HY_TRY(timed(c, hy::KID_DOWN_SHARED, s, [&] {
+                return hy::launch_ffn_down_mfma(wt, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
+                                                c->y, resid, out, s);
+            }));
+        else
+            HY_TRY(timed(c, hy::KID_COMBINE, s, [&] { return hy::launch_combine(R, c->y, iT, H, K, resid, out, s); }));
+        return HY_OK;
+    }
     HY_TRY(timed(c, hy::KID_UP, s, [&] {
-        return hy::launch_ffn_up_valu(wt, NT, routed_bound + shared_tiles, gu_view(c, L), R, X, x, iT, H, I, E, K,
-                                      c->hq, c->hd, c->hs, c->hf, s);
+        return hy::launch_gemv_up(wt, routed_bound + shared_tiles, gu_view(c, L), R, X, x, iT, H, I, E, K, c->hq,
+                                  c->hd, c->hs, c->hf, s);
     }));
     HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
-        return hy::launch_ffn_down_valu(wt, NT, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT,
-                                        H, I, E, K, c->y, nullptr, nullptr, s);
+        return hy::launch_gemv_down(wt, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT, H, I, E,
+                                    K, c->y, nullptr, nullptr, s);
     }));
     if (has_shared) {
         HY_TRY(timed(c, hy::KID_DOWN_SHARED, s, [&] {
-            return hy::launch_ffn_down_valu(wt, NT, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf,
-                                            iT, H, I, E, K, c->y, resid, out, s);
+            return hy::launch_gemv_down(wt, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT, H, I,
+                                        E, K, c->y, resid, out, s);
         }));
     } else {
         HY_TRY(timed(c, hy::KID_COMBINE, s, [&] { return hy::launch_combine(R, c->y, iT, H, K, resid, out, s); }));
@@ -454,7 +482,7 @@ int hy_moe_stack_forward(hy_moe_ctx* c, uint32_t first, uint32_t n, const float*
 // ---------------------------------------------------------------- stateless kernels
 int hy_router_topk(const float* x, const float* wr, uint32_t T, uint32_t H, uint32_t E, uint32_t K, int32_t norm,
                    float scale, float* lg, float* w, int32_t* idx, void* stream) {
-    if (!x || !wr || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
+    if (!x || !wr || !lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
     if (T == 0 || H == 0 || H % 4 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
         return fail(HY_ERR_INVALID, "bad router shape T=%u H=%u E=%u K=%u", T, H, E, K);
     HIP_TRY(hy::launch_router(x, wr, (int)T, (int)H, (int)E, (int)K, norm, scale, lg, w, idx,
@@ -582,6 +610,15 @@ int hy_synth_fill(float* dev, size_t n, uint64_t seed, uint32_t layer, uint32_t 
 }
 
 // ---------------------------------------------------------------- timing
+int hy_moe_set_path(hy_moe_ctx* c, int32_t path) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (path < HY_PATH_AUTO || path > HY_PATH_MFMA) return fail(HY_ERR_INVALID, "path %d", path);
+    if (path == HY_PATH_MFMA && !hy::mfma_path_ok(c->cfg.wtype, c->H, c->I))
+        return fail(HY_ERR_UNSUPPORTED, "the MFMA path needs Q8_0/Q4_0 weights and H, I multiples of 128");
+    c->path = path;
+    return HY_OK;
+}
+
 int hy_moe_prof_enable(hy_moe_ctx* c, int32_t on) {
     if (!c) return fail(HY_ERR_INVALID, "null ctx");
     HY_TRY(drain_prof(c));

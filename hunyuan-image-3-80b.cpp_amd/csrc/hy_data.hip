@@ -40,7 +40,8 @@ __device__ void quant_block_q8_0(const float* v, int8_t* qs32, uint16_t* dh) {
 }
 
 // Synthetic matrix of one expert: rows x cols ~ N(0,std) from stream key, element
-// index r*cols+c, quantized per 32-block and stored at packed row perm(r).
+// index r*cols+c, quantized per 32-block and stored at packed row perm(r) of the
+// row-group-interleaved layout.
 // One thread per block.
 __global__ void synth_matrix_kernel(int wtype, uint64_t key, float scale, int rows, int cols, int gu_I,
                                     uint8_t* __restrict__ qs, uint16_t* __restrict__ sc) {
@@ -51,14 +52,14 @@ __global__ void synth_matrix_kernel(int wtype, uint64_t key, float scale, int ro
     const int pr = gu_I > 0 ? gu_packed_row(r, gu_I) : r;
     float v[QK];
     for (int j = 0; j < QK; j++) v[j] = synth_normal(key, (uint64_t)r * cols + (uint64_t)b * QK + j, scale);
+    uint8_t* dq = qs + il_q_offset(pr, b, nb, block_bytes(wtype));
     if (wtype == HY_TYPE_F32) {
-        float* dst = reinterpret_cast<float*>(qs) + (size_t)pr * cols + (size_t)b * QK;
+        float* dst = reinterpret_cast<float*>(dq);
         for (int j = 0; j < QK; j++) dst[j] = v[j];
     } else if (wtype == HY_TYPE_Q8_0) {
-        quant_block_q8_0(v, reinterpret_cast<int8_t*>(qs) + (size_t)pr * cols + (size_t)b * QK,
-                         sc + (size_t)pr * nb + b);
+        quant_block_q8_0(v, reinterpret_cast<int8_t*>(dq), sc + il_s_offset(pr, b, nb));
     } else {
-        quant_block_q4_0(v, qs + (size_t)pr * (cols / 2) + (size_t)b * 16, sc + (size_t)pr * nb + b);
+        quant_block_q4_0(v, dq, sc + il_s_offset(pr, b, nb));
     }
 }
 
@@ -81,7 +82,8 @@ hipError_t launch_synth_fill(float* out, size_t n, uint64_t key, float scale, hi
     return hipGetLastError();
 }
 
-// GGUF rows (ggml layout, blocks of 34 / 18 bytes, or raw f32) -> resident layout.
+// GGUF rows (ggml layout, blocks of 34 / 18 bytes, or raw f32) -> resident
+// row-group-interleaved layout.
 __global__ void repack_kernel(int wtype, const uint8_t* __restrict__ src, int rows, int cols, int gu_I,
                               uint8_t* __restrict__ qs, uint16_t* __restrict__ sc) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -89,20 +91,19 @@ __global__ void repack_kernel(int wtype, const uint8_t* __restrict__ src, int ro
     if (idx >= (size_t)rows * nb) return;
     const int r = (int)(idx / nb), b = (int)(idx % nb);
     const int pr = gu_I > 0 ? gu_packed_row(r, gu_I) : r;
+    uint8_t* dq = qs + il_q_offset(pr, b, nb, block_bytes(wtype));
     if (wtype == HY_TYPE_F32) {
         const float* s = reinterpret_cast<const float*>(src) + (size_t)r * cols + (size_t)b * QK;
-        float* d = reinterpret_cast<float*>(qs) + (size_t)pr * cols + (size_t)b * QK;
+        float* d = reinterpret_cast<float*>(dq);
         for (int j = 0; j < QK; j++) d[j] = s[j];
     } else if (wtype == HY_TYPE_Q8_0) {
         const uint8_t* blk = src + ((size_t)r * nb + b) * 34;
-        sc[(size_t)pr * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
-        uint8_t* d = qs + (size_t)pr * cols + (size_t)b * QK;
-        for (int j = 0; j < QK; j++) d[j] = blk[2 + j];
+        sc[il_s_offset(pr, b, nb)] = (uint16_t)(blk[0] | (blk[1] << 8));
+        for (int j = 0; j < QK; j++) dq[j] = blk[2 + j];
     } else {
         const uint8_t* blk = src + ((size_t)r * nb + b) * 18;
-        sc[(size_t)pr * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
-        uint8_t* d = qs + (size_t)pr * (cols / 2) + (size_t)b * 16;
-        for (int j = 0; j < 16; j++) d[j] = blk[2 + j];
+        sc[il_s_offset(pr, b, nb)] = (uint16_t)(blk[0] | (blk[1] << 8));
+        for (int j = 0; j < 16; j++) dq[j] = blk[2 + j];
     }
 }
 

@@ -102,9 +102,30 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-// silu(g) * u exactly as the reference spells it (src/hunyuan_moe_full.cpp:484)
+// exp(x) spelled out so the CPU oracle evaluates the same operations: Cody-Waite
+// reduction x = n*ln2 + r (ln2 split in a 16-bit head, exact n*head, and a tail),
+// e^r by its Taylor series to degree 7 in Horner form with fmaf, scaling by 2^n.
+__device__ __forceinline__ float hy_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269504f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.42860682e-6f, r);
+    float p = 1.98412698e-4f;
+    p = fmaf(p, r, 1.38888889e-3f);
+    p = fmaf(p, r, 8.33333377e-3f);
+    p = fmaf(p, r, 4.16666679e-2f);
+    p = fmaf(p, r, 1.66666672e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
+
+// silu(g) * u as the reference spells it (src/hunyuan_moe_full.cpp:484), with hy_expf
 __device__ __forceinline__ float swiglu(float g, float u) {
-    return g * (1.0f / (1.0f + expf(-g))) * u;
+    return g * (1.0f / (1.0f + hy_expf(-g))) * u;
 }
 
 }  // namespace hy

@@ -1,0 +1,334 @@
+// hy_gemv.hip -- expert products for decode-sized batches: a dequant-GEMV that
+// streams each expert's weights once from HBM, plus the combine kernel.
+//
+// One wave owns one 64-row group of the row-group-interleaved weights: lane l owns
+// row l and walks the blocks b = 0, 1, ... in order, so per block the wave reads one
+// contiguous 64-row chunk (2 KB Q8_0 / 1 KB Q4_0 / 8 KB F32) plus 128 B of fp16
+// scales, and every output accumulates its blocks in the order the oracle does:
+//   acc = fmaf((float)s_b, d_w * d_x, acc)   (s_b = exact int32 block dot, dot4)
+//   acc = fmaf(w_k, x_k, acc)                (F32 rows)
+// The tile's activation rows sit in LDS and are read as broadcasts.
+//
+// Work item of the up kernel: (tile, 4 row groups).  A tile is up to NT tokens
+// routed to one expert (or NT consecutive tokens for the shared expert).  gate_up
+// rows are packed so a 64-row group is 32 SiLU rows + the matching 32 linear rows:
+// lanes 0..31 hold g, lanes 32..63 the matching u, and h = silu(g) * u
+// (src/hunyuan_moe_full.cpp:479-486) is quantized to Q8_0 by the 32 gate lanes
+// (ggml quantizes src1 of every quantized matmul).
+// The down kernel's work item is (tile, 4 groups of 64 output rows).  Routed tiles
+// write y[pair][row]; shared tiles fuse the combine
+//   out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e * y_e[t] )
+// (src/hunyuan_moe_full.cpp:503-515, einsum_combine order :387-397).
+#include "hy_device.hpp"
+#include "hy_launch.hpp"
+#include "hy_layout.hpp"
+
+namespace hy {
+
+constexpr int GV_WAVES = 4;
+constexpr int GV_THREADS = GV_WAVES * WAVE;
+constexpr int GV_UNROLL = 4;  // blocks whose weights are loaded ahead of use
+
+// exact int dot of one Q8_0 weight block with one Q8_0 activation block
+__device__ __forceinline__ int dot_q8_block(const int4 w0, const int4 w1, const int4 a0, const int4 a1) {
+    int s = dot4(w0.x, a0.x, 0);
+    s = dot4(w0.y, a0.y, s);
+    s = dot4(w0.z, a0.z, s);
+    s = dot4(w0.w, a0.w, s);
+    s = dot4(w1.x, a1.x, s);
+    s = dot4(w1.y, a1.y, s);
+    s = dot4(w1.z, a1.z, s);
+    s = dot4(w1.w, a1.w, s);
+    return s;
+}
+
+// exact int dot of one Q4_0 weight block (16 B, GGUF nibble order: byte j = element
+// j | element j+16 << 4) with a Q8_0 activation block whose int sum is asum:
+// sum (n-8)*x = sum n*x - 8*sum x.
+__device__ __forceinline__ int dot_q4_block(const int4 w, const int4 a0, const int4 a1, int asum) {
+    const int m = 0x0F0F0F0F;
+    int s = dot4(w.x & m, a0.x, 0);
+    s = dot4(w.y & m, a0.y, s);
+    s = dot4(w.z & m, a0.z, s);
+    s = dot4(w.w & m, a0.w, s);
+    s = dot4((w.x >> 4) & m, a1.x, s);
+    s = dot4((w.y >> 4) & m, a1.y, s);
+    s = dot4((w.z >> 4) & m, a1.z, s);
+    s = dot4((w.w >> 4) & m, a1.w, s);
+    return s - 8 * asum;
+}
+
+struct GvArgs {
+    MatView W;
+    Routing R;
+    const int8_t* aq;   // activations: x (mode 0) or h (modes 1, 2), int8 [rows][Kd]
+    const float* ad;    // scales [rows][Kd/32]
+    const int* as;      // block sums [rows][Kd/32]
+    const float* af;    // f32 activations (F32 weights): x or hf
+    int T, H, I, E, K;
+    int Kd;             // reduction length
+    int n_groups;       // 64-row groups of the weight matrix
+    int8_t* hq;         // mode 0 outputs
+    float* hd;
+    int* hs;
+    float* hf;
+    float* y;           // mode 1 output / mode 2 input
+    const float* resid;
+    float* out;
+};
+
+template <int WT, int NT, int MODE>
+__global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int tok_s[NT], slot_s[NT];
+    const int tile = (MODE == 2) ? a.R.meta[0] + (int)blockIdx.x : (int)blockIdx.x;
+    if (tile >= a.R.meta[MODE == 1 ? 0 : 1]) return;
+    const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
+    const bool shared = e == a.E;
+    const int Kd = a.Kd, nb = Kd / QK;
+    if (threadIdx.x < NT) {
+        const int i = threadIdx.x;
+        int tok = 0, slot = 0;
+        if (i < n) {
+            if (shared) {
+                tok = start + i;
+                slot = a.T * a.K + tok;
+            } else {
+                slot = a.R.off[e] + start + i;
+                tok = a.R.srt_tok[slot];
+            }
+        }
+        tok_s[i] = tok;
+        slot_s[i] = slot;
+    }
+    __syncthreads();
+    // stage the tile's quantized activation rows (int8), scales and block sums
+    int8_t* xs_l = reinterpret_cast<int8_t*>(smem);
+    float* xd_l = reinterpret_cast<float*>(smem + (size_t)NT * Kd);
+    int* xsum_l = reinterpret_cast<int*>(smem + (size_t)NT * Kd + (size_t)NT * nb * 4);
+    if (WT != HY_TYPE_F32) {
+        const int vec_per_row = Kd / 16;
+        for (int v = threadIdx.x; v < NT * vec_per_row; v += GV_THREADS) {
+            const int i = v / vec_per_row, c = v % vec_per_row;
+            int4 val = make_int4(0, 0, 0, 0);
+            if (i < n) {
+                const int row = MODE == 0 ? tok_s[i] : slot_s[i];
+                val = reinterpret_cast<const int4*>(a.aq + (size_t)row * Kd)[c];
+            }
+            reinterpret_cast<int4*>(xs_l + (size_t)i * Kd)[c] = val;
+        }
+        for (int v = threadIdx.x; v < NT * nb; v += GV_THREADS) {
+            const int i = v / nb, b = v % nb;
+            const int row = MODE == 0 ? tok_s[i] : slot_s[i];
+            xd_l[v] = i < n ? a.ad[(size_t)row * nb + b] : 0.0f;
+            if (WT == HY_TYPE_Q4_0) xsum_l[v] = i < n ? a.as[(size_t)row * nb + b] : 0;
+        }
+    }
+    __syncthreads();
+
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int G = blockIdx.y * GV_WAVES + wave;
+    if (G >= a.n_groups) return;
+    float acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) acc[i] = 0.0f;
+
+    if (WT == HY_TYPE_F32) {
+        const float* wbase = reinterpret_cast<const float*>(a.W.qs + (size_t)e * a.W.qs_stride) +
+                             ((size_t)G * nb * 64 + lane) * QK;
+        for (int b = 0; b < nb; b++) {
+            const float4* wv = reinterpret_cast<const float4*>(wbase + (size_t)b * 64 * QK);
+            float4 w[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) w[c] = wv[c];
+#pragma unroll
+            for (int i = 0; i < NT; i++) {
+                if (i < n) {
+                    const int row = MODE == 0 ? tok_s[i] : slot_s[i];
+                    const float4* xv = reinterpret_cast<const float4*>(a.af + (size_t)row * Kd + (size_t)b * QK);
+                    float s = acc[i];
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        const float4 xx = xv[c];
+                        s = fmaf(w[c].x, xx.x, s);
+                        s = fmaf(w[c].y, xx.y, s);
+                        s = fmaf(w[c].z, xx.z, s);
+                        s = fmaf(w[c].w, xx.w, s);
+                    }
+                    acc[i] = s;
+                }
+            }
+        }
+    } else {
+        constexpr int BPB = WT == HY_TYPE_Q8_0 ? 32 : 16;
+        const uint8_t* wbase = a.W.qs + (size_t)e * a.W.qs_stride + ((size_t)G * nb * 64 + lane) * BPB;
+        const uint16_t* sbase = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64 + lane;
+        for (int b0 = 0; b0 < nb; b0 += GV_UNROLL) {
+            int4 w0[GV_UNROLL], w1[GV_UNROLL];
+            float dw[GV_UNROLL];
+#pragma unroll
+            for (int u = 0; u < GV_UNROLL; u++) {
+                const int b = b0 + u;
+                if (b < nb) {
+                    const int4* p = reinterpret_cast<const int4*>(wbase + (size_t)b * 64 * BPB);
+                    w0[u] = p[0];
+                    if (WT == HY_TYPE_Q8_0) w1[u] = p[1];
+                    dw[u] = h2f(sbase[(size_t)b * 64]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < GV_UNROLL; u++) {
+                const int b = b0 + u;
+                if (b >= nb) break;
+#pragma unroll
+                for (int i = 0; i < NT; i++) {
+                    if (i < n) {
+                        const int4* xb = reinterpret_cast<const int4*>(xs_l + (size_t)i * Kd + b * QK);
+                        const int s = WT == HY_TYPE_Q8_0 ? dot_q8_block(w0[u], w1[u], xb[0], xb[1])
+                                                         : dot_q4_block(w0[u], xb[0], xb[1], xsum_l[i * nb + b]);
+                        acc[i] = fmaf((float)s, dw[u] * xd_l[i * nb + b], acc[i]);
+                    }
+                }
+            }
+        }
+    }
+
+    if (MODE == 0) {
+        // lanes 0..31: gate rows 32G+lane, lanes 32..63: the matching up rows
+        const int nb_i = a.I / QK;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (i >= n) break;
+            const float u = __shfl(acc[i], (lane + 32) % WAVE, WAVE);
+            const float h = swiglu(acc[i], u);
+            const size_t slot = (size_t)slot_s[i];
+            if (WT == HY_TYPE_F32) {
+                if (lane < 32) a.hf[slot * a.I + (size_t)G * QK + lane] = h;
+            } else {
+                const Q8Result r = quant_q8_0_lane32(h);
+                int s = r.q;
+#pragma unroll
+                for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
+                if (lane < 32) {
+                    a.hq[slot * a.I + (size_t)G * QK + lane] = r.q;
+                    if (lane == 0) {
+                        a.hd[slot * nb_i + G] = h2f(r.dh);
+                        a.hs[slot * nb_i + G] = s;
+                    }
+                }
+            }
+        }
+    } else {
+        const int row = G * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (i >= n) break;
+            if (MODE == 1) {
+                a.y[(size_t)slot_s[i] * a.H + row] = acc[i];
+            } else {
+                const int t = tok_s[i];
+                float comb = 0.0f;
+                for (int k = 0; k < a.K; k++)
+                    comb = fmaf(a.R.comb_w[t * a.K + k], a.y[(size_t)a.R.comb_pos[t * a.K + k] * a.H + row], comb);
+                const float o = acc[i] + comb;
+                a.out[(size_t)t * a.H + row] = a.resid ? a.resid[(size_t)t * a.H + row] + o : o;
+            }
+        }
+    }
+}
+
+// combine without a shared expert: out[t] = residual[t] + sum_{e ascending} w_e y_e[t]
+__global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __restrict__ y, int T, int H, int K,
+                                                      const float* __restrict__ resid, float* __restrict__ out) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)T * H) return;
+    const int t = (int)(idx / H), row = (int)(idx % H);
+    float comb = 0.0f;
+    for (int k = 0; k < K; k++) comb = fmaf(R.comb_w[t * K + k], y[(size_t)R.comb_pos[t * K + k] * H + row], comb);
+    out[idx] = resid ? resid[idx] + comb : comb;
+}
+
+// ---------------------------------------------------------------------------- launchers
+int gemv_tile_tokens() { return GEMV_NT; }
+
+size_t gemv_smem(int wtype, int Kd) {
+    if (wtype == HY_TYPE_F32) return 16;
+    return (size_t)GEMV_NT * Kd + (size_t)GEMV_NT * (Kd / QK) * 8;
+}
+
+template <int MODE>
+static hipError_t gemv_launch(int wtype, dim3 grid, size_t smem, hipStream_t s, const GvArgs& a) {
+    switch (wtype) {
+    case HY_TYPE_Q8_0:
+        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS), smem, s, a);
+        break;
+    case HY_TYPE_Q4_0:
+        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS), smem, s, a);
+        break;
+    default:
+        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_F32, GEMV_NT, MODE>), grid, dim3(GV_THREADS), smem, s, a);
+        break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
+                          int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
+                          hipStream_t s) {
+    GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, hq, hd, hs, hf, nullptr, nullptr, nullptr};
+    dim3 grid(max_tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
+    return gemv_launch<0>(wtype, grid, gemv_smem(wtype, H), s, a);
+}
+
+hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
+                            const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
+                            int E, int K, float* y, const float* resid, float* out, hipStream_t s) {
+    GvArgs a{W, R, hq, hd, hs, hf, T, H, I, E, K, I, H / 64, nullptr, nullptr, nullptr, nullptr, y, resid, out};
+    dim3 grid(n_tiles_bound, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
+    return mode == 0 ? gemv_launch<1>(wtype, grid, gemv_smem(wtype, I), s, a)
+                     : gemv_launch<2>(wtype, grid, gemv_smem(wtype, I), s, a);
+}
+
+hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, const float* resid, float* out,
+                          hipStream_t s) {
+    const size_t n = (size_t)T * H;
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, y, T, H, K, resid, out);
+    return hipGetLastError();
+}
+
+// per-block dots through the GEMV dot routines (parity entry point); GGUF blocks in,
+// one thread per (row, block)
+__global__ void block_dots_valu_kernel(int wtype, const uint8_t* __restrict__ w, const uint8_t* __restrict__ x,
+                                       int rows, int nb, int* __restrict__ out) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * nb) return;
+    const int r = idx / nb, b = idx % nb;
+    // GGUF blocks are only 2-byte aligned: assemble the dwords bytewise
+    auto dword = [](const uint8_t* p) {
+        return (int)((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24));
+    };
+    const uint8_t* xb = x + (size_t)b * 34 + 2;
+    const int4 a0 = make_int4(dword(xb), dword(xb + 4), dword(xb + 8), dword(xb + 12));
+    const int4 a1 = make_int4(dword(xb + 16), dword(xb + 20), dword(xb + 24), dword(xb + 28));
+    int s;
+    if (wtype == HY_TYPE_Q8_0) {
+        const uint8_t* wb = w + ((size_t)r * nb + b) * 34 + 2;
+        s = dot_q8_block(make_int4(dword(wb), dword(wb + 4), dword(wb + 8), dword(wb + 12)),
+                         make_int4(dword(wb + 16), dword(wb + 20), dword(wb + 24), dword(wb + 28)), a0, a1);
+    } else {
+        const uint8_t* wb = w + ((size_t)r * nb + b) * 18 + 2;
+        int asum = 0;
+        for (int j = 0; j < 32; j++) asum += (int8_t)xb[j];
+        s = dot_q4_block(make_int4(dword(wb), dword(wb + 4), dword(wb + 8), dword(wb + 12)), a0, a1, asum);
+    }
+    out[idx] = s;
+}
+
+hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
+                                  hipStream_t s) {
+    const int n = rows * nb;
+    hipLaunchKernelGGL(block_dots_valu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, wtype, w, x, rows, nb, out);
+    return hipGetLastError();
+}
+
+}  // namespace hy

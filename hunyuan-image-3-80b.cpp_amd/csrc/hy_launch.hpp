@@ -13,6 +13,8 @@ namespace hy {
 // routing side (hy_route.hip)
 hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                          float* logits, float* topw, int* topi, hipStream_t s);
+hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
+                           float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s);
 hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, float* topw, int* topi, hipStream_t s);
 hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s);
 hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
@@ -22,19 +24,28 @@ hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int
                            int* tile_start, int* tile_n, int* meta, hipStream_t s);
 hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s);
 
-// expert products, VALU path (hy_ffn.hip)
-size_t ffn_up_smem(int wtype, int NT, int H);
-size_t ffn_down_smem(int wtype, int NT, int I);
-hipError_t launch_ffn_up_valu(int wtype, int NT, int max_tiles, const MatView& W, const Routing& R, const ActQ& X,
-                              const float* xf, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
-                              float* hf, hipStream_t s);
-hipError_t launch_ffn_down_valu(int wtype, int NT, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
-                                const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H,
-                                int I, int E, int K, float* y, const float* resid, float* out, hipStream_t s);
+// expert products, decode GEMV path (hy_gemv.hip)
+constexpr int GEMV_NT = 8;  // tokens per GEMV tile
+int gemv_tile_tokens();
+hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
+                          int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
+                          hipStream_t s);
+hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
+                            const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
+                            int E, int K, float* y, const float* resid, float* out, hipStream_t s);
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, const float* resid, float* out,
                           hipStream_t s);
 hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
                                   hipStream_t s);
+
+// expert products, MFMA path (hy_mfma.hip)
+bool mfma_path_ok(int wtype, int H, int I);
+int mfma_tile_tokens();
+hipError_t launch_ffn_up_mfma(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const ActQ& X,
+                              int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, hipStream_t s);
+hipError_t launch_ffn_down_mfma(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
+                                const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
+                                const float* resid, float* out, hipStream_t s);
 
 // residency (hy_data.hip)
 hipError_t launch_synth_matrix(int wtype, uint64_t key, float scale, int rows, int cols, int gu_I, uint8_t* qs,

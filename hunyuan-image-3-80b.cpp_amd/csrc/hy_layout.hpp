@@ -2,14 +2,16 @@
 // kernels and the C ABI.
 //
 // Resident weights of one layer (per matrix kind, experts 0..E-1 then the shared
-// expert at index E):
-//   Q8_0: qs  int8   [E+1][rows][cols]        scale fp16 [E+1][rows][cols/32]
-//   Q4_0: qs  uint8  [E+1][rows][cols/2]      scale fp16 [E+1][rows][cols/32]
-//         (each 16-byte group keeps the GGUF block order: byte j = elem j | elem j+16 << 4)
-//   F32 : f32        [E+1][rows][cols]
-// gate_up rows are stored interleaved in groups of 32: packed row 64g+r holds gate
-// row 32g+r for r < 32 and up row I+32g+(r-32) for r >= 32, so one 64-row slab
-// carries matching SiLU and linear halves.  Down rows keep their natural order.
+// expert at index E), "row-group interleaved": rows are taken in groups of 64 and,
+// inside a group, block b of all 64 rows is contiguous:
+//   quant plane: [E+1][rows/64][cols/32][64 rows][bpb]  (bpb = 32 B Q8_0 int8,
+//                16 B Q4_0 nibbles in GGUF block order, 128 B F32)
+//   scale plane: [E+1][rows/64][cols/32][64 rows] fp16 (none for F32)
+// A wave whose lane l owns row l of a group reads one contiguous 64*bpb chunk per
+// block (the decode GEMV), and an MFMA row block stages 64-row x block chunks.
+// gate_up rows are packed so each 64-row group holds 32 SiLU rows then the
+// matching 32 linear rows: packed row 64g+r is gate row 32g+r for r < 32 and up
+// row I+32g+(r-32) for r >= 32.  Down rows keep their natural order.
 #pragma once
 
 #include <stddef.h>
@@ -30,6 +32,16 @@ __host__ __device__ inline int gu_packed_row(int orig, int I) {
     const int r = orig - I;
     return (r / 32) * 64 + 32 + (r % 32);
 }
+
+// byte offset of block b of row r in an interleaved quant plane (bpb bytes per block)
+__host__ __device__ inline size_t il_q_offset(int r, int b, int nb, int bpb) {
+    return (((size_t)(r / 64) * nb + b) * 64 + (r % 64)) * (size_t)bpb;
+}
+// element offset of the scale of block b of row r
+__host__ __device__ inline size_t il_s_offset(int r, int b, int nb) {
+    return ((size_t)(r / 64) * nb + b) * 64 + (r % 64);
+}
+__host__ __device__ inline int block_bytes(int wtype) { return wtype == 8 ? 32 : (wtype == 2 ? 16 : 128); }
 
 // Routing / dispatch products in the work arena.
 struct Routing {

@@ -14,11 +14,9 @@ namespace hy {
 // accumulates them with fmaf in increasing h; the 64 partials fold in the tree
 // p[l] += p[l+s], s = 32..1.  Top-k on the logits: K rounds of a wave max, lowest
 // lane among equal maxima (lower expert index wins ties), then weights
-// p_k = exp(l_k - m) / sum_e exp(l_e - m) renormalised by max(sum_k p_k, 1e-8).
-// One wave handles TPW tokens; experts are processed 8 at a time so each Wr
-// float4 feeds TPW tokens.
+// p_k = exp(l_k - m) / sum_e exp(l_e - m) renormalised by max(sum_k p_k, 1e-8),
+// exp = hy_expf and the denominator summed in the 64-lane tree.
 // ----------------------------------------------------------------------------
-constexpr int ROUTER_TPW = 4;
 constexpr int ROUTER_WAVES = 4;
 
 __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, float scale, int lane,
@@ -36,9 +34,10 @@ __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, fl
         if (lane == k) { selv = m; seli = sel; }
         if (lane == sel) v = -INFINITY;
     }
-    const float s = wave_sum(lane < E ? expf(orig - m0) : 0.0f);
+    // denominator: 64-lane tree of exp(l_e - m) (lanes >= E add 0)
+    const float s = wave_sum(lane < E ? hy_expf(orig - m0) : 0.0f);
     // p_k for the lane's own rank k = lane (lanes >= K carry 0)
-    const float p = lane < K ? expf(selv - m0) / s : 0.0f;
+    const float p = lane < K ? hy_expf(selv - m0) / s : 0.0f;
     // sum_k p_k in rank order (every lane computes the same value)
     float ps = 0.0f;
     for (int k = 0; k < K; k++) ps += __shfl(p, k, WAVE);
@@ -49,81 +48,111 @@ __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, fl
     }
 }
 
-__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_kernel(
-    const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, int K, int norm,
-    float scale, float* __restrict__ logits, float* __restrict__ topw, int* __restrict__ topi) {
-    __shared__ float lg[ROUTER_WAVES][ROUTER_TPW][MAX_E];
+// Router logits.  Work item of one wave = (TPW tokens) x (EPW experts); a block's
+// four waves take consecutive items, experts varying fastest so they share the
+// token rows in L1.  Small batches use <8,1> (64 experts -> 64 waves even at T=1),
+// large ones <4,8> (each Wr float4 feeds 4 tokens, 32 accumulators per lane).
+template <int TPW, int EPW>
+__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
+    const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, float* __restrict__ logits) {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int t0 = (blockIdx.x * ROUTER_WAVES + wave) * ROUTER_TPW;
-
-    for (int eg = 0; eg < E; eg += 8) {
-        float acc[ROUTER_TPW][8];
+    const int n_eg = (E + EPW - 1) / EPW;
+    const int item = blockIdx.x * ROUTER_WAVES + wave;
+    const int t0 = (item / n_eg) * TPW, e0 = (item % n_eg) * EPW;
+    if (t0 >= T) return;
+    float acc[TPW][EPW];
 #pragma unroll
-        for (int t = 0; t < ROUTER_TPW; t++)
+    for (int t = 0; t < TPW; t++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[t][e] = 0.0f;
-        for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
-            float4 xv[ROUTER_TPW], wv[8];
+        for (int e = 0; e < EPW; e++) acc[t][e] = 0.0f;
+    for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
+        float4 xv[TPW], wv[EPW];
 #pragma unroll
-            for (int t = 0; t < ROUTER_TPW; t++)
-                xv[t] = (t0 + t < T) ? *reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * H + h0)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int t = 0; t < TPW; t++)
+            xv[t] = (t0 + t < T) ? *reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * H + h0)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                wv[e] = (eg + e < E) ? *reinterpret_cast<const float4*>(wr + (size_t)(eg + e) * H + h0)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int e = 0; e < EPW; e++)
+            wv[e] = (e0 + e < E) ? *reinterpret_cast<const float4*>(wr + (size_t)(e0 + e) * H + h0)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int t = 0; t < ROUTER_TPW; t++)
+        for (int t = 0; t < TPW; t++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    float a = acc[t][e];
-                    a = fmaf(xv[t].x, wv[e].x, a);
-                    a = fmaf(xv[t].y, wv[e].y, a);
-                    a = fmaf(xv[t].z, wv[e].z, a);
-                    a = fmaf(xv[t].w, wv[e].w, a);
-                    acc[t][e] = a;
-                }
-        }
-#pragma unroll
-        for (int t = 0; t < ROUTER_TPW; t++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = tree_sum64(acc[t][e]);
-                if (lane == 0 && eg + e < E) lg[wave][t][eg + e] = v;
+            for (int e = 0; e < EPW; e++) {
+                float a = acc[t][e];
+                a = fmaf(xv[t].x, wv[e].x, a);
+                a = fmaf(xv[t].y, wv[e].y, a);
+                a = fmaf(xv[t].z, wv[e].z, a);
+                a = fmaf(xv[t].w, wv[e].w, a);
+                acc[t][e] = a;
             }
     }
-    __syncthreads();
-    for (int t = 0; t < ROUTER_TPW; t++) {
-        const int tok = t0 + t;
-        if (tok >= T) break;
-        const float v = lane < E ? lg[wave][t][lane] : 0.0f;
-        if (logits && lane < E) logits[(size_t)tok * E + lane] = v;
-        topk_wave(v, E, K, norm, scale, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int e = 0; e < EPW; e++) {
+            const float v = tree_sum64(acc[t][e]);
+            if (lane == 0 && t0 + t < T && e0 + e < E) logits[(size_t)(t0 + t) * E + e0 + e] = v;
+        }
+}
+
+// Top-k + weights per token (one wave each), optionally quantizing the token's
+// activation row to Q8_0 in the same pass (saves a launch in the decode regime).
+__global__ __launch_bounds__(256) void route_select_kernel(const float* __restrict__ logits, int T, int E, int K,
+                                                           int norm, float scale, float* __restrict__ topw,
+                                                           int* __restrict__ topi, const float* __restrict__ x,
+                                                           int H, int8_t* __restrict__ xq, float* __restrict__ xd,
+                                                           int* __restrict__ xs) {
+    const int tok = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (tok >= T) return;
+    const float v = lane < E ? logits[(size_t)tok * E + lane] : 0.0f;
+    topk_wave(v, E, K, norm, scale, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
+    if (xq) {
+        const float* xr = x + (size_t)tok * H;
+        for (int h = lane; h < H; h += WAVE) {
+            const Q8Result r = quant_q8_0_lane32(xr[h]);
+            int s = r.q;
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
+            xq[(size_t)tok * H + h] = r.q;
+            if ((h & 31) == 0) {
+                const size_t b = ((size_t)tok * H + h) / QK;
+                xd[b] = h2f(r.dh);
+                xs[b] = s;
+            }
+        }
     }
 }
 
 hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                          float* logits, float* topw, int* topi, hipStream_t s) {
-    const int per_block = ROUTER_WAVES * ROUTER_TPW;
-    dim3 grid((T + per_block - 1) / per_block);
-    hipLaunchKernelGGL(router_kernel, grid, dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, K, norm, scale,
-                       logits, topw, topi);
+    return launch_router_q(x, wr, T, H, E, K, norm, scale, logits, topw, topi, nullptr, nullptr, nullptr, s);
+}
+
+hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
+                           float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s) {
+    if (T <= 32) {
+        const int items = ((T + 7) / 8) * E;
+        hipLaunchKernelGGL((router_logits_kernel<8, 1>), dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES),
+                           dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, logits);
+    } else {
+        const int items = ((T + 3) / 4) * ((E + 7) / 8);
+        hipLaunchKernelGGL((router_logits_kernel<4, 8>), dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES),
+                           dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, logits);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, norm, scale, topw,
+                       topi, x, H, xq, xd, xs);
     return hipGetLastError();
 }
 
 // top-k gating from given logits (topkgating_easy, src/hunyuan_moe_full.cpp:88-113):
 // one wave per token.
-__global__ __launch_bounds__(256) void topk_from_logits_kernel(const float* __restrict__ logits, int T, int E,
-                                                               int K, float* topw, int* topi) {
-    const int tok = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    if (tok >= T) return;
-    const float v = lane < E ? logits[(size_t)tok * E + lane] : 0.0f;
-    topk_wave(v, E, K, 1, 1.0f, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
-}
-
 hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, float* topw, int* topi,
                                    hipStream_t s) {
-    hipLaunchKernelGGL(topk_from_logits_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, topw, topi);
+    hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, 1, 1.0f, topw,
+                       topi, nullptr, 0, nullptr, nullptr, nullptr);
     return hipGetLastError();
 }
 

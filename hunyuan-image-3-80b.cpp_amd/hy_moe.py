@@ -18,6 +18,7 @@ ROOT = os.path.dirname(HERE)
 HEADER = os.path.join(ROOT, "include", "hy_moe.h")
 
 F32, Q4_0, Q8_0 = 0, 2, 8
+PATH_AUTO, PATH_VALU, PATH_MFMA = 0, 1, 2
 TENSOR_X, TENSOR_ROUTER, TENSOR_GU, TENSOR_DN = 0, 1, 2, 3
 
 
@@ -47,6 +48,7 @@ _SIGS = {
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
     "hy_moe_forward_debug": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "hy_moe_stack_forward": (C.c_int, [_vp, _u32, _u32, _vp, _u32, _f, _vp, _vp]),
+    "hy_moe_set_path": (C.c_int, [_vp, _i32]),
     "hy_router_topk": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _i32, _f, _vp, _vp, _vp, _vp]),
     "hy_topkgating_easy": (C.c_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "hy_softmax_rows": (C.c_int, [_vp, _u32, _u32, _vp]),
@@ -221,6 +223,10 @@ class Moe:
 
     def stack_forward(self, first, n, x: Buf, T, eps, out: Buf, stream=None):
         check(lib().hy_moe_stack_forward(self.h, first, n, x.ptr, T, eps, out.ptr, stream))
+
+    def set_path(self, path):
+        """0 = auto, 1 = VALU dot4 kernels, 2 = int8 MFMA grouped GEMM."""
+        check(lib().hy_moe_set_path(self.h, path))
 
     def prof_enable(self, on=True):
         check(lib().hy_moe_prof_enable(self.h, int(on)))

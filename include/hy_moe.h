@@ -115,10 +115,20 @@ int hy_moe_forward_debug(hy_moe_ctx* ctx, uint32_t layer, const float* x_dev, ui
 int hy_moe_stack_forward(hy_moe_ctx* ctx, uint32_t first_layer, uint32_t n_layers,
                          const float* x_dev, uint32_t T, float eps, float* out_dev, void* stream);
 
+/* Expert-product kernels the forward uses: AUTO (default) takes the int8-MFMA grouped
+ * GEMM for T > 16 and the dequant-GEMV (VALU dot4) for decode batches; VALU / MFMA
+ * force one (MFMA needs Q8_0/Q4_0 weights and H, I multiples of 128).  Both compute
+ * the same float operations in the same order, so they agree bit for bit.  No
+ * counterpart in the reference (which has one scalar path); kept so both paths stay
+ * testable at any T. */
+enum { HY_PATH_AUTO = 0, HY_PATH_VALU = 1, HY_PATH_MFMA = 2 };
+int hy_moe_set_path(hy_moe_ctx* ctx, int32_t path);
+
 /* ---- stateless kernels (component parity) ----------------------------------- */
 
 /* Router: logits = x Wr^T (64-lane blocked fmaf order), top-k on logits with lower
  * index winning ties, weights = softmax at the selection renormalised (or scaled).
+ * logits_dev [T][E] is required (it is the intermediate of the two passes).
  * Replaces the router GEMV of src/hunyuan_moe_full.cpp:414-423 plus
  * topkgating_easy (src/hunyuan_moe_full.h:83-89). */
 int hy_router_topk(const float* x_dev, const float* wr_dev, uint32_t T, uint32_t H, uint32_t E,

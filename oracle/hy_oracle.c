@@ -747,6 +747,38 @@ int hyo_moe_forward_cpu(const float* x, const float* wr,
  * (b) q semantics: the GPU path's definition
  * ====================================================================== */
 
+/* exp(x) used by the q semantics (SiLU and the routing softmax), spelled out so the
+ * CPU and the GPU evaluate the same operations: Cody-Waite reduction
+ * x = n*ln2 + r with ln2 split in a 16-bit head (n*head exact) and a tail, e^r by
+ * its Taylor series to degree 7 in Horner form with fmaf (truncation < 6e-9
+ * relative on |r| <= ln2/2), then scaling by 2^n with ldexpf. */
+float hyo_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float n = rintf(x * 1.44269504f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.42860682e-6f, r);
+    float p = 1.98412698e-4f;           /* 1/7! */
+    p = fmaf(p, r, 1.38888889e-3f);     /* 1/6! */
+    p = fmaf(p, r, 8.33333377e-3f);     /* 1/5! */
+    p = fmaf(p, r, 4.16666679e-2f);     /* 1/4! */
+    p = fmaf(p, r, 1.66666672e-1f);     /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+/* 64-lane tree sum (lane l holds v[l], lanes >= n hold 0), the wave reduction order. */
+static float hyo_tree_sum64(const float* v, uint32_t n) {
+    float p[64];
+    for (uint32_t l = 0; l < 64; l++) p[l] = l < n ? v[l] : 0.0f;
+    for (int s = 32; s >= 1; s >>= 1)
+        for (int l = 0; l < s; l++) p[l] = p[l] + p[l + s];
+    return p[0];
+}
+
 /* One 64-lane blocked dot in the order the GPU router kernel uses. */
 static float hyo_blocked_dot(const float* a, const float* b, uint32_t H) {
     float p[64];
@@ -771,14 +803,13 @@ static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, floa
                           float* w, int32_t* idx) {
     float v[64];
     hyo_topk_f32(l, E, K, v, idx); /* selection on logits, ties -> lower index */
-    float m = l[0];
-    for (uint32_t e = 1; e < E; e++)
-        if (l[e] > m) m = l[e];
-    float s = 0.0f;
-    for (uint32_t e = 0; e < E; e++) s += expf(l[e] - m);
+    const float m = v[0]; /* the largest logit */
+    float ex[64];
+    for (uint32_t e = 0; e < E; e++) ex[e] = hyo_expf(l[e] - m);
+    const float s = hyo_tree_sum64(ex, E);
     float p[64], ps = 0.0f;
     for (uint32_t k = 0; k < K; k++) {
-        p[k] = expf(l[idx[k]] - m) / s;
+        p[k] = hyo_expf(l[idx[k]] - m) / s;
         ps += p[k];
     }
     if (ps < 1e-8f) ps = 1e-8f;
@@ -791,17 +822,43 @@ void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int
         hyo_route_one(logits + (size_t)t * E, E, K, norm, scale, w + (size_t)t * K, idx + (size_t)t * K);
 }
 
-/* y[r] = row r of W (type wt, n columns) . x  ; xq is x quantized to Q8_0 (unused for F32) */
+/* y[r] = row r of W (type wt, n columns) . x ; xq is x quantized to Q8_0 (unused for
+ * F32).  Quantized rows: exact int32 block dots s_b (ggml's vec_dot_q8_0_q8_0 /
+ * vec_dot_q4_0_q8_0 blocks), accumulated over b ascending as
+ * acc = fmaf((float)s_b, d_w*d_x, acc).  F32 rows: acc = fmaf(w_k, x_k, acc), k
+ * ascending.  (ggml fixes no float order across its ISAs; this is the one the GPU
+ * kernels compute.) */
 static float hyo_row_dot(int wt, const void* W, size_t r, size_t n, const float* x, const void* xq) {
     const uint8_t* row = (const uint8_t*)W + r * hyo_type_row_bytes(wt, n);
+    float acc = 0.0f;
     switch (wt) {
-    case HYO_Q8_0: return hyo_vec_dot_q8_0_q8_0(row, xq, n);
-    case HYO_Q4_0: return hyo_vec_dot_q4_0_q8_0(row, xq, n);
+    case HYO_Q8_0: {
+        const hyo_block_q8_0* w = (const hyo_block_q8_0*)row;
+        const hyo_block_q8_0* q = (const hyo_block_q8_0*)xq;
+        for (size_t b = 0; b < n / HYO_QK; b++) {
+            int32_t sb = 0;
+            for (int j = 0; j < HYO_QK; j++) sb += (int32_t)w[b].qs[j] * (int32_t)q[b].qs[j];
+            acc = fmaf((float)sb, hyo_fp16_to_fp32(w[b].d) * hyo_fp16_to_fp32(q[b].d), acc);
+        }
+        return acc;
+    }
+    case HYO_Q4_0: {
+        const hyo_block_q4_0* w = (const hyo_block_q4_0*)row;
+        const hyo_block_q8_0* q = (const hyo_block_q8_0*)xq;
+        for (size_t b = 0; b < n / HYO_QK; b++) {
+            int32_t sb = 0;
+            for (int j = 0; j < HYO_QK / 2; j++) {
+                sb += ((int32_t)(w[b].qs[j] & 0x0f) - 8) * (int32_t)q[b].qs[j];
+                sb += ((int32_t)(w[b].qs[j] >> 4) - 8) * (int32_t)q[b].qs[j + HYO_QK / 2];
+            }
+            acc = fmaf((float)sb, hyo_fp16_to_fp32(w[b].d) * hyo_fp16_to_fp32(q[b].d), acc);
+        }
+        return acc;
+    }
     default: {
         const float* wr = (const float*)row;
-        float s = 0.0f;
-        for (size_t k = 0; k < n; k++) s += x[k] * wr[k];
-        return s;
+        for (size_t k = 0; k < n; k++) acc = fmaf(wr[k], x[k], acc);
+        return acc;
     }
     }
 }
@@ -812,7 +869,7 @@ static void hyo_expert_q(int wt, const void* gu, const void* dn, uint32_t H, uin
     for (uint32_t j = 0; j < 2 * I; j++) gbuf[j] = hyo_row_dot(wt, gu, j, H, x, xq);
     for (uint32_t j = 0; j < I; j++) {
         float g = gbuf[j], u = gbuf[I + j];
-        hbuf[j] = g * (1.0f / (1.0f + expf(-g))) * u;
+        hbuf[j] = g * (1.0f / (1.0f + hyo_expf(-g))) * u;
     }
     if (wt != HYO_F32) hyo_quantize_row_q8_0(hbuf, hq, I);
     for (uint32_t r = 0; r < H; r++) y[r] = hyo_row_dot(wt, dn, r, I, hbuf, hq);
@@ -856,7 +913,7 @@ static void hyo_token_q(const hyo_qlayer* L, const float* xt, float* ot, float* 
         if (k < 0) continue;
         hyo_expert_q(wt, (const uint8_t*)L->gu + e * gu_bytes, (const uint8_t*)L->dn + e * dn_bytes,
                      H, I, xt, xq, y, gbuf, hbuf, hq);
-        for (uint32_t r = 0; r < H; r++) comb[r] += wl[k] * y[r];
+        for (uint32_t r = 0; r < H; r++) comb[r] = fmaf(wl[k], y[r], comb[r]);
     }
     if (L->shared_gu && L->shared_dn) {
         hyo_expert_q(wt, L->shared_gu, L->shared_dn, H, I, xt, xq, y, gbuf, hbuf, hq);

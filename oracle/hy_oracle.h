@@ -20,6 +20,11 @@
  *      expert products are exact int32 per-32-block dots rescaled in fp32
  *      (ggml's vec_dot_q8_0_q8_0 / vec_dot_q4_0_q8_0 definition).
  *
+ * The q semantics fix every float operation and its order (router: 64-lane blocked
+ * fmaf; softmax denominator: 64-lane tree; expert rows: block-sequential
+ * fmaf((float)s_b, d_w*d_x, acc); exp: hyo_expf; combine: fmaf in ascending expert
+ * order), so the GPU path reproduces them bit for bit.
+ *
  * Parity pins (see tests/test_oracle_*.py):
  *   - ref-semantics routing/dispatch/combine/moe_forward_full: bit-exact
  *     against the reference's own hunyuan_moe_full.cpp compiled into
@@ -132,6 +137,9 @@ int  hyo_moe_forward_cpu(const float* x, const float* wr,
                          float* out, float* dbg_probs, float* dbg_w, int32_t* dbg_idx);
 
 /* ---------------- (b) q semantics (the GPU path's definition) ---------------- */
+/* exp used by the q semantics: Cody-Waite reduction + degree-7 Taylor (fmaf Horner)
+ * + ldexpf, evaluated identically by the GPU kernels. */
+float hyo_expf(float x);
 /* Router logit order: lane l in [0,64) owns elements h with (h/4) % 64 == l and
  * accumulates them in increasing h with fmaf from 0; the 64 lane partials are
  * then folded p[l] += p[l+s] for s = 32,16,8,4,2,1; logit = p[0]. */

@@ -31,6 +31,15 @@ def assert_close(got, ref, what=""):
     assert e <= REL_TOL and c >= COS_TOL, f"{what}: rel_err={e:.3e} cos={c:.8f}"
 
 
+def assert_exact(got, ref, what=""):
+    """Layer outputs: the GPU path evaluates the oracle's q semantics operation for
+    operation, so the bar is bit equality (the 1e-3 / 0.99999 check runs first so a
+    failure says how far off it is)."""
+    assert_close(got, ref, what)
+    diff = got.view(np.uint32) != ref.view(np.uint32)
+    assert not diff.any(), f"{what}: {int(diff.sum())} of {diff.size} values differ (rel_err={rel_err(got, ref):.2e})"
+
+
 # ------------------------------------------------------------------ data kernels
 
 def test_synth_fill_bit_exact(gpu):
@@ -93,7 +102,7 @@ def test_router_logits_and_indices_bit_exact(gpu, T, H, E, K):
     np.testing.assert_array_equal(lg.view(np.uint32), ref_lg.view(np.uint32))
     ref_w, ref_idx = O.route_topk(ref_lg, K)
     np.testing.assert_array_equal(idx, ref_idx)
-    np.testing.assert_allclose(w, ref_w, rtol=2e-6, atol=1e-7)
+    np.testing.assert_array_equal(w.view(np.uint32), ref_w.view(np.uint32))
 
 
 def test_router_scaling_without_norm(gpu):
@@ -103,10 +112,12 @@ def test_router_scaling_without_norm(gpu):
     lg, w, idx = gpu.router_topk(x, wr, K, norm=False, scale=2.5)
     ref_w, ref_idx = O.route_topk(O.router_logits_blocked(x, wr), K, norm=False, scale=2.5)
     np.testing.assert_array_equal(idx, ref_idx)
-    np.testing.assert_allclose(w, ref_w, rtol=2e-6)
+    np.testing.assert_array_equal(w.view(np.uint32), ref_w.view(np.uint32))
 
 
 def test_topkgating_easy_from_logits(gpu):
+    """topkgating_easy (reference semantics: glibc expf, sequential softmax sum): the
+    GPU selects on logits, so indices match exactly and weights to float rounding."""
     rng = np.random.default_rng(5)
     T, E, K = 50, 64, 8
     lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
@@ -160,8 +171,55 @@ def test_layer_small(gpu, small_layers, wtype, T):
     ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
     np.testing.assert_array_equal(lg.view(np.uint32), rlg.view(np.uint32))
     np.testing.assert_array_equal(idx, ridx)
-    np.testing.assert_allclose(w, rw, rtol=2e-6, atol=1e-7)
-    assert_close(out, ref, f"wtype={wtype} T={T}")
+    np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+    assert_exact(out, ref, f"wtype={wtype} T={T}")
+    m.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("T", [1, 17, 64, 65, 130, 300])
+def test_layer_small_mfma_path(gpu, small_layers, wtype, T):
+    layer = small_layers[wtype]
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], wtype, max_tokens=512)
+    m.set_path(gpu.PATH_MFMA)
+    m.upload(0, layer)
+    x = O.synth(50 + T, 0, O.T_X, 0, (T, SMALL["H"]), 1.0)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+    np.testing.assert_array_equal(idx, ridx)
+    assert_exact(out, ref, f"mfma wtype={wtype} T={T}")
+    # the decode GEMV computes the same operations in the same order
+    m.set_path(gpu.PATH_VALU)
+    assert_exact(m.run(0, x), ref, f"gemv wtype={wtype} T={T}")
+    m.close()
+
+
+def test_mfma_path_rejected_for_f32(gpu, small_layers):
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.F32, max_tokens=8)
+    with pytest.raises(gpu.HyError):
+        m.set_path(gpu.PATH_MFMA)
+    m.close()
+
+
+def test_skewed_routing_single_hot_expert(gpu, small_layers):
+    """All tokens to one expert (capped at T per expert): many tiles of one expert."""
+    base = small_layers[O.Q4_0]
+    router = base.router.copy()
+    router[:, 0] = -50.0
+    router[5, 0] = 50.0       # x[:, 0] = 1 -> expert 5 dominates every token
+    layer = O.Layer(base.H, base.I, base.E, base.K, O.Q4_0, router, base.shared_gu, base.shared_dn, base.gu, base.dn)
+    T = 400
+    x = O.synth(60, 0, O.T_X, 0, (T, SMALL["H"]), 1.0)
+    x[:, 0] = 1.0
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q4_0, max_tokens=T)
+    m.upload(0, layer)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+    assert np.all(idx[:, 0] == 5)
+    np.testing.assert_array_equal(idx, ridx)
+    assert_exact(out, ref, "hot expert")
+    D, counts = m.last_routing()
+    assert counts[5] == T and counts.sum() == T * SMALL["K"]
     m.close()
 
 
@@ -171,7 +229,7 @@ def test_layer_without_shared_expert(gpu, small_layers):
     m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q8_0, max_tokens=32, has_shared=False)
     m.upload(0, layer)
     x = O.synth(30, 0, O.T_X, 0, (20, SMALL["H"]), 1.0)
-    assert_close(m.run(0, x), O.moe_forward_q(layer, x), "no shared")
+    assert_exact(m.run(0, x), O.moe_forward_q(layer, x), "no shared")
     m.close()
 
 
@@ -213,7 +271,7 @@ def test_stack_matches_oracle(gpu):
     m.stack_forward(0, L, xb, T, 1e-5, ob)
     got = ob.numpy()
     ref = O.moe_stack_q(layers, x, eps=1e-5)
-    assert_close(got, ref, "stack")
+    assert_exact(got, ref, "stack")
     m.close()
 
 

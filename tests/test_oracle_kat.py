@@ -201,6 +201,28 @@ def test_synth_generator_definition_and_moments():
     assert abs(big.mean()) < 5e-3 and abs(big.std() - 1.0) < 5e-3
 
 
+# ------------------------------------------------------------------ shared exp
+
+def test_expf_accuracy_and_specials():
+    L.hyo_expf.restype = C.c_float
+    L.hyo_expf.argtypes = [C.c_float]
+    rng = np.random.default_rng(11)
+    xs = np.concatenate([rng.uniform(-100, 88, 20000), rng.uniform(-1, 1, 5000), np.arange(-87, 88, 0.25)])
+    xs = xs.astype(np.float32)
+    got = np.array([L.hyo_expf(float(v)) for v in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64))
+    normal = ref > 1.2e-38
+    ulp = np.spacing(ref[normal].astype(np.float32)).astype(np.float64)
+    err_ulp = np.abs(got[normal].astype(np.float64) - ref[normal]) / ulp
+    assert err_ulp.max() <= 2.0, err_ulp.max()
+    assert L.hyo_expf(0.0) == 1.0
+    assert L.hyo_expf(89.0) == np.inf and L.hyo_expf(-104.0) == 0.0
+    assert np.isnan(L.hyo_expf(float("nan")))
+    # subnormal results stay close in absolute terms
+    sub = ~normal & (ref > 0)
+    assert np.all(np.abs(got[sub] - ref[sub]) <= 2 * 1.4e-45)
+
+
 # ------------------------------------------------------------------ router order
 
 def _f32_round(q: Fraction) -> np.float32:
