@@ -52,6 +52,37 @@ def _run(cmd):
     return out
 
 
+def build_oracle(with_ref=None):
+    """The CPU oracle (test infrastructure) and, when the reference tree is present,
+    oracle/_ref from the reference's own source."""
+    oracle = os.path.join(ROOT, "oracle")
+    subprocess.run(["make", "-s", "-C", oracle, "all"], check=True)
+    if with_ref is None:
+        with_ref = os.path.isdir("/root/reference/src")
+    if with_ref:
+        subprocess.run(["make", "-s", "-C", oracle, "ref"], check=True)
+
+
+def build_cxx_tests():
+    """tests/cxx/test_mirror: the C++ API mirror checked against the oracle."""
+    src = os.path.join(ROOT, "tests", "cxx", "test_mirror.cpp")
+    out = os.path.join(ROOT, "tests", "cxx", "test_mirror")
+    cmd = ["g++", "-std=c++17", "-O2", src, f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(ROOT, 'oracle')}",
+           f"-L{HERE}", "-lhy_moe", f"-L{os.path.join(ROOT, 'oracle')}", "-loracle",
+           "-Wl,-rpath,$ORIGIN/../../hunyuan-image-3-80b.cpp_amd", "-Wl,-rpath,$ORIGIN/../../oracle",
+           "-Wl,--allow-shlib-undefined", "-o", out + ".tmp"]
+    _run(cmd)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_all(asm=False, jobs=8, verbose=False):
+    build_oracle()
+    lib = build(asm=asm, jobs=jobs, verbose=verbose)
+    build_cxx_tests()
+    return lib
+
+
 def build(asm=False, jobs=8, verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     hips, cpps = sources()
@@ -82,5 +113,5 @@ if __name__ == "__main__":
     ap.add_argument("-j", type=int, default=8)
     ap.add_argument("-v", action="store_true")
     a = ap.parse_args()
-    print(build(asm=a.asm, jobs=a.j, verbose=a.v))
+    print(build_all(asm=a.asm, jobs=a.j, verbose=a.v))
     sys.exit(0)

@@ -272,25 +272,24 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
                                                 c->y, resid, out, s);
             }));
         else
-            HY_TRY(timed(c, hy::KID_COMBINE, s, [&] { return hy::launch_combine(R, c->y, iT, H, K, resid, out, s); }));
+            HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {
+                return hy::launch_combine(R, c->y, iT, H, K, 0, resid, out, s);
+            }));
         return HY_OK;
     }
     HY_TRY(timed(c, hy::KID_UP, s, [&] {
         return hy::launch_gemv_up(wt, routed_bound + shared_tiles, gu_view(c, L), R, X, x, iT, H, I, E, K, c->hq,
                                   c->hd, c->hs, c->hf, s);
     }));
+    // decode: routed and shared down products in one launch (the shared expert's rows
+    // no longer wait behind the routed ones), then the combine
     HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
-        return hy::launch_gemv_down(wt, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT, H, I, E,
-                                    K, c->y, nullptr, nullptr, s);
+        return hy::launch_gemv_down(wt, routed_bound + shared_tiles, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf,
+                                    iT, H, I, E, K, c->y, nullptr, nullptr, s);
     }));
-    if (has_shared) {
-        HY_TRY(timed(c, hy::KID_DOWN_SHARED, s, [&] {
-            return hy::launch_gemv_down(wt, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT, H, I,
-                                        E, K, c->y, resid, out, s);
-        }));
-    } else {
-        HY_TRY(timed(c, hy::KID_COMBINE, s, [&] { return hy::launch_combine(R, c->y, iT, H, K, resid, out, s); }));
-    }
+    HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {
+        return hy::launch_combine(R, c->y, iT, H, K, has_shared, resid, out, s);
+    }));
     return HY_OK;
 }
 
@@ -343,7 +342,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
         {(void**)&c->hq, slots * I},       {(void**)&c->hd, slots * (I / 32) * 4},
         {(void**)&c->hs, slots * (I / 32) * 4},
         {(void**)&c->hf, wt == HY_TYPE_F32 ? slots * I * 4 : 16},
-        {(void**)&c->y, pairs * H * 4},    {(void**)&c->xn, Tm * H * 4},
+        {(void**)&c->y, slots * H * 4},    {(void**)&c->xn, Tm * H * 4},
         {(void**)&c->cur, Tm * H * 4},
     };
     size_t total = 0;
@@ -494,7 +493,17 @@ int hy_topkgating_easy(const float* lg, uint32_t T, uint32_t E, uint32_t K, floa
     if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
     if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
         return fail(HY_ERR_INVALID, "bad gating shape");
-    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, w, idx, static_cast<hipStream_t>(stream)));
+    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, 1, 1.0f, w, idx, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_route_logits(const float* lg, uint32_t T, uint32_t E, uint32_t K, int32_t norm, float scale, float* w,
+                    int32_t* idx, void* stream) {
+    if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
+        return fail(HY_ERR_INVALID, "bad routing shape");
+    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, norm, scale, w, idx,
+                                        static_cast<hipStream_t>(stream)));
     return HY_OK;
 }
 
@@ -532,6 +541,62 @@ int hy_block_dots(int32_t wtype, const void* w, const void* x, uint32_t rows, ui
 int hy_rms_norm(const float* x, uint32_t T, uint32_t H, float eps, float* out, void* stream) {
     if (!x || !out || T == 0 || H == 0 || H % 4) return fail(HY_ERR_INVALID, "bad rms_norm args");
     HIP_TRY(hy::launch_rms_norm(x, (int)T, (int)H, eps, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_rms_norm_w(const float* x, const float* w, uint32_t T, uint32_t H, float eps, float* out, void* stream) {
+    if (!w) return hy_rms_norm(x, T, H, eps, out, stream);
+    if (!x || !out || T == 0 || H == 0 || H % 4) return fail(HY_ERR_INVALID, "bad rms_norm args");
+    HIP_TRY(hy::launch_rms_norm_w(x, w, (int)T, (int)H, eps, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_topk_rows(const float* x, uint32_t rows, uint32_t n, uint32_t k, float* vals, int32_t* idx, void* stream) {
+    if (!x || !vals || !idx || rows == 0 || n == 0 || n > 4096 || k == 0 || k > 64)
+        return fail(HY_ERR_INVALID, "bad top-k arguments (n <= 4096, 1 <= k <= 64)");
+    HIP_TRY(hy::launch_topk_rows(x, (int)rows, (int)n, (int)k, vals, idx, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_dispatch_pairs(const int32_t* topi, const float* topw, uint32_t T, uint32_t K, uint32_t E, int32_t* counts,
+                      int32_t* offsets, int32_t* pos, void* stream) {
+    if (!topi || !topw || !counts || !offsets || !pos) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || T > 16384 || K == 0 || K > (uint32_t)hy::MAX_K || E == 0 || E > (uint32_t)hy::MAX_E || K > E)
+        return fail(HY_ERR_INVALID, "bad dispatch shape T=%u K=%u E=%u", T, K, E);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // scratch for the lists the layer forward also builds
+    const size_t pairs = (size_t)T * K;
+    const int max_tiles = (int)((pairs + E * 7) / 8 + 1);
+    void* scratch = nullptr;
+    const size_t bytes = pairs * 4 * 3 + (size_t)max_tiles * 4 * 3 + 64;
+    if (hipMalloc(&scratch, bytes) != hipSuccess) return fail(HY_ERR_NOMEM, "dispatch scratch");
+    int* srt = static_cast<int*>(scratch);
+    int* cpos = srt + pairs;
+    float* cw = reinterpret_cast<float*>(cpos + pairs);
+    int* te = reinterpret_cast<int*>(cw + pairs);
+    int* ts = te + max_tiles;
+    int* tn = ts + max_tiles;
+    int* meta = tn + max_tiles;
+    hipError_t e = hy::launch_dispatch(topi, topw, (int)T, (int)K, (int)E, 8, 0, counts, offsets, srt, pos, cpos, cw,
+                                       te, ts, tn, meta, s);
+    hipError_t e2 = hipStreamSynchronize(s);
+    (void)hipFree(scratch);
+    if (e != hipSuccess || e2 != hipSuccess)
+        return fail(HY_ERR_HIP, "dispatch failed: %s", hipGetErrorString(e != hipSuccess ? e : e2));
+    return HY_OK;
+}
+
+int hy_einsum_dispatch(const float* x, uint32_t T, uint32_t H, const uint8_t* mask, uint32_t E, uint32_t C, float* out,
+                       void* stream) {
+    if (!x || !mask || !out || T == 0 || H == 0 || E == 0 || C == 0) return fail(HY_ERR_INVALID, "bad arguments");
+    HIP_TRY(hy::launch_einsum_dispatch(x, (int)T, (int)H, mask, (int)E, (int)C, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_einsum_combine(const float* cw, const float* eo, uint32_t T, uint32_t H, uint32_t E, uint32_t C, float* out,
+                      void* stream) {
+    if (!cw || !eo || !out || T == 0 || H == 0 || E == 0 || C == 0) return fail(HY_ERR_INVALID, "bad arguments");
+    HIP_TRY(hy::launch_einsum_combine(cw, eo, (int)T, (int)H, (int)E, (int)C, out, static_cast<hipStream_t>(stream)));
     return HY_OK;
 }
 

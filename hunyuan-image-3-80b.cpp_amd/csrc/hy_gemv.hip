@@ -15,10 +15,11 @@
 // lanes 0..31 hold g, lanes 32..63 the matching u, and h = silu(g) * u
 // (src/hunyuan_moe_full.cpp:479-486) is quantized to Q8_0 by the 32 gate lanes
 // (ggml quantizes src1 of every quantized matmul).
-// The down kernel's work item is (tile, 4 groups of 64 output rows).  Routed tiles
-// write y[pair][row]; shared tiles fuse the combine
+// The down kernel's work item is (tile, 4 groups of 64 output rows); every tile
+// (routed and shared, one launch) writes y[slot][row], then the combine kernel forms
 //   out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e * y_e[t] )
-// (src/hunyuan_moe_full.cpp:503-515, einsum_combine order :387-397).
+// (src/hunyuan_moe_full.cpp:503-515, einsum_combine order :387-397).  The fused
+// shared-tile combine (mode 2) stays available for callers that want one launch.
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_layout.hpp"
@@ -27,7 +28,7 @@ namespace hy {
 
 constexpr int GV_WAVES = 4;
 constexpr int GV_THREADS = GV_WAVES * WAVE;
-constexpr int GV_UNROLL = 4;  // blocks whose weights are loaded ahead of use
+constexpr int GV_UNROLL = 8;  // blocks per register set (two sets in flight)
 
 // exact int dot of one Q8_0 weight block with one Q8_0 activation block
 __device__ __forceinline__ int dot_q8_block(const int4 w0, const int4 w1, const int4 a0, const int4 a1) {
@@ -81,8 +82,9 @@ template <int WT, int NT, int MODE>
 __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int tok_s[NT], slot_s[NT];
+    // mode 1 covers every tile (routed and shared); mode 2 the shared tiles only
     const int tile = (MODE == 2) ? a.R.meta[0] + (int)blockIdx.x : (int)blockIdx.x;
-    if (tile >= a.R.meta[MODE == 1 ? 0 : 1]) return;
+    if (tile >= a.R.meta[1]) return;
     const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
     const int Kd = a.Kd, nb = Kd / QK;
@@ -163,19 +165,23 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
         constexpr int BPB = WT == HY_TYPE_Q8_0 ? 32 : 16;
         const uint8_t* wbase = a.W.qs + (size_t)e * a.W.qs_stride + ((size_t)G * nb * 64 + lane) * BPB;
         const uint16_t* sbase = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64 + lane;
-        for (int b0 = 0; b0 < nb; b0 += GV_UNROLL) {
-            int4 w0[GV_UNROLL], w1[GV_UNROLL];
-            float dw[GV_UNROLL];
+        // two register sets of GV_UNROLL blocks: the next chunk's loads are in flight
+        // while the current chunk is consumed (software pipelining)
+        int4 w0[2][GV_UNROLL], w1[2][GV_UNROLL];
+        float dw[2][GV_UNROLL];
+        auto load = [&](int set, int b0) {
 #pragma unroll
             for (int u = 0; u < GV_UNROLL; u++) {
                 const int b = b0 + u;
                 if (b < nb) {
                     const int4* p = reinterpret_cast<const int4*>(wbase + (size_t)b * 64 * BPB);
-                    w0[u] = p[0];
-                    if (WT == HY_TYPE_Q8_0) w1[u] = p[1];
-                    dw[u] = h2f(sbase[(size_t)b * 64]);
+                    w0[set][u] = p[0];
+                    if (WT == HY_TYPE_Q8_0) w1[set][u] = p[1];
+                    dw[set][u] = h2f(sbase[(size_t)b * 64]);
                 }
             }
+        };
+        auto consume = [&](int set, int b0) {
 #pragma unroll
             for (int u = 0; u < GV_UNROLL; u++) {
                 const int b = b0 + u;
@@ -184,12 +190,21 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
                 for (int i = 0; i < NT; i++) {
                     if (i < n) {
                         const int4* xb = reinterpret_cast<const int4*>(xs_l + (size_t)i * Kd + b * QK);
-                        const int s = WT == HY_TYPE_Q8_0 ? dot_q8_block(w0[u], w1[u], xb[0], xb[1])
-                                                         : dot_q4_block(w0[u], xb[0], xb[1], xsum_l[i * nb + b]);
-                        acc[i] = fmaf((float)s, dw[u] * xd_l[i * nb + b], acc[i]);
+                        const int s = WT == HY_TYPE_Q8_0
+                                          ? dot_q8_block(w0[set][u], w1[set][u], xb[0], xb[1])
+                                          : dot_q4_block(w0[set][u], xb[0], xb[1], xsum_l[i * nb + b]);
+                        acc[i] = fmaf((float)s, dw[set][u] * xd_l[i * nb + b], acc[i]);
                     }
                 }
             }
+        };
+        load(0, 0);
+        for (int b0 = 0; b0 < nb; b0 += 2 * GV_UNROLL) {
+            if (b0 + GV_UNROLL < nb) load(1, b0 + GV_UNROLL);
+            consume(0, b0);
+            if (b0 + GV_UNROLL >= nb) break;
+            if (b0 + 2 * GV_UNROLL < nb) load(0, b0 + 2 * GV_UNROLL);
+            consume(1, b0 + GV_UNROLL);
         }
     }
 
@@ -237,15 +252,18 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     }
 }
 
-// combine without a shared expert: out[t] = residual[t] + sum_{e ascending} w_e y_e[t]
+// combine: out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e y_e[t] ), the
+// shared expert's output at slot T*K + t when has_shared
 __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __restrict__ y, int T, int H, int K,
-                                                      const float* __restrict__ resid, float* __restrict__ out) {
+                                                      int has_shared, const float* __restrict__ resid,
+                                                      float* __restrict__ out) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (size_t)T * H) return;
     const int t = (int)(idx / H), row = (int)(idx % H);
     float comb = 0.0f;
     for (int k = 0; k < K; k++) comb = fmaf(R.comb_w[t * K + k], y[(size_t)R.comb_pos[t * K + k] * H + row], comb);
-    out[idx] = resid ? resid[idx] + comb : comb;
+    const float o = has_shared ? y[((size_t)T * K + t) * H + row] + comb : comb;
+    out[idx] = resid ? resid[idx] + o : o;
 }
 
 // ---------------------------------------------------------------------------- launchers
@@ -289,10 +307,11 @@ hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatVie
                      : gemv_launch<2>(wtype, grid, gemv_smem(wtype, I), s, a);
 }
 
-hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, const float* resid, float* out,
-                          hipStream_t s) {
+hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,
+                          float* out, hipStream_t s) {
     const size_t n = (size_t)T * H;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, y, T, H, K, resid, out);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, y, T, H, K, has_shared,
+                       resid, out);
     return hipGetLastError();
 }
 

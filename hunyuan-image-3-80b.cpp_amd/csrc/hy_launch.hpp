@@ -15,7 +15,8 @@ hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, i
                          float* logits, float* topw, int* topi, hipStream_t s);
 hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                            float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s);
-hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, float* topw, int* topi, hipStream_t s);
+hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, int norm, float scale, float* topw,
+                                   int* topi, hipStream_t s);
 hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s);
 hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
                              hipStream_t s);
@@ -33,8 +34,8 @@ hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Rout
 hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
                             const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
                             int E, int K, float* y, const float* resid, float* out, hipStream_t s);
-hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, const float* resid, float* out,
-                          hipStream_t s);
+hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,
+                          float* out, hipStream_t s);
 hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
                                   hipStream_t s);
 
@@ -54,6 +55,14 @@ hipError_t launch_synth_fill(float* out, size_t n, uint64_t key, float scale, hi
 hipError_t launch_repack(int wtype, const uint8_t* src, int rows, int cols, int gu_I, uint8_t* qs, uint16_t* sc,
                          hipStream_t s);
 hipError_t launch_dequant(int wtype, const uint8_t* src, size_t n, float* out, hipStream_t s);
+
+// dense routing helpers of the reference API (hy_gate.hip)
+hipError_t launch_topk_rows(const float* x, int rows, int n, int k, float* vals, int* idx, hipStream_t s);
+hipError_t launch_einsum_dispatch(const float* x, int T, int H, const uint8_t* mask, int E, int C, float* out,
+                                  hipStream_t s);
+hipError_t launch_einsum_combine(const float* cw, const float* eo, int T, int H, int E, int C, float* out,
+                                 hipStream_t s);
+hipError_t launch_rms_norm_w(const float* x, const float* w, int T, int H, float eps, float* out, hipStream_t s);
 
 // kernel ids for per-kernel timing
 enum KernelId {

@@ -1,16 +1,20 @@
 // hy_mfma.hip -- grouped expert GEMMs on the int8 matrix cores (prefill / image-token
 // batches).
 //
-// Work item = (tile, row block): a tile is up to 64 (token, expert) pairs of one
-// expert (or 64 consecutive tokens for the shared expert), a row block is 128 weight
-// rows (two 64-row groups of the row-group-interleaved weights).  Each K step stages
-// KB = 4 GGUF blocks (128 k) of the 128 weight rows and of the tile's 64 activation
-// rows in LDS (double buffered, register staging).  Every
-// wave owns 2 x (32 rows x 32 tokens) output tiles and, per 32-wide block, issues
+// Work item = (tile, row block): a tile is up to 128 (token, expert) pairs of one
+// expert (or 128 consecutive tokens for the shared expert), a row block is 128 weight
+// rows (two 64-row groups of the row-group-interleaved weights).  Each K step
+// copies KB = 4 GGUF blocks (128 k) of the 128 weight rows and of the tile's 128
+// activation rows straight from global memory into an LDS ring of 3 stages (two in
+// flight while one is consumed).  Eight waves = 2 row slabs x
+// 4 token quarters; every wave owns 2 x (32 rows x 32 tokens) output tiles and, per
+// 32-wide block, issues
 // v_mfma_i32_32x32x32_i8: K = 32 is exactly one GGUF block, so each MFMA result is the
 // exact int32 block dot sum_j w_j x_j of ggml's vec_dot, which is then rescaled in
 // fp32 with the blocks taken in order: acc = fmaf(float(S), d_w * d_x, acc) -- the
 // accumulation the oracle and the decode GEMV use, so all paths agree bit for bit.
+// The 32x32 scale products d_w * d_x come from a rank-1 f16 MFMA (exact), which
+// takes 16 multiplies per tile and block off the vector ALUs.
 //
 // MFMA operand / result layout (gfx950, checked on the device): A lane l holds 16
 // bytes of row l%32, B lane l 16 bytes of column l%32, both at the same k offset
@@ -29,20 +33,35 @@ namespace hy {
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 
-constexpr int MM_ROWS = 128;          // weight rows per work item
-constexpr int MM_TOK = 64;            // pairs (tokens) per tile
-constexpr int MM_KB = 4;              // GGUF blocks per K step
-constexpr int MM_PITCH = MM_KB * 32 + 16;  // LDS row pitch (bytes), padded against bank conflicts
-constexpr int MM_THREADS = 256;
+constexpr int MM_ROWS = 128;               // weight rows per work item (two 64-row groups)
+constexpr int MM_TOK = 128;                // pairs (tokens) per tile
+constexpr int MM_KB = 4;                   // GGUF blocks per K step
+constexpr int MM_WAVES = 8;                // 2 row slabs x 4 token quarters
+constexpr int MM_THREADS = MM_WAVES * WAVE;
+constexpr int MM_RING = 3;                 // LDS stages: one computed, two in flight
+constexpr int MM_XCD = 8;                  // XCDs of the device (work-group round robin)
+
+// LDS stage layout (bytes).  A: 8 chunks (2 row groups x 4 blocks) of 64 rows x 32 B
+// int8; A raw (Q4_0): 8 chunks of 64 rows x 16 B nibbles; B: 128 tokens x 128 B;
+// A scales: 8 chunks x 64 fp16; B scales: 128 tokens x 4 f32.
+constexpr int ST_A = 8 * 64 * 32;
+constexpr int ST_AR = 8 * 64 * 16;
+constexpr int ST_B = MM_TOK * MM_KB * 32;
+constexpr int ST_AS = 8 * 64 * 2;
+constexpr int ST_BS = MM_TOK * MM_KB * 4;
 
 struct MmArgs {
     MatView W;
     Routing R;
     const int8_t* aq;   // activations int8 [rows][Kdim] (x for mode 0, h for modes 1/2)
-    const float* ad;    // activation scales [rows][Kdim/32]
+    const float* ad;    // activation scales [rows][Kdim/32] (exact fp16 values)
     int T, H, I, E, K;
     int Kdim;           // reduction length (H for mode 0, I for modes 1/2)
+    int nrb;            // row blocks of the weight matrix
+    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD
     int8_t* hq;         // mode 0 outputs
     float* hd;
     int* hs;
@@ -59,22 +78,90 @@ __device__ __forceinline__ void unpack_q4(const int4 w, int4& lo, int4& hi) {
     hi = make_int4(cv((w.x >> 4) & m), cv((w.y >> 4) & m), cv((w.z >> 4) & m), cv((w.w >> 4) & m));
 }
 
-template <int WT, int MODE>
-__global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
-    __shared__ __align__(16) int8_t As[2][MM_ROWS][MM_PITCH];
-    __shared__ __align__(16) int8_t Bs[2][MM_TOK][MM_PITCH];
-    __shared__ __align__(16) float Asc[2][MM_KB][MM_ROWS];  // row-contiguous: float4 = 4 rows
-    __shared__ __align__(16) float Bsc[2][MM_KB][MM_TOK];
-    __shared__ int tok_s[MM_TOK], slot_s[MM_TOK];
+// Per-block scale products c[row][tok] = d_w[row] * d_x[tok] for a 32x32 tile from one
+// f16 MFMA: A holds d_w in k-slot 0 of lane group 0, B holds d_x in the same slot,
+// every other slot is zero.  The product of two fp16 values is exact in fp32, so c
+// equals the float multiply d_w * d_x bit for bit.
+__device__ __forceinline__ v16f_t scale_outer(_Float16 dw, _Float16 dx, int lg) {
+    v8h_t a = {}, b = {};
+    if (lg == 0) {
+        a[0] = dw;
+        b[0] = dx;
+    }
+    const v16f_t zero = {};
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, zero, 0, 0, 0);
+}
 
-    const int tile = (MODE == 2) ? a.R.meta[0] + (int)blockIdx.x : (int)blockIdx.x;
+// 16-byte global -> LDS copy (global_load_lds_dwordx4): lane i of the wave writes
+// lds_wave_base + 16*i.  The wave's loads are tracked by vmcnt, not by barriers.
+__device__ __forceinline__ void g2l16(const void* g, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
+#define MM_WAIT_VM_LGKM(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (((N) >> 4) << 14))
+
+// LDS reads of the ring are issued as plain ds_read instructions: the compiler does
+// not associate them with the in-flight global->LDS copies (it would otherwise wait
+// for every outstanding copy, including the stages being prefetched).  Their
+// completion is waited for explicitly (lds_wait) before any result is used; the
+// vmcnt wait + barrier at the top of each stage orders them after the copies.
+typedef __attribute__((address_space(3))) const uint8_t lds_u8_t;
+__device__ __forceinline__ uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)((lds_u8_t*)p); }
+__device__ __forceinline__ v4i_t lds_b128(const void* p) {
+    v4i_t r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_off(p)));
+    return r;
+}
+__device__ __forceinline__ uint32_t lds_u16(const void* p) {
+    uint32_t r;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_off(p)));
+    return r;
+}
+__device__ __forceinline__ uint32_t lds_b32(const void* p) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_off(p)));
+    return r;
+}
+__device__ __forceinline__ void lds_st128(void* p, v4i_t v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// wait for the ds_reads whose results are passed in: the values are threaded through
+// the asm so no consumer can be scheduled ahead of the wait
+__device__ __forceinline__ void lds_wait(v4i_t& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, uint32_t& d, uint32_t& e, uint32_t& f) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
+}
+
+template <int WT, int MODE>
+__global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
+    constexpr bool Q4 = WT == HY_TYPE_Q4_0;
+    constexpr int STAGE = ST_A * (Q4 ? 0 : 1) + (Q4 ? ST_AR : 0) + ST_B + ST_AS + ST_BS;
+    __shared__ __align__(16) uint8_t ring[MM_RING][STAGE];
+    __shared__ __align__(16) int8_t aun[Q4 ? ST_A : 16];  // Q4_0: unpacked A of the current stage
+    __shared__ int tok_s[MM_TOK], slot_s[MM_TOK];
+    constexpr int OFF_A = 0;                                  // Q8_0: int8 A; Q4_0: raw nibbles
+    constexpr int OFF_B = Q4 ? ST_AR : ST_A;
+    constexpr int OFF_AS = OFF_B + ST_B;
+    constexpr int OFF_BS = OFF_AS + ST_AS;
+    constexpr int LOADS = (Q4 ? 1 : 2) + 2 + 1 + 1;           // per wave per stage
+
+    // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
+    // all row blocks of a tile the same id mod MM_XCD (they share the tile's
+    // activation rows in that XCD's L2).
+    const int id = (int)blockIdx.x;
+    const int xcd = id % MM_XCD, local = id / MM_XCD;
+    const int tile_rel = xcd + MM_XCD * (local / a.nrb);
+    const int rb = local % a.nrb;
+    const int tile = (MODE == 2) ? a.R.meta[0] + tile_rel : tile_rel;
     if (tile >= a.R.meta[MODE == 1 ? 0 : 1]) return;
     const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
-    const int row0 = blockIdx.y * MM_ROWS;
+    const int row0 = rb * MM_ROWS;
     const int Kd = a.Kdim;
     const int nb = Kd / QK;
     const int tid = threadIdx.x;
+    const int wave = tid / WAVE, lane = tid % WAVE;
 
     if (tid < MM_TOK) {
         int tok = 0, slot = 0;
@@ -92,88 +179,43 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     }
     __syncthreads();
 
-    // ---- global -> register staging
     const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride;
     const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride;
-    constexpr int A_VEC = (WT == HY_TYPE_Q4_0) ? (MM_ROWS * MM_KB) / MM_THREADS       // int4 of nibbles
-                                               : (MM_ROWS * MM_KB * 2) / MM_THREADS;  // int4 of int8
-    constexpr int B_VEC = (MM_TOK * MM_KB * 2) / MM_THREADS;
-    int4 ra[A_VEC], rb[B_VEC];
-    float rasc[2], rbsc;
-    // activation row of this thread's B loads
-    auto act_row = [&](int i) -> int { return (MODE == 0) ? tok_s[i] : slot_s[i]; };
-
-    // weights are row-group interleaved: block b of a 64-row group is one contiguous
-    // chunk of 64 * BPB bytes; a stage is 2 groups x MM_KB blocks = 8 chunks
-    constexpr int BPB = WT == HY_TYPE_Q4_0 ? 16 : 32;
+    constexpr int BPB = Q4 ? 16 : 32;
     const int G0 = row0 / 64;
-    auto chunk_base = [&](int chunk, int kb0) -> size_t {
-        return (((size_t)(G0 + (chunk >> 2)) * nb + kb0 + (chunk & 3)) * 64) * BPB;
-    };
-    auto load_stage = [&](int s) {
+    // this thread's B rows (two 1 KB loads per wave: 8 tokens x 128 B each)
+    const int bt0 = (wave * 2 + 0) * 8 + lane / 8, bt1 = (wave * 2 + 1) * 8 + lane / 8;
+    const int8_t* brow0 = a.aq + (size_t)(MODE == 0 ? tok_s[bt0] : slot_s[bt0]) * Kd + (lane % 8) * 16;
+    const int8_t* brow1 = a.aq + (size_t)(MODE == 0 ? tok_s[bt1] : slot_s[bt1]) * Kd + (lane % 8) * 16;
+    const int bst = wave * 16 + (lane & 15);  // B-scale token of this lane (lanes < 16)
+    const float* bsrow = a.ad + (size_t)(MODE == 0 ? tok_s[bst] : slot_s[bst]) * nb;
+
+    // issue the asynchronous loads of stage s into ring slot s % MM_RING
+    auto issue = [&](int s) {
+        uint8_t* st = ring[s % MM_RING];
         const int kb0 = s * MM_KB;
-#pragma unroll
-        for (int v = 0; v < A_VEC; v++) {
-            const int idx = tid + v * MM_THREADS;
-            if (WT == HY_TYPE_Q4_0) {  // 64 int4 (rows) per chunk
-                ra[v] = *reinterpret_cast<const int4*>(wq + chunk_base(idx >> 6, kb0) + (size_t)(idx & 63) * 16);
-            } else {                   // 128 int4 (rows x halves) per chunk
-                ra[v] = *reinterpret_cast<const int4*>(wq + chunk_base(idx >> 7, kb0) + (size_t)(idx & 127) * 16);
-            }
+        // A: chunk c = wave (group c>>2, block c&3); Q8_0 2 KB = 2 loads, Q4_0 1 KB = 1 load
+        const size_t cbase = (((size_t)(G0 + (wave >> 2)) * nb + kb0 + (wave & 3)) * 64) * BPB;
+        if (Q4) {
+            g2l16(wq + cbase + lane * 16, st + OFF_A + wave * 1024);
+        } else {
+            g2l16(wq + cbase + lane * 16, st + OFF_A + wave * 2048);
+            g2l16(wq + cbase + 1024 + lane * 16, st + OFF_A + wave * 2048 + 1024);
         }
-#pragma unroll
-        for (int v = 0; v < 2; v++) {
-            const int idx = tid + v * MM_THREADS;  // 8 chunks x 64 rows
-            const int chunk = idx >> 6;
-            rasc[v] = h2f(wsc[((size_t)(G0 + (chunk >> 2)) * nb + kb0 + (chunk & 3)) * 64 + (idx & 63)]);
-        }
-#pragma unroll
-        for (int v = 0; v < B_VEC; v++) {
-            const int idx = tid + v * MM_THREADS;
-            const int i = idx / (MM_KB * 2), c = idx % (MM_KB * 2);
-            rb[v] = i < n ? *reinterpret_cast<const int4*>(a.aq + (size_t)act_row(i) * Kd + (size_t)kb0 * QK + c * 16)
-                          : make_int4(0, 0, 0, 0);
-        }
-        {
-            const int i = tid / MM_KB, b = tid % MM_KB;  // 64 x 4 = 256
-            rbsc = i < n ? a.ad[(size_t)act_row(i) * nb + kb0 + b] : 0.0f;
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int v = 0; v < A_VEC; v++) {
-            const int idx = tid + v * MM_THREADS;
-            if (WT == HY_TYPE_Q4_0) {
-                const int chunk = idx >> 6, row = (chunk >> 2) * 64 + (idx & 63), kb = chunk & 3;
-                int4 lo, hi;
-                unpack_q4(ra[v], lo, hi);
-                *reinterpret_cast<int4*>(&As[buf][row][kb * 32]) = lo;
-                *reinterpret_cast<int4*>(&As[buf][row][kb * 32 + 16]) = hi;
-            } else {
-                const int chunk = idx >> 7, w = idx & 127;
-                const int row = (chunk >> 2) * 64 + (w >> 1), kb = chunk & 3;
-                *reinterpret_cast<int4*>(&As[buf][row][kb * 32 + (w & 1) * 16]) = ra[v];
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < 2; v++) {
-            const int idx = tid + v * MM_THREADS;
-            const int chunk = idx >> 6;
-            Asc[buf][chunk & 3][(chunk >> 2) * 64 + (idx & 63)] = rasc[v];
-        }
-#pragma unroll
-        for (int v = 0; v < B_VEC; v++) {
-            const int idx = tid + v * MM_THREADS;
-            const int i = idx / (MM_KB * 2), c = idx % (MM_KB * 2);
-            *reinterpret_cast<int4*>(&Bs[buf][i][c * 16]) = rb[v];
-        }
-        Bsc[buf][tid % MM_KB][tid / MM_KB] = rbsc;
+        // B: tokens (2*wave+v)*8 .. +8, 128 B each
+        g2l16(brow0 + (size_t)kb0 * QK, st + OFF_B + (wave * 2 + 0) * 1024);
+        g2l16(brow1 + (size_t)kb0 * QK, st + OFF_B + (wave * 2 + 1) * 1024);
+        // A scales: chunk `wave` = 64 fp16 = 128 B (lanes 0..7)
+        if (lane < 8)
+            g2l16(wsc + (((size_t)(G0 + (wave >> 2)) * nb + kb0 + (wave & 3)) * 64) + lane * 8,
+                  st + OFF_AS + wave * 128);
+        // B scales: tokens wave*16 .. +16, 4 f32 each (lanes 0..15)
+        if (lane < 16) g2l16(bsrow + kb0, st + OFF_BS + wave * 256);
     };
 
-    const int wave = tid / WAVE, lane = tid % WAVE;
-    const int sl = wave & 1;          // 64-row slab within the row block
-    const int nh = wave >> 1;         // 32-token half of the tile
-    const bool active = nh * 32 < n;  // waves past the tile's last pair skip the math
+    const int sl = wave & 1;           // 64-row slab within the row block
+    const int nq = wave >> 1;          // 32-token quarter of the tile
+    const bool active = nq * 32 < n;   // waves past the tile's last pair skip the math
     const int lr = lane % 32, lg = lane / 32;
     float acc0[16], acc1[16];
 #pragma unroll
@@ -183,50 +225,71 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     }
 
     const int nstage = nb / MM_KB;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
+    issue(0);
+    if (nstage > 1) issue(1);
     for (int s = 0; s < nstage; s++) {
-        const int buf = s & 1;
-        if (s + 1 < nstage) load_stage(s + 1);
+        // stage s landed (this wave's loads), and every wave's (barrier)
+        if (s + 1 < nstage) {
+            MM_WAIT_VM_LGKM(LOADS);
+        } else {
+            MM_WAIT_VM_LGKM(0);
+        }
+        __builtin_amdgcn_s_barrier();
+        const uint8_t* st = ring[s % MM_RING];
+        const int8_t* As;
+        if (Q4) {
+            // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of chunk t/64
+            const int c = tid >> 6, r = tid & 63;
+            v4i_t wv = lds_b128(st + OFF_A + c * 1024 + r * 16);
+            lds_wait(wv);
+            int4 lo, hi;
+            unpack_q4(make_int4(wv[0], wv[1], wv[2], wv[3]), lo, hi);
+            lds_st128(aun + c * 2048 + r * 32, v4i_t{lo.x, lo.y, lo.z, lo.w});
+            lds_st128(aun + c * 2048 + r * 32 + 16, v4i_t{hi.x, hi.y, hi.z, hi.w});
+            lds_wait();
+            __builtin_amdgcn_s_barrier();
+            As = aun;
+        } else {
+            As = reinterpret_cast<const int8_t*>(st + OFF_A);
+        }
+        const int8_t* Bs = reinterpret_cast<const int8_t*>(st + OFF_B);
+        const _Float16* Asc = reinterpret_cast<const _Float16*>(st + OFF_AS);
+        const float* Bsc = reinterpret_cast<const float*>(st + OFF_BS);
         if (active) {
 #pragma unroll
             for (int kb = 0; kb < MM_KB; kb++) {
-                const v4i_t A0 = *reinterpret_cast<const v4i_t*>(&As[buf][sl * 64 + lr][kb * 32 + 16 * lg]);
-                const v4i_t A1 = *reinterpret_cast<const v4i_t*>(&As[buf][sl * 64 + 32 + lr][kb * 32 + 16 * lg]);
-                const v4i_t B = *reinterpret_cast<const v4i_t*>(&Bs[buf][nh * 32 + lr][kb * 32 + 16 * lg]);
+                const int8_t* ach = As + (sl * 4 + kb) * 2048;
+                v4i_t A0 = lds_b128(ach + lr * 32 + 16 * lg);
+                v4i_t A1 = lds_b128(ach + (32 + lr) * 32 + 16 * lg);
+                v4i_t B = lds_b128(Bs + (nq * 32 + lr) * 128 + kb * 32 + 16 * lg);
+                uint32_t dw0 = lds_u16(Asc + (sl * 4 + kb) * 64 + lr);
+                uint32_t dw1 = lds_u16(Asc + (sl * 4 + kb) * 64 + 32 + lr);
+                uint32_t dxb = lds_b32(Bsc + (nq * 32 + lr) * 4 + kb);
+                lds_wait(A0, A1, B, dw0, dw1, dxb);
                 const v16i_t zero = {};
                 const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
                 const v16i_t S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
-                const float dx = Bsc[buf][kb][nh * 32 + lr];
+                const _Float16 dx = (_Float16)__builtin_bit_cast(float, dxb);  // exact: an fp16 value
+                const v16f_t C0 = scale_outer(__builtin_bit_cast(_Float16, (uint16_t)dw0), dx, lg);
+                const v16f_t C1 = scale_outer(__builtin_bit_cast(_Float16, (uint16_t)dw1), dx, lg);
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int r = 8 * g + 4 * lg;
-                    const float4 d0 = *reinterpret_cast<const float4*>(&Asc[buf][kb][sl * 64 + r]);
-                    const float4 d1 = *reinterpret_cast<const float4*>(&Asc[buf][kb][sl * 64 + 32 + r]);
-                    acc0[4 * g + 0] = fmaf((float)S0[4 * g + 0], d0.x * dx, acc0[4 * g + 0]);
-                    acc0[4 * g + 1] = fmaf((float)S0[4 * g + 1], d0.y * dx, acc0[4 * g + 1]);
-                    acc0[4 * g + 2] = fmaf((float)S0[4 * g + 2], d0.z * dx, acc0[4 * g + 2]);
-                    acc0[4 * g + 3] = fmaf((float)S0[4 * g + 3], d0.w * dx, acc0[4 * g + 3]);
-                    acc1[4 * g + 0] = fmaf((float)S1[4 * g + 0], d1.x * dx, acc1[4 * g + 0]);
-                    acc1[4 * g + 1] = fmaf((float)S1[4 * g + 1], d1.y * dx, acc1[4 * g + 1]);
-                    acc1[4 * g + 2] = fmaf((float)S1[4 * g + 2], d1.z * dx, acc1[4 * g + 2]);
-                    acc1[4 * g + 3] = fmaf((float)S1[4 * g + 3], d1.w * dx, acc1[4 * g + 3]);
+                for (int v = 0; v < 16; v++) {
+                    acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
+                    acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
                 }
             }
         }
-        if (s + 1 < nstage) {
-            store_stage(buf ^ 1);
-        }
-        __syncthreads();
+        // refill: slot (s+2) % 3 was last read in iteration s-1, finished by every
+        // wave before this iteration's barrier
+        if (s + 2 < nstage) issue(s + 2);
     }
 
     // ---- epilogues
-    const int j = nh * 32 + lr;  // pair index within the tile
+    const int j = nq * 32 + lr;  // pair index within the tile
     if (!active || j >= n) return;
     if (MODE == 0) {
         // acc0 = gate rows, acc1 = matching up rows of slab (2*blockIdx.y + sl)
-        const int slab = 2 * blockIdx.y + sl;
+        const int slab = 2 * rb + sl;
         float h[16];
         float amax = 0.0f;
 #pragma unroll
@@ -321,7 +384,10 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
 }
 
 template <int MODE>
-static hipError_t launch_mode(int wtype, dim3 grid, hipStream_t s, const MmArgs& a) {
+static hipError_t launch_mode(int wtype, MmArgs a, int n_tiles_bound, int nrb, hipStream_t s) {
+    a.nrb = nrb;
+    a.tiles_pad = (n_tiles_bound + MM_XCD - 1) / MM_XCD * MM_XCD;
+    const dim3 grid(a.tiles_pad * nrb);
     if (wtype == HY_TYPE_Q4_0)
         hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE>), grid, dim3(MM_THREADS), 0, s, a);
     else
@@ -338,16 +404,16 @@ int mfma_tile_tokens() { return MM_TOK; }
 
 hipError_t launch_ffn_up_mfma(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const ActQ& X,
                               int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, hipStream_t s) {
-    MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, hq, hd, hs, nullptr, nullptr, nullptr};
-    return launch_mode<0>(wtype, dim3(n_tiles_bound, 2 * I / MM_ROWS), s, a);
+    MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr, nullptr, nullptr};
+    return launch_mode<0>(wtype, a, n_tiles_bound, 2 * I / MM_ROWS, s);
 }
 
 hipError_t launch_ffn_down_mfma(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
                                 const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
                                 const float* resid, float* out, hipStream_t s) {
-    MmArgs a{W, R, hq, hd, T, H, I, E, K, I, nullptr, nullptr, nullptr, y, resid, out};
-    dim3 grid(n_tiles_bound, H / MM_ROWS);
-    return mode == 0 ? launch_mode<1>(wtype, grid, s, a) : launch_mode<2>(wtype, grid, s, a);
+    MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y, resid, out};
+    return mode == 0 ? launch_mode<1>(wtype, a, n_tiles_bound, H / MM_ROWS, s)
+                     : launch_mode<2>(wtype, a, n_tiles_bound, H / MM_ROWS, s);
 }
 
 }  // namespace hy

@@ -51,7 +51,9 @@ __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, fl
 // Router logits.  Work item of one wave = (TPW tokens) x (EPW experts); a block's
 // four waves take consecutive items, experts varying fastest so they share the
 // token rows in L1.  Small batches use <8,1> (64 experts -> 64 waves even at T=1),
-// large ones <4,8> (each Wr float4 feeds 4 tokens, 32 accumulators per lane).
+// large ones <4,8> (each Wr float4 feeds 4 tokens, 32 accumulators per lane).  The
+// h loop is unrolled so a lane's loads are issued together; the per-lane
+// accumulation order is unchanged.
 template <int TPW, int EPW>
 __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
     const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, float* __restrict__ logits) {
@@ -65,6 +67,10 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
     for (int t = 0; t < TPW; t++)
 #pragma unroll
         for (int e = 0; e < EPW; e++) acc[t][e] = 0.0f;
+    // small work items issue several chunks' loads at once; the 4x8 item keeps one
+    // chunk in flight (its 12 float4 loads per chunk already overlap)
+    constexpr int UNR = TPW * EPW <= 8 ? 4 : 1;
+#pragma unroll UNR
     for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
         float4 xv[TPW], wv[EPW];
 #pragma unroll
@@ -131,10 +137,19 @@ hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, i
 
 hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                            float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s) {
-    if (T <= 32) {
-        const int items = ((T + 7) / 8) * E;
-        hipLaunchKernelGGL((router_logits_kernel<8, 1>), dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES),
-                           dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, logits);
+    const dim3 blk(ROUTER_WAVES * WAVE);
+    auto grid_for = [&](int tpw, int epw) {
+        const int items = ((T + tpw - 1) / tpw) * ((E + epw - 1) / epw);
+        return dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES);
+    };
+    if (T == 1) {
+        hipLaunchKernelGGL((router_logits_kernel<1, 1>), grid_for(1, 1), blk, 0, s, x, wr, T, H, E, logits);
+    } else if (T <= 2) {
+        hipLaunchKernelGGL((router_logits_kernel<2, 1>), grid_for(2, 1), blk, 0, s, x, wr, T, H, E, logits);
+    } else if (T <= 4) {
+        hipLaunchKernelGGL((router_logits_kernel<4, 1>), grid_for(4, 1), blk, 0, s, x, wr, T, H, E, logits);
+    } else if (T <= 32) {
+        hipLaunchKernelGGL((router_logits_kernel<8, 1>), grid_for(8, 1), blk, 0, s, x, wr, T, H, E, logits);
     } else {
         const int items = ((T + 3) / 4) * ((E + 7) / 8);
         hipLaunchKernelGGL((router_logits_kernel<4, 8>), dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES),
@@ -149,9 +164,9 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
 
 // top-k gating from given logits (topkgating_easy, src/hunyuan_moe_full.cpp:88-113):
 // one wave per token.
-hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, float* topw, int* topi,
-                                   hipStream_t s) {
-    hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, 1, 1.0f, topw,
+hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, int norm, float scale, float* topw,
+                                   int* topi, hipStream_t s) {
+    hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, norm, scale, topw,
                        topi, nullptr, 0, nullptr, nullptr, nullptr);
     return hipGetLastError();
 }
@@ -256,11 +271,30 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __rest
     __shared__ int off_s[MAX_E + 1];
     __shared__ int toff_s[MAX_E + 1];
     const int tid = threadIdx.x;
+    const int P = T * K;
+    if (tid < MAX_E) run_s[tid] = 0;
+    if (P <= DSP_THREADS) {
+        // few pairs (decode): each thread ranks its own pair directly against all
+        // others held in LDS (same k-major priority order as the bitmap path)
+        __shared__ int pe_s[DSP_THREADS];
+        if (tid < P) pe_s[tid] = topi[tid];
+        __syncthreads();
+        if (tid < P) {
+            const int e = pe_s[tid], k = tid % K, t = tid / K;
+            int rank = 0;
+            for (int q = 0; q < P; q++) {
+                const int kq = q % K, tq = q / K;
+                rank += (pe_s[q] == e) && (kq < k || (kq == k && tq < t));
+            }
+            o.pair_pos[tid] = rank;
+            atomicAdd(&run_s[e], 1);
+        }
+        __syncthreads();
+    } else {
     const int nwords = (T + 31) / 32;
     const int e = tid / 16, c = tid % 16;  // 16 threads per expert, each a run of words
     const int wpc = (nwords + 15) / 16;
     const int w0 = c * wpc, w1 = min(nwords, w0 + wpc);
-    if (tid < MAX_E) run_s[tid] = 0;
     for (int k = 0; k < K; k++) {
         for (int i = tid; i < MAX_E * nwords; i += DSP_THREADS) mask[i / nwords][i % nwords] = 0u;
         __syncthreads();
@@ -294,6 +328,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __rest
             run_s[e] += tot;
         }
         __syncthreads();
+    }
     }
     if (tid == 0) {
         int acc = 0, tacc = 0, distinct = 0;

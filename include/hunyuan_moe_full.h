@@ -1,0 +1,158 @@
+// hunyuan_moe_full.h -- the reference's MoE-block C++ API, served by the MI355X library.
+//
+// Same names, types and argument meaning as the reference's src/hunyuan_moe_full.h
+// (MoERoutingConfig, MoEGateOutput, topkgating_full/_easy, einsum_dispatch/_combine,
+// moe_forward_full, softmax_f32, topk_f32) and the MoE part of src/hunyuan_model.h
+// (HunyuanConfig, MoEWeights, swiglu_ffn_f32, moe_forward_cpu, rms_norm_f32).  Inputs
+// and outputs are host arrays as in the reference; every call runs on the GPU through
+// the C ABI of hy_moe.h (upload, HIP kernels, download) and blocks until done.
+//
+// Differences from the reference, all deliberate:
+//  * errors throw hy::Error (std::runtime_error) instead of undefined behaviour, and
+//    no output is written on error;
+//  * expert selection compares logits (softmax is monotone), so experts whose
+//    probabilities round to the same float but whose logits differ are ordered by
+//    logit rather than by index;
+//  * topkgating_full / moe_forward_full run the default routing subset on the GPU
+//    (group-limited greedy, token dropping and the aux loss throw hy::Error);
+//  * MoEGateOutput cannot be copied (the reference's implicit copy double-frees).
+// Beyond the reference: quantized-weight (GGUF Q8_0 / Q4_0) overloads and
+// hy::MoeStack, a resident multi-layer context.
+#pragma once
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "hy_moe.h"
+
+// src/hunyuan_moe_full.h:25-47
+struct MoERoutingConfig {
+    uint32_t num_experts = 64;
+    uint32_t moe_topk = 8;
+    bool group_limited_greedy = false;
+    uint32_t n_group = 0;
+    uint32_t topk_group = 0;
+    bool drop_tokens = false;
+    bool random_routing_dropped_token = false;
+    float capacity_factor = 1.0f;
+    uint32_t min_capacity = 8;
+    bool norm_topk_prob = true;
+    float routed_scaling_factor = 1.0f;
+    bool compute_aux_loss = false;
+};
+
+// src/hunyuan_moe_full.h:49-70
+struct MoEGateOutput {
+    float* combine_weights = nullptr;  // [tokens, experts, capacity]
+    bool* dispatch_mask = nullptr;     // [tokens, experts, capacity]
+    int32_t* exp_counts = nullptr;     // [num_experts]
+    float aux_loss = 0.0f;
+    float exp_capacity_rate = 0.0f;
+    uint32_t expert_capacity = 0;
+    float* topk_weights = nullptr;     // [tokens, topk]
+    int32_t* topk_indices = nullptr;   // [tokens, topk]
+    float* router_probs = nullptr;     // [tokens, experts]
+    uint32_t n_tokens = 0;
+    bool use_dispatch_mask = false;
+
+    MoEGateOutput() = default;
+    MoEGateOutput(const MoEGateOutput&) = delete;
+    MoEGateOutput& operator=(const MoEGateOutput&) = delete;
+    ~MoEGateOutput();
+    void alloc(uint32_t tokens, uint32_t experts, uint32_t topk, uint32_t capacity, bool dispatch);
+};
+
+void topkgating_full(const float* logits, uint32_t n_tokens, const MoERoutingConfig& cfg, MoEGateOutput& out);
+void topkgating_easy(const float* logits, uint32_t n_tokens, uint32_t num_experts, uint32_t topk,
+                     float* topk_weights, int32_t* topk_indices);
+void einsum_dispatch(const float* input, uint32_t n_tokens, uint32_t hidden_size, const bool* dispatch_mask,
+                     uint32_t num_experts, uint32_t expert_capacity, float* dispatched_input);
+void einsum_combine(const float* combine_weights, const float* expert_output, uint32_t n_tokens,
+                    uint32_t hidden_size, uint32_t num_experts, uint32_t expert_capacity, float* combined_output);
+void moe_forward_full(const float* hidden_states, uint32_t n_tokens, uint32_t hidden_size,
+                      const float* router_weight, const float* shared_gate_up, const float* shared_down,
+                      const float* expert_gate_up_stacked, const float* expert_down_stacked, uint32_t num_experts,
+                      uint32_t intermediate_size, const MoERoutingConfig& routing_cfg, float* output);
+void softmax_f32(float* x, uint32_t n);
+void topk_f32(const float* x, uint32_t n, uint32_t k, float* topk_vals, int32_t* topk_idx);
+
+// Quantized-weight overload: weights in ggml layout (ne0 = in-features) of type
+// ggml_type HY_TYPE_Q8_0 / HY_TYPE_Q4_0 / HY_TYPE_F32, experts stacked.
+void moe_forward_full(const float* hidden_states, uint32_t n_tokens, uint32_t hidden_size,
+                      const float* router_weight, const void* shared_gate_up, const void* shared_down,
+                      const void* expert_gate_up_stacked, const void* expert_down_stacked, int ggml_type,
+                      uint32_t num_experts, uint32_t intermediate_size, const MoERoutingConfig& routing_cfg,
+                      float* output);
+
+// The MoE part of src/hunyuan_model.h:13-45 (defaults of HunyuanConfig).
+struct HunyuanConfig {
+    uint32_t hidden_size = 4096;
+    uint32_t num_hidden_layers = 32;
+    uint32_t num_attention_heads = 32;
+    uint32_t num_key_value_heads = 8;
+    uint32_t attention_head_dim = 128;
+    uint32_t intermediate_size = 3072;
+    uint32_t moe_intermediate_size = 3072;
+    uint32_t num_experts = 64;
+    uint32_t moe_topk = 8;
+    uint32_t num_shared_expert = 1;
+    uint32_t vocab_size = 133120;
+    uint32_t max_position_embeddings = 22800;
+    float rms_norm_eps = 1e-5f;
+    float rope_theta = 10000.0f;
+    bool use_qk_norm = true;
+    bool use_mixed_mlp_moe = true;
+};
+
+// src/hunyuan_model.h:130-145
+struct MoEWeights {
+    std::vector<float> shared_gate_up;  // [2*intermediate, hidden_size]
+    std::vector<float> shared_down;     // [hidden_size, intermediate]
+    std::vector<float> router_weight;   // [num_experts, hidden_size]
+    struct ExpertW {
+        std::vector<float> gate_up;  // [2*intermediate, hidden_size]
+        std::vector<float> down;     // [hidden_size, intermediate]
+    };
+    std::vector<ExpertW> experts;
+    uint32_t num_experts = 0;
+};
+
+// src/hunyuan_model.h:118-125 / src/rms_norm.cpp:39-91
+void swiglu_ffn_f32(const float* x, const float* gate_up_weight, const float* down_weight, float* out, uint32_t n,
+                    uint32_t hidden_size, uint32_t intermediate_size);
+// src/hunyuan_model.h:147-156 / src/attention.cpp:191-313
+void moe_forward_cpu(const float* hidden_states, const MoEWeights& w, uint32_t n_tokens, const HunyuanConfig& cfg,
+                     float* output, float* debug_router_logits = nullptr, float* debug_router_weights = nullptr,
+                     int32_t* debug_router_indices = nullptr);
+// src/rms_norm.cpp:9-33
+void rms_norm_f32(const float* x, const float* weight, float* out, uint32_t n_tokens, uint32_t hidden_size, float eps);
+
+namespace hy {
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+// Resident multi-layer MoE context (RAII over hy_moe_ctx): upload each layer once,
+// then forward device buffers many times.
+class MoeStack {
+public:
+    explicit MoeStack(const hy_moe_config& cfg);
+    ~MoeStack();
+    MoeStack(const MoeStack&) = delete;
+    MoeStack& operator=(const MoeStack&) = delete;
+    void upload_layer(uint32_t layer, const float* router, const void* shared_gu, const void* shared_dn,
+                      const void* gu, const void* dn);
+    void forward(uint32_t layer, const float* x_dev, uint32_t T, float* out_dev, void* stream = nullptr);
+    void stack_forward(uint32_t first, uint32_t n, const float* x_dev, uint32_t T, float eps, float* out_dev,
+                       void* stream = nullptr);
+    hy_moe_ctx* handle() { return ctx_; }
+
+private:
+    hy_moe_ctx* ctx_ = nullptr;
+};
+
+}  // namespace hy

@@ -139,6 +139,12 @@ int hy_router_topk(const float* x_dev, const float* wr_dev, uint32_t T, uint32_t
 int hy_topkgating_easy(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K,
                        float* weights_dev, int32_t* indices_dev, void* stream);
 
+/* Top-k selection and weights from precomputed logits with the routing options of
+ * topkgating_full (src/hunyuan_moe_full.cpp:229-243): renormalise when norm_topk_prob,
+ * else scale by routed_scaling_factor. */
+int hy_route_logits(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K, int32_t norm_topk_prob,
+                    float routed_scaling_factor, float* weights_dev, int32_t* indices_dev, void* stream);
+
 /* softmax_f32 (src/hunyuan_moe_full.h:148) over each of `rows` rows of n (n <= 1024). */
 int hy_softmax_rows(float* x_dev, uint32_t rows, uint32_t n, void* stream);
 
@@ -157,8 +163,36 @@ int hy_dequantize(int32_t type, const void* blocks_dev, size_t n, float* out_dev
 int hy_block_dots(int32_t wtype, const void* w_blocks_dev, const void* x_blocks_dev, uint32_t rows,
                   uint32_t n, int32_t path, int32_t* out_dev, void* stream);
 
-/* RMSNorm with unit weight (blocked sum of squares, eps) over T rows of H. */
+/* RMSNorm over T rows of H: out = x * (1/sqrtf(ss/H + eps)) * w, ss in the router's
+ * blocked order; w_dev may be NULL for unit weight.  rms_norm_f32
+ * (src/rms_norm.cpp:9-33). */
 int hy_rms_norm(const float* x_dev, uint32_t T, uint32_t H, float eps, float* out_dev, void* stream);
+int hy_rms_norm_w(const float* x_dev, const float* w_dev, uint32_t T, uint32_t H, float eps,
+                  float* out_dev, void* stream);
+
+/* topk_f32 (src/hunyuan_moe_full.h:154-155, .cpp:56-82) over each of `rows` rows of n
+ * values (n <= 4096, k <= 64): descending, equal values keep the lower index. */
+int hy_topk_rows(const float* x_dev, uint32_t rows, uint32_t n, uint32_t k, float* vals_dev,
+                 int32_t* idx_dev, void* stream);
+
+/* Token -> expert dispatch of T*K routed pairs (indices_dev [T][K]): per-expert counts
+ * [E], list offsets [E+1], and each pair's position in the expert-sorted order
+ * (pos_dev [T][K]).  Inside an expert the order is the reference's capacity-slot
+ * priority (flat slot k*T + t ascending, src/hunyuan_moe_full.cpp:245-304), so
+ * pos - offsets[e] is the dispatch_mask slot c. */
+int hy_dispatch_pairs(const int32_t* indices_dev, const float* weights_dev, uint32_t T, uint32_t K,
+                      uint32_t E, int32_t* counts_dev, int32_t* offsets_dev, int32_t* pos_dev,
+                      void* stream);
+
+/* einsum_dispatch (src/hunyuan_moe_full.h:95-102): out[e][c][:] = sum of x[t][:] over
+ * t with mask[t][e][c] (mask: one byte per entry). */
+int hy_einsum_dispatch(const float* x_dev, uint32_t T, uint32_t H, const uint8_t* mask_dev,
+                       uint32_t E, uint32_t C, float* out_dev, void* stream);
+
+/* einsum_combine (src/hunyuan_moe_full.h:108-115): out[t][:] = sum over (e, c) of
+ * combine_weights[t][e][c] * expert_output[e][c][:], e and c ascending. */
+int hy_einsum_combine(const float* cw_dev, const float* eo_dev, uint32_t T, uint32_t H, uint32_t E,
+                      uint32_t C, float* out_dev, void* stream);
 
 /* ---- device memory / streams / timing helpers ------------------------------ */
 int hy_device_count(int* n);
