@@ -247,7 +247,7 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode
     const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) &&
                       (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
-    const int NT = mfma ? hy::mfma_tile_tokens() : hy::gemv_tile_tokens();
+    const int NT = mfma ? hy::mfma_tile_tokens(iT, K, E, H, I) : hy::gemv_tile_tokens();
     HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
         return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
                                    c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
@@ -259,16 +259,16 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int shared_tiles = has_shared ? (iT + NT - 1) / NT : 0;
     if (mfma) {
         HY_TRY(timed(c, hy::KID_UP, s, [&] {
-            return hy::launch_ffn_up_mfma(wt, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
+            return hy::launch_ffn_up_mfma(wt, NT, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
                                           c->hd, c->hs, s);
         }));
         HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
-            return hy::launch_ffn_down_mfma(wt, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
+            return hy::launch_ffn_down_mfma(wt, NT, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
                                             c->y, nullptr, nullptr, s);
         }));
         if (has_shared)
             HY_TRY(timed(c, hy::KID_DOWN_SHARED, s, [&] {
-                return hy::launch_ffn_down_mfma(wt, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
+                return hy::launch_ffn_down_mfma(wt, NT, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
                                                 c->y, resid, out, s);
             }));
         else

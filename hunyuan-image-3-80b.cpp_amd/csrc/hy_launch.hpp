@@ -41,12 +41,14 @@ hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x,
 
 // expert products, MFMA path (hy_mfma.hip)
 bool mfma_path_ok(int wtype, int H, int I);
-int mfma_tile_tokens();
-hipError_t launch_ffn_up_mfma(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const ActQ& X,
-                              int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, hipStream_t s);
-hipError_t launch_ffn_down_mfma(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
-                                const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
-                                const float* resid, float* out, hipStream_t s);
+// pairs per tile of the MFMA shape used for this batch (the dispatch must tile with it)
+int mfma_tile_tokens(int T, int K, int E, int H, int I);
+hipError_t launch_ffn_up_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+                              const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
+                              hipStream_t s);
+hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, int mode, const MatView& W,
+                                const Routing& R, const int8_t* hq, const float* hd, int T, int H, int I, int E,
+                                int K, float* y, const float* resid, float* out, hipStream_t s);
 
 // residency (hy_data.hip)
 hipError_t launch_synth_matrix(int wtype, uint64_t key, float scale, int rows, int cols, int gu_I, uint8_t* qs,

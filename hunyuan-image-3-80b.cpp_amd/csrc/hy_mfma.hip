@@ -1,13 +1,17 @@
 // hy_mfma.hip -- grouped expert GEMMs on the int8 matrix cores (prefill / image-token
 // batches).
 //
-// Work item = (tile, row block): a tile is up to 128 (token, expert) pairs of one
-// expert (or 128 consecutive tokens for the shared expert), a row block is 128 weight
-// rows (two 64-row groups of the row-group-interleaved weights).  Each K step
-// copies KB = 4 GGUF blocks (128 k) of the 128 weight rows and of the tile's 128
-// activation rows straight from global memory into an LDS ring of 3 stages (two in
-// flight while one is consumed).  Eight waves = 2 row slabs x
-// 4 token quarters; every wave owns 2 x (32 rows x 32 tokens) output tiles and, per
+// Work item = (tile, row block): a tile is up to TOK (token, expert) pairs of one
+// expert (or TOK consecutive tokens for the shared expert), a row block is ROWS weight
+// rows (ROWS/64 row groups of the row-group-interleaved weights).  Each K step copies
+// KB GGUF blocks of the ROWS weight rows and of the tile's TOK activation rows
+// straight from global memory into an LDS ring of 3 stages (two in flight while one is
+// consumed).  Two shapes, picked per call from the mean pairs per expert:
+//   wide  (ROWS 128, TOK 128, KB 4): 2 row slabs x 4 token quarters -- more reuse of
+//         each weight byte for large batches;
+//   tall  (ROWS 256, TOK  64, KB 2): 4 row slabs x 2 token halves -- keeps all eight
+//         waves busy when experts see ~64 pairs, two work groups per CU.
+// Eight waves; every wave owns 2 x (32 rows x 32 tokens) output tiles and, per
 // 32-wide block, issues
 // v_mfma_i32_32x32x32_i8: K = 32 is exactly one GGUF block, so each MFMA result is the
 // exact int32 block dot sum_j w_j x_j of ggml's vec_dot, which is then rescaled in
@@ -21,8 +25,8 @@
 // 16*(l/32) inside the block; result register v of lane l is row
 // 8*(v/4) + 4*(l/32) + v%4, column l%32.
 //
-// Modes: 0 = gate_up (packed rows: a 128-row block is two 64-row slabs of 32 SiLU +
-// 32 linear rows; epilogue h = silu(g) * u and Q8_0 quantization of h per token and
+// Modes: 0 = gate_up (packed rows: every 64-row slab holds 32 SiLU rows and the 32
+// matching linear rows; epilogue h = silu(g) * u and Q8_0 quantization of h per token and
 // slab); 1 = down for routed tiles (writes y[pair][row]); 2 = down for shared tiles
 // fused with the combine out = resid + (y_shared + sum_{e ascending} w_e y_e).
 #include "hy_device.hpp"
@@ -36,22 +40,35 @@ typedef int v16i_t __attribute__((ext_vector_type(16)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 
-constexpr int MM_ROWS = 128;               // weight rows per work item (two 64-row groups)
-constexpr int MM_TOK = 128;                // pairs (tokens) per tile
-constexpr int MM_KB = 4;                   // GGUF blocks per K step
-constexpr int MM_WAVES = 8;                // 2 row slabs x 4 token quarters
+constexpr int MM_WAVES = 8;
 constexpr int MM_THREADS = MM_WAVES * WAVE;
 constexpr int MM_RING = 3;                 // LDS stages: one computed, two in flight
 constexpr int MM_XCD = 8;                  // XCDs of the device (work-group round robin)
 
-// LDS stage layout (bytes).  A: 8 chunks (2 row groups x 4 blocks) of 64 rows x 32 B
-// int8; A raw (Q4_0): 8 chunks of 64 rows x 16 B nibbles; B: 128 tokens x 128 B;
-// A scales: 8 chunks x 64 fp16; B scales: 128 tokens x 4 f32.
-constexpr int ST_A = 8 * 64 * 32;
-constexpr int ST_AR = 8 * 64 * 16;
-constexpr int ST_B = MM_TOK * MM_KB * 32;
-constexpr int ST_AS = 8 * 64 * 2;
-constexpr int ST_BS = MM_TOK * MM_KB * 4;
+// Tile shape.  LDS stage layout (bytes): A = CHUNKS (row group x block) chunks of
+// 64 rows x 32 B int8 (Q4_0: 64 rows x 16 B raw nibbles); B = TOK tokens x KB*32 B;
+// A scales = CHUNKS x 64 fp16; B scales = TOK tokens x KB f32.
+template <int ROWS_, int TOK_, int KB_>
+struct MmShape {
+    static constexpr int ROWS = ROWS_, TOK = TOK_, KB = KB_;
+    static constexpr int SLABS = ROWS / 64;          // 64-row slabs (one per row group)
+    static constexpr int TQ = MM_WAVES / SLABS;      // 32-token column groups
+    static constexpr int CHUNKS = SLABS * KB;
+    static constexpr int ST_A = CHUNKS * 64 * 32;
+    static constexpr int ST_AR = CHUNKS * 64 * 16;
+    static constexpr int ST_B = TOK * KB * 32;
+    static constexpr int ST_AS = CHUNKS * 64 * 2;
+    static constexpr int ST_BS = TOK * KB * 4;
+    // B rows: each wave copies TOK/8 tokens x KB*32 B with 16-byte lanes
+    static constexpr int B_LANES = TOK / MM_WAVES * KB * 2;
+    static constexpr int B_LOADS = (B_LANES + WAVE - 1) / WAVE;
+    static_assert(CHUNKS == MM_WAVES, "one A chunk per wave per stage");
+    static_assert(TQ * 32 == TOK, "token groups must cover the tile");
+    static_assert(B_LANES % WAVE == 0 || B_LOADS == 1, "partial B loads only as a single load");
+    static_assert(KB == 4 || KB == 2, "B-scale copy handles 16 B or 8 B per token");
+};
+using ShapeWide = MmShape<128, 128, 4>;
+using ShapeTall = MmShape<256, 64, 2>;
 
 struct MmArgs {
     MatView W;
@@ -61,7 +78,7 @@ struct MmArgs {
     int T, H, I, E, K;
     int Kdim;           // reduction length (H for mode 0, I for modes 1/2)
     int nrb;            // row blocks of the weight matrix
-    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD
+    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD (unused by the kernel)
     int8_t* hq;         // mode 0 outputs
     float* hd;
     int* hs;
@@ -133,18 +150,20 @@ __device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, uint32_t&
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
 }
 
-template <int WT, int MODE>
-__global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
+template <int WT, int MODE, class SH>
+__global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_kernel(MmArgs a) {
+    constexpr int MM_ROWS = SH::ROWS, MM_TOK = SH::TOK, MM_KB = SH::KB, MM_SLABS = SH::SLABS;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
-    constexpr int STAGE = ST_A * (Q4 ? 0 : 1) + (Q4 ? ST_AR : 0) + ST_B + ST_AS + ST_BS;
+    constexpr int STAGE = SH::ST_A * (Q4 ? 0 : 1) + (Q4 ? SH::ST_AR : 0) + SH::ST_B + SH::ST_AS + SH::ST_BS;
     __shared__ __align__(16) uint8_t ring[MM_RING][STAGE];
-    __shared__ __align__(16) int8_t aun[Q4 ? ST_A : 16];  // Q4_0: unpacked A of the current stage
+    __shared__ __align__(16) int8_t aun[Q4 ? SH::ST_A : 16];  // Q4_0: unpacked A of the current stage
     __shared__ int tok_s[MM_TOK], slot_s[MM_TOK];
     constexpr int OFF_A = 0;                                  // Q8_0: int8 A; Q4_0: raw nibbles
-    constexpr int OFF_B = Q4 ? ST_AR : ST_A;
-    constexpr int OFF_AS = OFF_B + ST_B;
-    constexpr int OFF_BS = OFF_AS + ST_AS;
-    constexpr int LOADS = (Q4 ? 1 : 2) + 2 + 1 + 1;           // per wave per stage
+    constexpr int OFF_B = Q4 ? SH::ST_AR : SH::ST_A;
+    constexpr int OFF_AS = OFF_B + SH::ST_B;
+    constexpr int OFF_BS = OFF_AS + SH::ST_AS;
+    // copies per wave per stage (every wave issues the same number; vmcnt counts them)
+    constexpr int LOADS = (Q4 ? 1 : 2) + SH::B_LOADS + 1 + 1;
 
     // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
     // all row blocks of a tile the same id mod MM_XCD (they share the tile's
@@ -183,38 +202,57 @@ __global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
     const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride;
     constexpr int BPB = Q4 ? 16 : 32;
     const int G0 = row0 / 64;
-    // this thread's B rows (two 1 KB loads per wave: 8 tokens x 128 B each)
-    const int bt0 = (wave * 2 + 0) * 8 + lane / 8, bt1 = (wave * 2 + 1) * 8 + lane / 8;
-    const int8_t* brow0 = a.aq + (size_t)(MODE == 0 ? tok_s[bt0] : slot_s[bt0]) * Kd + (lane % 8) * 16;
-    const int8_t* brow1 = a.aq + (size_t)(MODE == 0 ? tok_s[bt1] : slot_s[bt1]) * Kd + (lane % 8) * 16;
-    const int bst = wave * 16 + (lane & 15);  // B-scale token of this lane (lanes < 16)
-    const float* bsrow = a.ad + (size_t)(MODE == 0 ? tok_s[bst] : slot_s[bst]) * nb;
+    // B rows: wave w copies tokens w*TOK/8 .. +TOK/8, KB*32 bytes each, as 16-byte
+    // pieces; piece p (load v, lane l: p = 64 v + l) is token p / (2 KB), offset
+    // 16 (p % (2 KB)) -- lane i of a copy lands at +16 i, i.e. tokens stay row-major
+    constexpr int BPT = 2 * MM_KB;  // 16-byte pieces per token row
+    const int8_t* brow[SH::B_LOADS];
+#pragma unroll
+    for (int v = 0; v < SH::B_LOADS; v++) {
+        const int p = v * WAVE + lane;
+        const int bt = wave * (MM_TOK / MM_WAVES) + (p % SH::B_LANES) / BPT;  // in range for masked lanes too
+        brow[v] = a.aq + (size_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * Kd + (p % BPT) * 16;
+    }
+    // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each: KB = 4 as one
+    // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces
+    constexpr int BS_LANES = MM_KB == 4 ? MM_TOK / MM_WAVES : MM_TOK / MM_WAVES * MM_KB;
+    const int bst = wave * (MM_TOK / MM_WAVES) + (MM_KB == 4 ? lane : lane / MM_KB) % (MM_TOK / MM_WAVES);
+    const float* bsrow = a.ad + (size_t)(MODE == 0 ? tok_s[bst] : slot_s[bst]) * nb + (MM_KB == 4 ? 0 : lane % MM_KB);
 
-    // issue the asynchronous loads of stage s into ring slot s % MM_RING
+    // issue the asynchronous copies of stage s into ring slot s % MM_RING; lanes
+    // outside a copy's range are masked (the wave still issues it once)
     auto issue = [&](int s) {
         uint8_t* st = ring[s % MM_RING];
         const int kb0 = s * MM_KB;
-        // A: chunk c = wave (group c>>2, block c&3); Q8_0 2 KB = 2 loads, Q4_0 1 KB = 1 load
-        const size_t cbase = (((size_t)(G0 + (wave >> 2)) * nb + kb0 + (wave & 3)) * 64) * BPB;
+        // A: chunk c = wave (row group c / KB, block c % KB); Q8_0 2 KB = 2 copies,
+        // Q4_0 1 KB = 1 copy
+        const size_t cidx = (size_t)(G0 + wave / MM_KB) * nb + kb0 + wave % MM_KB;
+        const size_t cbase = cidx * 64 * BPB;
         if (Q4) {
             g2l16(wq + cbase + lane * 16, st + OFF_A + wave * 1024);
         } else {
             g2l16(wq + cbase + lane * 16, st + OFF_A + wave * 2048);
             g2l16(wq + cbase + 1024 + lane * 16, st + OFF_A + wave * 2048 + 1024);
         }
-        // B: tokens (2*wave+v)*8 .. +8, 128 B each
-        g2l16(brow0 + (size_t)kb0 * QK, st + OFF_B + (wave * 2 + 0) * 1024);
-        g2l16(brow1 + (size_t)kb0 * QK, st + OFF_B + (wave * 2 + 1) * 1024);
+        // B rows of this wave's tokens
+        uint8_t* bdst = st + OFF_B + wave * (MM_TOK / MM_WAVES) * (MM_KB * 32);
+#pragma unroll
+        for (int v = 0; v < SH::B_LOADS; v++)
+            if (v * WAVE + lane < SH::B_LANES) g2l16(brow[v] + (size_t)kb0 * QK, bdst + v * 1024);
         // A scales: chunk `wave` = 64 fp16 = 128 B (lanes 0..7)
-        if (lane < 8)
-            g2l16(wsc + (((size_t)(G0 + (wave >> 2)) * nb + kb0 + (wave & 3)) * 64) + lane * 8,
-                  st + OFF_AS + wave * 128);
-        // B scales: tokens wave*16 .. +16, 4 f32 each (lanes 0..15)
-        if (lane < 16) g2l16(bsrow + kb0, st + OFF_BS + wave * 256);
+        if (lane < 8) g2l16(wsc + cidx * 64 + lane * 8, st + OFF_AS + wave * 128);
+        // B scales of this wave's tokens
+        uint8_t* sdst = st + OFF_BS + wave * (MM_TOK / MM_WAVES) * MM_KB * 4;
+        if (lane < BS_LANES) {
+            if (MM_KB == 4)
+                g2l16(bsrow + kb0, sdst);
+            else
+                __builtin_amdgcn_global_load_lds(bsrow + kb0, sdst, 4, 0, 0);
+        }
     };
 
-    const int sl = wave & 1;           // 64-row slab within the row block
-    const int nq = wave >> 1;          // 32-token quarter of the tile
+    const int sl = wave % MM_SLABS;    // 64-row slab within the row block
+    const int nq = wave / MM_SLABS;    // 32-token column group of the tile
     const bool active = nq * 32 < n;   // waves past the tile's last pair skip the math
     const int lr = lane % 32, lg = lane / 32;
     float acc0[16], acc1[16];
@@ -238,7 +276,8 @@ __global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
         const uint8_t* st = ring[s % MM_RING];
         const int8_t* As;
         if (Q4) {
-            // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of chunk t/64
+            // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of
+            // chunk t/64 (CHUNKS x 64 rows = MM_THREADS)
             const int c = tid >> 6, r = tid & 63;
             v4i_t wv = lds_b128(st + OFF_A + c * 1024 + r * 16);
             lds_wait(wv);
@@ -258,13 +297,13 @@ __global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
         if (active) {
 #pragma unroll
             for (int kb = 0; kb < MM_KB; kb++) {
-                const int8_t* ach = As + (sl * 4 + kb) * 2048;
+                const int8_t* ach = As + (sl * MM_KB + kb) * 2048;
                 v4i_t A0 = lds_b128(ach + lr * 32 + 16 * lg);
                 v4i_t A1 = lds_b128(ach + (32 + lr) * 32 + 16 * lg);
-                v4i_t B = lds_b128(Bs + (nq * 32 + lr) * 128 + kb * 32 + 16 * lg);
-                uint32_t dw0 = lds_u16(Asc + (sl * 4 + kb) * 64 + lr);
-                uint32_t dw1 = lds_u16(Asc + (sl * 4 + kb) * 64 + 32 + lr);
-                uint32_t dxb = lds_b32(Bsc + (nq * 32 + lr) * 4 + kb);
+                v4i_t B = lds_b128(Bs + (nq * 32 + lr) * (MM_KB * 32) + kb * 32 + 16 * lg);
+                uint32_t dw0 = lds_u16(Asc + (sl * MM_KB + kb) * 64 + lr);
+                uint32_t dw1 = lds_u16(Asc + (sl * MM_KB + kb) * 64 + 32 + lr);
+                uint32_t dxb = lds_b32(Bsc + (nq * 32 + lr) * MM_KB + kb);
                 lds_wait(A0, A1, B, dw0, dw1, dxb);
                 const v16i_t zero = {};
                 const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
@@ -288,8 +327,8 @@ __global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
     const int j = nq * 32 + lr;  // pair index within the tile
     if (!active || j >= n) return;
     if (MODE == 0) {
-        // acc0 = gate rows, acc1 = matching up rows of slab (2*blockIdx.y + sl)
-        const int slab = 2 * rb + sl;
+        // acc0 = gate rows, acc1 = matching up rows of slab (MM_SLABS * rb + sl)
+        const int slab = MM_SLABS * rb + sl;
         float h[16];
         float amax = 0.0f;
 #pragma unroll
@@ -383,37 +422,54 @@ __global__ __launch_bounds__(MM_THREADS, 1) void moe_mfma_kernel(MmArgs a) {
     }
 }
 
-template <int MODE>
-static hipError_t launch_mode(int wtype, MmArgs a, int n_tiles_bound, int nrb, hipStream_t s) {
-    a.nrb = nrb;
+template <int MODE, class SH>
+static hipError_t launch_mode(int wtype, MmArgs a, int n_tiles_bound, int rows, hipStream_t s) {
+    a.nrb = rows / SH::ROWS;
     a.tiles_pad = (n_tiles_bound + MM_XCD - 1) / MM_XCD * MM_XCD;
-    const dim3 grid(a.tiles_pad * nrb);
+    const dim3 grid(a.tiles_pad * a.nrb);
     if (wtype == HY_TYPE_Q4_0)
-        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE>), grid, dim3(MM_THREADS), 0, s, a);
+        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE, SH>), grid, dim3(MM_THREADS), 0, s, a);
     else
-        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q8_0, MODE>), grid, dim3(MM_THREADS), 0, s, a);
+        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q8_0, MODE, SH>), grid, dim3(MM_THREADS), 0, s, a);
     return hipGetLastError();
 }
 
+template <int MODE>
+static hipError_t launch_shape(int wtype, int tile_tokens, MmArgs a, int n_tiles_bound, int rows, hipStream_t s) {
+    if (tile_tokens == ShapeTall::TOK) return launch_mode<MODE, ShapeTall>(wtype, a, n_tiles_bound, rows, s);
+    return launch_mode<MODE, ShapeWide>(wtype, a, n_tiles_bound, rows, s);
+}
+
+template <class SH>
+static bool shape_fits(int H, int I) {
+    return H % SH::ROWS == 0 && (2 * I) % SH::ROWS == 0 && (H / QK) % SH::KB == 0 && (I / QK) % SH::KB == 0;
+}
+
 bool mfma_path_ok(int wtype, int H, int I) {
-    return (wtype == HY_TYPE_Q8_0 || wtype == HY_TYPE_Q4_0) && H % MM_ROWS == 0 && I % MM_ROWS == 0 &&
-           (H / QK) % MM_KB == 0 && (I / QK) % MM_KB == 0;
+    return (wtype == HY_TYPE_Q8_0 || wtype == HY_TYPE_Q4_0) && shape_fits<ShapeWide>(H, I);
 }
 
-int mfma_tile_tokens() { return MM_TOK; }
+// The tall shape (64-pair tiles, 256-row blocks) wins while experts see about 64
+// pairs each (a 128-pair tile would leave half its waves idle); beyond ~96 the wide
+// shape's reuse of every weight byte over 128 pairs wins.
+int mfma_tile_tokens(int T, int K, int E, int H, int I) {
+    const bool tall = shape_fits<ShapeTall>(H, I) && (int64_t)T * K < (int64_t)96 * E;
+    return tall ? ShapeTall::TOK : ShapeWide::TOK;
+}
 
-hipError_t launch_ffn_up_mfma(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const ActQ& X,
-                              int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, hipStream_t s) {
+hipError_t launch_ffn_up_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+                              const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
+                              hipStream_t s) {
     MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr, nullptr, nullptr};
-    return launch_mode<0>(wtype, a, n_tiles_bound, 2 * I / MM_ROWS, s);
+    return launch_shape<0>(wtype, tile_tokens, a, n_tiles_bound, 2 * I, s);
 }
 
-hipError_t launch_ffn_down_mfma(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
-                                const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
-                                const float* resid, float* out, hipStream_t s) {
+hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, int mode, const MatView& W,
+                                const Routing& R, const int8_t* hq, const float* hd, int T, int H, int I, int E,
+                                int K, float* y, const float* resid, float* out, hipStream_t s) {
     MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y, resid, out};
-    return mode == 0 ? launch_mode<1>(wtype, a, n_tiles_bound, H / MM_ROWS, s)
-                     : launch_mode<2>(wtype, a, n_tiles_bound, H / MM_ROWS, s);
+    return mode == 0 ? launch_shape<1>(wtype, tile_tokens, a, n_tiles_bound, H, s)
+                     : launch_shape<2>(wtype, tile_tokens, a, n_tiles_bound, H, s);
 }
 
 }  // namespace hy

@@ -176,11 +176,12 @@ def test_layer_small(gpu, small_layers, wtype, T):
     m.close()
 
 
+# with E=16, K=4 the grouped GEMM tiles 64 pairs up to T=383 and 128 pairs from T=384
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
-@pytest.mark.parametrize("T", [1, 17, 64, 65, 130, 300])
+@pytest.mark.parametrize("T", [1, 17, 64, 65, 130, 300, 383, 384, 700])
 def test_layer_small_mfma_path(gpu, small_layers, wtype, T):
     layer = small_layers[wtype]
-    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], wtype, max_tokens=512)
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], wtype, max_tokens=1024)
     m.set_path(gpu.PATH_MFMA)
     m.upload(0, layer)
     x = O.synth(50 + T, 0, O.T_X, 0, (T, SMALL["H"]), 1.0)
@@ -191,6 +192,20 @@ def test_layer_small_mfma_path(gpu, small_layers, wtype, T):
     # the decode GEMV computes the same operations in the same order
     m.set_path(gpu.PATH_VALU)
     assert_exact(m.run(0, x), ref, f"gemv wtype={wtype} T={T}")
+    m.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+def test_mfma_narrow_hidden(gpu, wtype):
+    """H = 128 fits only the 128-row tile shape: small batches must still run on it."""
+    H, I, E, K = 128, 128, 8, 2
+    layer = O.synth_layer(H, I, E, K, wtype, seed=21, std=0.05)
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=256)
+    m.set_path(gpu.PATH_MFMA)
+    m.upload(0, layer)
+    for T in (5, 40, 256):
+        x = O.synth(70 + T, 0, O.T_X, 0, (T, H), 1.0)
+        assert_exact(m.run(0, x), O.moe_forward_q(layer, x), f"H=128 wtype={wtype} T={T}")
     m.close()
 
 
