@@ -12,6 +12,12 @@ Other workloads (--config): c1 F32 T=16, c3 Q4_0 decode (--tokens 1/2/4/8),
 c4 Q4_0 T=4096 Zipf-skewed routing, c5 32-layer Q8_0 stack T=4096.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
+    python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
+
+roofline.traffic (HBM bytes per launch of the dominant kernel) is read from
+profiles/hbm_traffic.md, the table made from rocprofv3 FETCH_SIZE / WRITE_SIZE
+counter runs of this script, calibrated against the copy probe; it is null for a
+workload/kernel the table does not list.
 """
 import argparse
 import json
@@ -90,6 +96,47 @@ def kernel_ops(kname, T):
     return 0.0
 
 
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+
+
+def measured_traffic(workload, kname, path=TRAFFIC_TABLE):
+    """HBM bytes per launch for (workload, kernel) from the committed counter table:
+    rows '| workload | kernel | ... | bytes |' whose last cell is the calibrated
+    FETCH+WRITE bytes per dispatch."""
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 3 and cells[0] == workload and cells[1] == kname:
+                    return float(cells[-1])
+    except (OSError, ValueError):
+        return None
+    return None
+
+
+def copy_probe(hy, mib, steps):
+    """A plain device copy of `mib` MiB, `steps` times: the yardstick whose FETCH_SIZE
+    and WRITE_SIZE per dispatch must each read `mib` MiB."""
+    n = mib << 20
+    a, b = hy.Buf(n, np.uint8), hy.Buf(n, np.uint8)
+    hy.check(hy.lib().hy_memset(a.ptr, 1, n))
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    hy.check(hy.lib().hy_copy_d2d(b.ptr, a.ptr, n, None))
+    hy.sync()
+    hy.check(hy.lib().hy_event_record(ev0, None))
+    for _ in range(steps):
+        hy.check(hy.lib().hy_copy_d2d(b.ptr, a.ptr, n, None))
+    hy.check(hy.lib().hy_event_record(ev1, None))
+    hy.sync()
+    ms = hy.C.c_float()
+    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+    t = ms.value / steps / 1e3
+    print(json.dumps({"probe": "copy_d2d", "bytes": n, "steps": steps, "ms_per_copy": t * 1e3,
+                      "GBps_read_plus_write": 2 * n / t / 1e9}), flush=True)
+
+
 def cpu_baseline(wl, seed, budget_s=15.0):
     """The oracle's q-semantics layer (int8 block dots, OpenMP over all host
     threads) on a bounded token sample of the same workload."""
@@ -124,6 +171,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): this build has no multi-GPU path; "
@@ -133,6 +181,9 @@ def main():
     hy = load_pkg()
     if hy.device_count() < 1:
         sys.exit("no HIP device visible")
+    if a.copy_probe:
+        copy_probe(hy, a.copy_probe, a.steps)
+        return
     wl = dict(WORKLOADS[a.config])
     if a.tokens:
         wl["T"] = a.tokens
@@ -192,6 +243,7 @@ def main():
     avg_s = t_l / n_l / 1e3
     n_layer_launch = nl if wl.get("stack") else 1
     traffic = kernel_traffic(dom, wtype, T, D)
+    hbm_measured = measured_traffic(wl["name"] if not a.tokens else f"{wl['name']}_t{T}", dom)
     ops = kernel_ops(dom, T)
     layer_bytes = (D + 1) * expert_bytes(wtype) + E * H * 4 + 2 * T * H * 4
     layer_ops = 2.0 * T * (K + 1) * PARAMS_PER_EXPERT
@@ -200,11 +252,11 @@ def main():
     bound = "hbm" if layer_bytes / PEAK_HBM >= layer_ops / PEAK_INT8 else "mfma"
     if bound == "hbm":
         roof = {"bound": "hbm", "kernel": dom, "achieved": traffic / avg_s / 1e9, "peak": PEAK_HBM / 1e9,
-                "unit": "GB/s", "frac": traffic / avg_s / PEAK_HBM, "traffic": None,
+                "unit": "GB/s", "frac": traffic / avg_s / PEAK_HBM, "traffic": hbm_measured,
                 "algorithmic_bytes_per_launch": traffic, "avg_launch_ms": avg_s * 1e3}
     else:
         roof = {"bound": "mfma", "kernel": dom, "achieved": ops / avg_s / 1e12, "peak": PEAK_INT8 / 1e12,
-                "unit": "TFLOP/s", "frac": ops / avg_s / PEAK_INT8, "traffic": None,
+                "unit": "TFLOP/s", "frac": ops / avg_s / PEAK_INT8, "traffic": hbm_measured,
                 "algorithmic_ops_per_launch": ops, "avg_launch_ms": avg_s * 1e3}
 
     res = {

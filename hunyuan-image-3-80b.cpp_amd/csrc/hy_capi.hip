@@ -629,6 +629,11 @@ int hy_memset(void* d, int v, size_t b) {
     HIP_TRY(hipMemset(d, v, b));
     return HY_OK;
 }
+int hy_copy_d2d(void* d, const void* src, size_t b, void* stream) {
+    if (b && (!d || !src)) return fail(HY_ERR_INVALID, "null copy operand");
+    HIP_TRY(hy::launch_copy(d, src, b, (hipStream_t)stream));
+    return HY_OK;
+}
 int hy_device_synchronize(void) {
     HIP_TRY(hipDeviceSynchronize());
     return HY_OK;

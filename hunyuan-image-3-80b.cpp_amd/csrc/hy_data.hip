@@ -140,4 +140,23 @@ hipError_t launch_dequant(int wtype, const uint8_t* src, size_t n, float* out, h
     return hipGetLastError();
 }
 
+// Plain streaming copy: 16-byte vectors, grid-stride, tail bytes one by one.
+__global__ void copy_kernel(const int4* __restrict__ src, int4* __restrict__ dst, size_t n16,
+                            const uint8_t* __restrict__ src_tail, uint8_t* __restrict__ dst_tail, size_t ntail) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+    if (blockIdx.x == 0 && threadIdx.x < ntail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    const size_t n16 = bytes / 16, ntail = bytes % 16;
+    const int threads = 256;
+    const size_t want = (n16 + threads - 1) / threads;
+    const int blocks = (int)(want < 1 ? 1 : (want > 8192 ? 8192 : want));
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(threads), 0, s, (const int4*)src, (int4*)dst, n16,
+                       (const uint8_t*)src + n16 * 16, (uint8_t*)dst + n16 * 16, ntail);
+    return hipGetLastError();
+}
+
 }  // namespace hy

@@ -51,6 +51,7 @@ hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, i
                                 int K, float* y, const float* resid, float* out, hipStream_t s);
 
 // residency (hy_data.hip)
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 hipError_t launch_synth_matrix(int wtype, uint64_t key, float scale, int rows, int cols, int gu_I, uint8_t* qs,
                                uint16_t* sc, hipStream_t s);
 hipError_t launch_synth_fill(float* out, size_t n, uint64_t key, float scale, hipStream_t s);

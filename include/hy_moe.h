@@ -202,6 +202,10 @@ int hy_free(void* p);
 int hy_memcpy_h2d(void* dst_dev, const void* src_host, size_t bytes);
 int hy_memcpy_d2h(void* dst_host, const void* src_dev, size_t bytes);
 int hy_memset(void* dst_dev, int value, size_t bytes);
+/* Device-to-device copy by a plain streaming kernel (16-byte loads and stores, no
+ * copy engine).  Besides moving data it is the yardstick for the hardware byte
+ * counters: a copy of n bytes reads n and writes n. */
+int hy_copy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
 int hy_device_synchronize(void);
 int hy_stream_create(void** stream);
 int hy_stream_destroy(void* stream);

@@ -302,3 +302,15 @@ def test_invalid_token_count_rejected(gpu, small_layers):
     with pytest.raises(gpu.HyError):
         m.forward(0, xb, 0, ob)
     m.close()
+
+
+@pytest.mark.parametrize("nbytes", [0, 1, 17, 4096, (1 << 20) + 5])
+def test_copy_d2d(gpu, nbytes):
+    rng = np.random.default_rng(nbytes)
+    src = rng.integers(0, 256, size=max(nbytes, 1), dtype=np.uint8)
+    a = gpu.Buf.from_array(src)
+    b = gpu.Buf.from_array(np.zeros_like(src))
+    gpu.check(gpu.lib().hy_copy_d2d(b.ptr, a.ptr, nbytes, None))
+    got = b.numpy()
+    np.testing.assert_array_equal(got[:nbytes], src[:nbytes])
+    assert not got[nbytes:].any()
