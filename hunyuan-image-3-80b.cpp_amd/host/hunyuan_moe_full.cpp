@@ -1,6 +1,7 @@
 // hunyuan_moe_full.cpp -- the reference's MoE-block C++ API (include/hunyuan_moe_full.h)
 // on top of the C ABI.  Host arrays in and out; the work runs on the GPU.
 #include "../../include/hunyuan_moe_full.h"
+#include "../../include/hunyuan_model_moe.h"
 
 #include <algorithm>
 #include <cstdlib>

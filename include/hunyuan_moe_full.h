@@ -2,10 +2,12 @@
 //
 // Same names, types and argument meaning as the reference's src/hunyuan_moe_full.h
 // (MoERoutingConfig, MoEGateOutput, topkgating_full/_easy, einsum_dispatch/_combine,
-// moe_forward_full, softmax_f32, topk_f32) and the MoE part of src/hunyuan_model.h
-// (HunyuanConfig, MoEWeights, swiglu_ffn_f32, moe_forward_cpu, rms_norm_f32).  Inputs
-// and outputs are host arrays as in the reference; every call runs on the GPU through
-// the C ABI of hy_moe.h (upload, HIP kernels, download) and blocks until done.
+// moe_forward_full, softmax_f32, topk_f32).  The MoE part of src/hunyuan_model.h
+// (HunyuanConfig, MoEWeights, swiglu_ffn_f32, moe_forward_cpu, rms_norm_f32) is in
+// hunyuan_model_moe.h, so a code base that keeps its own hunyuan_model.h can use this
+// header alongside it.  Inputs and outputs are host arrays as in the reference; every
+// call runs on the GPU through the C ABI of hy_moe.h (upload, HIP kernels, download)
+// and blocks until done.
 //
 // Differences from the reference, all deliberate:
 //  * errors throw hy::Error (std::runtime_error) instead of undefined behaviour, and
@@ -85,49 +87,6 @@ void moe_forward_full(const float* hidden_states, uint32_t n_tokens, uint32_t hi
                       const void* expert_gate_up_stacked, const void* expert_down_stacked, int ggml_type,
                       uint32_t num_experts, uint32_t intermediate_size, const MoERoutingConfig& routing_cfg,
                       float* output);
-
-// The MoE part of src/hunyuan_model.h:13-45 (defaults of HunyuanConfig).
-struct HunyuanConfig {
-    uint32_t hidden_size = 4096;
-    uint32_t num_hidden_layers = 32;
-    uint32_t num_attention_heads = 32;
-    uint32_t num_key_value_heads = 8;
-    uint32_t attention_head_dim = 128;
-    uint32_t intermediate_size = 3072;
-    uint32_t moe_intermediate_size = 3072;
-    uint32_t num_experts = 64;
-    uint32_t moe_topk = 8;
-    uint32_t num_shared_expert = 1;
-    uint32_t vocab_size = 133120;
-    uint32_t max_position_embeddings = 22800;
-    float rms_norm_eps = 1e-5f;
-    float rope_theta = 10000.0f;
-    bool use_qk_norm = true;
-    bool use_mixed_mlp_moe = true;
-};
-
-// src/hunyuan_model.h:130-145
-struct MoEWeights {
-    std::vector<float> shared_gate_up;  // [2*intermediate, hidden_size]
-    std::vector<float> shared_down;     // [hidden_size, intermediate]
-    std::vector<float> router_weight;   // [num_experts, hidden_size]
-    struct ExpertW {
-        std::vector<float> gate_up;  // [2*intermediate, hidden_size]
-        std::vector<float> down;     // [hidden_size, intermediate]
-    };
-    std::vector<ExpertW> experts;
-    uint32_t num_experts = 0;
-};
-
-// src/hunyuan_model.h:118-125 / src/rms_norm.cpp:39-91
-void swiglu_ffn_f32(const float* x, const float* gate_up_weight, const float* down_weight, float* out, uint32_t n,
-                    uint32_t hidden_size, uint32_t intermediate_size);
-// src/hunyuan_model.h:147-156 / src/attention.cpp:191-313
-void moe_forward_cpu(const float* hidden_states, const MoEWeights& w, uint32_t n_tokens, const HunyuanConfig& cfg,
-                     float* output, float* debug_router_logits = nullptr, float* debug_router_weights = nullptr,
-                     int32_t* debug_router_indices = nullptr);
-// src/rms_norm.cpp:9-33
-void rms_norm_f32(const float* x, const float* weight, float* out, uint32_t n_tokens, uint32_t hidden_size, float eps);
 
 namespace hy {
 

@@ -8,6 +8,7 @@
 #include <string>
 #include <vector>
 
+#include "hunyuan_model_moe.h"
 #include "hunyuan_moe_full.h"
 #include "hy_oracle.h"
 

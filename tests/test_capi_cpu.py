@@ -20,9 +20,30 @@ def test_library_exports_header(hy):
 def test_cxx_mirror_header_lists_reference_names():
     txt = open(os.path.join(ROOT, "include", "hunyuan_moe_full.h")).read()
     for name in ("MoERoutingConfig", "MoEGateOutput", "topkgating_full", "topkgating_easy", "einsum_dispatch",
-                 "einsum_combine", "moe_forward_full", "softmax_f32", "topk_f32", "moe_forward_cpu",
-                 "swiglu_ffn_f32", "MoEWeights", "rms_norm_f32"):
+                 "einsum_combine", "moe_forward_full", "softmax_f32", "topk_f32"):
         assert name in txt, name
+    model = open(os.path.join(ROOT, "include", "hunyuan_model_moe.h")).read()
+    for name in ("HunyuanConfig", "moe_forward_cpu", "swiglu_ffn_f32", "MoEWeights", "rms_norm_f32",
+                 "compute_derived", "qkv_total"):
+        assert name in model, name
+
+
+def test_cxx_mirror_headers_compile_with_reference_layout(tmp_path):
+    """Both mirror headers compile together, and HunyuanConfig / MoEWeights have the
+    reference's field order (offsets of the last fields pin the layout)."""
+    import subprocess
+    src = tmp_path / "t.cpp"
+    src.write_text(
+        '#include "hunyuan_model_moe.h"\n#include "hunyuan_moe_full.h"\n#include <cstddef>\n'
+        'static_assert(offsetof(HunyuanConfig, rms_norm_eps) == 48, "");\n'
+        'static_assert(offsetof(HunyuanConfig, use_qk_norm) == 56, "");\n'
+        'static_assert(offsetof(HunyuanConfig, num_kv_groups) == 60, "");\n'
+        'static_assert(sizeof(HunyuanConfig) == 76, "");\n'
+        'static_assert(offsetof(MoEWeights, num_experts) == 4 * sizeof(std::vector<float>), "");\n'
+        'int main() { HunyuanConfig c; c.compute_derived(); return c.qkv_total == 6144 ? 0 : 1; }\n')
+    exe = tmp_path / "t"
+    subprocess.run(["g++", "-std=c++17", f"-I{os.path.join(ROOT, 'include')}", str(src), "-o", str(exe)], check=True)
+    assert subprocess.run([str(exe)]).returncode == 0
 
 
 def _cfg(hy, **kw):
