@@ -338,7 +338,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
         {(void**)&c->srt_tok, pairs * 4},  {(void**)&c->pair_pos, pairs * 4},
         {(void**)&c->comb_pos, pairs * 4}, {(void**)&c->comb_w, pairs * 4},
         {(void**)&c->tile_e, (size_t)c->max_tiles * 4}, {(void**)&c->tile_start, (size_t)c->max_tiles * 4},
-        {(void**)&c->tile_n, (size_t)c->max_tiles * 4}, {(void**)&c->meta, 16},
+        {(void**)&c->tile_n, (size_t)c->max_tiles * 4}, {(void**)&c->meta, (size_t)hy::META_INTS * 4},
         {(void**)&c->hq, slots * I},       {(void**)&c->hd, slots * (I / 32) * 4},
         {(void**)&c->hs, slots * (I / 32) * 4},
         {(void**)&c->hf, wt == HY_TYPE_F32 ? slots * I * 4 : 16},
@@ -568,7 +568,7 @@ int hy_dispatch_pairs(const int32_t* topi, const float* topw, uint32_t T, uint32
     const size_t pairs = (size_t)T * K;
     const int max_tiles = (int)((pairs + E * 7) / 8 + 1);
     void* scratch = nullptr;
-    const size_t bytes = pairs * 4 * 3 + (size_t)max_tiles * 4 * 3 + 64;
+    const size_t bytes = pairs * 4 * 3 + (size_t)max_tiles * 4 * 3 + (size_t)hy::META_INTS * 4;
     if (hipMalloc(&scratch, bytes) != hipSuccess) return fail(HY_ERR_NOMEM, "dispatch scratch");
     int* srt = static_cast<int*>(scratch);
     int* cpos = srt + pairs;

@@ -23,6 +23,7 @@
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_layout.hpp"
+#include "hy_lds.hpp"
 
 namespace hy {
 
@@ -69,6 +70,7 @@ struct GvArgs {
     int T, H, I, E, K;
     int Kd;             // reduction length
     int n_groups;       // 64-row groups of the weight matrix
+    int nx;             // activation rows staged per tile (min(NT, T)): sizes the LDS
     int8_t* hq;         // mode 0 outputs
     float* hd;
     int* hs;
@@ -252,6 +254,207 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     }
 }
 
+// Quantized weights (Q8_0 / Q4_0): the same per-row block-sequential accumulation as
+// gemv_kernel, with the weight stream decoupled from the arithmetic.  Each wave owns a
+// private LDS ring of DEPTH blocks of its 64-row group (1 KB / 2 KB of quants + 128 B
+// of fp16 scales per block) filled by global->LDS DMA: DEPTH blocks are always in
+// flight, completion is counted with vmcnt (in-order), and no barrier is needed
+// because a wave only reads what it copied.  The last DEPTH blocks are consumed by an
+// unrolled tail whose waits count down to zero, so the wave leaves no copy in flight.
+// consume the last DEPTH blocks, U at a time: before blocks base + J .. + U - 1, wait
+// until at most the DEPTH - U - J younger blocks' copies are outstanding
+template <int J, int DEPTH, int U, int LOADS, class F>
+__device__ __forceinline__ void gemv_tail(F& step, int base) {
+    if constexpr (J < DEPTH) {
+        MM_WAIT_VM_LGKM((DEPTH - U - J) * LOADS);
+        step(base + J);
+        gemv_tail<J + U, DEPTH, U, LOADS>(step, base);
+    }
+}
+
+constexpr int GQ_U = 4;  // blocks per step of gemv_q_kernel (DEPTH and nb are multiples)
+
+template <int WT>
+struct GqDepth {
+    static constexpr int value = WT == HY_TYPE_Q4_0 ? 16 : 12;
+};
+
+template <int WT, int NT, int MODE>
+__global__ __launch_bounds__(GV_THREADS) void gemv_q_kernel(GvArgs a) {
+    constexpr bool Q4 = WT == HY_TYPE_Q4_0;
+    constexpr int DEPTH = GqDepth<WT>::value;
+    constexpr int BPB = Q4 ? 16 : 32;
+    constexpr int WBYTES = 64 * BPB;   // one block of a 64-row group
+    constexpr int SLOT = WBYTES + 128; // + its 64 fp16 scales
+    constexpr int LOADS = (Q4 ? 1 : 2) + 1;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int tok_s[NT], slot_s[NT];
+    const int tile = (MODE == 2) ? a.R.meta[0] + (int)blockIdx.x : (int)blockIdx.x;
+    if (tile >= a.R.meta[1]) return;
+    const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
+    const bool shared = e == a.E;
+    const int Kd = a.Kd, nb = Kd / QK;
+    if (threadIdx.x < NT) {
+        const int i = threadIdx.x;
+        int tok = 0, slot = 0;
+        if (i < n) {
+            if (shared) {
+                tok = start + i;
+                slot = a.T * a.K + tok;
+            } else {
+                slot = a.R.off[e] + start + i;
+                tok = a.R.srt_tok[slot];
+            }
+        }
+        tok_s[i] = tok;
+        slot_s[i] = slot;
+    }
+    __syncthreads();
+    // the tile's activation rows (int8), scales and block sums; n <= nx rows
+    int8_t* xs_l = reinterpret_cast<int8_t*>(smem);
+    float* xd_l = reinterpret_cast<float*>(smem + (size_t)a.nx * Kd);
+    int* xsum_l = reinterpret_cast<int*>(smem + (size_t)a.nx * Kd + (size_t)a.nx * nb * 4);
+    const size_t ring_off = ((size_t)a.nx * Kd + (size_t)a.nx * nb * 8 + 15) & ~(size_t)15;
+    {
+        const int vec_per_row = Kd / 16;
+        for (int v = threadIdx.x; v < n * vec_per_row; v += GV_THREADS) {
+            const int i = v / vec_per_row, c = v % vec_per_row;
+            const int row = MODE == 0 ? tok_s[i] : slot_s[i];
+            reinterpret_cast<int4*>(xs_l + (size_t)i * Kd)[c] = reinterpret_cast<const int4*>(a.aq + (size_t)row * Kd)[c];
+        }
+        for (int v = threadIdx.x; v < n * nb; v += GV_THREADS) {
+            const int i = v / nb, b = v % nb;
+            const int row = MODE == 0 ? tok_s[i] : slot_s[i];
+            xd_l[v] = a.ad[(size_t)row * nb + b];
+            if (Q4) xsum_l[v] = a.as[(size_t)row * nb + b];
+        }
+    }
+    __syncthreads();
+
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int G = blockIdx.y * GV_WAVES + wave;
+    if (G >= a.n_groups) return;  // no barrier below
+    uint8_t* ring = smem + ring_off + (size_t)wave * DEPTH * SLOT;
+    const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride + (size_t)G * nb * WBYTES;
+    const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64;
+    auto issue = [&](int b) {
+        uint8_t* st = ring + (b % DEPTH) * SLOT;
+        g2l16(wq + (size_t)b * WBYTES + lane * 16, st);
+        if (!Q4) g2l16(wq + (size_t)b * WBYTES + 1024 + lane * 16, st + 1024);
+        if (lane < 8) g2l16(wsc + (size_t)b * 64 + lane * 8, st + WBYTES);
+    };
+    float acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) acc[i] = 0.0f;
+    // GQ_U blocks per step: one round of LDS reads (the blocks' weights and scales, and
+    // per token the activation blocks) and one wait per token, then the blocks'
+    // arithmetic in order
+    auto step = [&](int b0) {
+        v4i_t w0[GQ_U], w1[GQ_U];
+        uint32_t dwb[GQ_U];
+#pragma unroll
+        for (int u = 0; u < GQ_U; u++) {
+            const uint8_t* st = ring + ((b0 + u) % DEPTH) * SLOT;
+            w0[u] = lds_b128(st + lane * BPB);
+            if (!Q4) w1[u] = lds_b128(st + lane * BPB + 16);
+            dwb[u] = lds_u16(st + WBYTES + lane * 2);
+        }
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (i < n) {
+                v4i_t x0[GQ_U], x1[GQ_U];
+                uint32_t xdb[GQ_U], xsb[GQ_U];
+#pragma unroll
+                for (int u = 0; u < GQ_U; u++) {
+                    const int b = b0 + u;
+                    x0[u] = lds_b128(xs_l + (size_t)i * Kd + b * QK);
+                    x1[u] = lds_b128(xs_l + (size_t)i * Kd + b * QK + 16);
+                    xdb[u] = lds_b32(xd_l + i * nb + b);
+                    if (Q4) xsb[u] = lds_b32(xsum_l + i * nb + b);
+                }
+                lds_wait();
+                if (i == 0) {
+#pragma unroll
+                    for (int u = 0; u < GQ_U; u++) {
+                        lds_pin(w0[u]);
+                        if (!Q4) lds_pin(w1[u]);
+                        lds_pin(dwb[u]);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < GQ_U; u++) {
+                    lds_pin(x0[u]);
+                    lds_pin(x1[u]);
+                    lds_pin(xdb[u]);
+                    if (Q4) lds_pin(xsb[u]);
+                    const int4 W0 = make_int4(w0[u][0], w0[u][1], w0[u][2], w0[u][3]);
+                    const int4 X0 = make_int4(x0[u][0], x0[u][1], x0[u][2], x0[u][3]);
+                    const int4 X1 = make_int4(x1[u][0], x1[u][1], x1[u][2], x1[u][3]);
+                    int sdot;
+                    if (Q4) {
+                        sdot = dot_q4_block(W0, X0, X1, (int)xsb[u]);
+                    } else {
+                        const int4 W1 = make_int4(w1[u][0], w1[u][1], w1[u][2], w1[u][3]);
+                        sdot = dot_q8_block(W0, W1, X0, X1);
+                    }
+                    const float dw = h2f((uint16_t)dwb[u]);
+                    acc[i] = fmaf((float)sdot, dw * __builtin_bit_cast(float, xdb[u]), acc[i]);
+                }
+                pin_f32(acc[i]);  // token i done before token i+1's reads
+            }
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) issue(d);
+    int b0 = 0;
+    for (; b0 < nb - DEPTH; b0 += GQ_U) {
+        MM_WAIT_VM_LGKM((DEPTH - GQ_U) * LOADS);  // blocks b0.. b0+GQ_U-1 landed (in order)
+        step(b0);
+#pragma unroll
+        for (int u = 0; u < GQ_U; u++) issue(b0 + DEPTH + u);  // refill the slots just read
+    }
+    gemv_tail<0, DEPTH, GQ_U, LOADS>(step, nb - DEPTH);
+
+    if (MODE == 0) {
+        // lanes 0..31: gate rows 32G+lane, lanes 32..63: the matching up rows
+        const int nb_i = a.I / QK;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (i >= n) break;
+            const float u = __shfl(acc[i], (lane + 32) % WAVE, WAVE);
+            const float h = swiglu(acc[i], u);
+            const size_t slot = (size_t)slot_s[i];
+            const Q8Result r = quant_q8_0_lane32(h);
+            int s = r.q;
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
+            if (lane < 32) {
+                a.hq[slot * a.I + (size_t)G * QK + lane] = r.q;
+                if (lane == 0) {
+                    a.hd[slot * nb_i + G] = h2f(r.dh);
+                    a.hs[slot * nb_i + G] = s;
+                }
+            }
+        }
+    } else {
+        const int row = G * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (i >= n) break;
+            if (MODE == 1) {
+                a.y[(size_t)slot_s[i] * a.H + row] = acc[i];
+            } else {
+                const int t = tok_s[i];
+                float comb = 0.0f;
+                for (int k = 0; k < a.K; k++)
+                    comb = fmaf(a.R.comb_w[t * a.K + k], a.y[(size_t)a.R.comb_pos[t * a.K + k] * a.H + row], comb);
+                const float o = acc[i] + comb;
+                a.out[(size_t)t * a.H + row] = a.resid ? a.resid[(size_t)t * a.H + row] + o : o;
+            }
+        }
+    }
+}
+
 // combine: out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e y_e[t] ), the
 // shared expert's output at slot T*K + t when has_shared
 __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __restrict__ y, int T, int H, int K,
@@ -274,17 +477,38 @@ size_t gemv_smem(int wtype, int Kd) {
     return (size_t)GEMV_NT * Kd + (size_t)GEMV_NT * (Kd / QK) * 8;
 }
 
+// LDS of gemv_q_kernel: nx staged activation rows + GV_WAVES rings of DEPTH blocks
+template <int WT>
+static size_t gemv_q_smem(int nx, int Kd) {
+    constexpr int BPB = WT == HY_TYPE_Q4_0 ? 16 : 32;
+    const size_t xs = ((size_t)nx * Kd + (size_t)nx * (Kd / QK) * 8 + 15) & ~(size_t)15;
+    return xs + (size_t)GV_WAVES * GqDepth<WT>::value * (64 * BPB + 128);
+}
+
 template <int MODE>
-static hipError_t gemv_launch(int wtype, dim3 grid, size_t smem, hipStream_t s, const GvArgs& a) {
+static hipError_t gemv_launch(int wtype, dim3 grid, hipStream_t s, GvArgs a) {
+    const int nb = a.Kd / QK;
+    a.nx = a.T < GEMV_NT ? a.T : GEMV_NT;
     switch (wtype) {
     case HY_TYPE_Q8_0:
-        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS), smem, s, a);
+        if (nb >= GqDepth<HY_TYPE_Q8_0>::value && nb % GQ_U == 0)
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+                               gemv_q_smem<HY_TYPE_Q8_0>(a.nx, a.Kd), s, a);
+        else
+            hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+                               gemv_smem(wtype, a.Kd), s, a);
         break;
     case HY_TYPE_Q4_0:
-        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS), smem, s, a);
+        if (nb >= GqDepth<HY_TYPE_Q4_0>::value && nb % GQ_U == 0)
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+                               gemv_q_smem<HY_TYPE_Q4_0>(a.nx, a.Kd), s, a);
+        else
+            hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+                               gemv_smem(wtype, a.Kd), s, a);
         break;
     default:
-        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_F32, GEMV_NT, MODE>), grid, dim3(GV_THREADS), smem, s, a);
+        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_F32, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+                           gemv_smem(wtype, a.Kd), s, a);
         break;
     }
     return hipGetLastError();
@@ -293,18 +517,17 @@ static hipError_t gemv_launch(int wtype, dim3 grid, size_t smem, hipStream_t s, 
 hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
                           int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
                           hipStream_t s) {
-    GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, hq, hd, hs, hf, nullptr, nullptr, nullptr};
+    GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, 0, hq, hd, hs, hf, nullptr, nullptr, nullptr};
     dim3 grid(max_tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
-    return gemv_launch<0>(wtype, grid, gemv_smem(wtype, H), s, a);
+    return gemv_launch<0>(wtype, grid, s, a);
 }
 
 hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
                             const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
                             int E, int K, float* y, const float* resid, float* out, hipStream_t s) {
-    GvArgs a{W, R, hq, hd, hs, hf, T, H, I, E, K, I, H / 64, nullptr, nullptr, nullptr, nullptr, y, resid, out};
+    GvArgs a{W, R, hq, hd, hs, hf, T, H, I, E, K, I, H / 64, 0, nullptr, nullptr, nullptr, nullptr, y, resid, out};
     dim3 grid(n_tiles_bound, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
-    return mode == 0 ? gemv_launch<1>(wtype, grid, gemv_smem(wtype, I), s, a)
-                     : gemv_launch<2>(wtype, grid, gemv_smem(wtype, I), s, a);
+    return mode == 0 ? gemv_launch<1>(wtype, grid, s, a) : gemv_launch<2>(wtype, grid, s, a);
 }
 
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,

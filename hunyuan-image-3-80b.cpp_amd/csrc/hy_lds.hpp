@@ -1,0 +1,65 @@
+// hy_lds.hpp -- global->LDS DMA and explicitly waited LDS reads, shared by the kernels
+// that stream operands through LDS rings (grouped MFMA GEMM, decode GEMV).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace hy {
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// 16-byte global -> LDS copy (global_load_lds_dwordx4): lane i of the wave writes
+// lds_wave_base + 16*i.  The wave's loads are tracked by vmcnt, not by barriers.
+__device__ __forceinline__ void g2l16(const void* g, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
+#define MM_WAIT_VM_LGKM(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (((N) >> 4) << 14))
+
+// LDS reads of the ring are issued as plain ds_read instructions: the compiler does
+// not associate them with the in-flight global->LDS copies (it would otherwise wait
+// for every outstanding copy, including the stages being prefetched).  Their
+// completion is waited for explicitly (lds_wait) before any result is used; the
+// vmcnt wait + barrier at the top of each stage orders them after the copies.
+typedef __attribute__((address_space(3))) const uint8_t lds_u8_t;
+__device__ __forceinline__ uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)((lds_u8_t*)p); }
+__device__ __forceinline__ v4i_t lds_b128(const void* p) {
+    v4i_t r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_off(p)));
+    return r;
+}
+__device__ __forceinline__ uint32_t lds_u16(const void* p) {
+    uint32_t r;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_off(p)));
+    return r;
+}
+__device__ __forceinline__ uint32_t lds_b32(const void* p) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_off(p)));
+    return r;
+}
+__device__ __forceinline__ void lds_st128(void* p, v4i_t v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// After a bare lds_wait(): pin a ds_read result so none of its uses is scheduled above
+// the wait (volatile asm statements keep their program order).
+__device__ __forceinline__ void lds_pin(v4i_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void lds_pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+// Force a value to be computed here (before any later volatile asm, e.g. the next
+// round of ds_reads), which bounds how many loaded operands are live at once.
+__device__ __forceinline__ void pin_f32(float& v) { asm volatile("" : "+v"(v)); }
+// wait for the ds_reads whose results are passed in: the values are threaded through
+// the asm so no consumer can be scheduled ahead of the wait
+__device__ __forceinline__ void lds_wait(v4i_t& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, uint32_t& c) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
+}
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, uint32_t& c, uint32_t& d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
+}
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, uint32_t& d, uint32_t& e, uint32_t& f) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
+}
+
+}  // namespace hy

@@ -32,10 +32,10 @@
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_layout.hpp"
+#include "hy_lds.hpp"
 
 namespace hy {
 
-typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v16i_t __attribute__((ext_vector_type(16)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
@@ -78,7 +78,7 @@ struct MmArgs {
     int T, H, I, E, K;
     int Kdim;           // reduction length (H for mode 0, I for modes 1/2)
     int nrb;            // row blocks of the weight matrix
-    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD (unused by the kernel)
+    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD (sizes the grid)
     int8_t* hq;         // mode 0 outputs
     float* hd;
     int* hs;
@@ -109,47 +109,6 @@ __device__ __forceinline__ v16f_t scale_outer(_Float16 dw, _Float16 dx, int lg) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, zero, 0, 0, 0);
 }
 
-// 16-byte global -> LDS copy (global_load_lds_dwordx4): lane i of the wave writes
-// lds_wave_base + 16*i.  The wave's loads are tracked by vmcnt, not by barriers.
-__device__ __forceinline__ void g2l16(const void* g, void* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
-}
-// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
-#define MM_WAIT_VM_LGKM(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (((N) >> 4) << 14))
-
-// LDS reads of the ring are issued as plain ds_read instructions: the compiler does
-// not associate them with the in-flight global->LDS copies (it would otherwise wait
-// for every outstanding copy, including the stages being prefetched).  Their
-// completion is waited for explicitly (lds_wait) before any result is used; the
-// vmcnt wait + barrier at the top of each stage orders them after the copies.
-typedef __attribute__((address_space(3))) const uint8_t lds_u8_t;
-__device__ __forceinline__ uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)((lds_u8_t*)p); }
-__device__ __forceinline__ v4i_t lds_b128(const void* p) {
-    v4i_t r;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_off(p)));
-    return r;
-}
-__device__ __forceinline__ uint32_t lds_u16(const void* p) {
-    uint32_t r;
-    asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_off(p)));
-    return r;
-}
-__device__ __forceinline__ uint32_t lds_b32(const void* p) {
-    uint32_t r;
-    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_off(p)));
-    return r;
-}
-__device__ __forceinline__ void lds_st128(void* p, v4i_t v) {
-    asm volatile("ds_write_b128 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
-}
-__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-// wait for the ds_reads whose results are passed in: the values are threaded through
-// the asm so no consumer can be scheduled ahead of the wait
-__device__ __forceinline__ void lds_wait(v4i_t& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
-__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, uint32_t& d, uint32_t& e, uint32_t& f) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
-}
-
 template <int WT, int MODE, class SH>
 __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_kernel(MmArgs a) {
     constexpr int MM_ROWS = SH::ROWS, MM_TOK = SH::TOK, MM_KB = SH::KB, MM_SLABS = SH::SLABS;
@@ -167,14 +126,17 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
 
     // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
     // all row blocks of a tile the same id mod MM_XCD (they share the tile's
-    // activation rows in that XCD's L2).
+    // activation rows in that XCD's L2).  (Ordering whole experts onto one XCD, so
+    // that tiles sharing a weight block reuse it in L2, cut fetched bytes but ran
+    // 2-4 % slower: this kernel is not bound by HBM traffic.)
     const int id = (int)blockIdx.x;
     const int xcd = id % MM_XCD, local = id / MM_XCD;
     const int tile_rel = xcd + MM_XCD * (local / a.nrb);
     const int rb = local % a.nrb;
     const int tile = (MODE == 2) ? a.R.meta[0] + tile_rel : tile_rel;
     if (tile >= a.R.meta[MODE == 1 ? 0 : 1]) return;
-    const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
+    const int e = a.R.tile_e[tile];
+    const int start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
     const int row0 = rb * MM_ROWS;
     const int Kd = a.Kdim;

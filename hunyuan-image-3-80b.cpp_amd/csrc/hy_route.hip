@@ -104,30 +104,54 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
 
 // Top-k + weights per token (one wave each), optionally quantizing the token's
 // activation row to Q8_0 in the same pass (saves a launch in the decode regime).
+// Activation quantizer body (ggml quantize_row_q8_0 definition): one element per lane,
+// a half-wave per 32-block.  Writes the int8 plane, the scale as f32 (the exact value
+// of the fp16 scale), the block's int sum, and optionally GGUF blocks.
+__device__ __forceinline__ void quant_q8_0_elem(const float* __restrict__ x, size_t n, size_t idx,
+                                                int8_t* __restrict__ q, float* __restrict__ d,
+                                                int* __restrict__ qsum, uint8_t* __restrict__ blocks) {
+    const bool live = idx < n;  // n is a multiple of 32: a half-wave is all live or all dead
+    const float v = live ? x[idx] : 0.0f;
+    const Q8Result r = quant_q8_0_lane32(v);
+    int s = r.q;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
+    if (!live) return;
+    const size_t b = idx / QK;
+    const int j = (int)(idx % QK);
+    if (q) q[idx] = r.q;
+    if (j == 0) {
+        if (d) d[b] = h2f(r.dh);
+        if (qsum) qsum[b] = s;
+    }
+    if (blocks) {
+        uint8_t* blk = blocks + b * 34;
+        blk[2 + j] = (uint8_t)r.q;
+        if (j == 0) {
+            blk[0] = (uint8_t)(r.dh & 0xff);
+            blk[1] = (uint8_t)(r.dh >> 8);
+        }
+    }
+}
+
+// Selection (one wave per token, work groups [0, ceil(T/4))) and, when xq is given,
+// the Q8_0 quantization of x by the work groups after those (256 elements each), so
+// decode batches need no separate quantization launch.
 __global__ __launch_bounds__(256) void route_select_kernel(const float* __restrict__ logits, int T, int E, int K,
                                                            int norm, float scale, float* __restrict__ topw,
                                                            int* __restrict__ topi, const float* __restrict__ x,
                                                            int H, int8_t* __restrict__ xq, float* __restrict__ xd,
                                                            int* __restrict__ xs) {
+    const int sel_groups = (T + 3) / 4;
+    if ((int)blockIdx.x >= sel_groups) {
+        const size_t idx = (size_t)(blockIdx.x - sel_groups) * 256 + threadIdx.x;
+        quant_q8_0_elem(x, (size_t)T * H, idx, xq, xd, xs, nullptr);
+        return;
+    }
     const int tok = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (tok >= T) return;
     const float v = lane < E ? logits[(size_t)tok * E + lane] : 0.0f;
     topk_wave(v, E, K, norm, scale, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
-    if (xq) {
-        const float* xr = x + (size_t)tok * H;
-        for (int h = lane; h < H; h += WAVE) {
-            const Q8Result r = quant_q8_0_lane32(xr[h]);
-            int s = r.q;
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
-            xq[(size_t)tok * H + h] = r.q;
-            if ((h & 31) == 0) {
-                const size_t b = ((size_t)tok * H + h) / QK;
-                xd[b] = h2f(r.dh);
-                xs[b] = s;
-            }
-        }
-    }
 }
 
 hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
@@ -157,8 +181,9 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, norm, scale, topw,
-                       topi, x, H, xq, xd, xs);
+    const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + 255) / 256) : 0u;
+    hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4 + quant_groups), dim3(256), 0, s, logits, T, E, K, norm,
+                       scale, topw, topi, x, H, xq, xd, xs);
     return hipGetLastError();
 }
 
@@ -202,29 +227,7 @@ hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s) {
 __global__ __launch_bounds__(256) void quant_q8_0_kernel(const float* __restrict__ x, size_t n,
                                                          int8_t* __restrict__ q, float* __restrict__ d,
                                                          int* __restrict__ qsum, uint8_t* __restrict__ blocks) {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const bool live = idx < n;  // n is a multiple of 32: a half-wave is all live or all dead
-    const float v = live ? x[idx] : 0.0f;
-    const Q8Result r = quant_q8_0_lane32(v);
-    int s = r.q;
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
-    if (!live) return;
-    const size_t b = idx / QK;
-    const int j = (int)(idx % QK);
-    if (q) q[idx] = r.q;
-    if (j == 0) {
-        if (d) d[b] = h2f(r.dh);
-        if (qsum) qsum[b] = s;
-    }
-    if (blocks) {
-        uint8_t* blk = blocks + b * 34;
-        blk[2 + j] = (uint8_t)r.q;
-        if (j == 0) {
-            blk[0] = (uint8_t)(r.dh & 0xff);
-            blk[1] = (uint8_t)(r.dh >> 8);
-        }
-    }
+    quant_q8_0_elem(x, n, (size_t)blockIdx.x * blockDim.x + threadIdx.x, q, d, qsum, blocks);
 }
 
 hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
@@ -341,9 +344,11 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __rest
         }
         off_s[E] = acc;
         toff_s[E] = tacc;
+        const int all = tacc + (has_shared ? (T + NT - 1) / NT : 0);
         o.meta[0] = tacc;
-        o.meta[1] = tacc + (has_shared ? (T + NT - 1) / NT : 0);
+        o.meta[1] = all;
         o.meta[2] = distinct;
+        o.meta[META_TILE_OFF + E + 1] = all;
     }
     __syncthreads();
     if (tid < E) {
@@ -358,6 +363,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __rest
         }
     }
     if (tid == E) o.off[E] = off_s[E];
+    if (tid <= E) o.meta[META_TILE_OFF + tid] = toff_s[tid];
     if (has_shared) {
         const int ns = (T + NT - 1) / NT;
         for (int j = tid; j < ns; j += DSP_THREADS) {
