@@ -163,7 +163,14 @@ int timed(hy_moe_ctx* c, int kid, hipStream_t s, F&& launch) {
     return HY_OK;
 }
 
-int tile_bound_routed(int T, int K, int E, int NT) { return (T * K + E * (NT - 1)) / NT; }
+// Upper bound on routed tiles of at most NT pairs: an expert with c pairs takes
+// ceil(c / NT) tiles, at most min(E, T*K) experts are hit, and a tile holds >= 1 pair.
+int tile_bound_routed(int T, int K, int E, int NT) {
+    const int pairs = T * K;
+    const int hit = E < pairs ? E : pairs;
+    const int b = (pairs + hit * (NT - 1)) / NT;
+    return b < pairs ? b : pairs;
+}
 
 // largest batch the decode GEMV takes in AUTO mode; above it the MFMA grouped GEMM
 constexpr uint32_t kGemvMaxTokens = 16;
@@ -190,10 +197,10 @@ int check_cfg(const hy_moe_config* c) {
 }
 
 hy::MatView gu_view(const hy_moe_ctx* c, const LayerW& L) {
-    return {L.gu_qs, L.gu_sc, c->gu_qs_stride, c->gu_sc_stride, 2 * c->I, c->H};
+    return {L.gu_qs, L.gu_sc, c->gu_qs_stride, c->gu_sc_stride, 2 * c->I, c->H, c->X};
 }
 hy::MatView dn_view(const hy_moe_ctx* c, const LayerW& L) {
-    return {L.dn_qs, L.dn_sc, c->dn_qs_stride, c->dn_sc_stride, c->H, c->I};
+    return {L.dn_qs, L.dn_sc, c->dn_qs_stride, c->dn_sc_stride, c->H, c->I, c->X};
 }
 hy::Routing routing(const hy_moe_ctx* c) {
     return {c->topi, c->topw, c->cnt, c->off, c->srt_tok, c->comb_pos, c->comb_w, c->tile_e, c->tile_start,

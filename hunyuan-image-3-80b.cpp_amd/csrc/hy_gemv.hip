@@ -255,74 +255,106 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 }
 
 // Quantized weights (Q8_0 / Q4_0): the same per-row block-sequential accumulation as
-// gemv_kernel, with the weight stream decoupled from the arithmetic.  Each wave owns a
-// private LDS ring of DEPTH blocks of its 64-row group (1 KB / 2 KB of quants + 128 B
-// of fp16 scales per block) filled by global->LDS DMA: DEPTH blocks are always in
-// flight, completion is counted with vmcnt (in-order), and no barrier is needed
-// because a wave only reads what it copied.  The last DEPTH blocks are consumed by an
-// unrolled tail whose waits count down to zero, so the wave leaves no copy in flight.
-// consume the last DEPTH blocks, U at a time: before blocks base + J .. + U - 1, wait
-// until at most the DEPTH - U - J younger blocks' copies are outstanding
-template <int J, int DEPTH, int U, int LOADS, class F>
+// gemv_kernel, with the weight stream decoupled from the arithmetic.  Each work group
+// is one wave owning one 64-row group of one tile.  Its weights stream through a
+// private LDS ring of NSTEP steps; a step is GQ_U = 8 consecutive blocks of the group
+// (8 x 1 KB / 2 KB of quants, one DMA per block) plus the 8 blocks' fp16 scales, which
+// are contiguous in the scale plane (one 1 KB DMA).  Copies are global->LDS DMA,
+// counted with vmcnt (in order); no barrier is needed in the loop because a wave only
+// reads what it copied.  The stream starts before the routing lookups of the tile
+// (expert id read speculatively and clamped into the resident table), so their
+// latency overlaps the first copies.  The last NSTEP steps are consumed by an unrolled
+// tail whose waits count down to zero: the wave leaves no copy in flight.
+constexpr int GQ_U = 8;       // blocks per step
+constexpr int GQ_WAVES = 1;   // one wave per work group: work groups spread over every CU
+constexpr int GQ_THREADS = GQ_WAVES * WAVE;
+
+template <int WT>
+struct GqSteps {
+    static constexpr int value = WT == HY_TYPE_Q4_0 ? 3 : 2;  // copies in flight <= 34 < 64 (vmcnt)
+};
+
+// consume the last NSTEP steps: before step base + J, wait until at most the
+// NSTEP - 1 - J younger steps' copies are outstanding
+template <int J, int NSTEP, int LOADS, class F>
 __device__ __forceinline__ void gemv_tail(F& step, int base) {
-    if constexpr (J < DEPTH) {
-        MM_WAIT_VM_LGKM((DEPTH - U - J) * LOADS);
+    if constexpr (J < NSTEP) {
+        MM_WAIT_VM_LGKM((NSTEP - 1 - J) * LOADS);
         step(base + J);
-        gemv_tail<J + U, DEPTH, U, LOADS>(step, base);
+        gemv_tail<J + 1, NSTEP, LOADS>(step, base);
     }
 }
 
-constexpr int GQ_U = 4;  // blocks per step of gemv_q_kernel (DEPTH and nb are multiples)
-
-template <int WT>
-struct GqDepth {
-    static constexpr int value = WT == HY_TYPE_Q4_0 ? 16 : 12;
-};
-
 template <int WT, int NT, int MODE>
-__global__ __launch_bounds__(GV_THREADS) void gemv_q_kernel(GvArgs a) {
+__global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
+    static_assert(MODE == 0 || MODE == 1, "routed/shared products only (the combine runs separately)");
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
-    constexpr int DEPTH = GqDepth<WT>::value;
+    constexpr int NSTEP = GqSteps<WT>::value;
     constexpr int BPB = Q4 ? 16 : 32;
-    constexpr int WBYTES = 64 * BPB;   // one block of a 64-row group
-    constexpr int SLOT = WBYTES + 128; // + its 64 fp16 scales
-    constexpr int LOADS = (Q4 ? 1 : 2) + 1;
+    constexpr int WBYTES = 64 * BPB;            // one block of a 64-row group
+    constexpr int SSLOT = GQ_U * WBYTES + 1024; // one step: GQ_U blocks + their scales
+    constexpr int LOADS = GQ_U * (Q4 ? 1 : 2) + 1;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int tok_s[NT], slot_s[NT];
-    const int tile = (MODE == 2) ? a.R.meta[0] + (int)blockIdx.x : (int)blockIdx.x;
-    if (tile >= a.R.meta[1]) return;
-    const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
+    const int lane = threadIdx.x;
+    const int G = blockIdx.y;                  // 64-row group (grid.y == n_groups)
+    const int tile = blockIdx.x;
+    const int Kd = a.Kd, nb = Kd / QK, nsteps = nb / GQ_U;
+    uint8_t* ring = smem + ((((size_t)a.nx * Kd + (size_t)a.nx * nb * 8) + 15) & ~(size_t)15);
+
+    // start the weight stream first: tile_e[tile] is in the arena for every launched
+    // tile; a stale entry (tile past this call's count) is clamped into the table and
+    // its copies are drained before the work group exits
+    int e = a.R.tile_e[tile];
+    e = e < 0 ? 0 : (e >= a.W.n_mats ? a.W.n_mats - 1 : e);
+    const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride + (size_t)G * nb * WBYTES;
+    const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64;
+    auto issue = [&](int st_i) {
+        uint8_t* st = ring + (st_i % NSTEP) * SSLOT;
+        const uint8_t* src = wq + (size_t)st_i * GQ_U * WBYTES + lane * 16;
+#pragma unroll
+        for (int u = 0; u < GQ_U; u++) {
+            g2l16(src + u * WBYTES, st + u * WBYTES);
+            if (!Q4) g2l16(src + u * WBYTES + 1024, st + u * WBYTES + 1024);
+        }
+        g2l16(wsc + (size_t)st_i * GQ_U * 64 + lane * 8, st + GQ_U * WBYTES);
+    };
+#pragma unroll
+    for (int s = 0; s < NSTEP; s++) issue(s);
+
+    if (tile >= a.R.meta[1]) {
+        MM_WAIT_VM_LGKM(0);
+        return;
+    }
+    const int start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
-    const int Kd = a.Kd, nb = Kd / QK;
-    if (threadIdx.x < NT) {
-        const int i = threadIdx.x;
+    if (lane < NT) {
         int tok = 0, slot = 0;
-        if (i < n) {
+        if (lane < n) {
             if (shared) {
-                tok = start + i;
+                tok = start + lane;
                 slot = a.T * a.K + tok;
             } else {
-                slot = a.R.off[e] + start + i;
+                slot = a.R.off[e] + start + lane;
                 tok = a.R.srt_tok[slot];
             }
         }
-        tok_s[i] = tok;
-        slot_s[i] = slot;
+        tok_s[lane] = tok;
+        slot_s[lane] = slot;
     }
     __syncthreads();
     // the tile's activation rows (int8), scales and block sums; n <= nx rows
     int8_t* xs_l = reinterpret_cast<int8_t*>(smem);
     float* xd_l = reinterpret_cast<float*>(smem + (size_t)a.nx * Kd);
     int* xsum_l = reinterpret_cast<int*>(smem + (size_t)a.nx * Kd + (size_t)a.nx * nb * 4);
-    const size_t ring_off = ((size_t)a.nx * Kd + (size_t)a.nx * nb * 8 + 15) & ~(size_t)15;
     {
         const int vec_per_row = Kd / 16;
-        for (int v = threadIdx.x; v < n * vec_per_row; v += GV_THREADS) {
+        for (int v = lane; v < n * vec_per_row; v += GQ_THREADS) {
             const int i = v / vec_per_row, c = v % vec_per_row;
             const int row = MODE == 0 ? tok_s[i] : slot_s[i];
             reinterpret_cast<int4*>(xs_l + (size_t)i * Kd)[c] = reinterpret_cast<const int4*>(a.aq + (size_t)row * Kd)[c];
         }
-        for (int v = threadIdx.x; v < n * nb; v += GV_THREADS) {
+        for (int v = lane; v < n * nb; v += GQ_THREADS) {
             const int i = v / nb, b = v % nb;
             const int row = MODE == 0 ? tok_s[i] : slot_s[i];
             xd_l[v] = a.ad[(size_t)row * nb + b];
@@ -331,33 +363,21 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_q_kernel(GvArgs a) {
     }
     __syncthreads();
 
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int G = blockIdx.y * GV_WAVES + wave;
-    if (G >= a.n_groups) return;  // no barrier below
-    uint8_t* ring = smem + ring_off + (size_t)wave * DEPTH * SLOT;
-    const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride + (size_t)G * nb * WBYTES;
-    const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64;
-    auto issue = [&](int b) {
-        uint8_t* st = ring + (b % DEPTH) * SLOT;
-        g2l16(wq + (size_t)b * WBYTES + lane * 16, st);
-        if (!Q4) g2l16(wq + (size_t)b * WBYTES + 1024 + lane * 16, st + 1024);
-        if (lane < 8) g2l16(wsc + (size_t)b * 64 + lane * 8, st + WBYTES);
-    };
     float acc[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++) acc[i] = 0.0f;
-    // GQ_U blocks per step: one round of LDS reads (the blocks' weights and scales, and
-    // per token the activation blocks) and one wait per token, then the blocks'
-    // arithmetic in order
-    auto step = [&](int b0) {
+    // one step: one round of LDS reads (the step's weights and scales, then per token
+    // its activation blocks) and one wait per token, then the blocks in order
+    auto step = [&](int st_i) {
+        const uint8_t* st = ring + (st_i % NSTEP) * SSLOT;
+        const int b0 = st_i * GQ_U;
         v4i_t w0[GQ_U], w1[GQ_U];
         uint32_t dwb[GQ_U];
 #pragma unroll
         for (int u = 0; u < GQ_U; u++) {
-            const uint8_t* st = ring + ((b0 + u) % DEPTH) * SLOT;
-            w0[u] = lds_b128(st + lane * BPB);
-            if (!Q4) w1[u] = lds_b128(st + lane * BPB + 16);
-            dwb[u] = lds_u16(st + WBYTES + lane * 2);
+            w0[u] = lds_b128(st + u * WBYTES + lane * BPB);
+            if (!Q4) w1[u] = lds_b128(st + u * WBYTES + lane * BPB + 16);
+            dwb[u] = lds_u16(st + GQ_U * WBYTES + (u * 64 + lane) * 2);
         }
 #pragma unroll
         for (int i = 0; i < NT; i++) {
@@ -404,16 +424,12 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_q_kernel(GvArgs a) {
             }
         }
     };
-#pragma unroll
-    for (int d = 0; d < DEPTH; d++) issue(d);
-    int b0 = 0;
-    for (; b0 < nb - DEPTH; b0 += GQ_U) {
-        MM_WAIT_VM_LGKM((DEPTH - GQ_U) * LOADS);  // blocks b0.. b0+GQ_U-1 landed (in order)
-        step(b0);
-#pragma unroll
-        for (int u = 0; u < GQ_U; u++) issue(b0 + DEPTH + u);  // refill the slots just read
+    for (int s = 0; s < nsteps - NSTEP; s++) {
+        MM_WAIT_VM_LGKM((NSTEP - 1) * LOADS);  // step s landed (copies complete in order)
+        step(s);
+        issue(s + NSTEP);                      // refill the slot just read
     }
-    gemv_tail<0, DEPTH, GQ_U, LOADS>(step, nb - DEPTH);
+    gemv_tail<0, NSTEP, LOADS>(step, nsteps - NSTEP);
 
     if (MODE == 0) {
         // lanes 0..31: gate rows 32G+lane, lanes 32..63: the matching up rows
@@ -441,16 +457,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_q_kernel(GvArgs a) {
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (i >= n) break;
-            if (MODE == 1) {
-                a.y[(size_t)slot_s[i] * a.H + row] = acc[i];
-            } else {
-                const int t = tok_s[i];
-                float comb = 0.0f;
-                for (int k = 0; k < a.K; k++)
-                    comb = fmaf(a.R.comb_w[t * a.K + k], a.y[(size_t)a.R.comb_pos[t * a.K + k] * a.H + row], comb);
-                const float o = acc[i] + comb;
-                a.out[(size_t)t * a.H + row] = a.resid ? a.resid[(size_t)t * a.H + row] + o : o;
-            }
+            a.y[(size_t)slot_s[i] * a.H + row] = acc[i];
         }
     }
 }
@@ -477,37 +484,45 @@ size_t gemv_smem(int wtype, int Kd) {
     return (size_t)GEMV_NT * Kd + (size_t)GEMV_NT * (Kd / QK) * 8;
 }
 
-// LDS of gemv_q_kernel: nx staged activation rows + GV_WAVES rings of DEPTH blocks
+// LDS of gemv_q_kernel: nx staged activation rows + a ring of NSTEP steps
 template <int WT>
 static size_t gemv_q_smem(int nx, int Kd) {
     constexpr int BPB = WT == HY_TYPE_Q4_0 ? 16 : 32;
     const size_t xs = ((size_t)nx * Kd + (size_t)nx * (Kd / QK) * 8 + 15) & ~(size_t)15;
-    return xs + (size_t)GV_WAVES * GqDepth<WT>::value * (64 * BPB + 128);
+    return xs + (size_t)GqSteps<WT>::value * (GQ_U * 64 * BPB + 1024);
+}
+
+template <int WT>
+static bool gemv_q_fits(int Kd) {
+    const int nb = Kd / QK;
+    return nb % GQ_U == 0 && nb / GQ_U >= GqSteps<WT>::value;
 }
 
 template <int MODE>
-static hipError_t gemv_launch(int wtype, dim3 grid, hipStream_t s, GvArgs a) {
-    const int nb = a.Kd / QK;
+static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     a.nx = a.T < GEMV_NT ? a.T : GEMV_NT;
+    const dim3 grid_v(tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
+    const dim3 grid_q(tiles, a.n_groups);
+    constexpr int QM = MODE == 2 ? 1 : MODE;  // mode 2 (fused shared combine) only in gemv_kernel
     switch (wtype) {
     case HY_TYPE_Q8_0:
-        if (nb >= GqDepth<HY_TYPE_Q8_0>::value && nb % GQ_U == 0)
-            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+        if (MODE != 2 && gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, QM>), grid_q, dim3(GQ_THREADS),
                                gemv_q_smem<HY_TYPE_Q8_0>(a.nx, a.Kd), s, a);
         else
-            hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+            hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);
         break;
     case HY_TYPE_Q4_0:
-        if (nb >= GqDepth<HY_TYPE_Q4_0>::value && nb % GQ_U == 0)
-            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+        if (MODE != 2 && gemv_q_fits<HY_TYPE_Q4_0>(a.Kd))
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM>), grid_q, dim3(GQ_THREADS),
                                gemv_q_smem<HY_TYPE_Q4_0>(a.nx, a.Kd), s, a);
         else
-            hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+            hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);
         break;
     default:
-        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_F32, GEMV_NT, MODE>), grid, dim3(GV_THREADS),
+        hipLaunchKernelGGL((gemv_kernel<HY_TYPE_F32, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                            gemv_smem(wtype, a.Kd), s, a);
         break;
     }
@@ -518,16 +533,14 @@ hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Rout
                           int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
                           hipStream_t s) {
     GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, 0, hq, hd, hs, hf, nullptr, nullptr, nullptr};
-    dim3 grid(max_tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
-    return gemv_launch<0>(wtype, grid, s, a);
+    return gemv_launch<0>(wtype, max_tiles, s, a);
 }
 
 hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
                             const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
                             int E, int K, float* y, const float* resid, float* out, hipStream_t s) {
     GvArgs a{W, R, hq, hd, hs, hf, T, H, I, E, K, I, H / 64, 0, nullptr, nullptr, nullptr, nullptr, y, resid, out};
-    dim3 grid(n_tiles_bound, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
-    return mode == 0 ? gemv_launch<1>(wtype, grid, s, a) : gemv_launch<2>(wtype, grid, s, a);
+    return mode == 0 ? gemv_launch<1>(wtype, n_tiles_bound, s, a) : gemv_launch<2>(wtype, n_tiles_bound, s, a);
 }
 
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,

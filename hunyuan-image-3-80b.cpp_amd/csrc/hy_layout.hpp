@@ -25,6 +25,7 @@ struct MatView {
     size_t qs_stride;    // bytes between experts
     size_t sc_stride;    // scale elements between experts
     int rows, cols;
+    int n_mats;          // matrices in the table (routed experts + shared)
 };
 
 __host__ __device__ inline int gu_packed_row(int orig, int I) {

@@ -195,17 +195,19 @@ def test_layer_small_mfma_path(gpu, small_layers, wtype, T):
     m.close()
 
 
-# decode GEMV with the DMA ring: needs >= 16 (Q4_0) / 12 (Q8_0) blocks per row; the
-# shapes cover ring depth == blocks (no steady-state loop) and the plain kernel fallback
+# decode GEMV with the DMA ring: needs a multiple of 8 blocks per row and >= 3 (Q4_0) /
+# 2 (Q8_0) steps of 8; the shapes cover ring depth == steps (no steady-state loop) and
+# the plain-kernel fallback on one of the two matrices
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
-@pytest.mark.parametrize("H,I", [(512, 512), (1024, 384), (384, 768)])
-def test_decode_gemv_ring(gpu, wtype, H, I):
+@pytest.mark.parametrize("H,I,shared", [(768, 768, True), (1024, 640, True), (640, 1536, True),
+                                        (512, 1024, True), (1024, 768, False)])
+def test_decode_gemv_ring(gpu, wtype, H, I, shared):
     E, K = 16, 4
-    layer = O.synth_layer(H, I, E, K, wtype, seed=H + I, std=0.05)
-    m = gpu.Moe(H, I, E, K, wtype, max_tokens=16)
+    layer = O.synth_layer(H, I, E, K, wtype, seed=H + I, std=0.05, shared=shared)
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=16, has_shared=shared)
     m.set_path(gpu.PATH_VALU)
     m.upload(0, layer)
-    for T in (1, 2, 5, 8, 16):
+    for T in (1, 2, 5, 8, 16, 3):
         x = O.synth(90 + T, 0, O.T_X, 0, (T, H), 1.0)
         assert_exact(m.run(0, x), O.moe_forward_q(layer, x), f"gemv H={H} I={I} wtype={wtype} T={T}")
     m.close()
