@@ -332,7 +332,9 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
     // work arena
     const size_t Tm = cfg->max_tokens, H = c->H, I = c->I, E = c->E, K = c->K;
     const size_t pairs = Tm * K, slots = Tm * (K + 1);
-    c->max_tiles = tile_bound_routed((int)Tm, (int)K, (int)E, 8) + (int)((Tm + 7) / 8) + 1;
+    // tiles of the smallest tile size any path uses (the decode GEMV's)
+    const int nt_min = hy::GEMV_NT;
+    c->max_tiles = tile_bound_routed((int)Tm, (int)K, (int)E, nt_min) + (int)((Tm + nt_min - 1) / nt_min) + 1;
     struct Part {
         void** p;
         size_t bytes;

@@ -20,6 +20,8 @@
 //   out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e * y_e[t] )
 // (src/hunyuan_moe_full.cpp:503-515, einsum_combine order :387-397).  The fused
 // shared-tile combine (mode 2) stays available for callers that want one launch.
+#include <utility>
+
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_layout.hpp"
@@ -255,23 +257,41 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 }
 
 // Quantized weights (Q8_0 / Q4_0): the same per-row block-sequential accumulation as
-// gemv_kernel, with the weight stream decoupled from the arithmetic.  Each work group
-// is one wave owning one 64-row group of one tile.  Its weights stream through a
-// private LDS ring of NSTEP steps; a step is GQ_U = 8 consecutive blocks of the group
-// (8 x 1 KB / 2 KB of quants, one DMA per block) plus the 8 blocks' fp16 scales, which
-// are contiguous in the scale plane (one 1 KB DMA).  Copies are global->LDS DMA,
-// counted with vmcnt (in order); no barrier is needed in the loop because a wave only
-// reads what it copied.  The stream starts before the routing lookups of the tile
-// (expert id read speculatively and clamped into the resident table), so their
-// latency overlaps the first copies.  The last NSTEP steps are consumed by an unrolled
-// tail whose waits count down to zero: the wave leaves no copy in flight.
+// gemv_kernel, with the operand streams decoupled from the arithmetic.  Each work
+// group is one wave owning one 64-row group of one tile (<= NT tokens).  A private LDS
+// ring holds NSTEP steps; a step is GQ_U = 8 consecutive blocks:
+//   weights  GQ_U x (64 rows x 16 B / 32 B)   one DMA per block (two for Q8_0)
+//   scales   GQ_U x 64 fp16                   one 1 KB DMA (contiguous in the plane)
+//   x        NT tokens x GQ_U x 32 B int8     one DMA (token = lane / 16)
+//   x scales / block sums  NT x GQ_U x 4 B    one DMA (lanes 0..31 / 32..63)
+// Token slots past the tile's n read token 0's row (valid, never used), so every
+// step issues the same number of copies and the vmcnt waits are constants.  Copies
+// complete in order; no barrier is needed because a wave only reads what it copied.
+// The weight stream starts before the routing lookups of the tile (expert id read
+// speculatively and clamped into the resident table), so their latency overlaps the
+// first copies; the first activation copies follow, and one full wait joins both.
+// The last NSTEP steps are consumed by an unrolled tail whose waits count down to
+// zero: the wave leaves no copy in flight.
 constexpr int GQ_U = 8;       // blocks per step
 constexpr int GQ_WAVES = 1;   // one wave per work group: work groups spread over every CU
 constexpr int GQ_THREADS = GQ_WAVES * WAVE;
 
 template <int WT>
 struct GqSteps {
-    static constexpr int value = WT == HY_TYPE_Q4_0 ? 3 : 2;  // copies in flight <= 34 < 64 (vmcnt)
+    static constexpr int value = WT == HY_TYPE_Q4_0 ? 3 : 2;  // copies in flight <= 36 < 64 (vmcnt)
+};
+
+template <int WT, int NT>
+struct GqSlot {
+    static constexpr int BPB = WT == HY_TYPE_Q4_0 ? 16 : 32;
+    static constexpr int W = 0;                             // weights
+    static constexpr int S = W + GQ_U * 64 * BPB;           // weight scales
+    static constexpr int X = S + GQ_U * 64 * 2;             // activation quants
+    static constexpr int XD = X + NT * GQ_U * QK;           // activation scales, then block sums
+    static constexpr int BYTES = XD + 2 * NT * GQ_U * 4;
+    static constexpr int LOADS = GQ_U * (WT == HY_TYPE_Q4_0 ? 1 : 2) + 1 + 1 + 1;
+    static_assert(NT * GQ_U * QK == WAVE * 16, "one 16-byte copy per lane moves the step's activations");
+    static_assert(2 * NT * GQ_U == WAVE, "one 4-byte copy per lane moves the step's scales and sums");
 };
 
 // consume the last NSTEP steps: before step base + J, wait until at most the
@@ -285,42 +305,60 @@ __device__ __forceinline__ void gemv_tail(F& step, int base) {
     }
 }
 
+// ds_read_b128 / b32 at base + a compile-time byte offset (no address arithmetic)
+template <int OFF>
+__device__ __forceinline__ v4i_t lds_b128_at(uint32_t base) {
+    v4i_t r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_b32_at(uint32_t base) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_u16_at(uint32_t base) {
+    uint32_t r;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+    return r;
+}
+
 template <int WT, int NT, int MODE>
 __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     static_assert(MODE == 0 || MODE == 1, "routed/shared products only (the combine runs separately)");
+    using SL = GqSlot<WT, NT>;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
     constexpr int NSTEP = GqSteps<WT>::value;
-    constexpr int BPB = Q4 ? 16 : 32;
-    constexpr int WBYTES = 64 * BPB;            // one block of a 64-row group
-    constexpr int SSLOT = GQ_U * WBYTES + 1024; // one step: GQ_U blocks + their scales
-    constexpr int LOADS = GQ_U * (Q4 ? 1 : 2) + 1;
-    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int BPB = SL::BPB;
+    constexpr int WBYTES = 64 * BPB;  // one block of a 64-row group
+    extern __shared__ __align__(16) uint8_t ring[];
     __shared__ int tok_s[NT], slot_s[NT];
     const int lane = threadIdx.x;
-    const int G = blockIdx.y;                  // 64-row group (grid.y == n_groups)
+    const int G = blockIdx.y;  // 64-row group (grid.y == n_groups)
     const int tile = blockIdx.x;
     const int Kd = a.Kd, nb = Kd / QK, nsteps = nb / GQ_U;
-    uint8_t* ring = smem + ((((size_t)a.nx * Kd + (size_t)a.nx * nb * 8) + 15) & ~(size_t)15);
 
     // start the weight stream first: tile_e[tile] is in the arena for every launched
     // tile; a stale entry (tile past this call's count) is clamped into the table and
     // its copies are drained before the work group exits
     int e = a.R.tile_e[tile];
     e = e < 0 ? 0 : (e >= a.W.n_mats ? a.W.n_mats - 1 : e);
-    const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride + (size_t)G * nb * WBYTES;
-    const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64;
-    auto issue = [&](int st_i) {
-        uint8_t* st = ring + (st_i % NSTEP) * SSLOT;
-        const uint8_t* src = wq + (size_t)st_i * GQ_U * WBYTES + lane * 16;
+    const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride + (size_t)G * nb * WBYTES + lane * 16;
+    const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64 + lane * 8;
+    auto issue_w = [&](int st_i) {
+        uint8_t* st = ring + (st_i % NSTEP) * SL::BYTES;
+        const uint8_t* src = wq + (size_t)st_i * GQ_U * WBYTES;
 #pragma unroll
         for (int u = 0; u < GQ_U; u++) {
-            g2l16(src + u * WBYTES, st + u * WBYTES);
-            if (!Q4) g2l16(src + u * WBYTES + 1024, st + u * WBYTES + 1024);
+            g2l16(src + u * WBYTES, st + SL::W + u * WBYTES);
+            if (!Q4) g2l16(src + u * WBYTES + 1024, st + SL::W + u * WBYTES + 1024);
         }
-        g2l16(wsc + (size_t)st_i * GQ_U * 64 + lane * 8, st + GQ_U * WBYTES);
+        g2l16(wsc + (size_t)st_i * GQ_U * 64, st + SL::S);
     };
 #pragma unroll
-    for (int s = 0; s < NSTEP; s++) issue(s);
+    for (int s = 0; s < NSTEP; s++) issue_w(s);
 
     if (tile >= a.R.meta[1]) {
         MM_WAIT_VM_LGKM(0);
@@ -343,55 +381,55 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
         slot_s[lane] = slot;
     }
     __syncthreads();
-    // the tile's activation rows (int8), scales and block sums; n <= nx rows
-    int8_t* xs_l = reinterpret_cast<int8_t*>(smem);
-    float* xd_l = reinterpret_cast<float*>(smem + (size_t)a.nx * Kd);
-    int* xsum_l = reinterpret_cast<int*>(smem + (size_t)a.nx * Kd + (size_t)a.nx * nb * 4);
-    {
-        const int vec_per_row = Kd / 16;
-        for (int v = lane; v < n * vec_per_row; v += GQ_THREADS) {
-            const int i = v / vec_per_row, c = v % vec_per_row;
-            const int row = MODE == 0 ? tok_s[i] : slot_s[i];
-            reinterpret_cast<int4*>(xs_l + (size_t)i * Kd)[c] = reinterpret_cast<const int4*>(a.aq + (size_t)row * Kd)[c];
-        }
-        for (int v = lane; v < n * nb; v += GQ_THREADS) {
-            const int i = v / nb, b = v % nb;
-            const int row = MODE == 0 ? tok_s[i] : slot_s[i];
-            xd_l[v] = a.ad[(size_t)row * nb + b];
-            if (Q4) xsum_l[v] = a.as[(size_t)row * nb + b];
-        }
-    }
-    __syncthreads();
+    // this lane's activation sources: x piece (token lane/16, 16 B piece lane%16 of the
+    // step's 256 B) and the scale (lanes < 32) or block sum (lanes >= 32) of token
+    // (lane%32)/8, block lane%8; token slots >= n read token 0's row
+    const int xt = lane / 16, st_tok = (lane % 32) / 8;
+    const int xrow = MODE == 0 ? tok_s[xt < n ? xt : 0] : slot_s[xt < n ? xt : 0];
+    const int srow = MODE == 0 ? tok_s[st_tok < n ? st_tok : 0] : slot_s[st_tok < n ? st_tok : 0];
+    const int8_t* xsrc = a.aq + (size_t)xrow * Kd + (lane % 16) * 16;
+    const void* ssrc = lane < 32 ? (const void*)(a.ad + (size_t)srow * nb + lane % 8)
+                                 : (Q4 ? (const void*)(a.as + (size_t)srow * nb + lane % 8)
+                                       : (const void*)(a.ad + (size_t)srow * nb + lane % 8));
+    auto issue_x = [&](int st_i) {
+        uint8_t* st = ring + (st_i % NSTEP) * SL::BYTES;
+        g2l16(xsrc + (size_t)st_i * GQ_U * QK, st + SL::X);
+        __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(ssrc) + (size_t)st_i * GQ_U * 4, st + SL::XD, 4, 0,
+                                         0);
+    };
+#pragma unroll
+    for (int s = 0; s < NSTEP; s++) issue_x(s);
+    MM_WAIT_VM_LGKM(0);  // the first NSTEP steps have landed
 
     float acc[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++) acc[i] = 0.0f;
-    // one step: one round of LDS reads (the step's weights and scales, then per token
-    // its activation blocks) and one wait per token, then the blocks in order
+    // one step: the step's weights and scales, then per token its activation blocks, one
+    // wait per token, then the blocks in order
     auto step = [&](int st_i) {
-        const uint8_t* st = ring + (st_i % NSTEP) * SSLOT;
-        const int b0 = st_i * GQ_U;
+        const uint32_t st = lds_off(ring + (st_i % NSTEP) * SL::BYTES);
+        const uint32_t wrow = st + SL::W + lane * BPB;
+        const uint32_t srow_l = st + SL::S + lane * 2;
         v4i_t w0[GQ_U], w1[GQ_U];
         uint32_t dwb[GQ_U];
-#pragma unroll
-        for (int u = 0; u < GQ_U; u++) {
-            w0[u] = lds_b128(st + u * WBYTES + lane * BPB);
-            if (!Q4) w1[u] = lds_b128(st + u * WBYTES + lane * BPB + 16);
-            dwb[u] = lds_u16(st + GQ_U * WBYTES + (u * 64 + lane) * 2);
-        }
+        [&]<int... U>(std::integer_sequence<int, U...>) {
+            ((w0[U] = lds_b128_at<U * WBYTES>(wrow)), ...);
+            if constexpr (!Q4) ((w1[U] = lds_b128_at<U * WBYTES + 16>(wrow)), ...);
+            ((dwb[U] = lds_u16_at<U * 128>(srow_l)), ...);
+        }(std::make_integer_sequence<int, GQ_U>{});
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (i < n) {
+                const uint32_t xb = st + SL::X + i * GQ_U * QK;
+                const uint32_t db = st + SL::XD + i * GQ_U * 4;
                 v4i_t x0[GQ_U], x1[GQ_U];
                 uint32_t xdb[GQ_U], xsb[GQ_U];
-#pragma unroll
-                for (int u = 0; u < GQ_U; u++) {
-                    const int b = b0 + u;
-                    x0[u] = lds_b128(xs_l + (size_t)i * Kd + b * QK);
-                    x1[u] = lds_b128(xs_l + (size_t)i * Kd + b * QK + 16);
-                    xdb[u] = lds_b32(xd_l + i * nb + b);
-                    if (Q4) xsb[u] = lds_b32(xsum_l + i * nb + b);
-                }
+                [&]<int... U>(std::integer_sequence<int, U...>) {
+                    ((x0[U] = lds_b128_at<U * QK>(xb)), ...);
+                    ((x1[U] = lds_b128_at<U * QK + 16>(xb)), ...);
+                    ((xdb[U] = lds_b32_at<U * 4>(db)), ...);
+                    if constexpr (Q4) ((xsb[U] = lds_b32_at<NT * GQ_U * 4 + U * 4>(db)), ...);
+                }(std::make_integer_sequence<int, GQ_U>{});
                 lds_wait();
                 if (i == 0) {
 #pragma unroll
@@ -425,11 +463,12 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
         }
     };
     for (int s = 0; s < nsteps - NSTEP; s++) {
-        MM_WAIT_VM_LGKM((NSTEP - 1) * LOADS);  // step s landed (copies complete in order)
+        MM_WAIT_VM_LGKM((NSTEP - 1) * SL::LOADS);  // step s landed (copies complete in order)
         step(s);
-        issue(s + NSTEP);                      // refill the slot just read
+        issue_w(s + NSTEP);                        // refill the slot just read
+        issue_x(s + NSTEP);
     }
-    gemv_tail<0, NSTEP, LOADS>(step, nsteps - NSTEP);
+    gemv_tail<0, NSTEP, SL::LOADS>(step, nsteps - NSTEP);
 
     if (MODE == 0) {
         // lanes 0..31: gate rows 32G+lane, lanes 32..63: the matching up rows
@@ -484,12 +523,10 @@ size_t gemv_smem(int wtype, int Kd) {
     return (size_t)GEMV_NT * Kd + (size_t)GEMV_NT * (Kd / QK) * 8;
 }
 
-// LDS of gemv_q_kernel: nx staged activation rows + a ring of NSTEP steps
+// LDS of gemv_q_kernel: a ring of NSTEP steps
 template <int WT>
-static size_t gemv_q_smem(int nx, int Kd) {
-    constexpr int BPB = WT == HY_TYPE_Q4_0 ? 16 : 32;
-    const size_t xs = ((size_t)nx * Kd + (size_t)nx * (Kd / QK) * 8 + 15) & ~(size_t)15;
-    return xs + (size_t)GqSteps<WT>::value * (GQ_U * 64 * BPB + 1024);
+static size_t gemv_q_smem() {
+    return (size_t)GqSteps<WT>::value * GqSlot<WT, GEMV_NT>::BYTES;
 }
 
 template <int WT>
@@ -508,7 +545,7 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     case HY_TYPE_Q8_0:
         if (MODE != 2 && gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
             hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, QM>), grid_q, dim3(GQ_THREADS),
-                               gemv_q_smem<HY_TYPE_Q8_0>(a.nx, a.Kd), s, a);
+                               gemv_q_smem<HY_TYPE_Q8_0>(), s, a);
         else
             hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);
@@ -516,7 +553,7 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     case HY_TYPE_Q4_0:
         if (MODE != 2 && gemv_q_fits<HY_TYPE_Q4_0>(a.Kd))
             hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM>), grid_q, dim3(GQ_THREADS),
-                               gemv_q_smem<HY_TYPE_Q4_0>(a.nx, a.Kd), s, a);
+                               gemv_q_smem<HY_TYPE_Q4_0>(), s, a);
         else
             hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);

@@ -26,7 +26,7 @@ hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int
 hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s);
 
 // expert products, decode GEMV path (hy_gemv.hip)
-constexpr int GEMV_NT = 8;  // tokens per GEMV tile
+constexpr int GEMV_NT = 4;  // tokens per GEMV tile
 int gemv_tile_tokens();
 hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
                           int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
