@@ -240,26 +240,37 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int H = c->H, I = c->I, E = c->E, K = c->K, wt = c->cfg.wtype;
     const int iT = (int)T;
     const int has_shared = c->cfg.has_shared ? 1 : 0;
-    // small batches quantize the activations inside the selection pass, large ones in
-    // a bandwidth-shaped kernel of their own
-    const bool fuse_quant = wt != HY_TYPE_F32 && T <= 32;
-    if (wt != HY_TYPE_F32 && !fuse_quant)
-        HY_TRY(timed(c, hy::KID_QUANT, s, [&] {
-            return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
-        }));
-    HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
-        return hy::launch_router_q(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob, c->cfg.routed_scaling_factor,
-                                   c->logits, c->topw, c->topi, fuse_quant ? c->xq : nullptr, c->xd, c->xs, s);
-    }));
     // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode
     const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) &&
                       (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
     const int NT = mfma ? hy::mfma_tile_tokens(iT, K, E, H, I) : hy::gemv_tile_tokens();
-    HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
-        return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
-                                   c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
-                                   c->meta, s);
-    }));
+    if (!mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
+        // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
+        HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
+            return hy::launch_route_decode(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob,
+                                           c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi, c->xq, c->xd,
+                                           c->xs, NT, has_shared, c->cnt, c->off, c->srt_tok, c->pair_pos,
+                                           c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n, c->meta, s);
+        }));
+    } else {
+        // small batches quantize the activations inside the selection pass, large ones
+        // in a bandwidth-shaped kernel of their own
+        const bool fuse_quant = wt != HY_TYPE_F32 && T <= 32;
+        if (wt != HY_TYPE_F32 && !fuse_quant)
+            HY_TRY(timed(c, hy::KID_QUANT, s, [&] {
+                return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
+            }));
+        HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
+            return hy::launch_router_q(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob,
+                                       c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi,
+                                       fuse_quant ? c->xq : nullptr, c->xd, c->xs, s);
+        }));
+        HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
+            return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
+                                       c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
+                                       c->meta, s);
+        }));
+    }
     const hy::Routing R = routing(c);
     const hy::ActQ X{c->xq, c->xd, c->xs, H};
     const int routed_bound = tile_bound_routed(iT, K, E, NT);
@@ -289,7 +300,10 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
                                   c->hd, c->hs, c->hf, s);
     }));
     // decode: routed and shared down products in one launch (the shared expert's rows
-    // no longer wait behind the routed ones), then the combine
+    // no longer wait behind the routed ones), then the combine.  (Folding the combine
+    // into the down launch through per-row-group completion counters needs an
+    // agent-scope release per work group, which writes back the XCD's L2: it made the
+    // launch several times slower.)
     HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
         return hy::launch_gemv_down(wt, routed_bound + shared_tiles, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf,
                                     iT, H, I, E, K, c->y, nullptr, nullptr, s);

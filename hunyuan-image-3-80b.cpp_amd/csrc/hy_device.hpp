@@ -13,6 +13,7 @@ constexpr int MAX_K = 16;    // top-k bound
 // dispatch meta block: [0] routed tiles, [1] all tiles, [2] distinct experts, [3] unused,
 // [4 + e] first tile of expert e (e = 0..E, E = shared), [4 + E + 1] end of the tiles
 constexpr int META_TILE_OFF = 4;
+constexpr int MAX_DECODE_PAIRS = 256;  // T*K handled by the one-launch decode routing
 constexpr int META_INTS = META_TILE_OFF + MAX_E + 2;
 
 // ---------------------------------------------------------------- fp16

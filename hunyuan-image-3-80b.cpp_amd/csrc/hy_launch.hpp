@@ -14,12 +14,17 @@ namespace hy {
 hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                          float* logits, float* topw, int* topi, hipStream_t s);
 hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
-                           float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s);
+                           float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s,
+                           bool logits_only = false);
 hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, int norm, float scale, float* topw,
                                    int* topi, hipStream_t s);
 hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s);
 hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
                              hipStream_t s);
+hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
+                               float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, int NT,
+                               int has_shared, int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos,
+                               float* comb_w, int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s);
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared, int* cnt,
                            int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w, int* tile_e,
                            int* tile_start, int* tile_n, int* meta, hipStream_t s);

@@ -160,7 +160,8 @@ hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, i
 }
 
 hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
-                           float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s) {
+                           float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s,
+                           bool logits_only) {
     const dim3 blk(ROUTER_WAVES * WAVE);
     auto grid_for = [&](int tpw, int epw) {
         const int items = ((T + tpw - 1) / tpw) * ((E + epw - 1) / epw);
@@ -180,7 +181,7 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
                            dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, logits);
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || logits_only) return e;
     const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + 255) / 256) : 0u;
     hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4 + quant_groups), dim3(256), 0, s, logits, T, E, K, norm,
                        scale, topw, topi, x, H, xq, xd, xs);
@@ -409,6 +410,151 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __rest
             o.comb_w[t * K + k] = wk[k];
         }
     }
+}
+
+// ----------------------------------------------------------------------------
+// Decode routing after the router logits (T <= 16, T*K <= 256), one launch:
+//  * work group 0 selects the top-k of every token (one wave per token, topk_wave)
+//    and builds the dispatch lists exactly as dispatch_kernel: pairs ranked in
+//    k-major capacity-slot priority, per-expert offsets and tiles (then the shared
+//    expert's), per-token combine lists in ascending expert order;
+//  * work groups 1.. quantize x to Q8_0, 256 elements each.
+// (Folding the logits into this launch needs a device-scope handoff between work
+// groups -- an agent-scope release writes back the XCD's L2 -- which cost more than
+// the kernel boundary.)
+// ----------------------------------------------------------------------------
+struct DecodeRouteArgs {
+    const float* x;
+    const float* logits;
+    int T, H, E, K, norm;
+    float scale;
+    float* topw;
+    int* topi;
+    int8_t* xq;
+    float* xd;
+    int* xs;
+    int NT, has_shared;
+    DispatchOut o;
+};
+
+__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const int u = __shfl_up(incl, d, WAVE);
+        if (lane >= d) incl += u;
+    }
+    return incl - v;
+}
+
+__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(DecodeRouteArgs a) {
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    if (blockIdx.x > 0) {
+        const size_t idx = (size_t)(blockIdx.x - 1) * 256 + tid;
+        quant_q8_0_elem(a.x, (size_t)a.T * a.H, idx, a.xq, a.xd, a.xs, nullptr);
+        return;
+    }
+    const int T = a.T, E = a.E, K = a.K;
+
+    // ---- selection: one wave per token
+    __shared__ int sel_e[MAX_DECODE_PAIRS];
+    __shared__ float sel_w[MAX_DECODE_PAIRS];
+    __shared__ int rank_s[MAX_DECODE_PAIRS], pos_s[MAX_DECODE_PAIRS];
+    __shared__ int cnt_s[MAX_E], off_s[MAX_E + 1], toff_s[MAX_E + 2];
+    for (int t = wave; t < T; t += ROUTER_WAVES) {
+        const float v = lane < E ? a.logits[(size_t)t * E + lane] : 0.0f;
+        topk_wave(v, E, K, a.norm, a.scale, lane, sel_w + t * K, sel_e + t * K);
+        if (lane < K) {
+            a.topw[t * K + lane] = sel_w[t * K + lane];
+            a.topi[t * K + lane] = sel_e[t * K + lane];
+        }
+    }
+    if (tid < MAX_E) cnt_s[tid] = 0;
+    __syncthreads();
+    // ---- dispatch: rank of each pair inside its expert, k-major then token: the
+    // pairs of earlier ranks (any token) plus those of the same rank and earlier tokens
+    const int P = T * K;
+    const int pt = tid / K, pk = tid - pt * K;  // this thread's pair (token, rank)
+    if (tid < P) {
+        const int e = sel_e[tid];
+        int rank = 0;
+        for (int kq = 0; kq < pk; kq++)
+            for (int tq = 0; tq < T; tq++) rank += sel_e[tq * K + kq] == e;
+        for (int tq = 0; tq < pt; tq++) rank += sel_e[tq * K + pk] == e;
+        rank_s[tid] = rank;
+        atomicAdd(&cnt_s[e], 1);
+    }
+    __syncthreads();
+    const int NT = a.NT;
+    if (wave == 0) {
+        const int c = lane < E ? cnt_s[lane] : 0;
+        const int nt = (c + NT - 1) / NT;
+        const int off = wave_excl_scan(c, lane), toff = wave_excl_scan(nt, lane);
+        const int total = __shfl(off + c, WAVE - 1, WAVE), routed = __shfl(toff + nt, WAVE - 1, WAVE);
+        const int distinct = __popcll(__ballot(c > 0));
+        const int all = routed + (a.has_shared ? (T + NT - 1) / NT : 0);
+        if (lane < E) {
+            off_s[lane] = off;
+            toff_s[lane] = toff;
+            a.o.cnt[lane] = c;
+            a.o.off[lane] = off;
+            a.o.meta[META_TILE_OFF + lane] = toff;
+            for (int j = 0; j < nt; j++) {
+                a.o.tile_e[toff + j] = lane;
+                a.o.tile_start[toff + j] = j * NT;
+                a.o.tile_n[toff + j] = min(NT, c - j * NT);
+            }
+        }
+        if (lane == 0) {
+            off_s[E] = total;
+            toff_s[E] = routed;
+            a.o.off[E] = total;
+            a.o.meta[0] = routed;
+            a.o.meta[1] = all;
+            a.o.meta[2] = distinct;
+            a.o.meta[META_TILE_OFF + E] = routed;
+            a.o.meta[META_TILE_OFF + E + 1] = all;
+        }
+    }
+    __syncthreads();
+    if (a.has_shared) {
+        const int ns = (T + NT - 1) / NT;
+        for (int j = tid; j < ns; j += ROUTER_WAVES * WAVE) {
+            a.o.tile_e[toff_s[E] + j] = E;
+            a.o.tile_start[toff_s[E] + j] = j * NT;
+            a.o.tile_n[toff_s[E] + j] = min(NT, T - j * NT);
+        }
+    }
+    if (tid < P) {
+        const int pos = off_s[sel_e[tid]] + rank_s[tid];
+        pos_s[tid] = pos;
+        a.o.pair_pos[tid] = pos;
+        a.o.srt_tok[pos] = pt;
+    }
+    __syncthreads();
+    // combine lists: each token's pairs in ascending expert order (a token's experts
+    // are distinct, so a pair's place is the count of its token's smaller experts)
+    if (tid < P) {
+        const int e = sel_e[tid];
+        int r = 0;
+        for (int j = 0; j < K; j++) r += sel_e[pt * K + j] < e;
+        a.o.comb_pos[pt * K + r] = pos_s[tid];
+        a.o.comb_w[pt * K + r] = sel_w[tid];
+    }
+}
+
+hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
+                               float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, int NT,
+                               int has_shared, int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos,
+                               float* comb_w, int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s) {
+    hipError_t e = launch_router_q(x, wr, T, H, E, K, norm, scale, logits, topw, topi, nullptr, nullptr, nullptr, s,
+                                   /*logits_only=*/true);
+    if (e != hipSuccess) return e;
+    DecodeRouteArgs a{x, logits, T, H, E, K, norm, scale, topw, topi, xq, xd, xs, NT, has_shared,
+                      DispatchOut{cnt, off, srt_tok, pair_pos, comb_pos, comb_w, tile_e, tile_start, tile_n, meta}};
+    const unsigned quant_groups = (unsigned)(((size_t)T * H + 255) / 256);
+    hipLaunchKernelGGL(route_decode_kernel, dim3(1 + quant_groups), dim3(ROUTER_WAVES * WAVE), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared,
