@@ -94,6 +94,7 @@ struct hy_moe_ctx {
     int *cnt = nullptr, *off = nullptr, *srt_tok = nullptr, *pair_pos = nullptr, *comb_pos = nullptr;
     float* comb_w = nullptr;
     int *tile_e = nullptr, *tile_start = nullptr, *tile_n = nullptr, *meta = nullptr;
+    int* dsp_scratch = nullptr;  // per-block counts of the dispatch
     int8_t* hq = nullptr;
     float* hd = nullptr;
     int* hs = nullptr;
@@ -268,7 +269,7 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
         HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
             return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
                                        c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
-                                       c->meta, s);
+                                       c->meta, c->dsp_scratch, s);
         }));
     }
     const hy::Routing R = routing(c);
@@ -367,6 +368,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
         {(void**)&c->hf, wt == HY_TYPE_F32 ? slots * I * 4 : 16},
         {(void**)&c->y, slots * H * 4},    {(void**)&c->xn, Tm * H * 4},
         {(void**)&c->cur, Tm * H * 4},
+        {(void**)&c->dsp_scratch, hy::dispatch_scratch_bytes((int)Tm, (int)K, (int)E)},
     };
     size_t total = 0;
     for (auto& p : parts) total += align256(p.bytes);
@@ -591,7 +593,8 @@ int hy_dispatch_pairs(const int32_t* topi, const float* topw, uint32_t T, uint32
     const size_t pairs = (size_t)T * K;
     const int max_tiles = (int)((pairs + E * 7) / 8 + 1);
     void* scratch = nullptr;
-    const size_t bytes = pairs * 4 * 3 + (size_t)max_tiles * 4 * 3 + (size_t)hy::META_INTS * 4;
+    const size_t dsp = hy::dispatch_scratch_bytes((int)T, (int)K, (int)E);
+    const size_t bytes = pairs * 4 * 3 + (size_t)max_tiles * 4 * 3 + (size_t)hy::META_INTS * 4 + dsp;
     if (hipMalloc(&scratch, bytes) != hipSuccess) return fail(HY_ERR_NOMEM, "dispatch scratch");
     int* srt = static_cast<int*>(scratch);
     int* cpos = srt + pairs;
@@ -600,8 +603,9 @@ int hy_dispatch_pairs(const int32_t* topi, const float* topw, uint32_t T, uint32
     int* ts = te + max_tiles;
     int* tn = ts + max_tiles;
     int* meta = tn + max_tiles;
+    int* dscr = meta + hy::META_INTS;
     hipError_t e = hy::launch_dispatch(topi, topw, (int)T, (int)K, (int)E, 8, 0, counts, offsets, srt, pos, cpos, cw,
-                                       te, ts, tn, meta, s);
+                                       te, ts, tn, meta, dscr, s);
     hipError_t e2 = hipStreamSynchronize(s);
     (void)hipFree(scratch);
     if (e != hipSuccess || e2 != hipSuccess)

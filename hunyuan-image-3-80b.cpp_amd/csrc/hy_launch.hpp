@@ -25,9 +25,11 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
                                float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, int NT,
                                int has_shared, int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos,
                                float* comb_w, int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s);
+// scratch: dispatch_scratch_bytes(T, K, E) of device memory (per-block counts)
+size_t dispatch_scratch_bytes(int T, int K, int E);
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared, int* cnt,
                            int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w, int* tile_e,
-                           int* tile_start, int* tile_n, int* meta, hipStream_t s);
+                           int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s);
 hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s);
 
 // expert products, decode GEMV path (hy_gemv.hip)

@@ -247,11 +247,27 @@ hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int*
 // list is therefore the reference's dispatch_mask slot c.  Also builds the per-token
 // combine lists (pairs in ascending expert order, the einsum_combine summation
 // order of :387-397) and a list of tiles of at most NT pairs.
-// Single workgroup of 1024 threads; one token bitmap per expert in LDS per rank k
-// (T <= 16384).  Deterministic: no atomics except the bitmap ORs.
+// Three launches, no atomics outside LDS:
+//  1. dispatch_rank_kernel, one work group per (block of 1024 tokens, rank k): an LDS
+//     bitmap of the block's tokens per expert gives each pair its rank among the
+//     block's pairs of that expert and rank, and the block's count per expert;
+//  2. dispatch_scan_kernel, one work group: block counts -> exclusive bases in k-major
+//     order, expert offsets and tiles;
+//  3. dispatch_scatter_kernel, one thread per pair: position = offset + base + rank,
+//     the sorted token list and the combine lists.
 // ----------------------------------------------------------------------------
-constexpr int DSP_THREADS = 1024;
-constexpr int DSP_MAX_WORDS = 512;  // 16384 tokens
+constexpr int DSP_BLOCK = 1024;  // tokens per rank work group
+
+__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const int u = __shfl_up(incl, d, WAVE);
+        if (lane >= d) incl += u;
+    }
+    return incl - v;
+}
+
 
 struct DispatchOut {
     int* cnt;
@@ -266,156 +282,111 @@ struct DispatchOut {
     int* meta;
 };
 
-__global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int* __restrict__ topi,
-                                                               const float* __restrict__ topw, int T, int K,
-                                                               int E, int NT, int has_shared, DispatchOut o) {
-    __shared__ uint32_t mask[MAX_E][DSP_MAX_WORDS];
-    __shared__ int part[MAX_E][16];
-    __shared__ int run_s[MAX_E];
-    __shared__ int off_s[MAX_E + 1];
-    __shared__ int toff_s[MAX_E + 1];
-    const int tid = threadIdx.x;
-    const int P = T * K;
-    if (tid < MAX_E) run_s[tid] = 0;
-    if (P <= DSP_THREADS) {
-        // few pairs (decode): each thread ranks its own pair directly against all
-        // others held in LDS (same k-major priority order as the bitmap path)
-        __shared__ int pe_s[DSP_THREADS];
-        if (tid < P) pe_s[tid] = topi[tid];
-        __syncthreads();
-        if (tid < P) {
-            const int e = pe_s[tid], k = tid % K, t = tid / K;
-            int rank = 0;
-            for (int q = 0; q < P; q++) {
-                const int kq = q % K, tq = q / K;
-                rank += (pe_s[q] == e) && (kq < k || (kq == k && tq < t));
-            }
-            o.pair_pos[tid] = rank;
-            atomicAdd(&run_s[e], 1);
+__global__ __launch_bounds__(DSP_BLOCK) void dispatch_rank_kernel(const int* __restrict__ topi, int T, int K, int E,
+                                                                 int* __restrict__ blk_cnt, int* __restrict__ rank) {
+    __shared__ uint32_t mask[MAX_E][DSP_BLOCK / 32];
+    __shared__ int wpre[MAX_E][DSP_BLOCK / 32];
+    const int blk = blockIdx.x, k = blockIdx.y, tid = threadIdx.x;
+    const int nblk = gridDim.x;
+    for (int i = tid; i < MAX_E * (DSP_BLOCK / 32); i += DSP_BLOCK) (&mask[0][0])[i] = 0u;
+    __syncthreads();
+    const int t = blk * DSP_BLOCK + tid;
+    int e = t < T ? topi[(size_t)t * K + k] : -1;
+    if (e >= E) e = -1;  // an out-of-range id is dropped (never produced by the router)
+    if (e >= 0) atomicOr(&mask[e][tid / 32], 1u << (tid % 32));
+    __syncthreads();
+    // per expert: exclusive prefix of the 32 words' popcounts (a half-wave per expert)
+    for (int i = tid; i < MAX_E * (DSP_BLOCK / 32); i += DSP_BLOCK) {
+        const int ee = i / 32, w = i % 32;
+        const int c = __popc(mask[ee][w]);
+        int incl = c;
+#pragma unroll
+        for (int d = 1; d < 32; d <<= 1) {
+            const int u = __shfl_up(incl, d, 32);
+            if (w >= d) incl += u;
         }
-        __syncthreads();
-    } else {
-    const int nwords = (T + 31) / 32;
-    const int e = tid / 16, c = tid % 16;  // 16 threads per expert, each a run of words
-    const int wpc = (nwords + 15) / 16;
-    const int w0 = c * wpc, w1 = min(nwords, w0 + wpc);
-    for (int k = 0; k < K; k++) {
-        for (int i = tid; i < MAX_E * nwords; i += DSP_THREADS) mask[i / nwords][i % nwords] = 0u;
-        __syncthreads();
-        for (int t = tid; t < T; t += DSP_THREADS) {
-            const int ee = topi[t * K + k];
-            atomicOr(&mask[ee][t / 32], 1u << (t % 32));
-        }
-        __syncthreads();
-        int local = 0;
-        if (e < E)
-            for (int w = w0; w < w1; w++) local += __popc(mask[e][w]);
-        part[e][c] = local;
-        __syncthreads();
-        if (e < E) {
-            int rank = run_s[e];
-            for (int cc = 0; cc < c; cc++) rank += part[e][cc];
-            // relative position of each pair inside its expert, parked in pair_pos
-            for (int w = w0; w < w1; w++) {
-                uint32_t bits = mask[e][w];
-                while (bits) {
-                    const int bit = __builtin_ctz(bits);
-                    bits &= bits - 1;
-                    o.pair_pos[(w * 32 + bit) * K + k] = rank++;
-                }
-            }
-        }
-        __syncthreads();
-        if (c == 0 && e < E) {
-            int tot = 0;
-            for (int cc = 0; cc < 16; cc++) tot += part[e][cc];
-            run_s[e] += tot;
-        }
-        __syncthreads();
-    }
-    }
-    if (tid == 0) {
-        int acc = 0, tacc = 0, distinct = 0;
-        for (int ee = 0; ee < E; ee++) {
-            off_s[ee] = acc;
-            toff_s[ee] = tacc;
-            acc += run_s[ee];
-            tacc += (run_s[ee] + NT - 1) / NT;
-            distinct += run_s[ee] > 0;
-        }
-        off_s[E] = acc;
-        toff_s[E] = tacc;
-        const int all = tacc + (has_shared ? (T + NT - 1) / NT : 0);
-        o.meta[0] = tacc;
-        o.meta[1] = all;
-        o.meta[2] = distinct;
-        o.meta[META_TILE_OFF + E + 1] = all;
+        wpre[ee][w] = incl - c;
+        if (w == 31 && ee < E) blk_cnt[((size_t)k * nblk + blk) * E + ee] = incl;
     }
     __syncthreads();
+    if (e >= 0)
+        rank[(size_t)t * K + k] = wpre[e][tid / 32] + __popc(mask[e][tid / 32] & ((1u << (tid % 32)) - 1u));
+}
+
+// blk_cnt [K][nblk][E] (k-major: the priority order) -> exclusive bases in place
+__global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E, int NT, int has_shared, int nblk,
+                                                            int* __restrict__ blk_cnt, DispatchOut o) {
+    __shared__ int cnt_s[MAX_E];
+    const int tid = threadIdx.x, lane = tid % WAVE;
+    const int nkb = K * nblk;
     if (tid < E) {
-        o.cnt[tid] = run_s[tid];
-        o.off[tid] = off_s[tid];
-        const int nt = (run_s[tid] + NT - 1) / NT;
-        for (int j = 0; j < nt; j++) {
-            const int ti = toff_s[tid] + j;
-            o.tile_e[ti] = tid;
-            o.tile_start[ti] = j * NT;
-            o.tile_n[ti] = min(NT, run_s[tid] - j * NT);
+        int run = 0;
+        for (int kb = 0; kb < nkb; kb++) {
+            int* p = blk_cnt + (size_t)kb * E + tid;
+            const int c = *p;
+            *p = run;
+            run += c;
         }
-    }
-    if (tid == E) o.off[E] = off_s[E];
-    if (tid <= E) o.meta[META_TILE_OFF + tid] = toff_s[tid];
-    if (has_shared) {
-        const int ns = (T + NT - 1) / NT;
-        for (int j = tid; j < ns; j += DSP_THREADS) {
-            const int ti = toff_s[E] + j;
-            o.tile_e[ti] = E;
-            o.tile_start[ti] = j * NT;
-            o.tile_n[ti] = min(NT, T - j * NT);
-        }
-    }
-    // absolute positions and the sorted token list (each thread rewrites only the
-    // pairs it reads, so no barrier is needed between the read and the write)
-    for (int p = tid; p < T * K; p += DSP_THREADS) {
-        const int pos = off_s[topi[p]] + o.pair_pos[p];
-        o.pair_pos[p] = pos;
-        o.srt_tok[pos] = p / K;
+        cnt_s[tid] = run;
     }
     __syncthreads();
-    // combine lists: each token's pairs sorted by expert id
-    for (int t = tid; t < T; t += DSP_THREADS) {
-        int ek[MAX_K], pk[MAX_K];
-        float wk[MAX_K];
-        for (int k = 0; k < K; k++) {
-            ek[k] = topi[t * K + k];
-            pk[k] = o.pair_pos[t * K + k];
-            wk[k] = topw[t * K + k];
-        }
-        for (int a = 1; a < K; a++) {
-            const int ea = ek[a], pa = pk[a];
-            const float wa = wk[a];
-            int b = a - 1;
-            while (b >= 0 && ek[b] > ea) {
-                ek[b + 1] = ek[b];
-                pk[b + 1] = pk[b];
-                wk[b + 1] = wk[b];
-                b--;
+    if (tid < WAVE) {
+        const int c = lane < E ? cnt_s[lane] : 0;
+        const int nt = (c + NT - 1) / NT;
+        const int off = wave_excl_scan(c, lane), toff = wave_excl_scan(nt, lane);
+        const int total = __shfl(off + c, WAVE - 1, WAVE), routed = __shfl(toff + nt, WAVE - 1, WAVE);
+        const int distinct = __popcll(__ballot(c > 0));
+        const int ns = has_shared ? (T + NT - 1) / NT : 0;
+        if (lane < E) {
+            o.cnt[lane] = c;
+            o.off[lane] = off;
+            o.meta[META_TILE_OFF + lane] = toff;
+            for (int j = 0; j < nt; j++) {
+                o.tile_e[toff + j] = lane;
+                o.tile_start[toff + j] = j * NT;
+                o.tile_n[toff + j] = min(NT, c - j * NT);
             }
-            ek[b + 1] = ea;
-            pk[b + 1] = pa;
-            wk[b + 1] = wa;
         }
-        for (int k = 0; k < K; k++) {
-            o.comb_pos[t * K + k] = pk[k];
-            o.comb_w[t * K + k] = wk[k];
+        if (lane == 0) {
+            o.off[E] = total;
+            o.meta[0] = routed;
+            o.meta[1] = routed + ns;
+            o.meta[2] = distinct;
+            o.meta[META_TILE_OFF + E] = routed;
+            o.meta[META_TILE_OFF + E + 1] = routed + ns;
+        }
+        for (int j = lane; j < ns; j += WAVE) {
+            o.tile_e[routed + j] = E;
+            o.tile_start[routed + j] = j * NT;
+            o.tile_n[routed + j] = min(NT, T - j * NT);
         }
     }
+}
+
+__global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int* __restrict__ topi,
+                                                               const float* __restrict__ topw, int T, int K, int E,
+                                                               int nblk, const int* __restrict__ blk_base,
+                                                               DispatchOut o) {
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= T * K) return;
+    const int t = p / K, k = p - t * K;
+    const int e = topi[p];
+    if (e < 0 || e >= E) return;
+    const int pos = o.off[e] + blk_base[((size_t)k * nblk + t / DSP_BLOCK) * E + e] + o.pair_pos[p];
+    o.pair_pos[p] = pos;
+    o.srt_tok[pos] = t;
+    // combine list slot: the token's experts are distinct, so the pair's place in
+    // ascending expert order is the count of the token's smaller experts
+    int r = 0;
+    for (int j = 0; j < K; j++) r += topi[(size_t)t * K + j] < e;
+    o.comb_pos[(size_t)t * K + r] = pos;
+    o.comb_w[(size_t)t * K + r] = topw[p];
 }
 
 // ----------------------------------------------------------------------------
 // Decode routing after the router logits (T <= 16, T*K <= 256), one launch:
 //  * work group 0 selects the top-k of every token (one wave per token, topk_wave)
-//    and builds the dispatch lists exactly as dispatch_kernel: pairs ranked in
+//    and builds the dispatch lists exactly as launch_dispatch does: pairs ranked in
 //    k-major capacity-slot priority, per-expert offsets and tiles (then the shared
 //    expert's), per-token combine lists in ascending expert order;
 //  * work groups 1.. quantize x to Q8_0, 256 elements each.
@@ -437,15 +408,6 @@ struct DecodeRouteArgs {
     DispatchOut o;
 };
 
-__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const int u = __shfl_up(incl, d, WAVE);
-        if (lane >= d) incl += u;
-    }
-    return incl - v;
-}
 
 __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(DecodeRouteArgs a) {
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
@@ -557,11 +519,23 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
     return hipGetLastError();
 }
 
+size_t dispatch_scratch_bytes(int T, int K, int E) {
+    return (size_t)((T + DSP_BLOCK - 1) / DSP_BLOCK) * K * E * sizeof(int);
+}
+
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared,
                            int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w,
-                           int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s) {
+                           int* tile_e, int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s) {
     DispatchOut o{cnt, off, srt_tok, pair_pos, comb_pos, comb_w, tile_e, tile_start, tile_n, meta};
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), 0, s, topi, topw, T, K, E, NT, has_shared, o);
+    const int nblk = (T + DSP_BLOCK - 1) / DSP_BLOCK;
+    hipLaunchKernelGGL(dispatch_rank_kernel, dim3(nblk, K), dim3(DSP_BLOCK), 0, s, topi, T, K, E, scratch, pair_pos);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(256), 0, s, T, K, E, NT, has_shared, nblk, scratch, o);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3((T * K + 255) / 256), dim3(256), 0, s, topi, topw, T, K, E, nblk,
+                       scratch, o);
     return hipGetLastError();
 }
 

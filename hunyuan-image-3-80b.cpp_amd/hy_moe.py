@@ -64,6 +64,7 @@ _SIGS = {
     "hy_memcpy_d2h": (C.c_int, [_vp, _vp, C.c_size_t]),
     "hy_memset": (C.c_int, [_vp, C.c_int, C.c_size_t]),
     "hy_copy_d2d": (C.c_int, [_vp, _vp, C.c_size_t, _vp]),
+    "hy_dispatch_pairs": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]),
     "hy_device_synchronize": (C.c_int, []),
     "hy_stream_create": (C.c_int, [C.POINTER(_vp)]),
     "hy_stream_destroy": (C.c_int, [_vp]),

@@ -179,7 +179,8 @@ int hy_topk_rows(const float* x_dev, uint32_t rows, uint32_t n, uint32_t k, floa
  * [E], list offsets [E+1], and each pair's position in the expert-sorted order
  * (pos_dev [T][K]).  Inside an expert the order is the reference's capacity-slot
  * priority (flat slot k*T + t ascending, src/hunyuan_moe_full.cpp:245-304), so
- * pos - offsets[e] is the dispatch_mask slot c. */
+ * pos - offsets[e] is the dispatch_mask slot c.  Indices must lie in [0, E) (as the
+ * router produces them); a pair with an out-of-range index is left out. */
 int hy_dispatch_pairs(const int32_t* indices_dev, const float* weights_dev, uint32_t T, uint32_t K,
                       uint32_t E, int32_t* counts_dev, int32_t* offsets_dev, int32_t* pos_dev,
                       void* stream);

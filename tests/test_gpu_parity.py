@@ -332,3 +332,48 @@ def test_copy_d2d(gpu, nbytes):
     got = b.numpy()
     np.testing.assert_array_equal(got[:nbytes], src[:nbytes])
     assert not got[nbytes:].any()
+
+
+def _dispatch_expected(idx, E):
+    """Counts, offsets and positions of the capacity-slot priority order (k-major,
+    then token) by brute force."""
+    T, K = idx.shape
+    counts = np.bincount(idx.ravel(), minlength=E).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    pos = np.zeros((T, K), np.int32)
+    nxt = offsets[:-1].copy()
+    for k in range(K):
+        for t in range(T):
+            e = idx[t, k]
+            pos[t, k] = nxt[e]
+            nxt[e] += 1
+    return counts, offsets, pos
+
+
+@pytest.mark.parametrize("T,skew", [(1, False), (300, False), (1024, False), (1025, True), (3000, False),
+                                    (5000, True)])
+def test_dispatch_pairs_multiblock(gpu, T, skew):
+    E, K = 64, 8
+    rng = np.random.default_rng(T)
+    p = np.ones(E) if not skew else 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    idx = np.stack([rng.choice(E, size=K, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, K)).astype(np.float32)
+    ib, wb = gpu.Buf.from_array(idx), gpu.Buf.from_array(w)
+    cb, ob, pb = gpu.Buf.empty((E,), np.int32), gpu.Buf.empty((E + 1,), np.int32), gpu.Buf.empty((T, K), np.int32)
+    gpu.check(gpu.lib().hy_dispatch_pairs(ib.ptr, wb.ptr, T, K, E, cb.ptr, ob.ptr, pb.ptr, None))
+    counts, offsets, pos = _dispatch_expected(idx, E)
+    np.testing.assert_array_equal(cb.numpy(), counts)
+    np.testing.assert_array_equal(ob.numpy(), offsets)
+    np.testing.assert_array_equal(pb.numpy(), pos)
+
+
+def test_layer_mfma_multiblock_dispatch(gpu, small_layers):
+    """T > 1024 tokens: the dispatch ranks pairs in several token blocks."""
+    layer = small_layers[O.Q8_0]
+    T = 2100
+    m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q8_0, max_tokens=T)
+    m.upload(0, layer)
+    x = O.synth(77, 0, O.T_X, 0, (T, SMALL["H"]), 1.0)
+    assert_exact(m.run(0, x), O.moe_forward_q(layer, x), "T=2100")
+    m.close()
