@@ -305,26 +305,6 @@ __device__ __forceinline__ void gemv_tail(F& step, int base) {
     }
 }
 
-// ds_read_b128 / b32 at base + a compile-time byte offset (no address arithmetic)
-template <int OFF>
-__device__ __forceinline__ v4i_t lds_b128_at(uint32_t base) {
-    v4i_t r;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
-    return r;
-}
-template <int OFF>
-__device__ __forceinline__ uint32_t lds_b32_at(uint32_t base) {
-    uint32_t r;
-    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
-    return r;
-}
-template <int OFF>
-__device__ __forceinline__ uint32_t lds_u16_at(uint32_t base) {
-    uint32_t r;
-    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
-    return r;
-}
-
 template <int WT, int NT, int MODE>
 __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     static_assert(MODE == 0 || MODE == 1, "routed/shared products only (the combine runs separately)");

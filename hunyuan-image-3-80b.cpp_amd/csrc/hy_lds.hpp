@@ -62,4 +62,24 @@ __device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, uint32_t&
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
 }
 
+// ds_read_b128 / b32 at base + a compile-time byte offset (no address arithmetic)
+template <int OFF>
+__device__ __forceinline__ v4i_t lds_b128_at(uint32_t base) {
+    v4i_t r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_b32_at(uint32_t base) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_u16_at(uint32_t base) {
+    uint32_t r;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+    return r;
+}
+
 }  // namespace hy

@@ -29,6 +29,8 @@
 // matching linear rows; epilogue h = silu(g) * u and Q8_0 quantization of h per token and
 // slab); 1 = down for routed tiles (writes y[pair][row]); 2 = down for shared tiles
 // fused with the combine out = resid + (y_shared + sum_{e ascending} w_e y_e).
+#include <utility>
+
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_layout.hpp"
@@ -113,7 +115,10 @@ template <int WT, int MODE, class SH>
 __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_kernel(MmArgs a) {
     constexpr int MM_ROWS = SH::ROWS, MM_TOK = SH::TOK, MM_KB = SH::KB, MM_SLABS = SH::SLABS;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
-    constexpr int STAGE = SH::ST_A * (Q4 ? 0 : 1) + (Q4 ? SH::ST_AR : 0) + SH::ST_B + SH::ST_AS + SH::ST_BS;
+    // stage slot: A (int8, or Q4_0 nibbles), B, A scales, B scales, then a zero area
+    // the upper lane half reads its rank-1 scale operands from
+    constexpr int ZBYTES = 512;
+    constexpr int STAGE = SH::ST_A * (Q4 ? 0 : 1) + (Q4 ? SH::ST_AR : 0) + SH::ST_B + SH::ST_AS + SH::ST_BS + ZBYTES;
     __shared__ __align__(16) uint8_t ring[MM_RING][STAGE];
     __shared__ __align__(16) int8_t aun[Q4 ? SH::ST_A : 16];  // Q4_0: unpacked A of the current stage
     __shared__ int tok_s[MM_TOK], slot_s[MM_TOK];
@@ -121,6 +126,8 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
     constexpr int OFF_B = Q4 ? SH::ST_AR : SH::ST_A;
     constexpr int OFF_AS = OFF_B + SH::ST_B;
     constexpr int OFF_BS = OFF_AS + SH::ST_AS;
+    constexpr int OFF_Z = OFF_BS + SH::ST_BS;
+    static_assert(MM_KB * 128 <= ZBYTES, "scale offsets of the upper lanes stay in the zero area");
     // copies per wave per stage (every wave issues the same number; vmcnt counts them)
     constexpr int LOADS = (Q4 ? 1 : 2) + SH::B_LOADS + 1 + 1;
 
@@ -160,56 +167,65 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
     }
     __syncthreads();
 
-    const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride;
-    const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride;
+    // zero areas of the stage slots (never written by the copies)
+    for (int i = tid; i < MM_RING * ZBYTES / 4; i += MM_THREADS)
+        reinterpret_cast<uint32_t*>(ring[i / (ZBYTES / 4)] + OFF_Z)[i % (ZBYTES / 4)] = 0u;
+    __syncthreads();
+
     constexpr int BPB = Q4 ? 16 : 32;
     const int G0 = row0 / 64;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);  // wave index as a scalar
+    // copy sources: a wave-uniform base (advanced per stage) + a per-lane 32-bit offset
+    // A: chunk c = wave (row group c / KB, block c % KB); Q8_0 2 KB = 2 copies, Q4_0 1 KB
+    const uint8_t* a_src = a.W.qs + (size_t)e * a.W.qs_stride +
+                           ((size_t)(G0 + wv / MM_KB) * nb + wv % MM_KB) * 64 * BPB;
+    const uint16_t* as_src = a.W.sc + (size_t)e * a.W.sc_stride + ((size_t)(G0 + wv / MM_KB) * nb + wv % MM_KB) * 64;
     // B rows: wave w copies tokens w*TOK/8 .. +TOK/8, KB*32 bytes each, as 16-byte
-    // pieces; piece p (load v, lane l: p = 64 v + l) is token p / (2 KB), offset
+    // pieces; piece p (copy v, lane l: p = 64 v + l) is token p / (2 KB), offset
     // 16 (p % (2 KB)) -- lane i of a copy lands at +16 i, i.e. tokens stay row-major
     constexpr int BPT = 2 * MM_KB;  // 16-byte pieces per token row
-    const int8_t* brow[SH::B_LOADS];
+    uint32_t b_off[SH::B_LOADS];
 #pragma unroll
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
         const int bt = wave * (MM_TOK / MM_WAVES) + (p % SH::B_LANES) / BPT;  // in range for masked lanes too
-        brow[v] = a.aq + (size_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * Kd + (p % BPT) * 16;
+        b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (p % BPT) * 16;
     }
     // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each: KB = 4 as one
     // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces
     constexpr int BS_LANES = MM_KB == 4 ? MM_TOK / MM_WAVES : MM_TOK / MM_WAVES * MM_KB;
     const int bst = wave * (MM_TOK / MM_WAVES) + (MM_KB == 4 ? lane : lane / MM_KB) % (MM_TOK / MM_WAVES);
-    const float* bsrow = a.ad + (size_t)(MODE == 0 ? tok_s[bst] : slot_s[bst]) * nb + (MM_KB == 4 ? 0 : lane % MM_KB);
+    const uint32_t bs_off =
+        ((uint32_t)(MODE == 0 ? tok_s[bst] : slot_s[bst]) * (uint32_t)nb + (MM_KB == 4 ? 0 : lane % MM_KB)) * 4;
 
     // issue the asynchronous copies of stage s into ring slot s % MM_RING; lanes
     // outside a copy's range are masked (the wave still issues it once)
     auto issue = [&](int s) {
         uint8_t* st = ring[s % MM_RING];
         const int kb0 = s * MM_KB;
-        // A: chunk c = wave (row group c / KB, block c % KB); Q8_0 2 KB = 2 copies,
-        // Q4_0 1 KB = 1 copy
-        const size_t cidx = (size_t)(G0 + wave / MM_KB) * nb + kb0 + wave % MM_KB;
-        const size_t cbase = cidx * 64 * BPB;
+        const uint8_t* ab = a_src + (size_t)kb0 * 64 * BPB;
         if (Q4) {
-            g2l16(wq + cbase + lane * 16, st + OFF_A + wave * 1024);
+            g2l16(ab + lane * 16, st + OFF_A + wave * 1024);
         } else {
-            g2l16(wq + cbase + lane * 16, st + OFF_A + wave * 2048);
-            g2l16(wq + cbase + 1024 + lane * 16, st + OFF_A + wave * 2048 + 1024);
+            g2l16(ab + lane * 16, st + OFF_A + wave * 2048);
+            g2l16(ab + 1024 + lane * 16, st + OFF_A + wave * 2048 + 1024);
         }
         // B rows of this wave's tokens
+        const int8_t* bb = a.aq + (size_t)kb0 * QK;
         uint8_t* bdst = st + OFF_B + wave * (MM_TOK / MM_WAVES) * (MM_KB * 32);
 #pragma unroll
         for (int v = 0; v < SH::B_LOADS; v++)
-            if (v * WAVE + lane < SH::B_LANES) g2l16(brow[v] + (size_t)kb0 * QK, bdst + v * 1024);
+            if (v * WAVE + lane < SH::B_LANES) g2l16(bb + b_off[v], bdst + v * 1024);
         // A scales: chunk `wave` = 64 fp16 = 128 B (lanes 0..7)
-        if (lane < 8) g2l16(wsc + cidx * 64 + lane * 8, st + OFF_AS + wave * 128);
+        if (lane < 8) g2l16(as_src + (size_t)kb0 * 64 + lane * 8, st + OFF_AS + wave * 128);
         // B scales of this wave's tokens
+        const uint8_t* sb = reinterpret_cast<const uint8_t*>(a.ad + kb0);
         uint8_t* sdst = st + OFF_BS + wave * (MM_TOK / MM_WAVES) * MM_KB * 4;
         if (lane < BS_LANES) {
             if (MM_KB == 4)
-                g2l16(bsrow + kb0, sdst);
+                g2l16(sb + bs_off, sdst);
             else
-                __builtin_amdgcn_global_load_lds(bsrow + kb0, sdst, 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(sb + bs_off, sdst, 4, 0, 0);
         }
     };
 
@@ -223,6 +239,46 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
         acc0[v] = 0.0f;
         acc1[v] = 0.0f;
     }
+    // per-lane LDS offsets inside a stage slot (the block kb adds a constant):
+    //   A rows lr and 32+lr of this wave's slab, 16-byte half lg
+    //   B row (token) nq*32+lr, half lg
+    //   rank-1 scale operands: lanes of the lower half read d_w of rows lr / 32+lr and
+    //   d_x of token nq*32+lr; lanes of the upper half read zeros
+    const uint32_t a_lane = (uint32_t)((Q4 ? 0 : OFF_A) + sl * MM_KB * 2048 + lr * 32 + 16 * lg);
+    const uint32_t b_lane = (uint32_t)(OFF_B + (nq * 32 + lr) * (MM_KB * 32) + 16 * lg);
+    const uint32_t sw_lane = (uint32_t)(lg == 0 ? OFF_AS + sl * MM_KB * 128 + lr * 2 : OFF_Z);
+    const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 + lr) * MM_KB * 4 : OFF_Z);
+    const uint32_t ring0 = lds_off(ring[0]);
+    const uint32_t aun0 = lds_off(aun);
+
+    // one 32-wide block kb of the stage whose slot starts at st
+    auto block = [&]<int KBI>(uint32_t st, uint32_t abase) {
+        v4i_t A0 = lds_b128_at<KBI * 2048>(abase);
+        v4i_t A1 = lds_b128_at<KBI * 2048 + 1024>(abase);
+        v4i_t B = lds_b128_at<KBI * 32>(st + b_lane);
+        uint32_t dw0 = lds_u16_at<KBI * 128>(st + sw_lane);
+        uint32_t dw1 = lds_u16_at<KBI * 128 + 64>(st + sw_lane);
+        uint32_t dxb = lds_b32_at<KBI * 4>(st + sx_lane);
+        lds_wait(A0, A1, B, dw0, dw1, dxb);
+        const v16i_t zero = {};
+        const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
+        const v16i_t S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
+        // rank-1 operands {d, 0, 0, ...}: the upper lanes hold zeros already; d_x is an
+        // fp16 value stored as f32, so the truncating pack is exact
+        const v4i_t xa0 = {(int)dw0, 0, 0, 0}, xa1 = {(int)dw1, 0, 0, 0};
+        const v4i_t xb = {__builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, dxb), 0.0f)), 0,
+                          0, 0};
+        const v16f_t zf = {};
+        const v16f_t C0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa0),
+                                                                 __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
+        const v16f_t C1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa1),
+                                                                 __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
+            acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
+        }
+    };
 
     const int nstage = nb / MM_KB;
     issue(0);
@@ -235,50 +291,28 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
             MM_WAIT_VM_LGKM(0);
         }
         __builtin_amdgcn_s_barrier();
-        const uint8_t* st = ring[s % MM_RING];
-        const int8_t* As;
+        const uint32_t st = ring0 + (uint32_t)((s % MM_RING) * STAGE);
+        uint32_t abase;
         if (Q4) {
             // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of
             // chunk t/64 (CHUNKS x 64 rows = MM_THREADS)
             const int c = tid >> 6, r = tid & 63;
-            v4i_t wv = lds_b128(st + OFF_A + c * 1024 + r * 16);
-            lds_wait(wv);
+            v4i_t wv4 = lds_b128(ring[s % MM_RING] + OFF_A + c * 1024 + r * 16);
+            lds_wait(wv4);
             int4 lo, hi;
-            unpack_q4(make_int4(wv[0], wv[1], wv[2], wv[3]), lo, hi);
+            unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
             lds_st128(aun + c * 2048 + r * 32, v4i_t{lo.x, lo.y, lo.z, lo.w});
             lds_st128(aun + c * 2048 + r * 32 + 16, v4i_t{hi.x, hi.y, hi.z, hi.w});
             lds_wait();
             __builtin_amdgcn_s_barrier();
-            As = aun;
+            abase = aun0 + a_lane;
         } else {
-            As = reinterpret_cast<const int8_t*>(st + OFF_A);
+            abase = st + a_lane;
         }
-        const int8_t* Bs = reinterpret_cast<const int8_t*>(st + OFF_B);
-        const _Float16* Asc = reinterpret_cast<const _Float16*>(st + OFF_AS);
-        const float* Bsc = reinterpret_cast<const float*>(st + OFF_BS);
         if (active) {
-#pragma unroll
-            for (int kb = 0; kb < MM_KB; kb++) {
-                const int8_t* ach = As + (sl * MM_KB + kb) * 2048;
-                v4i_t A0 = lds_b128(ach + lr * 32 + 16 * lg);
-                v4i_t A1 = lds_b128(ach + (32 + lr) * 32 + 16 * lg);
-                v4i_t B = lds_b128(Bs + (nq * 32 + lr) * (MM_KB * 32) + kb * 32 + 16 * lg);
-                uint32_t dw0 = lds_u16(Asc + (sl * MM_KB + kb) * 64 + lr);
-                uint32_t dw1 = lds_u16(Asc + (sl * MM_KB + kb) * 64 + 32 + lr);
-                uint32_t dxb = lds_b32(Bsc + (nq * 32 + lr) * MM_KB + kb);
-                lds_wait(A0, A1, B, dw0, dw1, dxb);
-                const v16i_t zero = {};
-                const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
-                const v16i_t S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
-                const _Float16 dx = (_Float16)__builtin_bit_cast(float, dxb);  // exact: an fp16 value
-                const v16f_t C0 = scale_outer(__builtin_bit_cast(_Float16, (uint16_t)dw0), dx, lg);
-                const v16f_t C1 = scale_outer(__builtin_bit_cast(_Float16, (uint16_t)dw1), dx, lg);
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
-                    acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
-                }
-            }
+            [&]<int... KBI>(std::integer_sequence<int, KBI...>) {
+                (block.template operator()<KBI>(st, abase), ...);
+            }(std::make_integer_sequence<int, MM_KB>{});
         }
         // refill: slot (s+2) % 3 was last read in iteration s-1, finished by every
         // wave before this iteration's barrier
