@@ -7,10 +7,11 @@
 // KB GGUF blocks of the ROWS weight rows and of the tile's TOK activation rows
 // straight from global memory into an LDS ring of 3 stages (two in flight while one is
 // consumed).  Two shapes, picked per call from the mean pairs per expert:
-//   wide  (ROWS 128, TOK 128, KB 4): 2 row slabs x 4 token quarters -- more reuse of
-//         each weight byte for large batches;
+//   wide  (ROWS 128, TOK 128, KB 2): 2 row slabs x 4 token quarters -- more reuse of
+//         each weight byte for large batches (two waves share each A chunk's copies);
 //   tall  (ROWS 256, TOK  64, KB 2): 4 row slabs x 2 token halves -- keeps all eight
-//         waves busy when experts see ~64 pairs, two work groups per CU.
+//         waves busy when experts see ~64 pairs.
+// Both fit two work groups per CU.
 // Eight waves; every wave owns 2 x (32 rows x 32 tokens) output tiles and, per
 // 32-wide block, issues
 // v_mfma_i32_32x32x32_i8: K = 32 is exactly one GGUF block, so each MFMA result is the
@@ -64,12 +65,13 @@ struct MmShape {
     // B rows: each wave copies TOK/8 tokens x KB*32 B with 16-byte lanes
     static constexpr int B_LANES = TOK / MM_WAVES * KB * 2;
     static constexpr int B_LOADS = (B_LANES + WAVE - 1) / WAVE;
-    static_assert(CHUNKS == MM_WAVES, "one A chunk per wave per stage");
+    static constexpr int WPC = MM_WAVES / CHUNKS;     // waves sharing one A chunk's copies
+    static_assert(CHUNKS * WPC == MM_WAVES && (WPC == 1 || WPC == 2), "A chunks split evenly over the waves");
     static_assert(TQ * 32 == TOK, "token groups must cover the tile");
     static_assert(B_LANES % WAVE == 0 || B_LOADS == 1, "partial B loads only as a single load");
     static_assert(KB == 4 || KB == 2, "B-scale copy handles 16 B or 8 B per token");
 };
-using ShapeWide = MmShape<128, 128, 4>;
+using ShapeWide = MmShape<128, 128, 2>;
 using ShapeTall = MmShape<256, 64, 2>;
 
 struct MmArgs {
@@ -112,7 +114,7 @@ __device__ __forceinline__ v16f_t scale_outer(_Float16 dw, _Float16 dx, int lg) 
 }
 
 template <int WT, int MODE, class SH>
-__global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_kernel(MmArgs a) {
+__global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     constexpr int MM_ROWS = SH::ROWS, MM_TOK = SH::TOK, MM_KB = SH::KB, MM_SLABS = SH::SLABS;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
     // stage slot: A (int8, or Q4_0 nibbles), B, A scales, B scales, then a zero area
@@ -129,7 +131,9 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
     constexpr int OFF_Z = OFF_BS + SH::ST_BS;
     static_assert(MM_KB * 128 <= ZBYTES, "scale offsets of the upper lanes stay in the zero area");
     // copies per wave per stage (every wave issues the same number; vmcnt counts them)
-    constexpr int LOADS = (Q4 ? 1 : 2) + SH::B_LOADS + 1 + 1;
+    constexpr int WPC = SH::WPC;
+    constexpr int A_LOADS = Q4 ? 1 : 2 / WPC;
+    constexpr int LOADS = A_LOADS + SH::B_LOADS + 1 + 1;
 
     // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
     // all row blocks of a tile the same id mod MM_XCD (they share the tile's
@@ -176,10 +180,14 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
     const int G0 = row0 / 64;
     const int wv = __builtin_amdgcn_readfirstlane(wave);  // wave index as a scalar
     // copy sources: a wave-uniform base (advanced per stage) + a per-lane 32-bit offset
-    // A: chunk c = wave (row group c / KB, block c % KB); Q8_0 2 KB = 2 copies, Q4_0 1 KB
+    // A: chunk c = wave / WPC (row group c / KB, block c % KB) of 64 rows x BPB bytes;
+    // with WPC = 2 each of the chunk's two waves copies one half of it
+    constexpr int CHB = 64 * BPB;  // bytes per chunk
+    const int ch = wv / WPC, half = wv % WPC;
     const uint8_t* a_src = a.W.qs + (size_t)e * a.W.qs_stride +
-                           ((size_t)(G0 + wv / MM_KB) * nb + wv % MM_KB) * 64 * BPB;
-    const uint16_t* as_src = a.W.sc + (size_t)e * a.W.sc_stride + ((size_t)(G0 + wv / MM_KB) * nb + wv % MM_KB) * 64;
+                           ((size_t)(G0 + ch / MM_KB) * nb + ch % MM_KB) * CHB + half * (CHB / WPC);
+    const uint16_t* as_src = a.W.sc + (size_t)e * a.W.sc_stride + ((size_t)(G0 + ch / MM_KB) * nb + ch % MM_KB) * 64 +
+                             half * (64 / WPC);
     // B rows: wave w copies tokens w*TOK/8 .. +TOK/8, KB*32 bytes each, as 16-byte
     // pieces; piece p (copy v, lane l: p = 64 v + l) is token p / (2 KB), offset
     // 16 (p % (2 KB)) -- lane i of a copy lands at +16 i, i.e. tokens stay row-major
@@ -203,12 +211,13 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
     auto issue = [&](int s) {
         uint8_t* st = ring[s % MM_RING];
         const int kb0 = s * MM_KB;
-        const uint8_t* ab = a_src + (size_t)kb0 * 64 * BPB;
-        if (Q4) {
-            g2l16(ab + lane * 16, st + OFF_A + wave * 1024);
+        const uint8_t* ab = a_src + (size_t)kb0 * CHB;
+        uint8_t* ad = st + OFF_A + ch * CHB + half * (CHB / WPC);
+        if (Q4 && WPC == 2) {
+            if (lane < 32) g2l16(ab + lane * 16, ad);  // 512 B
         } else {
-            g2l16(ab + lane * 16, st + OFF_A + wave * 2048);
-            g2l16(ab + 1024 + lane * 16, st + OFF_A + wave * 2048 + 1024);
+#pragma unroll
+            for (int c = 0; c < A_LOADS; c++) g2l16(ab + c * 1024 + lane * 16, ad + c * 1024);
         }
         // B rows of this wave's tokens
         const int8_t* bb = a.aq + (size_t)kb0 * QK;
@@ -216,8 +225,8 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
 #pragma unroll
         for (int v = 0; v < SH::B_LOADS; v++)
             if (v * WAVE + lane < SH::B_LANES) g2l16(bb + b_off[v], bdst + v * 1024);
-        // A scales: chunk `wave` = 64 fp16 = 128 B (lanes 0..7)
-        if (lane < 8) g2l16(as_src + (size_t)kb0 * 64 + lane * 8, st + OFF_AS + wave * 128);
+        // A scales of the chunk: 64 fp16 = 128 B (lanes 0..7), or its half (lanes 0..3)
+        if (lane < 8 / WPC) g2l16(as_src + (size_t)kb0 * 64 + lane * 8, st + OFF_AS + ch * 128 + half * (128 / WPC));
         // B scales of this wave's tokens
         const uint8_t* sb = reinterpret_cast<const uint8_t*>(a.ad + kb0);
         uint8_t* sdst = st + OFF_BS + wave * (MM_TOK / MM_WAVES) * MM_KB * 4;
@@ -295,15 +304,17 @@ __global__ __launch_bounds__(MM_THREADS, (SH::TOK == 64 ? 2 : 1)) void moe_mfma_
         uint32_t abase;
         if (Q4) {
             // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of
-            // chunk t/64 (CHUNKS x 64 rows = MM_THREADS)
-            const int c = tid >> 6, r = tid & 63;
-            v4i_t wv4 = lds_b128(ring[s % MM_RING] + OFF_A + c * 1024 + r * 16);
-            lds_wait(wv4);
-            int4 lo, hi;
-            unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
-            lds_st128(aun + c * 2048 + r * 32, v4i_t{lo.x, lo.y, lo.z, lo.w});
-            lds_st128(aun + c * 2048 + r * 32 + 16, v4i_t{hi.x, hi.y, hi.z, hi.w});
-            lds_wait();
+            // chunk t/64 (CHUNKS x 64 rows <= MM_THREADS)
+            if (tid < SH::CHUNKS * 64) {
+                const int c = tid >> 6, r = tid & 63;
+                v4i_t wv4 = lds_b128(ring[s % MM_RING] + OFF_A + c * 1024 + r * 16);
+                lds_wait(wv4);
+                int4 lo, hi;
+                unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
+                lds_st128(aun + c * 2048 + r * 32, v4i_t{lo.x, lo.y, lo.z, lo.w});
+                lds_st128(aun + c * 2048 + r * 32 + 16, v4i_t{hi.x, hi.y, hi.z, hi.w});
+                lds_wait();
+            }
             __builtin_amdgcn_s_barrier();
             abase = aun0 + a_lane;
         } else {
