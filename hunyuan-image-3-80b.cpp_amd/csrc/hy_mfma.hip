@@ -221,7 +221,7 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
         }
         // B rows of this wave's tokens
         const int8_t* bb = a.aq + (size_t)kb0 * QK;
-        uint8_t* bdst = st + OFF_B + wave * (MM_TOK / MM_WAVES) * (MM_KB * 32);
+        uint8_t* bdst = st + OFF_B + wv * (MM_TOK / MM_WAVES) * (MM_KB * 32);
 #pragma unroll
         for (int v = 0; v < SH::B_LOADS; v++)
             if (v * WAVE + lane < SH::B_LANES) g2l16(bb + b_off[v], bdst + v * 1024);
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
         if (lane < 8 / WPC) g2l16(as_src + (size_t)kb0 * 64 + lane * 8, st + OFF_AS + ch * 128 + half * (128 / WPC));
         // B scales of this wave's tokens
         const uint8_t* sb = reinterpret_cast<const uint8_t*>(a.ad + kb0);
-        uint8_t* sdst = st + OFF_BS + wave * (MM_TOK / MM_WAVES) * MM_KB * 4;
+        uint8_t* sdst = st + OFF_BS + wv * (MM_TOK / MM_WAVES) * MM_KB * 4;
         if (lane < BS_LANES) {
             if (MM_KB == 4)
                 g2l16(sb + bs_off, sdst);
@@ -259,6 +259,8 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 + lr) * MM_KB * 4 : OFF_Z);
     const uint32_t ring0 = lds_off(ring[0]);
     const uint32_t aun0 = lds_off(aun);
+    // rank-1 operands {d, 0, 0, ...}: only element 0 changes, the zeros stay in place
+    v4i_t xa0 = {0, 0, 0, 0}, xa1 = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
 
     // one 32-wide block kb of the stage whose slot starts at st
     auto block = [&]<int KBI>(uint32_t st, uint32_t abase) {
@@ -272,11 +274,11 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
         const v16i_t zero = {};
         const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
         const v16i_t S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
-        // rank-1 operands {d, 0, 0, ...}: the upper lanes hold zeros already; d_x is an
-        // fp16 value stored as f32, so the truncating pack is exact
-        const v4i_t xa0 = {(int)dw0, 0, 0, 0}, xa1 = {(int)dw1, 0, 0, 0};
-        const v4i_t xb = {__builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, dxb), 0.0f)), 0,
-                          0, 0};
+        // the upper lanes read zeros; d_x is an fp16 value stored as f32, so the
+        // truncating pack is exact
+        xa0[0] = (int)dw0;
+        xa1[0] = (int)dw1;
+        xb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, dxb), 0.0f));
         const v16f_t zf = {};
         const v16f_t C0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa0),
                                                                  __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
