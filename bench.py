@@ -80,19 +80,17 @@ def kernel_traffic(kname, wtype, T, D, shared=True):
     if kname == "ffn_up":
         return n_exp * 2 * I * H * wb + T * H * act_b + (T * K + T) * I * act_b
     if kname == "ffn_down":
-        return D * H * I * wb + T * K * I * act_b + T * K * H * 4
-    if kname == "ffn_down_shared_combine":
-        return H * I * wb + T * I * act_b + T * K * H * 4 + T * H * 4
+        return n_exp * H * I * wb + (T * K + T) * I * act_b + (T * K + T) * H * 4
+    if kname == "combine":
+        return T * (K + 1) * H * 4 + T * H * 4 * 2
     return 0.0
 
 
 def kernel_ops(kname, T):
     if kname == "ffn_up":
         return 2.0 * T * (K + 1) * 2 * I * H
-    if kname in ("ffn_down",):
-        return 2.0 * T * K * H * I
-    if kname == "ffn_down_shared_combine":
-        return 2.0 * T * H * I
+    if kname == "ffn_down":
+        return 2.0 * T * (K + 1) * H * I
     return 0.0
 
 

@@ -118,7 +118,7 @@ struct hy_moe_ctx {
 namespace {
 
 const char* kKernelNames[hy::KID_COUNT] = {"quant_q8_0", "router", "dispatch", "ffn_up",
-                                           "ffn_down",   "ffn_down_shared_combine", "combine", "rms_norm"};
+                                           "ffn_down",   "combine", "rms_norm"};
 
 int get_event(hy_moe_ctx* c, hipEvent_t* ev) {
     if (!c->pool.empty()) {
@@ -281,19 +281,15 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
             return hy::launch_ffn_up_mfma(wt, NT, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
                                           c->hd, c->hs, s);
         }));
+        // routed and shared down products in one launch (y rows for every slot), then
+        // the combine
         HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
-            return hy::launch_ffn_down_mfma(wt, NT, routed_bound, 0, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
-                                            c->y, nullptr, nullptr, s);
+            return hy::launch_ffn_down_mfma(wt, NT, routed_bound + shared_tiles, dn_view(c, L), R, c->hq, c->hd, iT, H,
+                                            I, E, K, c->y, s);
         }));
-        if (has_shared)
-            HY_TRY(timed(c, hy::KID_DOWN_SHARED, s, [&] {
-                return hy::launch_ffn_down_mfma(wt, NT, shared_tiles, 1, dn_view(c, L), R, c->hq, c->hd, iT, H, I, E, K,
-                                                c->y, resid, out, s);
-            }));
-        else
-            HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {
-                return hy::launch_combine(R, c->y, iT, H, K, 0, resid, out, s);
-            }));
+        HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {
+            return hy::launch_combine(R, c->y, iT, H, K, has_shared, resid, out, s);
+        }));
         return HY_OK;
     }
     HY_TRY(timed(c, hy::KID_UP, s, [&] {

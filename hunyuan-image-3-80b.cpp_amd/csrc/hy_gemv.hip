@@ -482,17 +482,31 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 }
 
 // combine: out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e y_e[t] ), the
-// shared expert's output at slot T*K + t when has_shared
+// shared expert's output at slot T*K + t when has_shared.  One thread per 4 outputs
+// (16-byte loads of the y rows); each output keeps the scalar fmaf order.
 __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __restrict__ y, int T, int H, int K,
                                                       int has_shared, const float* __restrict__ resid,
                                                       float* __restrict__ out) {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)T * H) return;
-    const int t = (int)(idx / H), row = (int)(idx % H);
-    float comb = 0.0f;
-    for (int k = 0; k < K; k++) comb = fmaf(R.comb_w[t * K + k], y[(size_t)R.comb_pos[t * K + k] * H + row], comb);
-    const float o = has_shared ? y[((size_t)T * K + t) * H + row] + comb : comb;
-    out[idx] = resid ? resid[idx] + o : o;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 4 outputs
+    const int H4 = H / 4;
+    if (idx >= (size_t)T * H4) return;
+    const int t = (int)(idx / H4), r4 = (int)(idx % H4);
+    float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < K; k++) {
+        const float w = R.comb_w[t * K + k];
+        const float4 v = reinterpret_cast<const float4*>(y + (size_t)R.comb_pos[t * K + k] * H)[r4];
+        c = make_float4(fmaf(w, v.x, c.x), fmaf(w, v.y, c.y), fmaf(w, v.z, c.z), fmaf(w, v.w, c.w));
+    }
+    float4 o = c;
+    if (has_shared) {
+        const float4 v = reinterpret_cast<const float4*>(y + ((size_t)T * K + t) * H)[r4];
+        o = make_float4(v.x + c.x, v.y + c.y, v.z + c.z, v.w + c.w);
+    }
+    if (resid) {
+        const float4 q = reinterpret_cast<const float4*>(resid + (size_t)t * H)[r4];
+        o = make_float4(q.x + o.x, q.y + o.y, q.z + o.z, q.w + o.w);
+    }
+    reinterpret_cast<float4*>(out + (size_t)t * H)[r4] = o;
 }
 
 // ---------------------------------------------------------------------------- launchers
@@ -562,7 +576,7 @@ hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatVie
 
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,
                           float* out, hipStream_t s) {
-    const size_t n = (size_t)T * H;
+    const size_t n = (size_t)T * (H / 4);
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, y, T, H, K, has_shared,
                        resid, out);
     return hipGetLastError();

@@ -53,9 +53,9 @@ int mfma_tile_tokens(int T, int K, int E, int H, int I);
 hipError_t launch_ffn_up_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
                               const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
                               hipStream_t s);
-hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, int mode, const MatView& W,
-                                const Routing& R, const int8_t* hq, const float* hd, int T, int H, int I, int E,
-                                int K, float* y, const float* resid, float* out, hipStream_t s);
+hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+                                const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
+                                hipStream_t s);
 
 // residency (hy_data.hip)
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
@@ -81,7 +81,6 @@ enum KernelId {
     KID_DISPATCH,
     KID_UP,
     KID_DOWN,
-    KID_DOWN_SHARED,
     KID_COMBINE,
     KID_RMSNORM,
     KID_COUNT

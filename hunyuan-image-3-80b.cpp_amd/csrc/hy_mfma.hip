@@ -28,8 +28,8 @@
 //
 // Modes: 0 = gate_up (packed rows: every 64-row slab holds 32 SiLU rows and the 32
 // matching linear rows; epilogue h = silu(g) * u and Q8_0 quantization of h per token and
-// slab); 1 = down for routed tiles (writes y[pair][row]); 2 = down for shared tiles
-// fused with the combine out = resid + (y_shared + sum_{e ascending} w_e y_e).
+// slab); 1 = down for every tile, routed and shared (writes y[slot][row]; the combine
+// kernel then forms out = resid + (y_shared + sum_{e ascending} w_e y_e)).
 #include <utility>
 
 #include "hy_device.hpp"
@@ -86,9 +86,7 @@ struct MmArgs {
     int8_t* hq;         // mode 0 outputs
     float* hd;
     int* hs;
-    float* y;           // mode 1 output / mode 2 input
-    const float* resid; // mode 2
-    float* out;         // mode 2
+    float* y;           // mode 1 output
 };
 
 // Q4_0 nibbles (16 bytes, GGUF order) -> 32 int8 values n-8 in element order.
@@ -144,8 +142,8 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     const int xcd = id % MM_XCD, local = id / MM_XCD;
     const int tile_rel = xcd + MM_XCD * (local / a.nrb);
     const int rb = local % a.nrb;
-    const int tile = (MODE == 2) ? a.R.meta[0] + tile_rel : tile_rel;
-    if (tile >= a.R.meta[MODE == 1 ? 0 : 1]) return;
+    const int tile = tile_rel;
+    if (tile >= a.R.meta[1]) return;
     const int e = a.R.tile_e[tile];
     const int start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
@@ -373,60 +371,14 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
         }
     } else {
         const int rbase = row0 + sl * 64;
-        if (MODE == 1) {
-            float* yr = a.y + (size_t)slot_s[j] * a.H;
+        float* yr = a.y + (size_t)slot_s[j] * a.H;
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int r = 8 * g + 4 * lg;
-                *reinterpret_cast<float4*>(yr + rbase + r) =
-                    make_float4(acc0[4 * g], acc0[4 * g + 1], acc0[4 * g + 2], acc0[4 * g + 3]);
-                *reinterpret_cast<float4*>(yr + rbase + 32 + r) =
-                    make_float4(acc1[4 * g], acc1[4 * g + 1], acc1[4 * g + 2], acc1[4 * g + 3]);
-            }
-        } else {
-            const int t = tok_s[j];
-            float o0[16], o1[16];
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                o0[v] = 0.0f;
-                o1[v] = 0.0f;
-            }
-            for (int k = 0; k < a.K; k++) {
-                const float w = a.R.comb_w[t * a.K + k];
-                const float* yr = a.y + (size_t)a.R.comb_pos[t * a.K + k] * a.H + rbase;
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int r = 8 * g + 4 * lg;
-                    const float4 y0 = *reinterpret_cast<const float4*>(yr + r);
-                    const float4 y1 = *reinterpret_cast<const float4*>(yr + 32 + r);
-                    o0[4 * g] = fmaf(w, y0.x, o0[4 * g]);
-                    o0[4 * g + 1] = fmaf(w, y0.y, o0[4 * g + 1]);
-                    o0[4 * g + 2] = fmaf(w, y0.z, o0[4 * g + 2]);
-                    o0[4 * g + 3] = fmaf(w, y0.w, o0[4 * g + 3]);
-                    o1[4 * g] = fmaf(w, y1.x, o1[4 * g]);
-                    o1[4 * g + 1] = fmaf(w, y1.y, o1[4 * g + 1]);
-                    o1[4 * g + 2] = fmaf(w, y1.z, o1[4 * g + 2]);
-                    o1[4 * g + 3] = fmaf(w, y1.w, o1[4 * g + 3]);
-                }
-            }
-            float* orow = a.out + (size_t)t * a.H + rbase;
-            const float* rrow = a.resid ? a.resid + (size_t)t * a.H + rbase : nullptr;
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int r = 8 * g + 4 * lg;
-                float4 v0 = make_float4(acc0[4 * g] + o0[4 * g], acc0[4 * g + 1] + o0[4 * g + 1],
-                                        acc0[4 * g + 2] + o0[4 * g + 2], acc0[4 * g + 3] + o0[4 * g + 3]);
-                float4 v1 = make_float4(acc1[4 * g] + o1[4 * g], acc1[4 * g + 1] + o1[4 * g + 1],
-                                        acc1[4 * g + 2] + o1[4 * g + 2], acc1[4 * g + 3] + o1[4 * g + 3]);
-                if (rrow) {
-                    const float4 q0 = *reinterpret_cast<const float4*>(rrow + r);
-                    const float4 q1 = *reinterpret_cast<const float4*>(rrow + 32 + r);
-                    v0 = make_float4(q0.x + v0.x, q0.y + v0.y, q0.z + v0.z, q0.w + v0.w);
-                    v1 = make_float4(q1.x + v1.x, q1.y + v1.y, q1.z + v1.z, q1.w + v1.w);
-                }
-                *reinterpret_cast<float4*>(orow + r) = v0;
-                *reinterpret_cast<float4*>(orow + 32 + r) = v1;
-            }
+        for (int g = 0; g < 4; g++) {
+            const int r = 8 * g + 4 * lg;
+            *reinterpret_cast<float4*>(yr + rbase + r) =
+                make_float4(acc0[4 * g], acc0[4 * g + 1], acc0[4 * g + 2], acc0[4 * g + 3]);
+            *reinterpret_cast<float4*>(yr + rbase + 32 + r) =
+                make_float4(acc1[4 * g], acc1[4 * g + 1], acc1[4 * g + 2], acc1[4 * g + 3]);
         }
     }
 }
@@ -469,16 +421,15 @@ int mfma_tile_tokens(int T, int K, int E, int H, int I) {
 hipError_t launch_ffn_up_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
                               const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
                               hipStream_t s) {
-    MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr, nullptr, nullptr};
+    MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr};
     return launch_shape<0>(wtype, tile_tokens, a, n_tiles_bound, 2 * I, s);
 }
 
-hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, int mode, const MatView& W,
-                                const Routing& R, const int8_t* hq, const float* hd, int T, int H, int I, int E,
-                                int K, float* y, const float* resid, float* out, hipStream_t s) {
-    MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y, resid, out};
-    return mode == 0 ? launch_shape<1>(wtype, tile_tokens, a, n_tiles_bound, H, s)
-                     : launch_shape<2>(wtype, tile_tokens, a, n_tiles_bound, H, s);
+hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+                                const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
+                                hipStream_t s) {
+    MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y};
+    return launch_shape<1>(wtype, tile_tokens, a, n_tiles_bound, H, s);
 }
 
 }  // namespace hy
