@@ -231,9 +231,58 @@ __global__ __launch_bounds__(256) void quant_q8_0_kernel(const float* __restrict
     quant_q8_0_elem(x, n, (size_t)blockIdx.x * blockDim.x + threadIdx.x, q, d, qsum, blocks);
 }
 
+// The same quantizer for the activation planes only (no GGUF blocks), 8 elements per
+// lane: a 32-block is 4 lanes (max and sum over 2 xor steps).  max and the int sum
+// are order-free, and each element takes the same operations, so the bytes equal
+// quant_q8_0_elem's.
+__global__ __launch_bounds__(256) void quant_q8_0_vec_kernel(const float* __restrict__ x, size_t n8,
+                                                             int8_t* __restrict__ q, float* __restrict__ d,
+                                                             int* __restrict__ qsum) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 8 elements
+    const bool live = i < n8;  // n8 is a multiple of 4: a block's 4 lanes are all live or all dead
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (live) {
+        v0 = reinterpret_cast<const float4*>(x)[2 * i];
+        v1 = reinterpret_cast<const float4*>(x)[2 * i + 1];
+    }
+    const float xs[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(xs[j]));
+    amax = fmaxf(amax, shfl_xor(amax, 1, 4));
+    amax = fmaxf(amax, shfl_xor(amax, 2, 4));
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    int sum = 0;
+    uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int qv = (int)__builtin_roundf(xs[j] * id);
+        sum += qv;
+        if (j < 4)
+            p0 |= ((uint32_t)(qv & 0xff)) << (8 * j);
+        else
+            p1 |= ((uint32_t)(qv & 0xff)) << (8 * (j - 4));
+    }
+    sum += shfl_xor(sum, 1, 4);
+    sum += shfl_xor(sum, 2, 4);
+    if (!live) return;
+    reinterpret_cast<uint2*>(q)[i] = make_uint2(p0, p1);
+    if ((i & 3) == 0) {
+        d[i / 4] = h2f(f2h(dd));
+        qsum[i / 4] = sum;
+    }
+}
+
 hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
                              hipStream_t s) {
     if (n == 0) return hipSuccess;
+    if (!blocks && q && d && qsum) {
+        const size_t n8 = n / 8;
+        hipLaunchKernelGGL(quant_q8_0_vec_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, x, n8, q, d,
+                           qsum);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(quant_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, q, d, qsum,
                        blocks);
     return hipGetLastError();
