@@ -13,6 +13,7 @@ c4 Q4_0 T=4096 Zipf-skewed routing, c5 32-layer Q8_0 stack T=4096.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
     python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
+    python bench.py --gguf-load /tmp/l.gguf [--config c2]   # layer load from a GGUF file
 
 roofline.traffic (HBM bytes per launch of the dominant kernel) is read from
 profiles/hbm_traffic.md, the table made from rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -135,6 +136,34 @@ def copy_probe(hy, mib, steps):
                       "GBps_read_plus_write": 2 * n / t / 1e9}), flush=True)
 
 
+def gguf_load(hy, wtype, path, seed=42):
+    """Write one real-shape layer (H=4096, I=3072, 64 + 1 experts) as a GGUF file with
+    the reference converter's tensor names, then time hy_gguf_open + the upload into
+    the resident tables (page-cache reads, host->device copies, on-device repack)."""
+    import hy_oracle as O
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_io as G
+    layer = O.synth_layer(H, I, E, K, wtype, seed=seed, std=0.02)
+    blob_ts = G.layer_tensors(layer, 0)
+    with open(path, "wb") as f:
+        f.write(G.gguf_bytes(G.layer_meta(layer), blob_ts))
+    size = os.path.getsize(path)
+    m = hy.Moe(H, I, E, K, wtype, num_layers=1, max_tokens=8)
+    t0 = time.perf_counter()
+    g = hy.Gguf(path)
+    m.upload_gguf(0, g, 0)
+    hy.sync()
+    dt = time.perf_counter() - t0
+    # one forward checked against the oracle on the loaded weights
+    x = O.synth(seed + 1, 0, O.T_X, 0, (2, H), 1.0)
+    same = bool(np.array_equal(m.run(0, x).view(np.uint32), O.moe_forward_q(layer, x).view(np.uint32)))
+    g.close()
+    m.close()
+    os.remove(path)
+    print(json.dumps({"probe": "gguf_load", "weights": {0: "F32", 2: "Q4_0", 8: "Q8_0"}[wtype], "file_bytes": size,
+                      "seconds": dt, "GBps": size / dt / 1e9, "forward_bit_exact": same}), flush=True)
+
+
 def cpu_baseline(wl, seed, budget_s=15.0):
     """The oracle's q-semantics layer (int8 block dots, OpenMP over all host
     threads) on a bounded token sample of the same workload."""
@@ -170,6 +199,8 @@ def main():
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
+    ap.add_argument("--gguf-load", default=None, metavar="PATH",
+                    help="time loading one real-shape layer from a GGUF file written at PATH")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): this build has no multi-GPU path; "
@@ -181,6 +212,9 @@ def main():
         sys.exit("no HIP device visible")
     if a.copy_probe:
         copy_probe(hy, a.copy_probe, a.steps)
+        return
+    if a.gguf_load:
+        gguf_load(hy, WORKLOADS[a.config]["wtype"], a.gguf_load, a.seed)
         return
     wl = dict(WORKLOADS[a.config])
     if a.tokens:

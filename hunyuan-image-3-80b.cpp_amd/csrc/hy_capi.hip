@@ -13,6 +13,7 @@
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_layout.hpp"
+#include "../host/hy_gguf.hpp"
 
 namespace {
 
@@ -313,6 +314,14 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
 
 }  // namespace
 
+namespace hy {
+int set_last_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+const GgufFile& gguf_file(const hy_gguf* g);  // host/hy_gguf.cpp
+}  // namespace hy
+
 // =====================================================================================
 extern "C" {
 
@@ -403,12 +412,14 @@ int hy_moe_destroy(hy_moe_ctx* c) {
 
 size_t hy_moe_layer_bytes(const hy_moe_ctx* c) { return c ? c->layer_bytes : 0; }
 
-int hy_moe_upload_layer(hy_moe_ctx* c, uint32_t layer, const float* router, const void* sgu, const void* sdn,
-                        const void* gu, const void* dn) {
-    if (!c) return fail(HY_ERR_INVALID, "null ctx");
-    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
-    if (!router || !gu || !dn) return fail(HY_ERR_INVALID, "null router/gu/dn");
-    if (c->cfg.has_shared && (!sgu || !sdn)) return fail(HY_ERR_INVALID, "config has a shared expert: pass it");
+extern "C++" {
+namespace {
+
+// Upload one layer: the router (f32 [E][H]) and, for every resident matrix e
+// (routed experts, then the shared one), gate_up [2I][H] and down [H][I] in ggml
+// layout from host memory; each is staged on the device and repacked.
+template <class GU, class DN>
+int upload_layer(hy_moe_ctx* c, uint32_t layer, const float* router, GU gu_of, DN dn_of) {
     HIP_TRY(hipSetDevice(c->cfg.device));
     LayerW& L = c->layers[layer];
     HY_TRY(alloc_layer(c, L));
@@ -424,14 +435,10 @@ int hy_moe_upload_layer(hy_moe_ctx* c, uint32_t layer, const float* router, cons
         return HY_OK;
     };
     for (int e = 0; e < c->X && rc == HY_OK; e++) {
-        const uint8_t* gsrc = e < E ? static_cast<const uint8_t*>(gu) + (size_t)e * gu_b
-                                    : static_cast<const uint8_t*>(sgu);
-        const uint8_t* dsrc = e < E ? static_cast<const uint8_t*>(dn) + (size_t)e * dn_b
-                                    : static_cast<const uint8_t*>(sdn);
-        rc = up(gsrc, gu_b, 2 * I, H, I, L.gu_qs + (size_t)e * c->gu_qs_stride,
+        rc = up(gu_of(e), gu_b, 2 * I, H, I, L.gu_qs + (size_t)e * c->gu_qs_stride,
                 L.gu_sc ? L.gu_sc + (size_t)e * c->gu_sc_stride : nullptr);
         if (rc == HY_OK)
-            rc = up(dsrc, dn_b, H, I, 0, L.dn_qs + (size_t)e * c->dn_qs_stride,
+            rc = up(dn_of(e), dn_b, H, I, 0, L.dn_qs + (size_t)e * c->dn_qs_stride,
                     L.dn_sc ? L.dn_sc + (size_t)e * c->dn_sc_stride : nullptr);
     }
     if (rc == HY_OK && hipMemcpy(L.router, router, (size_t)E * H * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -440,6 +447,69 @@ int hy_moe_upload_layer(hy_moe_ctx* c, uint32_t layer, const float* router, cons
     (void)hipFree(staging);
     if (rc == HY_OK) L.loaded = true;
     return rc;
+}
+
+}  // namespace
+}  // extern "C++"
+
+int hy_moe_upload_layer(hy_moe_ctx* c, uint32_t layer, const float* router, const void* sgu, const void* sdn,
+                        const void* gu, const void* dn) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    if (!router || !gu || !dn) return fail(HY_ERR_INVALID, "null router/gu/dn");
+    if (c->cfg.has_shared && (!sgu || !sdn)) return fail(HY_ERR_INVALID, "config has a shared expert: pass it");
+    const int wt = c->cfg.wtype, H = c->H, I = c->I, E = c->E;
+    const size_t gu_b = gguf_row_bytes(wt, H) * 2 * I, dn_b = gguf_row_bytes(wt, I) * H;
+    return upload_layer(
+        c, layer, router,
+        [&](int e) -> const void* { return e < E ? static_cast<const uint8_t*>(gu) + (size_t)e * gu_b : sgu; },
+        [&](int e) -> const void* { return e < E ? static_cast<const uint8_t*>(dn) + (size_t)e * dn_b : sdn; });
+}
+
+int hy_moe_upload_layer_gguf(hy_moe_ctx* c, uint32_t layer, const hy_gguf* g, uint32_t block) {
+    if (!c || !g) return fail(HY_ERR_INVALID, "null ctx/file");
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    const hy::GgufFile& f = hy::gguf_file(g);
+    const int wt = c->cfg.wtype, H = c->H, I = c->I, E = c->E;
+    // metadata the converter writes, when present, must describe this context
+    const struct {
+        const char* key;
+        uint32_t want;
+    } meta[] = {{"hunyuan.hidden_size", (uint32_t)H},
+                {"hunyuan.moe_intermediate_size", (uint32_t)I},
+                {"hunyuan.num_experts", (uint32_t)E},
+                {"hunyuan.moe_topk", (uint32_t)c->K}};
+    for (const auto& m : meta) {
+        const hy::GgufValue* v = f.kv(m.key);
+        if (v && (v->type == hy::GGUF_U32 || v->type == hy::GGUF_U64) && v->u != m.want)
+            return fail(HY_ERR_INVALID, "%s = %llu in the file, the context has %u", m.key, (unsigned long long)v->u,
+                        m.want);
+    }
+    // every tensor first: nothing is uploaded from an incomplete or mismatched file
+    auto need = [&](const std::string& name, int type, uint64_t ne0, uint64_t ne1, const uint8_t** data) -> int {
+        const hy::GgufTensor* t = f.find(name);
+        if (!t) return fail(HY_ERR_INVALID, "GGUF file has no tensor %s", name.c_str());
+        if (t->type != type)
+            return fail(HY_ERR_INVALID, "%s has ggml type %d, the context wants %d", name.c_str(), t->type, type);
+        if (t->n_dims != 2 || t->ne[0] != ne0 || t->ne[1] != ne1)
+            return fail(HY_ERR_INVALID, "%s has shape [%llu, %llu], the context wants [%llu, %llu]", name.c_str(),
+                        (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)ne0,
+                        (unsigned long long)ne1);
+        *data = t->data;
+        return HY_OK;
+    };
+    const std::string pfx = "blk." + std::to_string(block) + ".";
+    const uint8_t* router = nullptr;
+    HY_TRY(need(pfx + "ffn_gate.weight", HY_TYPE_F32, (uint64_t)H, (uint64_t)E, &router));
+    std::vector<const uint8_t*> gus(c->X), dns(c->X);
+    for (int e = 0; e < c->X; e++) {
+        const std::string base = e < E ? pfx + "ffn_expert_" + std::to_string(e) + "_" : pfx + "ffn_shared_";
+        HY_TRY(need(base + "gate_up.weight", wt, (uint64_t)H, (uint64_t)2 * I, &gus[e]));
+        HY_TRY(need(base + "down.weight", wt, (uint64_t)I, (uint64_t)H, &dns[e]));
+    }
+    return upload_layer(
+        c, layer, reinterpret_cast<const float*>(router), [&](int e) -> const void* { return gus[e]; },
+        [&](int e) -> const void* { return dns[e]; });
 }
 
 int hy_moe_synth_layer(hy_moe_ctx* c, uint32_t layer, uint64_t seed, float std, const float* bias) {

@@ -64,6 +64,14 @@ _SIGS = {
     "hy_memcpy_d2h": (C.c_int, [_vp, _vp, C.c_size_t]),
     "hy_memset": (C.c_int, [_vp, C.c_int, C.c_size_t]),
     "hy_copy_d2d": (C.c_int, [_vp, _vp, C.c_size_t, _vp]),
+    "hy_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "hy_gguf_close": (C.c_int, [_vp]),
+    "hy_gguf_n_tensors": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
+    "hy_gguf_tensor": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int32), C.POINTER(C.c_uint32),
+                                 C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(_vp)]),
+    "hy_gguf_get_u32": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "hy_gguf_get_f32": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_float)]),
+    "hy_moe_upload_layer_gguf": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint32]),
     "hy_dispatch_pairs": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]),
     "hy_device_synchronize": (C.c_int, []),
     "hy_stream_create": (C.c_int, [C.POINTER(_vp)]),
@@ -210,6 +218,10 @@ class Moe:
                                         p(layer.gu), p(layer.dn)))
         del keep
 
+    def upload_gguf(self, layer_idx, gguf, block):
+        """Upload layer layer_idx from block `block` of an open Gguf file."""
+        check(lib().hy_moe_upload_layer_gguf(self.h, layer_idx, gguf.h, block))
+
     def synth(self, layer_idx, seed=42, std=0.02, router_bias=None):
         b = None
         if router_bias is not None:
@@ -337,3 +349,46 @@ def header_symbols(path=HEADER):
     txt = open(path).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(hy_[a-z_0-9]+)\s*\(", txt, flags=re.M)))
+
+
+class Gguf:
+    """A GGUF file opened by the library's reader (memory mapped)."""
+
+    def __init__(self, path):
+        h = _vp()
+        check(lib().hy_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h.value
+
+    def n_tensors(self):
+        n = C.c_uint64()
+        check(lib().hy_gguf_n_tensors(self.h, C.byref(n)))
+        return n.value
+
+    def tensor(self, name):
+        """(ggml_type, n_dims, ne[4], nbytes, bytes or None)"""
+        t, nd, nb, d = C.c_int32(), C.c_uint32(), C.c_uint64(), _vp()
+        ne = (C.c_uint64 * 4)()
+        check(lib().hy_gguf_tensor(self.h, name.encode(), C.byref(t), C.byref(nd), ne, C.byref(nb), C.byref(d)))
+        data = C.string_at(d.value, nb.value) if d.value else None
+        return t.value, nd.value, list(ne), nb.value, data
+
+    def get_u32(self, key):
+        v = C.c_uint32()
+        check(lib().hy_gguf_get_u32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_f32(self, key):
+        v = C.c_float()
+        check(lib().hy_gguf_get_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def close(self):
+        if self.h:
+            lib().hy_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

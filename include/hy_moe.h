@@ -92,6 +92,40 @@ int hy_moe_upload_layer(hy_moe_ctx* ctx, uint32_t layer, const float* router_hos
 int hy_moe_synth_layer(hy_moe_ctx* ctx, uint32_t layer, uint64_t seed, float std,
                        const float* router_bias_host);
 
+/* ---- GGUF files ------------------------------------------------------------ */
+
+/* A GGUF file (format versions 2 and 3), memory mapped read-only.  Replaces the
+ * gguf_* use of HunyuanGGUFLoader::open_layer / load_tensor
+ * (src/hunyuan_gguf_loader.cpp:84-190) for the MoE tensors; tensor data is handed
+ * out as the file's bytes (no dequantization). */
+typedef struct hy_gguf hy_gguf;
+int hy_gguf_open(const char* path, hy_gguf** out);
+int hy_gguf_close(hy_gguf* f);
+int hy_gguf_n_tensors(const hy_gguf* f, uint64_t* n);
+/* Tensor by name: ggml type, dims (ne[0] innermost, unused dims 1), byte size and a
+ * host pointer into the mapping (nbytes 0 and data NULL for a type the reader does
+ * not size).  Any output may be NULL. */
+int hy_gguf_tensor(const hy_gguf* f, const char* name, int32_t* ggml_type, uint32_t* n_dims, uint64_t* ne4,
+                   uint64_t* nbytes, const void** data);
+/* Metadata (HunyuanGGUFLoader::get_metadata_u32 / _f32, src/hunyuan_gguf_loader.cpp:286-297),
+ * but a missing key or a value of another type is an error instead of a default. */
+int hy_gguf_get_u32(const hy_gguf* f, const char* key, uint32_t* out);
+int hy_gguf_get_f32(const hy_gguf* f, const char* key, float* out);
+
+/* Upload layer `layer` of the context from block `block` of a GGUF file with the
+ * tensor names the reference's converter writes and its loader reads
+ * (scripts/convert_to_gguf.py:70-137, src/hunyuan_gguf_loader.cpp:229-280):
+ *   blk.N.ffn_gate.weight                  f32    ne {H, E}   (router)
+ *   blk.N.ffn_shared_gate_up.weight        wtype  ne {H, 2I}
+ *   blk.N.ffn_shared_down.weight           wtype  ne {I, H}
+ *   blk.N.ffn_expert_<e>_gate_up.weight    wtype  ne {H, 2I}, e = 0..E-1
+ *   blk.N.ffn_expert_<e>_down.weight       wtype  ne {I, H}
+ * Types and shapes must match the context (else HY_ERR_INVALID naming the tensor);
+ * hunyuan.hidden_size / moe_intermediate_size / num_experts / moe_topk, when present,
+ * must agree with it too.  Replaces load_layer_weights + StackedExpertWeights
+ * (src/hunyuan_extended.cpp:8-26): the blocks are repacked on the device once. */
+int hy_moe_upload_layer_gguf(hy_moe_ctx* ctx, uint32_t layer, const hy_gguf* f, uint32_t block);
+
 /* ---- forward ------------------------------------------------------------- */
 
 /* One MoE layer: out = shared(x) + sum_k w_k expert_k(x).

@@ -1,0 +1,177 @@
+"""GGUF reader (host code, runs without a GPU) and layer upload from GGUF files (GPU).
+
+The files are written by tests/gguf_io.py from the public GGUF layout; the reader
+must give back exactly the bytes, dims, types and metadata written, reject corrupt
+files with an error, and the layer uploaded from a file must compute bit for bit
+what the oracle computes from the same weights."""
+import struct
+
+import numpy as np
+import pytest
+
+import gguf_io as G
+import hy_oracle as O
+
+
+def _write(tmp_path, name, blob):
+    p = tmp_path / name
+    p.write_bytes(blob)
+    return str(p)
+
+
+def _tensors(rng):
+    f32 = rng.standard_normal((3, 40)).astype(np.float32)
+    f16 = rng.standard_normal((2, 64)).astype(np.float16)
+    q8 = rng.integers(0, 256, size=(5, 2 * 34), dtype=np.uint8)    # 5 rows x 64 elements
+    q4 = rng.integers(0, 256, size=(4, 3 * 18), dtype=np.uint8)    # 4 rows x 96 elements
+    return [("a.f32", G.GGML_F32, [40, 3], f32.tobytes()),
+            ("b.f16", G.GGML_F16, [64, 2], f16.tobytes()),
+            ("c.q8_0", G.GGML_Q8_0, [64, 5], q8.tobytes()),
+            ("d.q4_0", G.GGML_Q4_0, [96, 2, 2], q4.tobytes()),
+            ("e.unknown", 12, [256, 1], b"\x01" * 144)]
+
+
+KVS = [("k.u8", G.T_U8, 200), ("k.i8", G.T_I8, -5), ("k.u16", G.T_U16, 60000), ("k.i32", G.T_I32, 7),
+       ("k.u32", G.T_U32, 4096), ("k.u64", G.T_U64, 123456789), ("k.f32", G.T_F32, 0.25),
+       ("k.f64", G.T_F64, 1.5), ("k.bool", G.T_BOOL, True), ("k.str", G.T_STR, "hunyuan3"),
+       ("k.arr", G.T_ARR, (G.T_U32, [1, 2, 3])), ("k.sarr", G.T_ARR, (G.T_STR, ["x", "yz"])),
+       ("k.neg", G.T_I32, -1)]
+
+
+@pytest.mark.parametrize("version,alignment", [(3, None), (3, 64), (2, None), (3, 256)])
+def test_roundtrip(hy, tmp_path, version, alignment):
+    rng = np.random.default_rng(version * 1000 + (alignment or 0))
+    ts = _tensors(rng)
+    path = _write(tmp_path, "t.gguf", G.gguf_bytes(KVS, ts, version=version, alignment=alignment))
+    f = hy.Gguf(path)
+    assert f.n_tensors() == len(ts)
+    for name, gt, ne, data in ts:
+        t, nd, ne4, nbytes, got = f.tensor(name)
+        assert t == gt and nd == len(ne) and ne4[:nd] == ne and all(v == 1 for v in ne4[nd:])
+        if gt == 12:
+            assert nbytes == 0 and got is None   # a type the reader does not size
+        else:
+            assert nbytes == len(data) and got == data
+    assert f.get_u32("k.u8") == 200 and f.get_u32("k.u16") == 60000 and f.get_u32("k.u32") == 4096
+    assert f.get_u32("k.u64") == 123456789 and f.get_u32("k.i32") == 7 and f.get_u32("k.bool") == 1
+    assert f.get_f32("k.f32") == 0.25 and f.get_f32("k.f64") == 1.5
+    for bad in ("k.i8", "k.neg", "k.str", "k.arr", "missing"):
+        with pytest.raises(hy.HyError):
+            f.get_u32(bad)
+    with pytest.raises(hy.HyError):
+        f.get_f32("k.u32")
+    with pytest.raises(hy.HyError):
+        f.tensor("no.such.tensor")
+    f.close()
+
+
+def test_data_offset_is_aligned(hy, tmp_path):
+    """The data section starts at the next multiple of general.alignment."""
+    ts = [("t", G.GGML_F32, [8], np.arange(8, dtype=np.float32).tobytes())]
+    blob = G.gguf_bytes([("pad", G.T_STR, "x" * 13)], ts, alignment=128)
+    path = _write(tmp_path, "a.gguf", blob)
+    f = hy.Gguf(path)
+    *_, data = f.tensor("t")
+    assert np.frombuffer(data, np.float32).tolist() == list(range(8))
+    f.close()
+
+
+def _corrupt_cases():
+    ts = [("t", G.GGML_Q8_0, [64, 2], bytes(136))]
+    good = G.gguf_bytes([("k", G.T_U32, 1)], ts)
+    yield "bad magic", b"GGUX" + good[4:]
+    yield "version 1", good[:4] + struct.pack("<I", 1) + good[8:]
+    yield "version 4", good[:4] + struct.pack("<I", 4) + good[8:]
+    yield "truncated header", good[:20]
+    yield "truncated kv", good[:30]
+    yield "tensor past the end", good[:-64]
+    yield "misaligned offset", G.gguf_bytes([], ts, data_offsets=[8])
+    yield "offset past the end", G.gguf_bytes([], ts, data_offsets=[1 << 40])
+    yield "huge tensor count", good[:8] + struct.pack("<Q", 1 << 60) + good[16:]
+    yield "bad alignment", G.gguf_bytes([("general.alignment", G.T_U32, 24)], ts)
+    yield "zero dims", G.gguf_bytes([], [("t", G.GGML_F32, [], b"")])
+    yield "five dims", G.gguf_bytes([], [("t", G.GGML_F32, [1, 1, 1, 1, 1], bytes(4))])
+
+
+@pytest.mark.parametrize("case,blob", list(_corrupt_cases()), ids=[c for c, _ in _corrupt_cases()])
+def test_corrupt_files_rejected(hy, tmp_path, case, blob):
+    path = _write(tmp_path, "bad.gguf", blob)
+    with pytest.raises(hy.HyError):
+        hy.Gguf(path)
+
+
+def test_missing_file(hy, tmp_path):
+    with pytest.raises(hy.HyError):
+        hy.Gguf(str(tmp_path / "nope.gguf"))
+
+
+# ------------------------------------------------------------------ GPU: layer upload
+
+SHAPE = dict(H=256, I=128, E=16, K=4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+def test_layer_from_gguf_matches_oracle(gpu, tmp_path, wtype):
+    """Two layers in one file (blocks 3 and 7, as a converter writes per-layer
+    names); each uploaded layer computes what the oracle computes on its weights."""
+    H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
+    layers = {b: O.synth_layer(H, I, E, K, wtype, seed=31 + b, layer=b, std=0.05) for b in (3, 7)}
+    ts = G.layer_tensors(layers[3], 3) + G.layer_tensors(layers[7], 7)
+    path = _write(tmp_path, "layers.gguf", G.gguf_bytes(G.layer_meta(layers[3]), ts))
+    f = gpu.Gguf(path)
+    m = gpu.Moe(H, I, E, K, wtype, num_layers=2, max_tokens=64)
+    m.upload_gguf(0, f, 7)
+    m.upload_gguf(1, f, 3)
+    f.close()   # the weights are resident: the mapping may go
+    for T in (1, 5, 40):
+        x = O.synth(200 + T, 0, O.T_X, 0, (T, H), 1.0)
+        for slot, block in ((0, 7), (1, 3)):
+            got = m.run(slot, x)
+            ref = O.moe_forward_q(layers[block], x)
+            np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32),
+                                          err_msg=f"wtype={wtype} T={T} block={block}")
+    m.close()
+
+
+@pytest.mark.gpu
+def test_layer_from_gguf_without_shared_expert(gpu, tmp_path):
+    H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=5, std=0.05, shared=False)
+    path = _write(tmp_path, "noshared.gguf", G.gguf_bytes(G.layer_meta(layer), G.layer_tensors(layer, 0)))
+    f = gpu.Gguf(path)
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=16, has_shared=False)
+    m.upload_gguf(0, f, 0)
+    x = O.synth(9, 0, O.T_X, 0, (7, H), 1.0)
+    np.testing.assert_array_equal(m.run(0, x).view(np.uint32), O.moe_forward_q(layer, x).view(np.uint32))
+    m.close()
+    f.close()
+
+
+@pytest.mark.gpu
+def test_layer_from_gguf_mismatches_rejected(gpu, tmp_path):
+    H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=6, std=0.05)
+    good = G.layer_tensors(layer, 0)
+    cases = {
+        "missing expert": [t for t in good if "ffn_expert_5_down" not in t[0]],
+        "wrong type": [(n, G.GGML_Q4_0, ne, d[: len(d) * 18 // 34]) if "expert_2_gate_up" in n else (n, gt, ne, d)
+                       for n, gt, ne, d in good],
+        "wrong shape": [(n, gt, [ne[0], ne[1] // 2], d[: len(d) // 2]) if "shared_down" in n else (n, gt, ne, d)
+                        for n, gt, ne, d in good],
+    }
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=8)
+    for case, ts in cases.items():
+        f = gpu.Gguf(_write(tmp_path, "m.gguf", G.gguf_bytes(G.layer_meta(layer), ts)))
+        with pytest.raises(gpu.HyError):
+            m.upload_gguf(0, f, 0)
+        f.close()
+    meta = [(k, t, (v * 2 if k == "hunyuan.num_experts" else v)) for k, t, v in G.layer_meta(layer)]
+    f = gpu.Gguf(_write(tmp_path, "meta.gguf", G.gguf_bytes(meta, good)))
+    with pytest.raises(gpu.HyError):
+        m.upload_gguf(0, f, 0)
+    with pytest.raises(gpu.HyError):   # the layer was never loaded
+        xb, ob = gpu.Buf.empty((2, H)), gpu.Buf.empty((2, H))
+        m.forward(0, xb, 2, ob)
+    f.close()
+    m.close()
