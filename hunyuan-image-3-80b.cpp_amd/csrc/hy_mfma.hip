@@ -49,8 +49,14 @@ constexpr int MM_RING = 3;                 // LDS stages: one computed, two in f
 constexpr int MM_XCD = 8;                  // XCDs of the device (work-group round robin)
 
 // Tile shape.  LDS stage layout (bytes): A = CHUNKS (row group x block) chunks of
-// 64 rows x 32 B int8 (Q4_0: 64 rows x 16 B raw nibbles); B = TOK tokens x KB*32 B;
-// A scales = CHUNKS x 64 fp16; B scales = TOK tokens x KB f32.
+// 64 rows x 32 B int8 (Q4_0: 64 rows x 16 B raw nibbles); B = KB blocks of TOK tokens
+// x 32 B; A scales = CHUNKS x 64 fp16; B scales = TOK tokens x KB f32.
+//
+// Bank swizzle of the 32-byte operand rows (A rows and B token rows): the two 16-byte
+// halves of row r sit in swapped order when bit 3 of r is set.  An MFMA operand read
+// (lane l: row l%32, half l/32) then touches 64 distinct banks per 16 lanes; without
+// the swap rows r and r+8 share banks and every read takes two passes.  The copies
+// keep their contiguous LDS destinations and fetch the swapped halves instead.
 template <int ROWS_, int TOK_, int KB_>
 struct MmShape {
     static constexpr int ROWS = ROWS_, TOK = TOK_, KB = KB_;
@@ -62,14 +68,16 @@ struct MmShape {
     static constexpr int ST_B = TOK * KB * 32;
     static constexpr int ST_AS = CHUNKS * 64 * 2;
     static constexpr int ST_BS = TOK * KB * 4;
-    // B rows: each wave copies TOK/8 tokens x KB*32 B with 16-byte lanes
-    static constexpr int B_LANES = TOK / MM_WAVES * KB * 2;
+    // B rows: wave w copies block w % KB of TPW tokens x 32 B with 16-byte lanes
+    static constexpr int TPW = TOK * KB / MM_WAVES;
+    static constexpr int B_LANES = TPW * 2;
     static constexpr int B_LOADS = (B_LANES + WAVE - 1) / WAVE;
     static constexpr int WPC = MM_WAVES / CHUNKS;     // waves sharing one A chunk's copies
     static_assert(CHUNKS * WPC == MM_WAVES && (WPC == 1 || WPC == 2), "A chunks split evenly over the waves");
     static_assert(TQ * 32 == TOK, "token groups must cover the tile");
     static_assert(B_LANES % WAVE == 0 || B_LOADS == 1, "partial B loads only as a single load");
     static_assert(KB == 4 || KB == 2, "B-scale copy handles 16 B or 8 B per token");
+    static_assert(MM_WAVES % KB == 0 && TPW % 16 == 0, "B copies: whole 16-row swizzle groups per wave");
 };
 using ShapeWide = MmShape<128, 128, 2>;
 using ShapeTall = MmShape<256, 64, 2>;
@@ -186,17 +194,22 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
                            ((size_t)(G0 + ch / MM_KB) * nb + ch % MM_KB) * CHB + half * (CHB / WPC);
     const uint16_t* as_src = a.W.sc + (size_t)e * a.W.sc_stride + ((size_t)(G0 + ch / MM_KB) * nb + ch % MM_KB) * 64 +
                              half * (64 / WPC);
-    // B rows: wave w copies tokens w*TOK/8 .. +TOK/8, KB*32 bytes each, as 16-byte
-    // pieces; piece p (copy v, lane l: p = 64 v + l) is token p / (2 KB), offset
-    // 16 (p % (2 KB)) -- lane i of a copy lands at +16 i, i.e. tokens stay row-major
-    constexpr int BPT = 2 * MM_KB;  // 16-byte pieces per token row
+    // B rows: wave w copies block w % KB of tokens (w / KB) * TPW .. + TPW, as 16-byte
+    // pieces; lane position p (copy v, lane l: p = 64 v + l) lands at +16 p, i.e. token
+    // row p / 2, position p % 2, which holds half (p % 2) ^ (bit 3 of the row)
+    constexpr int TPW = SH::TPW;
     uint32_t b_off[SH::B_LOADS];
 #pragma unroll
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
-        const int bt = wave * (MM_TOK / MM_WAVES) + (p % SH::B_LANES) / BPT;  // in range for masked lanes too
-        b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (p % BPT) * 16;
+        const int bt = (wave / MM_KB) * TPW + (p % SH::B_LANES) / 2;  // in range for masked lanes too
+        const int hb = (p & 1) ^ ((p >> 4) & 1);
+        b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (wave % MM_KB) * 32 + hb * 16;
     }
+    // A rows (int8): copy lane l lands at +16 l (row l / 2 of a 32-row piece, position
+    // l % 2) and fetches half (l % 2) ^ (bit 3 of the row); Q4_0 nibbles are copied as
+    // they are and swizzled when unpacked
+    const uint32_t a_sw = 16u * (uint32_t)(lane ^ ((lane >> 4) & 1));
     // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each: KB = 4 as one
     // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces
     constexpr int BS_LANES = MM_KB == 4 ? MM_TOK / MM_WAVES : MM_TOK / MM_WAVES * MM_KB;
@@ -215,11 +228,11 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
             if (lane < 32) g2l16(ab + lane * 16, ad);  // 512 B
         } else {
 #pragma unroll
-            for (int c = 0; c < A_LOADS; c++) g2l16(ab + c * 1024 + lane * 16, ad + c * 1024);
+            for (int c = 0; c < A_LOADS; c++) g2l16(ab + c * 1024 + (Q4 ? 16u * lane : a_sw), ad + c * 1024);
         }
         // B rows of this wave's tokens
         const int8_t* bb = a.aq + (size_t)kb0 * QK;
-        uint8_t* bdst = st + OFF_B + wv * (MM_TOK / MM_WAVES) * (MM_KB * 32);
+        uint8_t* bdst = st + OFF_B + (wv % MM_KB) * (MM_TOK * 32) + (wv / MM_KB) * (TPW * 32);
 #pragma unroll
         for (int v = 0; v < SH::B_LOADS; v++)
             if (v * WAVE + lane < SH::B_LANES) g2l16(bb + b_off[v], bdst + v * 1024);
@@ -247,12 +260,13 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
         acc1[v] = 0.0f;
     }
     // per-lane LDS offsets inside a stage slot (the block kb adds a constant):
-    //   A rows lr and 32+lr of this wave's slab, 16-byte half lg
-    //   B row (token) nq*32+lr, half lg
+    //   A rows lr and 32+lr of this wave's slab, 16-byte half lg (swizzled)
+    //   B row (token) nq*32+lr of the block, half lg (swizzled)
     //   rank-1 scale operands: lanes of the lower half read d_w of rows lr / 32+lr and
     //   d_x of token nq*32+lr; lanes of the upper half read zeros
-    const uint32_t a_lane = (uint32_t)((Q4 ? 0 : OFF_A) + sl * MM_KB * 2048 + lr * 32 + 16 * lg);
-    const uint32_t b_lane = (uint32_t)(OFF_B + (nq * 32 + lr) * (MM_KB * 32) + 16 * lg);
+    const int hsw = lg ^ ((lr >> 3) & 1);
+    const uint32_t a_lane = (uint32_t)((Q4 ? 0 : OFF_A) + sl * MM_KB * 2048 + lr * 32 + 16 * hsw);
+    const uint32_t b_lane = (uint32_t)(OFF_B + (nq * 32 + lr) * 32 + 16 * hsw);
     const uint32_t sw_lane = (uint32_t)(lg == 0 ? OFF_AS + sl * MM_KB * 128 + lr * 2 : OFF_Z);
     const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 + lr) * MM_KB * 4 : OFF_Z);
     const uint32_t ring0 = lds_off(ring[0]);
@@ -264,7 +278,7 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     auto block = [&]<int KBI>(uint32_t st, uint32_t abase) {
         v4i_t A0 = lds_b128_at<KBI * 2048>(abase);
         v4i_t A1 = lds_b128_at<KBI * 2048 + 1024>(abase);
-        v4i_t B = lds_b128_at<KBI * 32>(st + b_lane);
+        v4i_t B = lds_b128_at<KBI * MM_TOK * 32>(st + b_lane);
         uint32_t dw0 = lds_u16_at<KBI * 128>(st + sw_lane);
         uint32_t dw1 = lds_u16_at<KBI * 128 + 64>(st + sw_lane);
         uint32_t dxb = lds_b32_at<KBI * 4>(st + sx_lane);
@@ -300,6 +314,10 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
             MM_WAIT_VM_LGKM(0);
         }
         __builtin_amdgcn_s_barrier();
+        // refill: slot (s+2) % 3 was last read in iteration s-1, finished by every
+        // wave before this barrier -- issue it now so that two stages are in flight
+        // during this stage's math
+        if (s + 2 < nstage) issue(s + 2);
         const uint32_t st = ring0 + (uint32_t)((s % MM_RING) * STAGE);
         uint32_t abase;
         if (Q4) {
@@ -311,8 +329,9 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
                 lds_wait(wv4);
                 int4 lo, hi;
                 unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
-                lds_st128(aun + c * 2048 + r * 32, v4i_t{lo.x, lo.y, lo.z, lo.w});
-                lds_st128(aun + c * 2048 + r * 32 + 16, v4i_t{hi.x, hi.y, hi.z, hi.w});
+                const int sw = 16 * ((r >> 3) & 1);
+                lds_st128(aun + c * 2048 + r * 32 + sw, v4i_t{lo.x, lo.y, lo.z, lo.w});
+                lds_st128(aun + c * 2048 + r * 32 + (16 ^ sw), v4i_t{hi.x, hi.y, hi.z, hi.w});
                 lds_wait();
             }
             __builtin_amdgcn_s_barrier();
@@ -325,9 +344,6 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
                 (block.template operator()<KBI>(st, abase), ...);
             }(std::make_integer_sequence<int, MM_KB>{});
         }
-        // refill: slot (s+2) % 3 was last read in iteration s-1, finished by every
-        // wave before this iteration's barrier
-        if (s + 2 < nstage) issue(s + 2);
     }
 
     // ---- epilogues
