@@ -245,7 +245,8 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode
     const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) &&
                       (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
-    const int NT = mfma ? hy::mfma_tile_tokens(iT, K, E, H, I) : hy::gemv_tile_tokens();
+    const int shape = mfma ? hy::mfma_shape(iT, K, E, H, I) : -1;
+    const int NT = mfma ? hy::mfma_shape_tokens(shape) : hy::gemv_tile_tokens();
     if (!mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
         // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
@@ -279,13 +280,13 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int shared_tiles = has_shared ? (iT + NT - 1) / NT : 0;
     if (mfma) {
         HY_TRY(timed(c, hy::KID_UP, s, [&] {
-            return hy::launch_ffn_up_mfma(wt, NT, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
+            return hy::launch_ffn_up_mfma(wt, shape, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
                                           c->hd, c->hs, s);
         }));
         // routed and shared down products in one launch (y rows for every slot), then
         // the combine
         HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
-            return hy::launch_ffn_down_mfma(wt, NT, routed_bound + shared_tiles, dn_view(c, L), R, c->hq, c->hd, iT, H,
+            return hy::launch_ffn_down_mfma(wt, shape, routed_bound + shared_tiles, dn_view(c, L), R, c->hq, c->hd, iT, H,
                                             I, E, K, c->y, s);
         }));
         HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {

@@ -48,12 +48,15 @@ hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x,
 
 // expert products, MFMA path (hy_mfma.hip)
 bool mfma_path_ok(int wtype, int H, int I);
-// pairs per tile of the MFMA shape used for this batch (the dispatch must tile with it)
-int mfma_tile_tokens(int T, int K, int E, int H, int I);
-hipError_t launch_ffn_up_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+// tile shape of the MFMA path for this batch, and its pairs per tile (the dispatch
+// must tile with it)
+enum MfmaShape { MM_SHAPE_WIDE = 0, MM_SHAPE_TALL = 1 };
+int mfma_shape(int T, int K, int E, int H, int I);
+int mfma_shape_tokens(int shape);
+hipError_t launch_ffn_up_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                               const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
                               hipStream_t s);
-hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+hipError_t launch_ffn_down_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                                 const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
                                 hipStream_t s);
 

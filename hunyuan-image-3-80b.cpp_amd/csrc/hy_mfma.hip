@@ -43,9 +43,6 @@ typedef int v16i_t __attribute__((ext_vector_type(16)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 
-constexpr int MM_WAVES = 8;
-constexpr int MM_THREADS = MM_WAVES * WAVE;
-constexpr int MM_RING = 3;                 // LDS stages: one computed, two in flight
 constexpr int MM_XCD = 8;                  // XCDs of the device (work-group round robin)
 
 // Tile shape.  LDS stage layout (bytes): A = CHUNKS (row group x block) chunks of
@@ -57,11 +54,17 @@ constexpr int MM_XCD = 8;                  // XCDs of the device (work-group rou
 // (lane l: row l%32, half l/32) then touches 64 distinct banks per 16 lanes; without
 // the swap rows r and r+8 share banks and every read takes two passes.  The copies
 // keep their contiguous LDS destinations and fetch the swapped halves instead.
-template <int ROWS_, int TOK_, int KB_>
+//
+// WAVES waves per work group (one 64-row slab x 32-token group each); RING LDS stage
+// slots (one computed, RING - 1 in flight).  8-wave shapes run two work groups per
+// CU, the 16-wave shape one, with a deeper ring in the LDS that frees.
+template <int ROWS_, int TOK_, int KB_, int WAVES_ = 8, int RING_ = 3>
 struct MmShape {
-    static constexpr int ROWS = ROWS_, TOK = TOK_, KB = KB_;
+    static constexpr int ROWS = ROWS_, TOK = TOK_, KB = KB_, WAVES = WAVES_, RING = RING_;
+    static constexpr int THREADS = WAVES * WAVE;
+    static constexpr int WG_PER_CU = WAVES == 16 ? 1 : 2;
     static constexpr int SLABS = ROWS / 64;          // 64-row slabs (one per row group)
-    static constexpr int TQ = MM_WAVES / SLABS;      // 32-token column groups
+    static constexpr int TQ = WAVES / SLABS;         // 32-token column groups
     static constexpr int CHUNKS = SLABS * KB;
     static constexpr int ST_A = CHUNKS * 64 * 32;
     static constexpr int ST_AR = CHUNKS * 64 * 16;
@@ -69,15 +72,17 @@ struct MmShape {
     static constexpr int ST_AS = CHUNKS * 64 * 2;
     static constexpr int ST_BS = TOK * KB * 4;
     // B rows: wave w copies block w % KB of TPW tokens x 32 B with 16-byte lanes
-    static constexpr int TPW = TOK * KB / MM_WAVES;
+    static constexpr int TPW = TOK * KB / WAVES;
     static constexpr int B_LANES = TPW * 2;
     static constexpr int B_LOADS = (B_LANES + WAVE - 1) / WAVE;
-    static constexpr int WPC = MM_WAVES / CHUNKS;     // waves sharing one A chunk's copies
-    static_assert(CHUNKS * WPC == MM_WAVES && (WPC == 1 || WPC == 2), "A chunks split evenly over the waves");
+    static constexpr int WPC = WAVES / CHUNKS;        // waves sharing one A chunk's copies
+    static_assert(CHUNKS * WPC == WAVES && (WPC == 1 || WPC == 2), "A chunks split evenly over the waves");
+    static_assert(WAVES == 8 || WAVES == 16, "two 8-wave or one 16-wave work group per CU");
+    static_assert(RING >= 3, "at least one stage in flight while one is refilled");
     static_assert(TQ * 32 == TOK, "token groups must cover the tile");
     static_assert(B_LANES % WAVE == 0 || B_LOADS == 1, "partial B loads only as a single load");
-    static_assert(KB == 4 || KB == 2, "B-scale copy handles 16 B or 8 B per token");
-    static_assert(MM_WAVES % KB == 0 && TPW % 16 == 0, "B copies: whole 16-row swizzle groups per wave");
+    static_assert(KB == 4 || KB == 2 || KB == 1, "B-scale copy handles 16, 8 or 4 B per token");
+    static_assert(WAVES % KB == 0 && TPW % 2 == 0, "B copies: whole token rows per wave");
 };
 using ShapeWide = MmShape<128, 128, 2>;
 using ShapeTall = MmShape<256, 64, 2>;
@@ -119,9 +124,25 @@ __device__ __forceinline__ v16f_t scale_outer(_Float16 dw, _Float16 dx, int lg) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, zero, 0, 0, 0);
 }
 
+// vmcnt wait for the stage being consumed: the R stages issued after it may stay in
+// flight (R = min(RING - 2, stages left after it), LOADS copies per stage and wave)
+template <int LOADS, int R>
+__device__ __forceinline__ void wait_stage(int left) {
+    if constexpr (R == 0) {
+        MM_WAIT_VM_LGKM(0);
+    } else {
+        if (left >= R) {
+            MM_WAIT_VM_LGKM(R * LOADS);
+        } else {
+            wait_stage<LOADS, R - 1>(left);
+        }
+    }
+}
+
 template <int WT, int MODE, class SH>
-__global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
+__global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(MmArgs a) {
     constexpr int MM_ROWS = SH::ROWS, MM_TOK = SH::TOK, MM_KB = SH::KB, MM_SLABS = SH::SLABS;
+    constexpr int MM_WAVES = SH::WAVES, MM_THREADS = SH::THREADS, MM_RING = SH::RING;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
     // stage slot: A (int8, or Q4_0 nibbles), B, A scales, B scales, then a zero area
     // the upper lane half reads its rank-1 scale operands from
@@ -140,6 +161,7 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     constexpr int WPC = SH::WPC;
     constexpr int A_LOADS = Q4 ? 1 : 2 / WPC;
     constexpr int LOADS = A_LOADS + SH::B_LOADS + 1 + 1;
+    static_assert((MM_RING - 2) * LOADS <= 63, "vmcnt counts at most 63 outstanding copies");
 
     // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
     // all row blocks of a tile the same id mod MM_XCD (they share the tile's
@@ -203,7 +225,7 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
         const int bt = (wave / MM_KB) * TPW + (p % SH::B_LANES) / 2;  // in range for masked lanes too
-        const int hb = (p & 1) ^ ((p >> 4) & 1);
+        const int hb = (p & 1) ^ ((bt >> 3) & 1);
         b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (wave % MM_KB) * 32 + hb * 16;
     }
     // A rows (int8): copy lane l lands at +16 l (row l / 2 of a 32-row piece, position
@@ -304,20 +326,17 @@ __global__ __launch_bounds__(MM_THREADS, 2) void moe_mfma_kernel(MmArgs a) {
     };
 
     const int nstage = nb / MM_KB;
-    issue(0);
-    if (nstage > 1) issue(1);
+#pragma unroll
+    for (int i = 0; i < MM_RING - 1; i++)
+        if (i < nstage) issue(i);
     for (int s = 0; s < nstage; s++) {
         // stage s landed (this wave's loads), and every wave's (barrier)
-        if (s + 1 < nstage) {
-            MM_WAIT_VM_LGKM(LOADS);
-        } else {
-            MM_WAIT_VM_LGKM(0);
-        }
+        wait_stage<LOADS, MM_RING - 2>(nstage - 1 - s);
         __builtin_amdgcn_s_barrier();
-        // refill: slot (s+2) % 3 was last read in iteration s-1, finished by every
-        // wave before this barrier -- issue it now so that two stages are in flight
-        // during this stage's math
-        if (s + 2 < nstage) issue(s + 2);
+        // refill: slot (s + RING - 1) % RING was last read in iteration s-1, finished
+        // by every wave before this barrier -- issue it now so that RING - 1 stages are
+        // in flight during this stage's math
+        if (s + MM_RING - 1 < nstage) issue(s + MM_RING - 1);
         const uint32_t st = ring0 + (uint32_t)((s % MM_RING) * STAGE);
         uint32_t abase;
         if (Q4) {
@@ -405,15 +424,15 @@ static hipError_t launch_mode(int wtype, MmArgs a, int n_tiles_bound, int rows, 
     a.tiles_pad = (n_tiles_bound + MM_XCD - 1) / MM_XCD * MM_XCD;
     const dim3 grid(a.tiles_pad * a.nrb);
     if (wtype == HY_TYPE_Q4_0)
-        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE, SH>), grid, dim3(MM_THREADS), 0, s, a);
+        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE, SH>), grid, dim3(SH::THREADS), 0, s, a);
     else
-        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q8_0, MODE, SH>), grid, dim3(MM_THREADS), 0, s, a);
+        hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q8_0, MODE, SH>), grid, dim3(SH::THREADS), 0, s, a);
     return hipGetLastError();
 }
 
 template <int MODE>
-static hipError_t launch_shape(int wtype, int tile_tokens, MmArgs a, int n_tiles_bound, int rows, hipStream_t s) {
-    if (tile_tokens == ShapeTall::TOK) return launch_mode<MODE, ShapeTall>(wtype, a, n_tiles_bound, rows, s);
+static hipError_t launch_shape(int wtype, int shape, MmArgs a, int n_tiles_bound, int rows, hipStream_t s) {
+    if (shape == MM_SHAPE_TALL) return launch_mode<MODE, ShapeTall>(wtype, a, n_tiles_bound, rows, s);
     return launch_mode<MODE, ShapeWide>(wtype, a, n_tiles_bound, rows, s);
 }
 
@@ -429,23 +448,27 @@ bool mfma_path_ok(int wtype, int H, int I) {
 // The tall shape (64-pair tiles, 256-row blocks) wins while experts see about 64
 // pairs each (a 128-pair tile would leave half its waves idle); beyond ~96 the wide
 // shape's reuse of every weight byte over 128 pairs wins.
-int mfma_tile_tokens(int T, int K, int E, int H, int I) {
+int mfma_shape(int T, int K, int E, int H, int I) {
     const bool tall = shape_fits<ShapeTall>(H, I) && (int64_t)T * K < (int64_t)96 * E;
-    return tall ? ShapeTall::TOK : ShapeWide::TOK;
+    return tall ? MM_SHAPE_TALL : MM_SHAPE_WIDE;
 }
 
-hipError_t launch_ffn_up_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+int mfma_shape_tokens(int shape) {
+    return shape == MM_SHAPE_TALL ? ShapeTall::TOK : ShapeWide::TOK;
+}
+
+hipError_t launch_ffn_up_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                               const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
                               hipStream_t s) {
     MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr};
-    return launch_shape<0>(wtype, tile_tokens, a, n_tiles_bound, 2 * I, s);
+    return launch_shape<0>(wtype, shape, a, n_tiles_bound, 2 * I, s);
 }
 
-hipError_t launch_ffn_down_mfma(int wtype, int tile_tokens, int n_tiles_bound, const MatView& W, const Routing& R,
+hipError_t launch_ffn_down_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                                 const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
                                 hipStream_t s) {
     MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y};
-    return launch_shape<1>(wtype, tile_tokens, a, n_tiles_bound, H, s);
+    return launch_shape<1>(wtype, shape, a, n_tiles_bound, H, s);
 }
 
 }  // namespace hy
