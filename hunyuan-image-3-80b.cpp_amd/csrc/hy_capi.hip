@@ -67,7 +67,9 @@ struct LayerW {
     uint16_t* gu_sc = nullptr;
     uint8_t* dn_qs = nullptr;
     uint16_t* dn_sc = nullptr;
+    float* ffn_norm = nullptr;  // post-attention RMSNorm weight [H] (used when has_norm)
     bool loaded = false;
+    bool has_norm = false;
 };
 
 struct ProfRec {
@@ -226,12 +228,15 @@ int alloc_layer(hy_moe_ctx* c, LayerW& L) {
     L.dn_qs = b + o;
     o += align256(c->dn_qs_stride * c->X);
     L.dn_sc = reinterpret_cast<uint16_t*>(b + o);
+    o += align256(c->dn_sc_stride * 2 * c->X);
+    L.ffn_norm = reinterpret_cast<float*>(b + o);
     return HY_OK;
 }
 
-// forward of one layer; resid may be null.
+// forward of one layer; resid may be null.  prequant: c->xq/xd/xs already hold the
+// Q8_0 form of x (the stack's fused RMSNorm + quantization wrote them).
 int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, float* out, const float* resid,
-                 hipStream_t s) {
+                 hipStream_t s, bool prequant = false) {
     if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
     const LayerW& L = c->layers[layer];
     if (!L.loaded) return fail(HY_ERR_STATE, "layer %u has no weights", layer);
@@ -251,15 +256,15 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
         // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
             return hy::launch_route_decode(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob,
-                                           c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi, c->xq, c->xd,
-                                           c->xs, NT, has_shared, c->cnt, c->off, c->srt_tok, c->pair_pos,
+                                           c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi,
+                                           prequant ? nullptr : c->xq, c->xd, c->xs, NT, has_shared, c->cnt, c->off, c->srt_tok, c->pair_pos,
                                            c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n, c->meta, s);
         }));
     } else {
         // small batches quantize the activations inside the selection pass, large ones
         // in a bandwidth-shaped kernel of their own
-        const bool fuse_quant = wt != HY_TYPE_F32 && T <= 32;
-        if (wt != HY_TYPE_F32 && !fuse_quant)
+        const bool fuse_quant = wt != HY_TYPE_F32 && T <= 32 && !prequant;
+        if (wt != HY_TYPE_F32 && !fuse_quant && !prequant)
             HY_TRY(timed(c, hy::KID_QUANT, s, [&] {
                 return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
             }));
@@ -347,7 +352,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
     c->dn_sc_stride = wt == HY_TYPE_F32 ? 0 : (size_t)c->H * (c->I / 32);
     c->layer_bytes = align256((size_t)c->E * c->H * 4) + align256(c->gu_qs_stride * c->X) +
                      align256(c->gu_sc_stride * 2 * c->X) + align256(c->dn_qs_stride * c->X) +
-                     align256(c->dn_sc_stride * 2 * c->X);
+                     align256(c->dn_sc_stride * 2 * c->X) + align256((size_t)c->H * 4);
     c->layers.resize(cfg->num_layers);
 
     // work arena
@@ -508,9 +513,19 @@ int hy_moe_upload_layer_gguf(hy_moe_ctx* c, uint32_t layer, const hy_gguf* g, ui
         HY_TRY(need(base + "gate_up.weight", wt, (uint64_t)H, (uint64_t)2 * I, &gus[e]));
         HY_TRY(need(base + "down.weight", wt, (uint64_t)I, (uint64_t)H, &dns[e]));
     }
-    return upload_layer(
+    // the post-attention RMSNorm weight (post_attention_layernorm -> ffn_norm), F32 [H];
+    // optional: a file without it leaves the layer at unit weight
+    const uint8_t* norm = nullptr;
+    if (const hy::GgufTensor* t = f.find(pfx + "ffn_norm.weight")) {
+        if (t->type != HY_TYPE_F32 || t->n_dims != 1 || t->ne[0] != (uint64_t)H)
+            return fail(HY_ERR_INVALID, "%sffn_norm.weight must be F32 [%d] (type %d, %u dims, ne0 %llu)", pfx.c_str(),
+                        H, t->type, t->n_dims, (unsigned long long)t->ne[0]);
+        norm = t->data;
+    }
+    HY_TRY(upload_layer(
         c, layer, reinterpret_cast<const float*>(router), [&](int e) -> const void* { return gus[e]; },
-        [&](int e) -> const void* { return dns[e]; });
+        [&](int e) -> const void* { return dns[e]; }));
+    return hy_moe_set_ffn_norm(c, layer, reinterpret_cast<const float*>(norm));
 }
 
 int hy_moe_synth_layer(hy_moe_ctx* c, uint32_t layer, uint64_t seed, float std, const float* bias) {
@@ -534,6 +549,21 @@ int hy_moe_synth_layer(hy_moe_ctx* c, uint32_t layer, uint64_t seed, float std, 
     }
     HIP_TRY(hipDeviceSynchronize());
     L.loaded = true;
+    return HY_OK;
+}
+
+int hy_moe_set_ffn_norm(hy_moe_ctx* c, uint32_t layer, const float* w) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    LayerW& L = c->layers[layer];
+    if (!w) {
+        L.has_norm = false;
+        return HY_OK;
+    }
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    HY_TRY(alloc_layer(c, L));
+    HIP_TRY(hipMemcpy(L.ffn_norm, w, (size_t)c->H * 4, hipMemcpyHostToDevice));
+    L.has_norm = true;
     return HY_OK;
 }
 
@@ -562,9 +592,18 @@ int hy_moe_stack_forward(hy_moe_ctx* c, uint32_t first, uint32_t n, const float*
     const size_t bytes = (size_t)T * c->H * 4;
     HIP_TRY(hipMemcpyAsync(c->cur, x, bytes, hipMemcpyDeviceToDevice, s));
     for (uint32_t l = 0; l < n; l++) {
-        HY_TRY(timed(c, hy::KID_RMSNORM, s, [&] { return hy::launch_rms_norm(c->cur, (int)T, c->H, eps, c->xn, s); }));
+        const LayerW& L = c->layers[first + l];
+        const float* w = L.has_norm ? L.ffn_norm : nullptr;
+        // quantized weights: the RMSNorm also writes the Q8_0 activations, so the
+        // layer's routing pass does not quantize again
+        const bool pq = c->cfg.wtype != HY_TYPE_F32;
+        HY_TRY(timed(c, hy::KID_RMSNORM, s, [&] {
+            if (pq) return hy::launch_rms_norm_quant(c->cur, w, (int)T, c->H, eps, c->xn, c->xq, c->xd, c->xs, s);
+            return w ? hy::launch_rms_norm_w(c->cur, w, (int)T, c->H, eps, c->xn, s)
+                     : hy::launch_rms_norm(c->cur, (int)T, c->H, eps, c->xn, s);
+        }));
         // residual fused into the combine; in place on cur (each element read then written by one thread)
-        HY_TRY(forward_impl(c, first + l, c->xn, T, c->cur, c->cur, s));
+        HY_TRY(forward_impl(c, first + l, c->xn, T, c->cur, c->cur, s, pq));
     }
     HIP_TRY(hipMemcpyAsync(out, c->cur, bytes, hipMemcpyDeviceToDevice, s));
     return HY_OK;

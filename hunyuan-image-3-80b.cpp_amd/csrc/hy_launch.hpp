@@ -31,6 +31,9 @@ hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int
                            int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w, int* tile_e,
                            int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s);
 hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s);
+// RMSNorm (w may be null: unit weight) fused with the Q8_0 quantization of its output
+hipError_t launch_rms_norm_quant(const float* x, const float* w, int T, int H, float eps, float* xn, int8_t* q,
+                                 float* d, int* qsum, hipStream_t s);
 
 // expert products, decode GEMV path (hy_gemv.hip)
 constexpr int GEMV_NT = 4;  // tokens per GEMV tile

@@ -563,7 +563,8 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
     if (e != hipSuccess) return e;
     DecodeRouteArgs a{x, logits, T, H, E, K, norm, scale, topw, topi, xq, xd, xs, NT, has_shared,
                       DispatchOut{cnt, off, srt_tok, pair_pos, comb_pos, comb_w, tile_e, tile_start, tile_n, meta}};
-    const unsigned quant_groups = (unsigned)(((size_t)T * H + 255) / 256);
+    // no quantization work groups when the caller quantized x already (xq == null)
+    const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + 255) / 256) : 0u;
     hipLaunchKernelGGL(route_decode_kernel, dim3(1 + quant_groups), dim3(ROUTER_WAVES * WAVE), 0, s, a);
     return hipGetLastError();
 }
@@ -616,6 +617,89 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
 
 hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s) {
     hipLaunchKernelGGL(rms_norm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, T, H, eps, out);
+    return hipGetLastError();
+}
+
+// RMSNorm (optionally weighted) fused with the Q8_0 quantization of its output, one
+// wave per row: the sum of squares in the same blocked order as rms_norm_kernel, then
+// xn = x * rms (* w) written as f32 (the router's input) and quantized 8 elements per
+// lane exactly as quant_q8_0_vec_kernel does (4 lanes per 32-block).  The values
+// equal rms_norm_kernel / rms_norm_w_kernel followed by quant_q8_0_vec_kernel bit for
+// bit; x is read twice from cache instead of xn being written and read back.
+__global__ __launch_bounds__(256) void rms_norm_quant_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             int T, int H, float eps, float* __restrict__ xn,
+                                                             int8_t* __restrict__ q, float* __restrict__ d,
+                                                             int* __restrict__ qsum) {
+    const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (row >= T) return;  // whole waves: the shuffles below stay within live waves
+    const float* xr = x + (size_t)row * H;
+    float a = 0.0f;
+    for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + h0);
+        a = fmaf(v.x, v.x, a);
+        a = fmaf(v.y, v.y, a);
+        a = fmaf(v.z, v.z, a);
+        a = fmaf(v.w, v.w, a);
+    }
+    const float ss = __shfl(tree_sum64(a), 0, WAVE);
+    const float rms = 1.0f / sqrtf(ss / (float)H + eps);
+    const int nb = H / QK;
+    for (int base = 0; base < H; base += 8 * WAVE) {  // the same trip count on every lane
+        const int h8 = base + 8 * lane;
+        const bool live = h8 < H;  // H is a multiple of 32: a block's 4 lanes agree
+        float xs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            const float4 v0 = *reinterpret_cast<const float4*>(xr + h8);
+            const float4 v1 = *reinterpret_cast<const float4*>(xr + h8 + 4);
+            const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if (w) {
+                const float4 w0 = *reinterpret_cast<const float4*>(w + h8);
+                const float4 w1 = *reinterpret_cast<const float4*>(w + h8 + 4);
+                const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) xs[j] = vv[j] * rms * ww[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) xs[j] = vv[j] * rms;
+            }
+            float* o = xn + (size_t)row * H + h8;
+            *reinterpret_cast<float4*>(o) = make_float4(xs[0], xs[1], xs[2], xs[3]);
+            *reinterpret_cast<float4*>(o + 4) = make_float4(xs[4], xs[5], xs[6], xs[7]);
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(xs[j]));
+        amax = fmaxf(amax, shfl_xor(amax, 1, 4));
+        amax = fmaxf(amax, shfl_xor(amax, 2, 4));
+        const float dd = amax / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        int sum = 0;
+        uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int qv = (int)__builtin_roundf(xs[j] * id);
+            sum += qv;
+            if (j < 4)
+                p0 |= ((uint32_t)(qv & 0xff)) << (8 * j);
+            else
+                p1 |= ((uint32_t)(qv & 0xff)) << (8 * (j - 4));
+        }
+        sum += shfl_xor(sum, 1, 4);
+        sum += shfl_xor(sum, 2, 4);
+        if (!live) continue;
+        const size_t i8 = ((size_t)row * H + h8) / 8;
+        reinterpret_cast<uint2*>(q)[i8] = make_uint2(p0, p1);
+        if ((lane & 3) == 0) {
+            const size_t b = (size_t)row * nb + h8 / QK;
+            d[b] = h2f(f2h(dd));
+            qsum[b] = sum;
+        }
+    }
+}
+
+hipError_t launch_rms_norm_quant(const float* x, const float* w, int T, int H, float eps, float* xn, int8_t* q,
+                                 float* d, int* qsum, hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_quant_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, T, H, eps, xn, q, d, qsum);
     return hipGetLastError();
 }
 

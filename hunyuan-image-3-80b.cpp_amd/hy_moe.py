@@ -45,6 +45,7 @@ _SIGS = {
     "hy_moe_layer_bytes": (C.c_size_t, [_vp]),
     "hy_moe_upload_layer": (C.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "hy_moe_synth_layer": (C.c_int, [_vp, _u32, _u64, _f, _vp]),
+    "hy_moe_set_ffn_norm": (C.c_int, [_vp, _u32, _vp]),
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
     "hy_moe_forward_debug": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "hy_moe_stack_forward": (C.c_int, [_vp, _u32, _u32, _vp, _u32, _f, _vp, _vp]),
@@ -227,6 +228,16 @@ class Moe:
         if router_bias is not None:
             b = np.ascontiguousarray(router_bias, dtype=np.float32)
         check(lib().hy_moe_synth_layer(self.h, layer_idx, seed, std, None if b is None else b.ctypes.data))
+
+    def set_ffn_norm(self, layer_idx, w=None):
+        """Post-attention RMSNorm weight [H] of a layer (None: unit weight)."""
+        if w is None:
+            check(lib().hy_moe_set_ffn_norm(self.h, layer_idx, None))
+            return
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        if w.shape != (self.H,):
+            raise ValueError(f"ffn_norm weight must have shape ({self.H},), got {w.shape}")
+        check(lib().hy_moe_set_ffn_norm(self.h, layer_idx, w.ctypes.data))
 
     def forward(self, layer_idx, x: Buf, T, out: Buf, stream=None):
         check(lib().hy_moe_forward(self.h, layer_idx, x.ptr, T, out.ptr, stream))

@@ -92,6 +92,13 @@ int hy_moe_upload_layer(hy_moe_ctx* ctx, uint32_t layer, const float* router_hos
 int hy_moe_synth_layer(hy_moe_ctx* ctx, uint32_t layer, uint64_t seed, float std,
                        const float* router_bias_host);
 
+/* The layer's post-attention RMSNorm weight [H] (post_attention_layernorm, GGUF
+ * blk.N.ffn_norm.weight), applied by hy_moe_stack_forward before the layer's MoE:
+ * DecoderLayerWeights::post_attn_ln_weight as decoder_layer_forward_cpu uses it
+ * (src/decoder_layer.cpp:33-34, src/hunyuan_gguf_loader.cpp:251).  w_host NULL
+ * returns the layer to unit weight (the default). */
+int hy_moe_set_ffn_norm(hy_moe_ctx* ctx, uint32_t layer, const float* w_host);
+
 /* ---- GGUF files ------------------------------------------------------------ */
 
 /* A GGUF file (format versions 2 and 3), memory mapped read-only.  Replaces the
@@ -120,6 +127,7 @@ int hy_gguf_get_f32(const hy_gguf* f, const char* key, float* out);
  *   blk.N.ffn_shared_down.weight           wtype  ne {I, H}
  *   blk.N.ffn_expert_<e>_gate_up.weight    wtype  ne {H, 2I}, e = 0..E-1
  *   blk.N.ffn_expert_<e>_down.weight       wtype  ne {I, H}
+ *   blk.N.ffn_norm.weight                  F32    ne {H}   (optional; absent: unit)
  * Types and shapes must match the context (else HY_ERR_INVALID naming the tensor);
  * hunyuan.hidden_size / moe_intermediate_size / num_experts / moe_topk, when present,
  * must agree with it too.  Replaces load_layer_weights + StackedExpertWeights
@@ -142,10 +150,12 @@ int hy_moe_forward_debug(hy_moe_ctx* ctx, uint32_t layer, const float* x_dev, ui
                          float* out_dev, float* logits_dev, float* weights_dev,
                          int32_t* indices_dev, void* stream);
 
-/* n_layers x [ RMSNorm(eps, unit weight) -> MoE -> residual add ] over resident
- * layers first..first+n_layers-1.  The decoder-layer MoE half of
- * decoder_layer_forward_cpu (src/decoder_layer.cpp:33-42) with rms_norm_f32
- * (src/rms_norm.cpp:9-33), stacked. */
+/* n_layers x [ h -> h + MoE(RMSNorm(h) * w) ] over resident layers
+ * first..first+n_layers-1, w the layer's ffn_norm weight (hy_moe_set_ffn_norm; unit
+ * by default).  The decoder-layer MoE half of decoder_layer_forward_cpu
+ * (src/decoder_layer.cpp:33-42) with rms_norm_f32 (src/rms_norm.cpp:9-33), stacked.
+ * For quantized weights the RMSNorm and the Q8_0 quantization of its output run as
+ * one pass, and the residual add is part of the combine. */
 int hy_moe_stack_forward(hy_moe_ctx* ctx, uint32_t first_layer, uint32_t n_layers,
                          const float* x_dev, uint32_t T, float eps, float* out_dev, void* stream);
 

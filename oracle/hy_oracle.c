@@ -955,16 +955,22 @@ int hyo_moe_forward_q(const hyo_qlayer* L, const float* x, uint32_t T, float* ou
     return 0;
 }
 
-/* RMSNorm with unit weight, sum of squares in the 64-lane blocked fmaf order shared
- * with the GPU kernel, then x * (1/sqrtf(ss/H + eps)) as src/rms_norm.cpp:26-30. */
-static void hyo_rms_norm_blocked_unit(const float* x, float* out, uint32_t H, float eps) {
+/* RMSNorm, sum of squares in the 64-lane blocked fmaf order shared with the GPU
+ * kernel, then x * (1/sqrtf(ss/H + eps)) * w as src/rms_norm.cpp:26-30 (w NULL: unit
+ * weight, the last multiply dropped). */
+static void hyo_rms_norm_blocked(const float* x, const float* w, float* out, uint32_t H, float eps) {
     float ss = hyo_blocked_dot(x, x, H);
     float rms = 1.0f / sqrtf(ss / (float)H + eps);
-    for (uint32_t j = 0; j < H; j++) out[j] = x[j] * rms;
+    if (w)
+        for (uint32_t j = 0; j < H; j++) out[j] = x[j] * rms * w[j];
+    else
+        for (uint32_t j = 0; j < H; j++) out[j] = x[j] * rms;
 }
 
-int hyo_moe_stack_q(const hyo_qlayer* layers, uint32_t n_layers, const float* x, uint32_t T,
-                    float eps, float* out, int nthreads) {
+/* The decoder layer's MoE half (src/decoder_layer.cpp:33-42), stacked: per layer
+ * h <- h + MoE(RMSNorm(h) * w_l), w_l = norm_w[l] (NULL array or entry: unit). */
+int hyo_moe_stack_qw(const hyo_qlayer* layers, const float* const* norm_w, uint32_t n_layers, const float* x,
+                     uint32_t T, float eps, float* out, int nthreads) {
     if (n_layers == 0) return -1;
     const uint32_t H = layers[0].H;
     for (uint32_t l = 0; l < n_layers; l++)
@@ -974,12 +980,23 @@ int hyo_moe_stack_q(const hyo_qlayer* layers, uint32_t n_layers, const float* x,
     float* y = (float*)malloc((size_t)T * H * sizeof(float));
     memcpy(cur, x, (size_t)T * H * sizeof(float));
     for (uint32_t l = 0; l < n_layers; l++) {
+        const float* w = norm_w ? norm_w[l] : NULL;
         for (uint32_t t = 0; t < T; t++)
-            hyo_rms_norm_blocked_unit(cur + (size_t)t * H, xn + (size_t)t * H, H, eps);
+            hyo_rms_norm_blocked(cur + (size_t)t * H, w, xn + (size_t)t * H, H, eps);
         hyo_moe_forward_q(&layers[l], xn, T, y, NULL, NULL, NULL, nthreads);
         for (size_t i = 0; i < (size_t)T * H; i++) cur[i] = cur[i] + y[i];
     }
     memcpy(out, cur, (size_t)T * H * sizeof(float));
     free(cur); free(xn); free(y);
     return 0;
+}
+
+/* RMSNorm in the blocked order on T rows (the GPU's rms_norm kernels' restatement). */
+void hyo_rms_norm_blocked_rows(const float* x, const float* w, float* out, uint32_t T, uint32_t H, float eps) {
+    for (uint32_t t = 0; t < T; t++) hyo_rms_norm_blocked(x + (size_t)t * H, w, out + (size_t)t * H, H, eps);
+}
+
+int hyo_moe_stack_q(const hyo_qlayer* layers, uint32_t n_layers, const float* x, uint32_t T,
+                    float eps, float* out, int nthreads) {
+    return hyo_moe_stack_qw(layers, NULL, n_layers, x, T, eps, out, nthreads);
 }

@@ -174,6 +174,12 @@ int hyo_moe_forward_q_rows(const hyo_qlayer* L, const float* x, uint32_t T,
 /* RMSNorm(eps, unit weight) -> MoE -> residual, over n_layers layers. */
 int hyo_moe_stack_q(const hyo_qlayer* layers, uint32_t n_layers, const float* x, uint32_t T,
                     float eps, float* out, int nthreads);
+/* The same with a post-attention RMSNorm weight per layer (norm_w or an entry NULL:
+ * unit weight): h <- h + MoE(RMSNorm(h) * w_l), src/decoder_layer.cpp:33-42. */
+int hyo_moe_stack_qw(const hyo_qlayer* layers, const float* const* norm_w, uint32_t n_layers, const float* x,
+                     uint32_t T, float eps, float* out, int nthreads);
+/* RMSNorm of T rows in the GPU kernels' blocked order (w NULL: unit weight). */
+void hyo_rms_norm_blocked_rows(const float* x, const float* w, float* out, uint32_t T, uint32_t H, float eps);
 
 void hyo_free(void* p);
 

@@ -104,6 +104,9 @@ def lib():
             "hyo_moe_forward_q": (C.c_int, [C.POINTER(QLayer), _fp, C.c_uint32, _fp, _fp, _fp, _ip, C.c_int]),
             "hyo_moe_forward_q_rows": (C.c_int, [C.POINTER(QLayer), _fp, C.c_uint32, _up, C.c_uint32, _fp, C.c_int]),
             "hyo_moe_stack_q": (C.c_int, [C.POINTER(QLayer), C.c_uint32, _fp, C.c_uint32, C.c_float, _fp, C.c_int]),
+            "hyo_moe_stack_qw": (C.c_int, [C.POINTER(QLayer), C.POINTER(_fp), C.c_uint32, _fp, C.c_uint32,
+                                           C.c_float, _fp, C.c_int]),
+            "hyo_rms_norm_blocked_rows": (None, [_fp, _fp, _fp, C.c_uint32, C.c_uint32, C.c_float]),
             "hyo_free": (None, [_vp]),
         }
         for name, (res, args) in sig.items():
@@ -307,6 +310,28 @@ def moe_stack_q(layers, x, eps=1e-5, nthreads=1):
     rc = lib().hyo_moe_stack_q(arr, len(layers), fp(x), x.shape[0], eps, fp(out), nthreads)
     if rc != 0:
         raise ValueError("hyo_moe_stack_q rejected the layers")
+    return out
+
+
+def moe_stack_qw(layers, norm_ws, x, eps=1e-5, nthreads=1):
+    """The stack with a post-attention RMSNorm weight per layer (None entries: unit)."""
+    x = f32(x)
+    arr = (QLayer * len(layers))(*[l.c() for l in layers])
+    keep = [None if w is None else f32(w) for w in norm_ws]
+    ptrs = (_fp * len(layers))(*[None if w is None else fp(w) for w in keep])
+    out = np.empty_like(x)
+    rc = lib().hyo_moe_stack_qw(arr, ptrs, len(layers), fp(x), x.shape[0], eps, fp(out), nthreads)
+    if rc != 0:
+        raise ValueError("hyo_moe_stack_qw rejected the layers")
+    return out
+
+
+def rms_norm_blocked(x, w=None, eps=1e-5):
+    """RMSNorm in the GPU kernels' blocked sum order (w None: unit weight)."""
+    x = f32(x)
+    out = np.empty_like(x)
+    wk = None if w is None else f32(w)
+    lib().hyo_rms_norm_blocked_rows(fp(x), None if wk is None else fp(wk), fp(out), x.shape[0], x.shape[1], eps)
     return out
 
 

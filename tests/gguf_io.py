@@ -65,12 +65,15 @@ def gguf_bytes(kvs, tensors, version=3, alignment=None, data_offsets=None):
     return bytes(out)
 
 
-def layer_tensors(layer, block):
+def layer_tensors(layer, block, ffn_norm=None):
     """The reference converter's tensor names for one MoE layer (oracle Layer, GGUF
-    layout: ne0 = in-features)."""
+    layout: ne0 = in-features); ffn_norm: the post-attention RMSNorm weight [H]."""
     H, I, E, wt = layer.H, layer.I, layer.E, layer.wtype
     p = f"blk.{block}."
     ts = [(p + "ffn_gate.weight", GGML_F32, [H, E], np.ascontiguousarray(layer.router, np.float32).tobytes())]
+    if ffn_norm is not None:
+        nw = np.ascontiguousarray(ffn_norm, np.float32)
+        ts.append((p + "ffn_norm.weight", GGML_F32, [nw.size], nw.tobytes()))
     if layer.shared_gu is not None:
         ts.append((p + "ffn_shared_gate_up.weight", wt, [H, 2 * I], layer.shared_gu.tobytes()))
         ts.append((p + "ffn_shared_down.weight", wt, [I, H], layer.shared_dn.tobytes()))

@@ -135,6 +135,36 @@ def test_layer_from_gguf_matches_oracle(gpu, tmp_path, wtype):
 
 
 @pytest.mark.gpu
+def test_layer_from_gguf_with_ffn_norm(gpu, tmp_path):
+    """blk.N.ffn_norm.weight (post_attention_layernorm) is picked up with the layer and
+    applied by the stack; a file without it leaves unit weight; a wrong shape is an
+    error."""
+    H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=21, std=0.05)
+    w = (0.5 + np.random.default_rng(21).random(H)).astype(np.float32)
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=32)
+    x = O.synth(22, 0, O.T_X, 0, (20, H), 1.0)
+    xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((20, H))
+    f = gpu.Gguf(_write(tmp_path, "n.gguf", G.gguf_bytes(G.layer_meta(layer), G.layer_tensors(layer, 2, ffn_norm=w))))
+    m.upload_gguf(0, f, 2)
+    f.close()
+    m.stack_forward(0, 1, xb, 20, 1e-5, ob)
+    np.testing.assert_array_equal(ob.numpy().view(np.uint32),
+                                  O.moe_stack_qw([layer], [w], x, eps=1e-5).view(np.uint32))
+    f = gpu.Gguf(_write(tmp_path, "u.gguf", G.gguf_bytes(G.layer_meta(layer), G.layer_tensors(layer, 2))))
+    m.upload_gguf(0, f, 2)
+    f.close()
+    m.stack_forward(0, 1, xb, 20, 1e-5, ob)
+    np.testing.assert_array_equal(ob.numpy().view(np.uint32), O.moe_stack_q([layer], x, eps=1e-5).view(np.uint32))
+    f = gpu.Gguf(_write(tmp_path, "b.gguf", G.gguf_bytes(G.layer_meta(layer),
+                                                           G.layer_tensors(layer, 2, ffn_norm=w[:-32]))))
+    with pytest.raises(gpu.HyError):
+        m.upload_gguf(0, f, 2)
+    f.close()
+    m.close()
+
+
+@pytest.mark.gpu
 def test_layer_from_gguf_without_shared_expert(gpu, tmp_path):
     H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
     layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=5, std=0.05, shared=False)

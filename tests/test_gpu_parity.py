@@ -308,6 +308,41 @@ def test_stack_matches_oracle(gpu):
     m.close()
 
 
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+def test_stack_with_norm_weights_matches_oracle(gpu, wtype):
+    """The decoder layer's MoE half with per-layer post-attention RMSNorm weights,
+    h <- h + MoE(RMSNorm(h) * w_l): quantized weights run the fused RMSNorm + Q8_0
+    pass.  Every token regime: decode routing (T <= 16), fused selection (T <= 32),
+    the batch path, and both expert paths."""
+    H, I, E, K, L = 256, 128, 16, 4, 3
+    layers = [O.synth_layer(H, I, E, K, wtype, seed=15, layer=l, std=0.05) for l in range(L)]
+    rng = np.random.default_rng(15)
+    ws = [rng.standard_normal(H).astype(np.float32), None, (0.5 + rng.random(H)).astype(np.float32)]
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=100, num_layers=L)
+    for l in range(L):
+        m.synth(l, seed=15, std=0.05)
+        m.set_ffn_norm(l, ws[l])
+    paths = [gpu.PATH_AUTO] + ([gpu.PATH_VALU, gpu.PATH_MFMA] if wtype != O.F32 else [])
+    for T in (1, 3, 24, 100):
+        x = O.synth(60 + T, 0, O.T_X, 0, (T, H), 1.0)
+        ref = O.moe_stack_qw(layers, ws, x, eps=1e-5)
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((T, H))
+        for path in paths:
+            m.set_path(path)
+            m.stack_forward(0, L, xb, T, 1e-5, ob)
+            assert_exact(ob.numpy(), ref, f"wtype={wtype} T={T} path={path}")
+    m.set_path(gpu.PATH_AUTO)
+    for l in range(L):
+        m.set_ffn_norm(l, None)
+    x = O.synth(7, 0, O.T_X, 0, (40, H), 1.0)
+    xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((40, H))
+    m.stack_forward(0, L, xb, 40, 1e-5, ob)
+    assert_exact(ob.numpy(), O.moe_stack_q(layers, x, eps=1e-5), "unit weight restored")
+    with pytest.raises(ValueError):
+        m.set_ffn_norm(0, np.ones(H + 1, np.float32))
+    m.close()
+
+
 def test_invalid_token_count_rejected(gpu, small_layers):
     m = gpu.Moe(SMALL["H"], SMALL["I"], SMALL["E"], SMALL["K"], O.Q8_0, max_tokens=8)
     xb = gpu.Buf.empty((16, SMALL["H"]))

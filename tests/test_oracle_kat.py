@@ -428,6 +428,46 @@ def test_q_stack_is_composition():
     np.testing.assert_array_equal(got, cur)
 
 
+def test_blocked_rms_norm_weight_properties():
+    """The weighted blocked RMSNorm: unit weight and w = 1 agree bit for bit; a
+    power-of-two weight scales the output exactly; a constant row has the closed form
+    c / sqrt(c^2 + eps) * w; and it stays within float rounding of the reference's
+    sequential-order rms_norm_f32 (src/rms_norm.cpp:9-33)."""
+    rng = np.random.default_rng(11)
+    T, H = 5, 4096
+    x = rng.standard_normal((T, H)).astype(np.float32) * 3
+    unit = O.rms_norm_blocked(x)
+    np.testing.assert_array_equal(O.rms_norm_blocked(x, np.ones(H, np.float32)), unit)
+    pw = np.exp2(rng.integers(-3, 4, size=H)).astype(np.float32)
+    np.testing.assert_array_equal(O.rms_norm_blocked(x, pw), unit * pw)
+    w = rng.standard_normal(H).astype(np.float32)
+    got = O.rms_norm_blocked(x, w, eps=1e-5)
+    np.testing.assert_array_equal(got, (unit * w).astype(np.float32))
+    ref = np.empty_like(x)
+    L = O.lib()
+    L.hyo_rms_norm_f32(O.fp(x), O.fp(w), O.fp(ref), T, H, np.float32(1e-5))
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-6
+    c = np.full((1, 64), 2.0, np.float32)   # sum of squares 256 is exact in any order
+    want = np.float32(2.0) * (np.float32(1.0) / np.sqrt(np.float32(4.0) + np.float32(1e-5)))
+    np.testing.assert_array_equal(O.rms_norm_blocked(c, eps=1e-5)[0], np.full(64, want, np.float32))
+
+
+def test_q_stack_with_norm_weights_is_composition():
+    """h <- h + MoE(RMSNorm(h) * w_l) per layer (src/decoder_layer.cpp:33-42), built
+    from the layer forward and the blocked RMSNorm; None weights give the unit stack."""
+    T, H, I, E, K = 4, 64, 32, 8, 2
+    layers = [O.synth_layer(H, I, E, K, O.Q4_0, seed=9, layer=l, std=0.05) for l in range(3)]
+    rng = np.random.default_rng(4)
+    ws = [rng.standard_normal(H).astype(np.float32), None, 0.5 + rng.random(H).astype(np.float32)]
+    x = O.synth(9, 0, O.T_X, 0, (T, H), 1.0)
+    got = O.moe_stack_qw(layers, ws, x, eps=1e-5)
+    cur = x.copy()
+    for lyr, w in zip(layers, ws):
+        cur = (cur + O.moe_forward_q(lyr, O.rms_norm_blocked(cur, w, eps=1e-5))).astype(np.float32)
+    np.testing.assert_array_equal(got, cur)
+    np.testing.assert_array_equal(O.moe_stack_qw(layers, [None] * 3, x), O.moe_stack_q(layers, x))
+
+
 def test_rows_match_full_layer():
     T, H, I, E, K = 9, 64, 32, 8, 3
     layer = O.synth_layer(H, I, E, K, O.Q4_0, seed=5, std=0.05)
