@@ -1,0 +1,373 @@
+// hy_attn.hip -- the attention half of a HunyuanImage-3 decoder layer on gfx950, in
+// fp32 (the reference's precision): attention_forward_cpu (src/attention.cpp:10-185)
+// and the KV-cache branch of decoder_layer_extended_f32
+// (src/hunyuan_extended.cpp:52-176), with rope_f32 (src/rms_norm.cpp:97-152) and the
+// 2D rotary tables (src/hunyuan_image_gen.cpp:11-117).
+//
+// Kernels:
+//  * gemm_nt_f32_kernel: C[M][N] = A[M][K] . W[N][K]^T on v_mfma_f32_32x32x2f32 (the
+//    QKV and output projections).  Work group 128 x 128, four waves of 64 x 64 (2 x 2
+//    MFMA tiles), K in steps of 16 straight from global memory into registers (the
+//    next step's loads are in flight while the current one multiplies).
+//  * rope_qknorm_kernel: one wave per (token, head): rotary embedding (1D positions,
+//    2D tables or none), per-head RMSNorm, written to q [T][nh][hd] and, for key
+//    heads, k / v into a [nkv][L][hd] cache at row pos0 + t.
+//  * flash_attn_kernel<HD>: one work group per (32-query tile, kv group), one wave
+//    per query head of the group (4 heads share the group's K / V blocks in LDS).
+//    Scores are computed transposed, S^T = K Q^T (keys on MFMA rows, queries on the
+//    lanes), so a query's online-softmax statistics stay in its lane pair; P^T then
+//    feeds O^T += V^T P^T straight from the score registers.
+//
+// fp32 MFMA layouts (v_mfma_f32_32x32x2f32, checked on the device): A lane l holds
+// A[l%32][l/32], B lane l holds B[l/32][l%32], result register v of lane l is
+// C[8*(v/4) + 4*(l/32) + v%4][l%32].  Operand k-slots can be any permutation of the
+// reduction index as long as A and B use the same one: lane half h takes k = 8h + j
+// at step j of a 16-wide chunk, so each lane reads 8 consecutive floats.
+#include "hy_device.hpp"
+#include "hy_launch.hpp"
+
+namespace hy {
+
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f_t mfma_f32(float a, float b, v16f_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- GEMM (NT)
+constexpr int GM_TILE = 128;
+
+__global__ __launch_bounds__(256, 2) void gemm_nt_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
+                                                             float* __restrict__ C, int M, int N, int K) {
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int lr = lane % 32, h = lane / 32;
+    const int m0 = blockIdx.y * GM_TILE + (wave / 2) * 64, n0 = blockIdx.x * GM_TILE + (wave % 2) * 64;
+    // operand rows of this lane (clamped for loads; the stores are guarded)
+    const float* pa[2];
+    const float* pb[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = min(m0 + 32 * i + lr, M - 1), c = min(n0 + 32 * i + lr, N - 1);
+        pa[i] = A + (size_t)r * K + 8 * h;
+        pb[i] = W + (size_t)c * K + 8 * h;
+    }
+    v16f_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
+    float4 a[2][2], b[2][2];  // [tile][lo/hi 4 floats]
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            a[i][0] = *reinterpret_cast<const float4*>(pa[i] + k0);
+            a[i][1] = *reinterpret_cast<const float4*>(pa[i] + k0 + 4);
+            b[i][0] = *reinterpret_cast<const float4*>(pb[i] + k0);
+            b[i][1] = *reinterpret_cast<const float4*>(pb[i] + k0 + 4);
+        }
+    };
+    load(0);
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        float av[2][8], bv[2][8];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const float4 x0 = a[i][0], x1 = a[i][1], y0 = b[i][0], y1 = b[i][1];
+            av[i][0] = x0.x; av[i][1] = x0.y; av[i][2] = x0.z; av[i][3] = x0.w;
+            av[i][4] = x1.x; av[i][5] = x1.y; av[i][6] = x1.z; av[i][7] = x1.w;
+            bv[i][0] = y0.x; bv[i][1] = y0.y; bv[i][2] = y0.z; bv[i][3] = y0.w;
+            bv[i][4] = y1.x; bv[i][5] = y1.y; bv[i][6] = y1.z; bv[i][7] = y1.w;
+        }
+        if (k0 + 16 < K) load(k0 + 16);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++) acc[ti][tj] = mfma_f32(av[ti][j], bv[tj][j], acc[ti][tj]);
+    }
+#pragma unroll
+    for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+        for (int tj = 0; tj < 2; tj++) {
+            const int col = n0 + 32 * tj + lr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = m0 + 32 * ti + 8 * (v / 4) + 4 * h + v % 4;
+                if (row < M) C[(size_t)row * N + col] = acc[ti][tj][v];
+            }
+        }
+}
+
+hipError_t launch_gemm_nt_f32(const float* A, const float* W, float* C, int M, int N, int K, hipStream_t s) {
+    const dim3 grid((N + GM_TILE - 1) / GM_TILE, (M + GM_TILE - 1) / GM_TILE);
+    hipLaunchKernelGGL(gemm_nt_f32_kernel, grid, dim3(256), 0, s, A, W, C, M, N, K);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- RoPE + QK-norm
+__global__ __launch_bounds__(256) void rope_qknorm_kernel(RopeNormArgs a) {
+    const int wid = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int heads = a.nh + a.nkv;
+    if (wid >= a.T * heads) return;
+    const int t = wid / heads, hh = wid % heads;
+    const bool is_q = hh < a.nh;
+    const int hd = a.hd, npair = hd / 2;
+    const float* src = a.qkv + (size_t)t * a.nqkv + (size_t)hh * hd;  // q heads, then k heads
+    const float pos = a.positions ? (float)a.positions[t] : (float)t;
+    constexpr int MAXP = 2;  // pairs per lane: hd <= 256
+    float r0[MAXP], r1[MAXP];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {
+        const int d = lane + WAVE * i;
+        r0[i] = r1[i] = 0.0f;
+        if (d >= npair) continue;
+        const float x0 = src[2 * d], x1 = src[2 * d + 1];
+        float c = 1.0f, sn = 0.0f;
+        bool rot = true;
+        if (a.mode == ROPE_1D) {
+            const float freq = 1.0f / powf(a.theta, (2.0f * (float)d) / (float)hd);
+            c = cosf(pos * freq);
+            sn = sinf(pos * freq);
+        } else if (a.mode == ROPE_TABLE) {
+            c = a.cos_t[(size_t)t * hd + 2 * d];
+            sn = a.sin_t[(size_t)t * hd + 2 * d];
+        } else {
+            rot = false;
+        }
+        if (rot) {
+            r0[i] = x0 * c - x1 * sn;
+            r1[i] = x0 * sn + x1 * c;
+        } else {
+            r0[i] = x0;
+            r1[i] = x1;
+        }
+        ss += r0[i] * r0[i];
+        ss += r1[i] * r1[i];
+    }
+    ss = wave_sum(ss);
+    const float rms = 1.0f / sqrtf(ss / (float)hd + a.eps);
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    float* dst = is_q ? a.q + ((size_t)t * a.nh + hh) * hd : a.k + ((size_t)(hh - a.nh) * a.L + a.pos0 + t) * hd;
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {
+        const int d = lane + WAVE * i;
+        if (d >= npair) continue;
+        const float w0 = w[2 * d], w1 = w[2 * d + 1];
+        // (x * rms) * w as attention_forward_cpu; x * (rms * w) as the cache branch
+        dst[2 * d] = a.norm_assoc ? r0[i] * (rms * w0) : r0[i] * rms * w0;
+        dst[2 * d + 1] = a.norm_assoc ? r1[i] * (rms * w1) : r1[i] * rms * w1;
+    }
+    if (!is_q) {  // the value row of this kv head, unchanged
+        const float* vs = a.qkv + (size_t)t * a.nqkv + (size_t)(a.nh + a.nkv) * hd + (size_t)(hh - a.nh) * hd;
+        float* vd = a.v + ((size_t)(hh - a.nh) * a.L + a.pos0 + t) * hd;
+        for (int d = lane; d < hd; d += WAVE) vd[d] = vs[d];
+    }
+}
+
+hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s) {
+    const int waves = a.T * (a.nh + a.nkv);
+    hipLaunchKernelGGL(rope_qknorm_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- 2D rotary tables
+// build_2d_rope (src/hunyuan_image_gen.cpp:11-69): one thread per (position, pair).
+__global__ void rope2d_table_kernel(int seq, int n_elem, int text_len, int img_h, int img_w, float base,
+                                    float* __restrict__ cos_out, float* __restrict__ sin_out) {
+    const int half = n_elem / 2;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= seq * half) return;
+    const int p = idx / half, d = idx % half;
+    float py, px;
+    if (p < text_len) {
+        py = (float)p;
+        px = (float)p;
+    } else {
+        const int i = p - text_len, row = i / img_w, col = i % img_w;
+        py = (float)text_len + (float)(img_h * img_w - img_h) / 2.0f + (float)row;
+        px = (float)text_len + (float)(img_h * img_w - img_w) / 2.0f + (float)col;
+    }
+    const float th = 1.0f / powf(base, (2.0f * (float)d) / (float)n_elem);
+    const float ang = (((d / 2) % 2) == 0 ? py : px) * th;
+    const float c = cosf(ang), sn = sinf(ang);
+    cos_out[(size_t)p * n_elem + 2 * d] = c;
+    cos_out[(size_t)p * n_elem + 2 * d + 1] = c;
+    sin_out[(size_t)p * n_elem + 2 * d] = sn;
+    sin_out[(size_t)p * n_elem + 2 * d + 1] = sn;
+}
+
+hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,
+                               float* sin_out, hipStream_t s) {
+    const int n = seq * (n_elem / 2);
+    hipLaunchKernelGGL(rope2d_table_kernel, dim3((n + 255) / 256), dim3(256), 0, s, seq, n_elem, text_len, img_h,
+                       img_w, base, cos_out, sin_out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- flash attention
+// LDS row pitches (floats): K rows are read 16 B per lane by 32 rows (pitch = 4 mod
+// 64 banks: 16 consecutive rows hit 16 distinct bank quads); V rows 4 B per lane by
+// two rows 4 apart per instruction (pitch = 8 mod 16: the two half-waves land on
+// opposite bank halves).
+template <int HD>
+struct FaShape {
+    static constexpr int KP = HD + 4, VP = HD + 8;
+    static constexpr int KV_F4 = 32 * HD / 4;        // float4 per K (or V) block
+    static constexpr int PER_THREAD = 2 * KV_F4 / 256;
+    static_assert((2 * KV_F4) % 256 == 0, "K and V blocks split evenly over the work group");
+};
+
+template <int HD>
+__global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
+    using S = FaShape<HD>;
+    __shared__ __align__(16) float ks[32 * S::KP];
+    __shared__ __align__(16) float vs[32 * S::VP];
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int lr = lane % 32, h = lane / 32;
+    const int n_qt = (a.T + 31) / 32;
+    // longest (causal) query tiles first
+    const int qt = n_qt - 1 - (int)(blockIdx.x / a.nkv);
+    const int g = (int)(blockIdx.x % a.nkv);
+    const int q0 = qt * 32;
+    const int head = g * 4 + wave;  // 4 query heads per kv group
+    const int qrow = min(q0 + lr, a.T - 1);
+
+    // Q resident: lane (query lr, half h) holds Q[q][16c + 8h + j]
+    float qv[HD / 2];
+    {
+        const float* qp = a.q + ((size_t)qrow * a.nh + head) * HD + 8 * h;
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++) {
+            const float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * c);
+            const float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
+            qv[8 * c + 0] = x0.x; qv[8 * c + 1] = x0.y; qv[8 * c + 2] = x0.z; qv[8 * c + 3] = x0.w;
+            qv[8 * c + 4] = x1.x; qv[8 * c + 5] = x1.y; qv[8 * c + 6] = x1.z; qv[8 * c + 7] = x1.w;
+        }
+    }
+    // visible keys: all kv_len, or (causal) keys <= q_pos0 + q
+    const int last_q = min(q0 + 31, a.T - 1);
+    const int key_end = a.causal ? min(a.kv_len, a.q_pos0 + last_q + 1) : a.kv_len;
+    const int nblk = (key_end + 31) / 32;
+
+    const float* kg = a.k + (size_t)g * a.L * HD;
+    const float* vg = a.v + (size_t)g * a.L * HD;
+    float4 pre[S::PER_THREAD];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < S::PER_THREAD; i++) {
+            const int f = tid + 256 * i;                   // float4 index over [K block | V block]
+            const int which = f / S::KV_F4, r = (f % S::KV_F4) / (HD / 4), c4 = f % (HD / 4);
+            const int key = min(kb * 32 + r, a.kv_len - 1);
+            pre[i] = *reinterpret_cast<const float4*>((which ? vg : kg) + (size_t)key * HD + 4 * c4);
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < S::PER_THREAD; i++) {
+            const int f = tid + 256 * i;
+            const int which = f / S::KV_F4, r = (f % S::KV_F4) / (HD / 4), c4 = f % (HD / 4);
+            float* dst = which ? vs + r * S::VP + 4 * c4 : ks + r * S::KP + 4 * c4;
+            *reinterpret_cast<float4*>(dst) = pre[i];
+        }
+    };
+
+    v16f_t o[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) o[c] = v16f_t{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int my_q = a.q_pos0 + q0 + lr;  // key index of this lane's query (causal bound)
+
+    fetch(0);
+    for (int kb = 0; kb < nblk; kb++) {
+        __syncthreads();  // the previous block's LDS reads are done
+        stash();
+        if (kb + 1 < nblk) fetch(kb + 1);
+        __syncthreads();
+        // S^T[key][q] = sum_d K[key][d] Q[q][d]
+        v16f_t s = v16f_t{};
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++) {
+            const float* kr = ks + lr * S::KP + 16 * c + 8 * h;
+            const float4 k0 = *reinterpret_cast<const float4*>(kr);
+            const float4 k1 = *reinterpret_cast<const float4*>(kr + 4);
+            const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) s = mfma_f32(kk[j], qv[8 * c + j], s);
+        }
+        // scale, mask, online softmax over this lane pair's 32 keys
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int key = kb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+            float x = s[v] * a.scale;
+            if (key >= a.kv_len || (a.causal && key > my_q)) x = -INFINITY;
+            s[v] = x;
+            mloc = fmaxf(mloc, x);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, WAVE));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+        float psum = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float p = s[v] == -INFINITY ? 0.0f : expf(s[v] - m_new);
+            s[v] = p;
+            psum += p;
+        }
+        psum += __shfl_xor(psum, 32, WAVE);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++) o[c] *= alpha;
+        // O^T[d][q] += sum_key V[key][d] P^T[key][q]
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int key = 8 * (v / 4) + 4 * h + v % 4;
+                o[c] = mfma_f32(vs[key * S::VP + 32 * c + lr], s[v], o[c]);
+            }
+    }
+    if (q0 + lr >= a.T) return;
+    const float inv = 1.0f / l_run;
+    float* op = a.out + ((size_t)(q0 + lr) * a.nh + head) * HD;
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; v4++) {
+            const int d = 32 * c + 8 * v4 + 4 * h;
+            *reinterpret_cast<float4*>(op + d) = make_float4(o[c][4 * v4] * inv, o[c][4 * v4 + 1] * inv,
+                                                             o[c][4 * v4 + 2] * inv, o[c][4 * v4 + 3] * inv);
+        }
+}
+
+hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)(((a.T + 31) / 32) * a.nkv));
+    if (a.hd == 128)
+        hipLaunchKernelGGL(flash_attn_kernel<128>, grid, dim3(256), 0, s, a);
+    else if (a.hd == 64)
+        hipLaunchKernelGGL(flash_attn_kernel<64>, grid, dim3(256), 0, s, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// k / v rows of the [nkv][L][hd] buffers back to the reference's [T][nkv][hd] layout
+__global__ void gather_kv_kernel(const float* __restrict__ src, int nkv, int L, int pos0, int T, int hd,
+                                 float* __restrict__ dst) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)T * nkv * hd) return;
+    const int d = (int)(idx % hd), g = (int)((idx / hd) % nkv), t = (int)(idx / ((size_t)hd * nkv));
+    dst[idx] = src[((size_t)g * L + pos0 + t) * hd + d];
+}
+
+hipError_t launch_gather_kv(const float* src, int nkv, int L, int pos0, int T, int hd, float* dst, hipStream_t s) {
+    const size_t n = (size_t)T * nkv * hd;
+    hipLaunchKernelGGL(gather_kv_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nkv, L, pos0, T, hd,
+                       dst);
+    return hipGetLastError();
+}
+
+}  // namespace hy

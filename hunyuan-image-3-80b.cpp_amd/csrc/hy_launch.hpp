@@ -92,4 +92,41 @@ enum KernelId {
     KID_COUNT
 };
 
+// attention half of the decoder layer (hy_attn.hip)
+enum { ROPE_NONE = 0, ROPE_1D = 1, ROPE_TABLE = 2 };
+struct RopeNormArgs {
+    const float* qkv;         // [T][nqkv] projection output
+    int T, nh, nkv, hd, nqkv;
+    int mode;                 // ROPE_NONE / ROPE_1D (positions or 0..T-1) / ROPE_TABLE (cos_t, sin_t rows)
+    const int* positions;
+    float theta;
+    const float* cos_t;
+    const float* sin_t;
+    const float* q_norm;
+    const float* k_norm;
+    float eps;
+    int norm_assoc;           // 0: (x * rms) * w, 1: x * (rms * w)
+    float* q;                 // [T][nh][hd]
+    float* k;                 // [nkv][L][hd], rows pos0 + t
+    float* v;
+    int L, pos0;
+};
+struct FlashArgs {
+    const float* q;           // [T][nh][hd]
+    const float* k;           // [nkv][L][hd]
+    const float* v;
+    float* out;               // [T][nh][hd]
+    int T, nh, nkv, hd, L;
+    int kv_len;               // keys 0..kv_len-1 exist
+    int q_pos0;               // key index of query 0 (causal bound: key <= q_pos0 + t)
+    int causal;
+    float scale;
+};
+hipError_t launch_gemm_nt_f32(const float* A, const float* W, float* C, int M, int N, int K, hipStream_t s);
+hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s);
+hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s);
+hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,
+                               float* sin_out, hipStream_t s);
+hipError_t launch_gather_kv(const float* src, int nkv, int L, int pos0, int T, int hd, float* dst, hipStream_t s);
+
 }  // namespace hy

@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhy_moe.so")
 ROOT = os.path.dirname(HERE)
 HEADER = os.path.join(ROOT, "include", "hy_moe.h")
+ATTN_HEADER = os.path.join(ROOT, "include", "hy_attn.h")
 
 F32, Q4_0, Q8_0 = 0, 2, 8
 PATH_AUTO, PATH_VALU, PATH_MFMA = 0, 1, 2
@@ -36,6 +37,14 @@ class Config(C.Structure):
     ]
 
 
+class AttnConfig(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32), ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+        ("max_tokens", C.c_uint32), ("max_cache", C.c_uint32), ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_float), ("device", C.c_int32),
+    ]
+
+
 _vp = C.c_void_p
 _u32, _i32, _u64, _f = C.c_uint32, C.c_int32, C.c_uint64, C.c_float
 _SIGS = {
@@ -46,6 +55,16 @@ _SIGS = {
     "hy_moe_upload_layer": (C.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "hy_moe_synth_layer": (C.c_int, [_vp, _u32, _u64, _f, _vp]),
     "hy_moe_set_ffn_norm": (C.c_int, [_vp, _u32, _vp]),
+    "hy_attn_create": (C.c_int, [C.POINTER(AttnConfig), C.POINTER(_vp)]),
+    "hy_attn_destroy": (C.c_int, [_vp]),
+    "hy_attn_upload": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "hy_attn_forward": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hy_attn_forward_cached": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "hy_attn_cache_reset": (C.c_int, [_vp]),
+    "hy_attn_cache_len": (C.c_int, [_vp, C.POINTER(_u32)]),
+    "hy_build_2d_rope": (C.c_int, [_u32, _u32, _u32, _u32, _u32, _f, _vp, _vp, _vp]),
+    "hy_attn_prof_enable": (C.c_int, [_vp, _i32]),
+    "hy_attn_prof_read": (C.c_int, [_vp, _u32, C.POINTER(_u64), C.POINTER(C.c_double)]),
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
     "hy_moe_forward_debug": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "hy_moe_stack_forward": (C.c_int, [_vp, _u32, _u32, _vp, _u32, _f, _vp, _vp]),
@@ -355,7 +374,7 @@ def synth_fill(n, seed, layer, tensor, expert, std):
 
 
 def header_symbols(path=HEADER):
-    """Function names declared in include/hy_moe.h."""
+    """Function names declared in a C header (default include/hy_moe.h)."""
     import re
     txt = open(path).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
@@ -403,3 +422,81 @@ class Gguf:
             self.close()
         except Exception:
             pass
+
+
+ATTN_KERNELS = ("qkv_proj", "rope_qknorm", "attention", "o_proj")
+
+
+class Attn:
+    """One resident attention layer (include/hy_attn.h): weights, key / value cache
+    and the fp32 kernels of attention_forward_cpu and the KV-cache branch."""
+
+    def __init__(self, H, nh, nkv, hd, max_tokens, max_cache=0, eps=1e-5, theta=10000.0, device=0):
+        cfg = AttnConfig(H, nh, nkv, hd, max_tokens, max_cache, eps, theta, device)
+        h = _vp()
+        check(lib().hy_attn_create(C.byref(cfg), C.byref(h)))
+        self.h = h
+        self.H, self.nh, self.nkv, self.hd = H, nh, nkv, hd
+
+    def close(self):
+        if self.h:
+            check(lib().hy_attn_destroy(self.h))
+            self.h = None
+
+    def upload(self, qkv_w, o_w, q_norm, k_norm):
+        arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (qkv_w, o_w, q_norm, k_norm)]
+        nq, nk = self.nh * self.hd, self.nkv * self.hd
+        want = [(nq + 2 * nk, self.H), (self.H, nq), (self.hd,), (self.hd,)]
+        for a, w in zip(arrs, want):
+            if a.shape != w:
+                raise ValueError(f"attention weight shape {a.shape}, want {w}")
+        check(lib().hy_attn_upload(self.h, *[a.ctypes.data for a in arrs]))
+
+    def forward(self, x: Buf, T, out: Buf, positions=None, dq=None, dk=None, dv=None, stream=None):
+        check(lib().hy_attn_forward(self.h, x.ptr, T, positions.ptr if positions is not None else None, out.ptr,
+                                    dq.ptr if dq is not None else None, dk.ptr if dk is not None else None,
+                                    dv.ptr if dv is not None else None, stream))
+
+    def forward_cached(self, x: Buf, T, out: Buf, cos=None, sin=None, stream=None):
+        check(lib().hy_attn_forward_cached(self.h, x.ptr, T, cos.ptr if cos is not None else None,
+                                           sin.ptr if sin is not None else None, out.ptr, stream))
+
+    def cache_reset(self):
+        check(lib().hy_attn_cache_reset(self.h))
+
+    def cache_len(self):
+        n = _u32()
+        check(lib().hy_attn_cache_len(self.h, C.byref(n)))
+        return n.value
+
+    def prof_enable(self, on):
+        check(lib().hy_attn_prof_enable(self.h, 1 if on else 0))
+
+    def prof_read(self):
+        out = {}
+        for k, name in enumerate(ATTN_KERNELS):
+            n, ms = _u64(), C.c_double()
+            check(lib().hy_attn_prof_read(self.h, k, C.byref(n), C.byref(ms)))
+            out[name] = (n.value, ms.value)
+        return out
+
+    def run(self, x, positions=None, debug=False):
+        """Host convenience: x [T][H] -> out (and q, k, v when debug)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        xb, ob = Buf.from_array(x), Buf.empty((T, self.H))
+        pb = Buf.from_array(np.ascontiguousarray(positions, dtype=np.int32)) if positions is not None else None
+        dq = Buf.empty((T, self.nh, self.hd)) if debug else None
+        dk = Buf.empty((T, self.nkv, self.hd)) if debug else None
+        dv = Buf.empty((T, self.nkv, self.hd)) if debug else None
+        self.forward(xb, T, ob, pb, dq, dk, dv)
+        if debug:
+            return ob.numpy(), dq.numpy(), dk.numpy(), dv.numpy()
+        return ob.numpy()
+
+
+def build_2d_rope(seq, n_elem, text_len, img_h, img_w, base=10000.0):
+    """Device rotary tables (cos, sin) as Bufs [seq][n_elem]."""
+    cos, sin = Buf.empty((seq, n_elem)), Buf.empty((seq, n_elem))
+    check(lib().hy_build_2d_rope(seq, n_elem, text_len, img_h, img_w, base, cos.ptr, sin.ptr, None))
+    return cos, sin

@@ -1,0 +1,91 @@
+/*
+ * hy_attn.h -- C ABI of the MI355X (gfx950) attention half of a HunyuanImage-3
+ * decoder layer: GQA self-attention with QK RMSNorm and rotary embeddings, in fp32.
+ *
+ * Conventions as hy_moe.h: plain pointers and sizes, "dev" = device (HBM) address,
+ * "host" = host memory, `stream` = hipStream_t as void* (NULL: default stream), every
+ * function returns HY_OK or a negative hy_status with hy_last_error() set, and
+ * nothing is written to caller-owned outputs on failure.
+ *
+ * The reference's interface for this path is attention_forward_cpu and its
+ * AttentionWeights / HunyuanConfig (src/hunyuan_model.h:13-40, 93-101), the KV-cache branch of
+ * decoder_layer_extended_f32 (src/hunyuan_extended.cpp:52-176), rope_f32
+ * (src/rms_norm.cpp:97-152) and build_2d_rope / apply_rope_2d_f32
+ * (src/hunyuan_image_gen.cpp:11-117).  One context holds one layer's weights and
+ * key / value cache, resident on the device.
+ */
+#ifndef HY_ATTN_H
+#define HY_ATTN_H
+
+#include <stdint.h>
+
+#include "hy_moe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The attention fields of HunyuanConfig (src/hunyuan_model.h:13-40): hidden_size,
+ * num_attention_heads, num_key_value_heads, attention_head_dim, rms_norm_eps,
+ * rope_theta.  The GPU kernels take head_dim 64 or 128 and 4 query heads per kv
+ * head (HunyuanImage-3: 32 / 8); other shapes are HY_ERR_UNSUPPORTED.
+ * max_tokens bounds T per call; max_cache the key / value cache length. */
+typedef struct {
+    uint32_t hidden;      /* H */
+    uint32_t n_heads;     /* query heads */
+    uint32_t n_kv_heads;  /* key / value heads */
+    uint32_t head_dim;    /* 64 or 128 */
+    uint32_t max_tokens;  /* 1..16384 */
+    uint32_t max_cache;   /* cache positions (0: no cache) */
+    float rms_norm_eps;
+    float rope_theta;
+    int32_t device;
+} hy_attn_config;
+
+typedef struct hy_attn_ctx hy_attn_ctx;
+
+int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out);
+int hy_attn_destroy(hy_attn_ctx* ctx);
+
+/* AttentionWeights (src/hunyuan_model.h:93-101), F32, host memory, reference layout:
+ * qkv_weight [(n_heads + 2 n_kv_heads) head_dim][hidden] (query head rows, then key
+ * heads, then value heads), o_weight [hidden][n_heads head_dim], q_norm_weight and
+ * k_norm_weight [head_dim].  Uploaded once. */
+int hy_attn_upload(hy_attn_ctx* ctx, const float* qkv_weight_host, const float* o_weight_host,
+                   const float* q_norm_host, const float* k_norm_host);
+
+/* attention_forward_cpu (src/attention.cpp:10-185): out = o_proj(causal GQA
+ * attention of RMSNorm(RoPE(q)), RMSNorm(RoPE(k)), v) for T tokens of x [T][hidden].
+ * positions_dev: int32 [T] rotary positions (NULL: 0..T-1).  debug_q_dev
+ * [T][n_heads][head_dim], debug_k_dev / debug_v_dev [T][n_kv_heads][head_dim]
+ * (each may be NULL) receive q, k, v after RoPE and norm, as the reference's debug
+ * outputs.  Does not touch the cache. */
+int hy_attn_forward(hy_attn_ctx* ctx, const float* x_dev, uint32_t T, const int32_t* positions_dev, float* out_dev,
+                    float* debug_q_dev, float* debug_k_dev, float* debug_v_dev, void* stream);
+
+/* The KV-cache branch of decoder_layer_extended_f32 (src/hunyuan_extended.cpp:52-176):
+ * project the T new tokens, rotate them by rows 0..T-1 of the 2D tables cos_dev /
+ * sin_dev [T][head_dim] (both NULL: no rotation, as use_2d_rope = false), QK RMSNorm,
+ * append k / v at the cache's current length, and let every new token attend to
+ * all cached positions (no mask among the new tokens, as the reference).
+ * HY_ERR_INVALID when the cache would overflow (the cache is left unchanged). */
+int hy_attn_forward_cached(hy_attn_ctx* ctx, const float* x_dev, uint32_t T, const float* cos_dev,
+                           const float* sin_dev, float* out_dev, void* stream);
+/* KVCache::reset / current_len (src/hunyuan_image_gen.h:179-193), for this layer. */
+int hy_attn_cache_reset(hy_attn_ctx* ctx);
+int hy_attn_cache_len(const hy_attn_ctx* ctx, uint32_t* len);
+
+/* build_2d_rope (src/hunyuan_image_gen.cpp:11-69) on the device: cos_dev / sin_dev
+ * [seq][n_elem] for text_len text positions followed by an img_h x img_w grid. */
+int hy_build_2d_rope(uint32_t seq, uint32_t n_elem, uint32_t text_len, uint32_t img_h, uint32_t img_w, float base,
+                     float* cos_dev, float* sin_dev, void* stream);
+
+/* Per-kernel timing of this context's launches (as hy_moe_prof_*): kernel ids
+ * 0 = qkv_proj, 1 = rope_qknorm, 2 = attention, 3 = o_proj. */
+int hy_attn_prof_enable(hy_attn_ctx* ctx, int32_t on);
+int hy_attn_prof_read(hy_attn_ctx* ctx, uint32_t kid, uint64_t* launches, double* total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,141 @@
+"""GPU attention (include/hy_attn.h) against the attention oracle
+(oracle/hy_oracle_attn.c, the reference's fp32 algorithm).
+
+The GPU computes the same fp32 mathematics in other summation orders (MFMA tiles,
+online softmax), so the bar is a float tolerance, stated here: normwise relative error
+max|a-b| / max|b| <= 1e-4 (ten times tighter than the 1e-3 the layer outputs are held
+to) and cosine similarity >= 0.99999."""
+import numpy as np
+import pytest
+
+import hy_oracle_attn as A
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def check(got, ref, what):
+    got, ref = got.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
+    err = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+    cos = got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref) + 1e-300)
+    assert err <= TOL and cos >= 0.99999, f"{what}: rel_err={err:.3e} cos={cos:.8f}"
+
+
+SHAPES = [dict(H=256, nh=8, nkv=2, hd=64), dict(H=512, nh=4, nkv=1, hd=128)]
+
+
+def _ctx(gpu, shp, max_tokens=128, max_cache=0, seed=0):
+    w = A.synth_weights(shp["H"], shp["nh"], shp["nkv"], shp["hd"], seed=seed, std=0.05, norm_jitter=0.2)
+    m = gpu.Attn(shp["H"], shp["nh"], shp["nkv"], shp["hd"], max_tokens, max_cache=max_cache)
+    m.upload(w.qkv_w, w.o_w, w.q_norm, w.k_norm)
+    return m, w
+
+
+@pytest.mark.parametrize("shp", SHAPES, ids=["hd64", "hd128"])
+@pytest.mark.parametrize("T", [1, 5, 32, 33, 100])
+def test_forward_matches_oracle(gpu, shp, T):
+    m, w = _ctx(gpu, shp, seed=T)
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((T, shp["H"])).astype(np.float32)
+    for positions in (None, rng.integers(0, 3 * T + 5, size=T).astype(np.int32)):
+        out, dq, dk, dv = m.run(x, positions=positions, debug=True)
+        ref, rq, rk, rv = A.attention_forward(w, x, positions=positions)
+        tag = f"T={T} hd={shp['hd']} positions={'given' if positions is not None else 'none'}"
+        check(dq, rq, tag + " q")
+        check(dk, rk, tag + " k")
+        check(dv, rv, tag + " v")
+        check(out, ref, tag + " out")
+    m.close()
+
+
+def test_forward_full_head_shape(gpu):
+    """HunyuanImage-3's attention shape (hidden 4096, 32 query / 8 kv heads of 128)
+    at 64 tokens."""
+    shp = dict(H=4096, nh=32, nkv=8, hd=128)
+    m, w = _ctx(gpu, shp, max_tokens=64, seed=3)
+    x = np.random.default_rng(3).standard_normal((64, 4096)).astype(np.float32)
+    out = m.run(x)
+    ref, *_ = A.attention_forward(w, x)
+    check(out, ref, "full shape")
+    m.close()
+
+
+def test_forward_is_causal(gpu):
+    shp = SHAPES[0]
+    m, _ = _ctx(gpu, shp)
+    x = np.random.default_rng(1).standard_normal((70, shp["H"])).astype(np.float32)
+    a = m.run(x)
+    x2 = x.copy()
+    x2[40:] += 1.0
+    b = m.run(x2)
+    np.testing.assert_array_equal(a[:40], b[:40])
+    m.close()
+
+
+def test_2d_tables_match_oracle(gpu):
+    for text, ih, iw in ((5, 3, 4), (0, 8, 8), (16, 1, 1)):
+        seq = text + ih * iw
+        for hd in (64, 128):
+            cos, sin = gpu.build_2d_rope(seq, hd, text, ih, iw)
+            rc, rs = A.build_2d_rope(seq, hd, text, ih, iw)
+            assert np.abs(cos.numpy() - rc).max() < 4e-6 and np.abs(sin.numpy() - rs).max() < 4e-6
+
+
+@pytest.mark.parametrize("shp", SHAPES, ids=["hd64", "hd128"])
+def test_cached_matches_oracle(gpu, shp):
+    """Chunks of new tokens through the KV cache with 2D rotary tables (device-built,
+    the same tables given to the oracle), then a chunk without rotation."""
+    m, w = _ctx(gpu, shp, max_tokens=64, max_cache=80, seed=11)
+    cache = A.KVCache(shp["nkv"], shp["hd"], max_len=80)
+    rng = np.random.default_rng(11)
+    text, ih, iw = 4, 6, 6
+    cos_d, sin_d = gpu.build_2d_rope(text + ih * iw, shp["hd"], text, ih, iw)
+    cos, sin = cos_d.numpy(), sin_d.numpy()
+    pos = 0
+    for n in (3, 1, 36):
+        x = rng.standard_normal((n, shp["H"])).astype(np.float32)
+        cs, sn = gpu.Buf.from_array(cos[pos:pos + n]), gpu.Buf.from_array(sin[pos:pos + n])
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((n, shp["H"]))
+        m.forward_cached(xb, n, ob, cs, sn)
+        ref = A.attention_cached(w, x, cache, cos=cos[pos:pos + n], sin=sin[pos:pos + n])
+        check(ob.numpy(), ref, f"cached chunk at {pos} (+{n})")
+        pos += n
+        assert m.cache_len() == pos == cache.cur_len
+    x = rng.standard_normal((5, shp["H"])).astype(np.float32)
+    xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((5, shp["H"]))
+    m.forward_cached(xb, 5, ob)
+    check(ob.numpy(), A.attention_cached(w, x, cache), "cached chunk without rotation")
+    m.close()
+
+
+def test_cache_overflow_and_reset(gpu):
+    shp = SHAPES[0]
+    m, _ = _ctx(gpu, shp, max_tokens=16, max_cache=10)
+    x = np.random.default_rng(2).standard_normal((8, shp["H"])).astype(np.float32)
+    xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((8, shp["H"]))
+    m.forward_cached(xb, 8, ob)
+    first = ob.numpy()
+    with pytest.raises(gpu.HyError):
+        m.forward_cached(xb, 8, ob)
+    assert m.cache_len() == 8
+    m.cache_reset()
+    assert m.cache_len() == 0
+    m.forward_cached(xb, 8, ob)
+    np.testing.assert_array_equal(ob.numpy(), first)
+    m.close()
+
+
+def test_invalid_calls_rejected(gpu):
+    shp = SHAPES[0]
+    m = gpu.Attn(shp["H"], shp["nh"], shp["nkv"], shp["hd"], 16)
+    xb, ob = gpu.Buf.empty((4, shp["H"])), gpu.Buf.empty((4, shp["H"]))
+    with pytest.raises(gpu.HyError):   # weights not uploaded
+        m.forward(xb, 4, ob)
+    w = A.synth_weights(shp["H"], shp["nh"], shp["nkv"], shp["hd"])
+    m.upload(w.qkv_w, w.o_w, w.q_norm, w.k_norm)
+    with pytest.raises(gpu.HyError):   # T above max_tokens
+        m.forward(xb, 17, ob)
+    with pytest.raises(gpu.HyError):   # no cache configured
+        m.forward_cached(xb, 4, ob)
+    m.close()

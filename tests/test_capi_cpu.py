@@ -17,6 +17,23 @@ def test_library_exports_header(hy):
     assert not missing, missing
 
 
+def test_library_exports_attention_header(hy):
+    syms = hy.header_symbols(hy.ATTN_HEADER)
+    assert len(syms) >= 10
+    L = hy.lib()
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+
+
+def test_attention_config_rejected_before_device(hy):
+    """Unsupported shapes are refused before any device call."""
+    for kw in (dict(hd=96), dict(nh=8, nkv=4), dict(max_tokens=0)):
+        args = dict(H=256, nh=8, nkv=2, hd=64, max_tokens=16)
+        args.update(kw)
+        with pytest.raises(hy.HyError):
+            hy.Attn(args["H"], args["nh"], args["nkv"], args["hd"], args["max_tokens"])
+
+
 def test_cxx_mirror_header_lists_reference_names():
     txt = open(os.path.join(ROOT, "include", "hunyuan_moe_full.h")).read()
     for name in ("MoERoutingConfig", "MoEGateOutput", "topkgating_full", "topkgating_easy", "einsum_dispatch",
