@@ -14,6 +14,7 @@ c4 Q4_0 T=4096 Zipf-skewed routing, c5 32-layer Q8_0 stack T=4096.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
     python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
     python bench.py --gguf-load /tmp/l.gguf [--config c2]   # layer load from a GGUF file
+    python bench.py --attn [--tokens 4096]   # attention half of a decoder layer (fp32)
 
 roofline.traffic (HBM bytes per launch of the dominant kernel) is read from
 profiles/hbm_traffic.md, the table made from rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -35,6 +36,8 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 H, I, E, K = 4096, 3072, 64, 8
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_INT8 = 5.0e15         # ops/s, dense int8 MFMA
+PEAK_FP32_MFMA = 157.3e12  # FLOP/s, dense fp32 MFMA
+ATTN = dict(H=4096, nh=32, nkv=8, hd=128)   # HunyuanImage-3 attention shape
 PARAMS_PER_EXPERT = 3 * H * I
 BYTES = {0: 4.0, 8: 34.0 / 32.0, 2: 18.0 / 32.0}   # bytes per weight element
 
@@ -188,6 +191,86 @@ def cpu_baseline(wl, seed, budget_s=15.0):
                       f"layer, {nthreads} OpenMP threads, {dt:.1f} s"}
 
 
+def attn_flops(kname, T):
+    """Algorithmic FLOPs of one attention kernel launch at T tokens (causal)."""
+    Hh, nh, nkv, hd = ATTN["H"], ATTN["nh"], ATTN["nkv"], ATTN["hd"]
+    if kname == "qkv_proj":
+        return 2.0 * T * (nh + 2 * nkv) * hd * Hh
+    if kname == "o_proj":
+        return 2.0 * T * Hh * nh * hd
+    if kname == "attention":
+        return 4.0 * hd * nh * T * (T + 1) / 2      # QK^T and PV over the causal triangle
+    return 0.0
+
+
+def attn_cpu_baseline(w, T_sample=192):
+    """attention_forward_cpu restated (the oracle, one thread, the reference's scalar
+    fp32 loops) on a T_sample-token sequence of the same shape."""
+    import hy_oracle_attn as A
+    x = np.random.default_rng(7).standard_normal((T_sample, ATTN["H"])).astype(np.float32)
+    t0 = time.perf_counter()
+    A.attention_forward(w, x)
+    dt = time.perf_counter() - t0
+    return {"value": T_sample / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"one {T_sample}-token causal sequence through the oracle's attention_forward_cpu "
+                      f"restatement (scalar fp32, 1 thread), {dt:.1f} s"}
+
+
+def attn_main(a, hy):
+    """Attention half of a decoder layer: x [T][4096] -> QKV projection -> RoPE ->
+    QK-norm -> causal GQA attention -> o_proj, fp32, weights N(0, 0.02) resident."""
+    import hy_oracle_attn as A
+    T = a.tokens or 4096
+    w = A.synth_weights(ATTN["H"], ATTN["nh"], ATTN["nkv"], ATTN["hd"], seed=a.seed, std=0.02)
+    m = hy.Attn(ATTN["H"], ATTN["nh"], ATTN["nkv"], ATTN["hd"], T)
+    m.upload(w.qkv_w, w.o_w, w.q_norm, w.k_norm)
+    x = hy.Buf.from_array(np.random.default_rng(a.seed).standard_normal((T, ATTN["H"])).astype(np.float32))
+    out = hy.Buf.empty((T, ATTN["H"]))
+    for _ in range(a.warmup):
+        m.forward(x, T, out)
+    hy.sync()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    t0 = time.perf_counter()
+    hy.check(hy.lib().hy_event_record(ev0, None))
+    for _ in range(a.steps):
+        m.forward(x, T, out)
+    hy.check(hy.lib().hy_event_record(ev1, None))
+    hy.sync()
+    wall = time.perf_counter() - t0
+    ms = hy.C.c_float()
+    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+    ms_per_step = ms.value / a.steps
+    m.prof_enable(True)
+    for _ in range(a.steps):
+        m.forward(x, T, out)
+    hy.sync()
+    prof = {k: v for k, v in m.prof_read().items() if v[0] > 0}
+    m.prof_enable(False)
+    dom = max(prof, key=lambda k: prof[k][1])
+    avg_s = prof[dom][1] / prof[dom][0] / 1e3
+    fl = attn_flops(dom, T)
+    total = sum(attn_flops(k, T) for k in prof)
+    res = {
+        "metric": "attention tokens/sec (fp32, causal GQA), 1 MI355X", "value": T / (ms_per_step / 1e3),
+        "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"attention_f32_t{T}", "hidden": ATTN["H"], "heads": ATTN["nh"],
+                   "kv_heads": ATTN["nkv"], "head_dim": ATTN["hd"], "tokens": T, "causal": True},
+        "step_tflops": total / (ms_per_step / 1e3) / 1e12,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": fl / avg_s / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
+                     "unit": "TFLOP/s", "frac": fl / avg_s / PEAK_FP32_MFMA, "traffic": None,
+                     "algorithmic_flops_per_launch": fl, "avg_launch_ms": avg_s * 1e3},
+        "kernels_ms": {k: round(t / n, 5) for k, (n, t) in prof.items()},
+        "wall_s": wall,
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = attn_cpu_baseline(w)
+    print(json.dumps(res), flush=True)
+    m.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +282,7 @@ def main():
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
+    ap.add_argument("--attn", action="store_true", help="time the attention half instead of the MoE layer")
     ap.add_argument("--gguf-load", default=None, metavar="PATH",
                     help="time loading one real-shape layer from a GGUF file written at PATH")
     a = ap.parse_args()
@@ -215,6 +299,9 @@ def main():
         return
     if a.gguf_load:
         gguf_load(hy, WORKLOADS[a.config]["wtype"], a.gguf_load, a.seed)
+        return
+    if a.attn:
+        attn_main(a, hy)
         return
     wl = dict(WORKLOADS[a.config])
     if a.tokens:
