@@ -5,8 +5,9 @@
 // 2D rotary tables (src/hunyuan_image_gen.cpp:11-117).
 //
 // Kernels:
-//  * gemm_nt_f32_kernel: C[M][N] = A[M][K] . W[N][K]^T on v_mfma_f32_32x32x2f32 (the
-//    QKV and output projections).  Work group 128 x 128, four waves of 64 x 64 (2 x 2
+//  * gemm_nt_f32_kernel: C[M][N] = (R[M][N] +) A[M][K] . W[N][K]^T on
+//    v_mfma_f32_32x32x2f32 (the QKV and output projections; R is the decoder layer's
+//    residual stream when the output projection adds it).  Work group 128 x 128, four waves of 64 x 64 (2 x 2
 //    MFMA tiles), K in steps of 16 straight from global memory into registers (the
 //    next step's loads are in flight while the current one multiplies).
 //  * rope_qknorm_kernel: one wave per (token, head): rotary embedding (1D positions,
@@ -38,7 +39,8 @@ __device__ __forceinline__ v16f_t mfma_f32(float a, float b, v16f_t c) {
 constexpr int GM_TILE = 128;
 
 __global__ __launch_bounds__(256, 2) void gemm_nt_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
-                                                             float* __restrict__ C, int M, int N, int K) {
+                                                             const float* __restrict__ R, float* __restrict__ C, int M,
+                                                             int N, int K) {
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int lr = lane % 32, h = lane / 32;
     const int m0 = blockIdx.y * GM_TILE + (wave / 2) * 64, n0 = blockIdx.x * GM_TILE + (wave % 2) * 64;
@@ -94,14 +96,17 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f32_kernel(const float* __rest
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const int row = m0 + 32 * ti + 8 * (v / 4) + 4 * h + v % 4;
-                if (row < M) C[(size_t)row * N + col] = acc[ti][tj][v];
+                if (row >= M) continue;
+                const size_t o = (size_t)row * N + col;
+                C[o] = R ? R[o] + acc[ti][tj][v] : acc[ti][tj][v];  // optional residual: R + A.W^T
             }
         }
 }
 
-hipError_t launch_gemm_nt_f32(const float* A, const float* W, float* C, int M, int N, int K, hipStream_t s) {
+hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
+                              hipStream_t s) {
     const dim3 grid((N + GM_TILE - 1) / GM_TILE, (M + GM_TILE - 1) / GM_TILE);
-    hipLaunchKernelGGL(gemm_nt_f32_kernel, grid, dim3(256), 0, s, A, W, C, M, N, K);
+    hipLaunchKernelGGL(gemm_nt_f32_kernel, grid, dim3(256), 0, s, A, W, R, C, M, N, K);
     return hipGetLastError();
 }
 

@@ -12,6 +12,8 @@
 
 namespace hy {
 int set_last_error(int code, const std::string& msg);  // hy_capi.hip
+int moe_hidden(const hy_moe_ctx* c);                   // hy_capi.hip
+int moe_device(const hy_moe_ctx* c);
 }
 
 namespace {
@@ -62,8 +64,12 @@ struct hy_attn_ctx {
     float* kc = nullptr;      // [nkv][Lc][hd] cache
     float* vc = nullptr;
     float* merged = nullptr;  // [Tm][nh*hd]
+    float* in_norm = nullptr; // input_layernorm weight [H] (used when has_in_norm)
+    float* xn = nullptr;      // decoder layer: normed input [Tm][H]
+    float* hres = nullptr;    // decoder layer: x + attention [Tm][H]
     uint32_t cache_len = 0;
     bool loaded = false;
+    bool has_in_norm = false;
     bool prof = false;
     std::vector<ProfRec> pending;
     std::vector<hipEvent_t> free_events;
@@ -121,8 +127,9 @@ int timed(hy_attn_ctx* c, int kid, hipStream_t s, F&& launch) {
 // values land in k / v ([nkv][L][hd]) at row pos0 + t
 int run(hy_attn_ctx* c, const float* x, int T, int mode, const int32_t* positions, const float* cos_t,
         const float* sin_t, int norm_assoc, float* k, float* v, int L, int pos0, int kv_len, int causal, float* out,
-        hipStream_t s) {
-    HY_TRY(timed(c, AK_QKV, s, [&] { return hy::launch_gemm_nt_f32(x, c->qkv_w, c->qkv, T, c->nqkv, c->H, s); }));
+        hipStream_t s, const float* resid = nullptr) {
+    HY_TRY(timed(c, AK_QKV, s,
+                 [&] { return hy::launch_gemm_nt_f32(x, c->qkv_w, nullptr, c->qkv, T, c->nqkv, c->H, s); }));
     hy::RopeNormArgs r{c->qkv, T, c->nh, c->nkv, c->hd, c->nqkv, mode, positions, c->cfg.rope_theta, cos_t, sin_t,
                        c->q_norm, c->k_norm, c->cfg.rms_norm_eps, norm_assoc, c->q, k, v, L, pos0};
     HY_TRY(timed(c, AK_ROPE, s, [&] { return hy::launch_rope_qknorm(r, s); }));
@@ -130,7 +137,7 @@ int run(hy_attn_ctx* c, const float* x, int T, int mode, const int32_t* position
                     1.0f / sqrtf((float)c->hd)};
     HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s); }));
     HY_TRY(timed(c, AK_OPROJ, s,
-                 [&] { return hy::launch_gemm_nt_f32(c->merged, c->o_w, out, T, c->H, c->nh * c->hd, s); }));
+                 [&] { return hy::launch_gemm_nt_f32(c->merged, c->o_w, resid, out, T, c->H, c->nh * c->hd, s); }));
     return HY_OK;
 }
 
@@ -169,7 +176,8 @@ int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out) {
     } parts[] = {{&c->qkv_w, (size_t)c->nqkv * H}, {&c->o_w, H * nq},        {&c->q_norm, (size_t)c->hd},
                  {&c->k_norm, (size_t)c->hd},      {&c->qkv, Tm * c->nqkv},  {&c->q, Tm * nq},
                  {&c->kf, Tm * nk},                {&c->vf, Tm * nk},        {&c->kc, Lc * nk},
-                 {&c->vc, Lc * nk},                {&c->merged, Tm * nq}};
+                 {&c->vc, Lc * nk},                {&c->merged, Tm * nq},    {&c->in_norm, H},
+                 {&c->xn, Tm * H},                 {&c->hres, Tm * H}};
     size_t total = 0;
     for (auto& p : parts) total += al256(p.n * 4);
     if (hipMalloc(&c->arena, total) != hipSuccess) {
@@ -247,6 +255,40 @@ int hy_attn_forward_cached(hy_attn_ctx* c, const float* x, uint32_t T, const flo
                pos0, pos0 + (int)T, 0, out, s));
     c->cache_len += T;
     return HY_OK;
+}
+
+int hy_attn_set_input_norm(hy_attn_ctx* c, const float* w) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (!w) {
+        c->has_in_norm = false;
+        return HY_OK;
+    }
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    HIP_TRY(hipMemcpy(c->in_norm, w, (size_t)c->H * 4, hipMemcpyHostToDevice));
+    c->has_in_norm = true;
+    return HY_OK;
+}
+
+int hy_decoder_layer_forward(hy_attn_ctx* c, hy_moe_ctx* moe, uint32_t moe_layer, const float* x, uint32_t T,
+                             const int32_t* positions, float* out, float* debug_h, void* stream) {
+    if (!c || !moe) return fail(HY_ERR_INVALID, "null context");
+    if (hy::moe_hidden(moe) != c->H || hy::moe_device(moe) != c->cfg.device)
+        return fail(HY_ERR_INVALID, "the MoE context (hidden %d, device %d) does not match the attention context "
+                    "(hidden %d, device %d)", hy::moe_hidden(moe), hy::moe_device(moe), c->H, c->cfg.device);
+    if (!c->loaded) return fail(HY_ERR_STATE, "attention weights not uploaded");
+    if (!x || !out) return fail(HY_ERR_INVALID, "null x/out");
+    if (T == 0 || T > (uint32_t)c->Tm) return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%d", T, c->Tm);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int iT = (int)T;
+    const float eps = c->cfg.rms_norm_eps;
+    // input_layernorm -> self-attention -> h = x + attention (in the output projection)
+    HIP_TRY(c->has_in_norm ? hy::launch_rms_norm_w(x, c->in_norm, iT, c->H, eps, c->xn, s)
+                           : hy::launch_rms_norm(x, iT, c->H, eps, c->xn, s));
+    HY_TRY(run(c, c->xn, iT, hy::ROPE_1D, positions, nullptr, nullptr, 0, c->kf, c->vf, c->Tm, 0, iT, 1, c->hres, s,
+               x));
+    if (debug_h) HIP_TRY(hipMemcpyAsync(debug_h, c->hres, (size_t)T * c->H * 4, hipMemcpyDeviceToDevice, s));
+    // post_attention_layernorm -> MoE -> out = h + MoE (the MoE context's layer and norm)
+    return hy_moe_stack_forward(moe, moe_layer, 1, c->hres, T, eps, out, stream);
 }
 
 int hy_attn_cache_reset(hy_attn_ctx* c) {

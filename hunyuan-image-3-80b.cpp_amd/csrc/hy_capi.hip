@@ -325,6 +325,8 @@ int set_last_error(int code, const std::string& msg) {
     g_last_error = msg;
     return code;
 }
+int moe_hidden(const hy_moe_ctx* c) { return c ? c->H : 0; }
+int moe_device(const hy_moe_ctx* c) { return c ? c->cfg.device : -1; }
 const GgufFile& gguf_file(const hy_gguf* g);  // host/hy_gguf.cpp
 }  // namespace hy
 

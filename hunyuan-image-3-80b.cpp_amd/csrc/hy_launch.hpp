@@ -122,7 +122,9 @@ struct FlashArgs {
     int causal;
     float scale;
 };
-hipError_t launch_gemm_nt_f32(const float* A, const float* W, float* C, int M, int N, int K, hipStream_t s);
+// C = A . W^T, plus R elementwise when R is not null (R may alias nothing written here)
+hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
+                              hipStream_t s);
 hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s);
 hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s);
 hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,

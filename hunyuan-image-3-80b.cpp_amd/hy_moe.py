@@ -63,6 +63,8 @@ _SIGS = {
     "hy_attn_cache_reset": (C.c_int, [_vp]),
     "hy_attn_cache_len": (C.c_int, [_vp, C.POINTER(_u32)]),
     "hy_build_2d_rope": (C.c_int, [_u32, _u32, _u32, _u32, _u32, _f, _vp, _vp, _vp]),
+    "hy_attn_set_input_norm": (C.c_int, [_vp, _vp]),
+    "hy_decoder_layer_forward": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
     "hy_attn_prof_enable": (C.c_int, [_vp, _i32]),
     "hy_attn_prof_read": (C.c_int, [_vp, _u32, C.POINTER(_u64), C.POINTER(C.c_double)]),
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
@@ -460,6 +462,23 @@ class Attn:
     def forward_cached(self, x: Buf, T, out: Buf, cos=None, sin=None, stream=None):
         check(lib().hy_attn_forward_cached(self.h, x.ptr, T, cos.ptr if cos is not None else None,
                                            sin.ptr if sin is not None else None, out.ptr, stream))
+
+    def set_input_norm(self, w=None):
+        """input_layernorm weight [H] (None: unit) for decoder_layer_forward."""
+        if w is None:
+            check(lib().hy_attn_set_input_norm(self.h, None))
+            return
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        if w.shape != (self.H,):
+            raise ValueError(f"input norm weight must have shape ({self.H},), got {w.shape}")
+        check(lib().hy_attn_set_input_norm(self.h, w.ctypes.data))
+
+    def decoder_layer_forward(self, moe, moe_layer, x: Buf, T, out: Buf, positions=None, debug_h=None,
+                              stream=None):
+        """decoder_layer_forward_cpu: out = h + MoE(RMSNorm(h)), h = x + attention(RMSNorm(x))."""
+        check(lib().hy_decoder_layer_forward(self.h, moe.h, moe_layer, x.ptr, T,
+                                             positions.ptr if positions is not None else None, out.ptr,
+                                             debug_h.ptr if debug_h is not None else None, stream))
 
     def cache_reset(self):
         check(lib().hy_attn_cache_reset(self.h))

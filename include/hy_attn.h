@@ -80,6 +80,19 @@ int hy_attn_cache_len(const hy_attn_ctx* ctx, uint32_t* len);
 int hy_build_2d_rope(uint32_t seq, uint32_t n_elem, uint32_t text_len, uint32_t img_h, uint32_t img_w, float base,
                      float* cos_dev, float* sin_dev, void* stream);
 
+/* decoder_layer_forward_cpu (src/decoder_layer.cpp:9-48) on the device, the attention
+ * context supplying input_layernorm + self-attention and the MoE context the
+ * post-attention half:
+ *   h   = x + attention(RMSNorm(x) * w_in)            (residual 1, in the o_proj)
+ *   out = h + MoE_layer(RMSNorm(h) * w_post)           (hy_moe_stack_forward, 1 layer)
+ * w_in: hy_attn_set_input_norm (input_layernorm, GGUF blk.N.attn_norm.weight; NULL:
+ * unit); w_post: the MoE layer's hy_moe_set_ffn_norm.  The contexts must share
+ * hidden size and device; eps is this context's rms_norm_eps.  debug_h_dev
+ * (nullable) receives h [T][hidden]. */
+int hy_attn_set_input_norm(hy_attn_ctx* ctx, const float* w_host);
+int hy_decoder_layer_forward(hy_attn_ctx* attn, hy_moe_ctx* moe, uint32_t moe_layer, const float* x_dev, uint32_t T,
+                             const int32_t* positions_dev, float* out_dev, float* debug_h_dev, void* stream);
+
 /* Per-kernel timing of this context's launches (as hy_moe_prof_*): kernel ids
  * 0 = qkv_proj, 1 = rope_qknorm, 2 = attention, 3 = o_proj. */
 int hy_attn_prof_enable(hy_attn_ctx* ctx, int32_t on);

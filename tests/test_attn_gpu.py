@@ -139,3 +139,40 @@ def test_invalid_calls_rejected(gpu):
     with pytest.raises(gpu.HyError):   # no cache configured
         m.forward_cached(xb, 4, ob)
     m.close()
+
+
+def test_decoder_layer_matches_oracle(gpu):
+    """decoder_layer_forward_cpu (src/decoder_layer.cpp:9-48) on the device: the
+    residual stream h = x + attention(RMSNorm(x) * w_in) to the float tolerance above,
+    and out = h + MoE(RMSNorm(h) * w_post) bit for bit against the oracle's MoE half
+    evaluated on the device's h (the MoE path is exact given its input)."""
+    import hy_oracle as O
+    H, I, E, K = 256, 128, 16, 4
+    shp = dict(H=H, nh=8, nkv=2, hd=64)
+    att, w = _ctx(gpu, shp, max_tokens=64, seed=21)
+    rng = np.random.default_rng(21)
+    w_in = (0.5 + rng.random(H)).astype(np.float32)
+    w_post = (0.5 + rng.random(H)).astype(np.float32)
+    att.set_input_norm(w_in)
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=21, layer=0, std=0.05)
+    moe = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=64)
+    moe.synth(0, seed=21, std=0.05)
+    moe.set_ffn_norm(0, w_post)
+    for T in (1, 20, 64):
+        x = rng.standard_normal((T, H)).astype(np.float32)
+        xb, ob, hb = gpu.Buf.from_array(x), gpu.Buf.empty((T, H)), gpu.Buf.empty((T, H))
+        att.decoder_layer_forward(moe, 0, xb, T, ob, debug_h=hb)
+        h = hb.numpy()
+        xn = np.empty_like(x)
+        O.lib().hyo_rms_norm_f32(O.fp(x), O.fp(w_in), O.fp(xn), T, H, np.float32(1e-5))
+        h_ref = (x + A.attention_forward(w, xn)[0]).astype(np.float32)
+        check(h, h_ref, f"T={T} residual stream")
+        ref = O.moe_stack_qw([layer], [w_post], h, eps=1e-5)
+        np.testing.assert_array_equal(ob.numpy().view(np.uint32), ref.view(np.uint32), err_msg=f"T={T} out")
+    other = gpu.Moe(2 * H, I, E, K, O.Q8_0, max_tokens=8)
+    xb, ob = gpu.Buf.empty((4, H)), gpu.Buf.empty((4, H))
+    with pytest.raises(gpu.HyError):
+        att.decoder_layer_forward(other, 0, xb, 4, ob)
+    other.close()
+    moe.close()
+    att.close()
