@@ -359,6 +359,38 @@ hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// embedding_lookup_f32 (src/hunyuan_full_model.cpp:276-290): row ids[t] of the table;
+// an id outside the vocabulary gives a zero row instead of an out-of-bounds read
+__global__ void embed_kernel(const int* __restrict__ ids, const float* __restrict__ table, int T, int H, int vocab,
+                             float* __restrict__ out) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
+    const int h4 = H / 4;
+    if (idx >= (size_t)T * h4) return;
+    const int t = (int)(idx / h4), c = (int)(idx % h4);
+    const int id = ids[t];
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (id >= 0 && id < vocab) v = reinterpret_cast<const float4*>(table + (size_t)id * H)[c];
+    reinterpret_cast<float4*>(out)[idx] = v;
+}
+
+hipError_t launch_embed(const int* ids, const float* table, int T, int H, int vocab, float* out, hipStream_t s) {
+    const size_t n = (size_t)T * (H / 4);
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ids, table, T, H, vocab,
+                       out);
+    return hipGetLastError();
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ out, size_t n, float v) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < n) out[idx] = v;
+}
+
+hipError_t launch_fill_f32(float* out, size_t n, float v, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, n, v);
+    return hipGetLastError();
+}
+
 // k / v rows of the [nkv][L][hd] buffers back to the reference's [T][nkv][hd] layout
 __global__ void gather_kv_kernel(const float* __restrict__ src, int nkv, int L, int pos0, int T, int hd,
                                  float* __restrict__ dst) {

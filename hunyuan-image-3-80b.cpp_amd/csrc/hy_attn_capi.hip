@@ -1,19 +1,25 @@
-// hy_attn_capi.hip -- the C ABI of the attention half (include/hy_attn.h): context,
-// resident weights and key / value cache, forward orchestration, timing.
+// hy_attn_capi.hip -- the C ABI of the attention half and of the resident backbone
+// (include/hy_attn.h): per-layer attention weights and key / value caches, a work
+// arena shared by the layers, forward orchestration, timing; the model context
+// (embedding, decoder layers, final norm, lm_head).
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <string>
 #include <vector>
 
 #include "../../include/hy_attn.h"
+#include "../host/hy_gguf.hpp"
+#include "hy_device.hpp"
 #include "hy_launch.hpp"
 
 namespace hy {
 int set_last_error(int code, const std::string& msg);  // hy_capi.hip
 int moe_hidden(const hy_moe_ctx* c);                   // hy_capi.hip
 int moe_device(const hy_moe_ctx* c);
+const GgufFile& gguf_file(const hy_gguf* g);           // host/hy_gguf.cpp
 }
 
 namespace {
@@ -47,29 +53,36 @@ struct ProfRec {
     hipEvent_t a, b;
 };
 
+struct AttnLayer {
+    void* base = nullptr;      // one allocation: weights, norms, cache
+    float* qkv_w = nullptr;    // [nqkv][H]
+    float* o_w = nullptr;      // [H][nh*hd]
+    float* q_norm = nullptr;   // [hd]
+    float* k_norm = nullptr;
+    float* in_norm = nullptr;  // input_layernorm [H] (used when has_in_norm)
+    float* kc = nullptr;       // [nkv][Lc][hd]
+    float* vc = nullptr;
+    uint32_t cache_len = 0;
+    bool loaded = false;
+    bool has_in_norm = false;
+};
+
+size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+
 }  // namespace
 
 struct hy_attn_ctx {
     hy_attn_config cfg{};
     int H = 0, nh = 0, nkv = 0, hd = 0, nqkv = 0, Tm = 0, Lc = 0;
-    void* arena = nullptr;
-    float* qkv_w = nullptr;   // [nqkv][H]
-    float* o_w = nullptr;     // [H][nh*hd]
-    float* q_norm = nullptr;  // [hd]
-    float* k_norm = nullptr;
-    float* qkv = nullptr;     // [Tm][nqkv]
-    float* q = nullptr;       // [Tm][nh][hd]
-    float* kf = nullptr;      // [nkv][Tm][hd] (forward without cache)
+    std::vector<AttnLayer> layers;
+    void* arena = nullptr;     // work buffers shared by the layers
+    float* qkv = nullptr;      // [Tm][nqkv]
+    float* q = nullptr;        // [Tm][nh][hd]
+    float* kf = nullptr;       // [nkv][Tm][hd] (forward without cache)
     float* vf = nullptr;
-    float* kc = nullptr;      // [nkv][Lc][hd] cache
-    float* vc = nullptr;
-    float* merged = nullptr;  // [Tm][nh*hd]
-    float* in_norm = nullptr; // input_layernorm weight [H] (used when has_in_norm)
-    float* xn = nullptr;      // decoder layer: normed input [Tm][H]
-    float* hres = nullptr;    // decoder layer: x + attention [Tm][H]
-    uint32_t cache_len = 0;
-    bool loaded = false;
-    bool has_in_norm = false;
+    float* merged = nullptr;   // [Tm][nh*hd]
+    float* xn = nullptr;       // decoder layer: normed input [Tm][H]
+    float* hres = nullptr;     // decoder layer: x + attention [Tm][H]
     bool prof = false;
     std::vector<ProfRec> pending;
     std::vector<hipEvent_t> free_events;
@@ -77,9 +90,21 @@ struct hy_attn_ctx {
     double prof_ms[AK_COUNT] = {};
 };
 
-namespace {
+struct hy_model_ctx {
+    hy_model_config cfg{};
+    hy_attn_ctx* attn = nullptr;
+    hy_moe_ctx* moe = nullptr;
+    int H = 0, V = 0, Tm = 0, L = 0;
+    void* arena = nullptr;
+    float* embed = nullptr;    // [V][H]
+    float* fnorm = nullptr;    // [H]
+    float* lm_head = nullptr;  // [V][H]
+    float* ha = nullptr;       // hidden ping-pong [Tm][H]
+    float* hb = nullptr;
+    float* normed = nullptr;   // [Tm][H]
+};
 
-size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+namespace {
 
 int get_event(hy_attn_ctx* c, hipEvent_t* ev) {
     if (!c->free_events.empty()) {
@@ -123,21 +148,83 @@ int timed(hy_attn_ctx* c, int kid, hipStream_t s, F&& launch) {
     return HY_OK;
 }
 
+int check_layer(const hy_attn_ctx* c, uint32_t layer, bool need_loaded) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (layer >= c->layers.size()) return fail(HY_ERR_INVALID, "layer %u out of range", layer);
+    if (need_loaded && !c->layers[layer].loaded) return fail(HY_ERR_STATE, "attention layer %u not uploaded", layer);
+    return HY_OK;
+}
+
+int alloc_layer(hy_attn_ctx* c, AttnLayer& L) {
+    if (L.base) return HY_OK;
+    const size_t H = c->H, nq = (size_t)c->nh * c->hd, nk = (size_t)c->nkv * c->hd;
+    const size_t parts[] = {(size_t)c->nqkv * H, H * nq, (size_t)c->hd, (size_t)c->hd, H, (size_t)c->Lc * nk,
+                            (size_t)c->Lc * nk};
+    float** ptrs[] = {&L.qkv_w, &L.o_w, &L.q_norm, &L.k_norm, &L.in_norm, &L.kc, &L.vc};
+    size_t total = 0;
+    for (size_t n : parts) total += al256(n * 4);
+    if (hipMalloc(&L.base, total) != hipSuccess) {
+        L.base = nullptr;
+        return fail(HY_ERR_NOMEM, "hipMalloc of %zu bytes for an attention layer failed", total);
+    }
+    size_t o = 0;
+    for (int i = 0; i < 7; i++) {
+        *ptrs[i] = reinterpret_cast<float*>(static_cast<uint8_t*>(L.base) + o);
+        o += al256(parts[i] * 4);
+    }
+    return HY_OK;
+}
+
 // projection, rotary + norm, attention, output projection for T tokens whose keys /
-// values land in k / v ([nkv][L][hd]) at row pos0 + t
-int run(hy_attn_ctx* c, const float* x, int T, int mode, const int32_t* positions, const float* cos_t,
-        const float* sin_t, int norm_assoc, float* k, float* v, int L, int pos0, int kv_len, int causal, float* out,
-        hipStream_t s, const float* resid = nullptr) {
+// values land in k / v ([nkv][Lrows][hd]) at row pos0 + t; resid (nullable) is added
+// in the output projection
+int run(hy_attn_ctx* c, const AttnLayer& W, const float* x, int T, int mode, const int32_t* positions,
+        const float* cos_t, const float* sin_t, int norm_assoc, float* k, float* v, int Lrows, int pos0, int kv_len,
+        int causal, float* out, hipStream_t s, const float* resid = nullptr) {
     HY_TRY(timed(c, AK_QKV, s,
-                 [&] { return hy::launch_gemm_nt_f32(x, c->qkv_w, nullptr, c->qkv, T, c->nqkv, c->H, s); }));
+                 [&] { return hy::launch_gemm_nt_f32(x, W.qkv_w, nullptr, c->qkv, T, c->nqkv, c->H, s); }));
     hy::RopeNormArgs r{c->qkv, T, c->nh, c->nkv, c->hd, c->nqkv, mode, positions, c->cfg.rope_theta, cos_t, sin_t,
-                       c->q_norm, c->k_norm, c->cfg.rms_norm_eps, norm_assoc, c->q, k, v, L, pos0};
+                       W.q_norm, W.k_norm, c->cfg.rms_norm_eps, norm_assoc, c->q, k, v, Lrows, pos0};
     HY_TRY(timed(c, AK_ROPE, s, [&] { return hy::launch_rope_qknorm(r, s); }));
-    hy::FlashArgs f{c->q, k, v, c->merged, T, c->nh, c->nkv, c->hd, L, kv_len, pos0, causal,
+    hy::FlashArgs f{c->q, k, v, c->merged, T, c->nh, c->nkv, c->hd, Lrows, kv_len, pos0, causal,
                     1.0f / sqrtf((float)c->hd)};
     HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s); }));
     HY_TRY(timed(c, AK_OPROJ, s,
-                 [&] { return hy::launch_gemm_nt_f32(c->merged, c->o_w, resid, out, T, c->H, c->nh * c->hd, s); }));
+                 [&] { return hy::launch_gemm_nt_f32(c->merged, W.o_w, resid, out, T, c->H, c->nh * c->hd, s); }));
+    return HY_OK;
+}
+
+// F32 / F16 / BF16 GGUF tensor -> f32 host copy (row-major as stored: ne0 innermost)
+int gguf_f32(const hy::GgufFile& f, const std::string& name, uint64_t ne0, uint64_t ne1, bool optional,
+             std::vector<float>& out, bool* present) {
+    const hy::GgufTensor* t = f.find(name);
+    if (present) *present = t != nullptr;
+    if (!t) return optional ? HY_OK : fail(HY_ERR_INVALID, "GGUF file has no tensor %s", name.c_str());
+    const uint32_t want_dims = ne1 > 1 ? 2u : 1u;
+    if (t->n_dims != want_dims || t->ne[0] != ne0 || (want_dims == 2 && t->ne[1] != ne1))
+        return fail(HY_ERR_INVALID, "%s has shape [%llu, %llu], want [%llu, %llu]", name.c_str(),
+                    (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)ne0,
+                    (unsigned long long)ne1);
+    const size_t n = (size_t)ne0 * ne1;
+    out.resize(n);
+    if (t->type == hy::GGML_F32) {
+        std::memcpy(out.data(), t->data, n * 4);
+    } else if (t->type == hy::GGML_F16) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(t->data);
+        for (size_t i = 0; i < n; i++) {
+            _Float16 h;
+            std::memcpy(&h, src + i, 2);
+            out[i] = (float)h;
+        }
+    } else if (t->type == hy::GGML_BF16) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(t->data);
+        for (size_t i = 0; i < n; i++) {
+            const uint32_t b = (uint32_t)src[i] << 16;
+            std::memcpy(&out[i], &b, 4);
+        }
+    } else {
+        return fail(HY_ERR_UNSUPPORTED, "%s has ggml type %d; F32, F16 or BF16 expected", name.c_str(), t->type);
+    }
     return HY_OK;
 }
 
@@ -156,6 +243,8 @@ int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out) {
     if (cfg->n_kv_heads == 0 || cfg->n_heads != 4 * cfg->n_kv_heads)
         return fail(HY_ERR_UNSUPPORTED, "n_heads=%u n_kv_heads=%u: the kernels take 4 query heads per kv head",
                     cfg->n_heads, cfg->n_kv_heads);
+    if (cfg->num_layers == 0 || cfg->num_layers > 4096)
+        return fail(HY_ERR_INVALID, "num_layers=%u must be in 1..4096", cfg->num_layers);
     if (cfg->max_tokens == 0 || cfg->max_tokens > 16384)
         return fail(HY_ERR_INVALID, "max_tokens=%u must be in 1..16384", cfg->max_tokens);
     if (cfg->max_cache > 1u << 20) return fail(HY_ERR_INVALID, "max_cache=%u too large", cfg->max_cache);
@@ -169,30 +258,23 @@ int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out) {
     c->nqkv = (c->nh + 2 * c->nkv) * c->hd;
     c->Tm = (int)cfg->max_tokens;
     c->Lc = (int)cfg->max_cache;
-    const size_t H = c->H, nq = (size_t)c->nh * c->hd, nk = (size_t)c->nkv * c->hd, Tm = c->Tm, Lc = c->Lc;
+    c->layers.resize(cfg->num_layers);
+    const size_t H = c->H, nq = (size_t)c->nh * c->hd, nk = (size_t)c->nkv * c->hd, Tm = c->Tm;
     struct Part {
         float** p;
         size_t n;
-    } parts[] = {{&c->qkv_w, (size_t)c->nqkv * H}, {&c->o_w, H * nq},        {&c->q_norm, (size_t)c->hd},
-                 {&c->k_norm, (size_t)c->hd},      {&c->qkv, Tm * c->nqkv},  {&c->q, Tm * nq},
-                 {&c->kf, Tm * nk},                {&c->vf, Tm * nk},        {&c->kc, Lc * nk},
-                 {&c->vc, Lc * nk},                {&c->merged, Tm * nq},    {&c->in_norm, H},
-                 {&c->xn, Tm * H},                 {&c->hres, Tm * H}};
+    } parts[] = {{&c->qkv, Tm * c->nqkv}, {&c->q, Tm * nq},  {&c->kf, Tm * nk},   {&c->vf, Tm * nk},
+                 {&c->merged, Tm * nq},   {&c->xn, Tm * H}, {&c->hres, Tm * H}};
     size_t total = 0;
     for (auto& p : parts) total += al256(p.n * 4);
     if (hipMalloc(&c->arena, total) != hipSuccess) {
         delete c;
-        return fail(HY_ERR_NOMEM, "hipMalloc of %zu bytes for the attention context failed", total);
+        return fail(HY_ERR_NOMEM, "hipMalloc of %zu bytes for the attention work arena failed", total);
     }
     size_t o = 0;
     for (auto& p : parts) {
         *p.p = reinterpret_cast<float*>(static_cast<uint8_t*>(c->arena) + o);
         o += al256(p.n * 4);
-    }
-    if (hipMemset(c->arena, 0, total) != hipSuccess) {
-        (void)hipFree(c->arena);
-        delete c;
-        return fail(HY_ERR_HIP, "hipMemset of the attention context failed");
     }
     *out = c;
     return HY_OK;
@@ -207,32 +289,89 @@ int hy_attn_destroy(hy_attn_ctx* c) {
         (void)hipEventDestroy(r.b);
     }
     for (auto e : c->free_events) (void)hipEventDestroy(e);
+    for (auto& L : c->layers)
+        if (L.base) (void)hipFree(L.base);
     if (c->arena) (void)hipFree(c->arena);
     delete c;
     return HY_OK;
 }
 
-int hy_attn_upload(hy_attn_ctx* c, const float* qkv_w, const float* o_w, const float* qn, const float* kn) {
-    if (!c || !qkv_w || !o_w || !qn || !kn) return fail(HY_ERR_INVALID, "null argument");
+int hy_attn_upload(hy_attn_ctx* c, uint32_t layer, const float* qkv_w, const float* o_w, const float* qn,
+                   const float* kn) {
+    HY_TRY(check_layer(c, layer, false));
+    if (!qkv_w || !o_w || !qn || !kn) return fail(HY_ERR_INVALID, "null weight");
     HIP_TRY(hipSetDevice(c->cfg.device));
+    AttnLayer& L = c->layers[layer];
+    HY_TRY(alloc_layer(c, L));
     const size_t nq = (size_t)c->nh * c->hd;
-    HIP_TRY(hipMemcpy(c->qkv_w, qkv_w, (size_t)c->nqkv * c->H * 4, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(c->o_w, o_w, (size_t)c->H * nq * 4, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(c->q_norm, qn, (size_t)c->hd * 4, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(c->k_norm, kn, (size_t)c->hd * 4, hipMemcpyHostToDevice));
-    c->loaded = true;
+    HIP_TRY(hipMemcpy(L.qkv_w, qkv_w, (size_t)c->nqkv * c->H * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(L.o_w, o_w, (size_t)c->H * nq * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(L.q_norm, qn, (size_t)c->hd * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(L.k_norm, kn, (size_t)c->hd * 4, hipMemcpyHostToDevice));
+    L.loaded = true;
     return HY_OK;
 }
 
-int hy_attn_forward(hy_attn_ctx* c, const float* x, uint32_t T, const int32_t* positions, float* out, float* dq,
-                    float* dk, float* dv, void* stream) {
-    if (!c) return fail(HY_ERR_INVALID, "null ctx");
-    if (!c->loaded) return fail(HY_ERR_STATE, "attention weights not uploaded");
+int hy_attn_upload_gguf(hy_attn_ctx* c, uint32_t layer, const hy_gguf* g, uint32_t block) {
+    HY_TRY(check_layer(c, layer, false));
+    if (!g) return fail(HY_ERR_INVALID, "null file");
+    const hy::GgufFile& f = hy::gguf_file(g);
+    const std::string p = "blk." + std::to_string(block) + ".";
+    const uint64_t H = c->H, nq = (uint64_t)c->nh * c->hd, hd = c->hd;
+    std::vector<float> qkv, o, qn, kn, in;
+    bool has_in = false;
+    // every tensor first: nothing is uploaded from an incomplete or mismatched file
+    HY_TRY(gguf_f32(f, p + "attn_qkv.weight", H, (uint64_t)c->nqkv, false, qkv, nullptr));
+    HY_TRY(gguf_f32(f, p + "attn_output.weight", nq, H, false, o, nullptr));
+    HY_TRY(gguf_f32(f, p + "attn_q_norm.weight", hd, 1, false, qn, nullptr));
+    HY_TRY(gguf_f32(f, p + "attn_k_norm.weight", hd, 1, false, kn, nullptr));
+    HY_TRY(gguf_f32(f, p + "attn_norm.weight", H, 1, true, in, &has_in));
+    HY_TRY(hy_attn_upload(c, layer, qkv.data(), o.data(), qn.data(), kn.data()));
+    return hy_attn_set_input_norm(c, layer, has_in ? in.data() : nullptr);
+}
+
+int hy_attn_synth_layer(hy_attn_ctx* c, uint32_t layer, uint64_t seed, float std) {
+    HY_TRY(check_layer(c, layer, false));
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    AttnLayer& L = c->layers[layer];
+    HY_TRY(alloc_layer(c, L));
+    const float scale = std * hy::NORM_SCALE;
+    const size_t nq = (size_t)c->nh * c->hd;
+    HIP_TRY(hy::launch_synth_fill(L.qkv_w, (size_t)c->nqkv * c->H, hy::stream_key(seed, layer, hy::TENSOR_QKV, 0),
+                                  scale, nullptr));
+    HIP_TRY(hy::launch_synth_fill(L.o_w, (size_t)c->H * nq, hy::stream_key(seed, layer, hy::TENSOR_O, 0), scale,
+                                  nullptr));
+    HIP_TRY(hy::launch_fill_f32(L.q_norm, (size_t)c->hd, 1.0f, nullptr));
+    HIP_TRY(hy::launch_fill_f32(L.k_norm, (size_t)c->hd, 1.0f, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    L.loaded = true;
+    L.has_in_norm = false;
+    return HY_OK;
+}
+
+int hy_attn_set_input_norm(hy_attn_ctx* c, uint32_t layer, const float* w) {
+    HY_TRY(check_layer(c, layer, false));
+    AttnLayer& L = c->layers[layer];
+    if (!w) {
+        L.has_in_norm = false;
+        return HY_OK;
+    }
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    HY_TRY(alloc_layer(c, L));
+    HIP_TRY(hipMemcpy(L.in_norm, w, (size_t)c->H * 4, hipMemcpyHostToDevice));
+    L.has_in_norm = true;
+    return HY_OK;
+}
+
+int hy_attn_forward(hy_attn_ctx* c, uint32_t layer, const float* x, uint32_t T, const int32_t* positions, float* out,
+                    float* dq, float* dk, float* dv, void* stream) {
+    HY_TRY(check_layer(c, layer, true));
     if (!x || !out) return fail(HY_ERR_INVALID, "null x/out");
     if (T == 0 || T > (uint32_t)c->Tm) return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%d", T, c->Tm);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int iT = (int)T;
-    HY_TRY(run(c, x, iT, hy::ROPE_1D, positions, nullptr, nullptr, 0, c->kf, c->vf, c->Tm, 0, iT, 1, out, s));
+    HY_TRY(run(c, c->layers[layer], x, iT, hy::ROPE_1D, positions, nullptr, nullptr, 0, c->kf, c->vf, c->Tm, 0, iT,
+               1, out, s));
     const size_t nq = (size_t)c->nh * c->hd;
     if (dq) HIP_TRY(hipMemcpyAsync(dq, c->q, (size_t)T * nq * 4, hipMemcpyDeviceToDevice, s));
     if (dk) HIP_TRY(hy::launch_gather_kv(c->kf, c->nkv, c->Tm, 0, iT, c->hd, dk, s));
@@ -240,67 +379,59 @@ int hy_attn_forward(hy_attn_ctx* c, const float* x, uint32_t T, const int32_t* p
     return HY_OK;
 }
 
-int hy_attn_forward_cached(hy_attn_ctx* c, const float* x, uint32_t T, const float* cos_t, const float* sin_t,
-                           float* out, void* stream) {
-    if (!c) return fail(HY_ERR_INVALID, "null ctx");
-    if (!c->loaded) return fail(HY_ERR_STATE, "attention weights not uploaded");
+int hy_attn_forward_cached(hy_attn_ctx* c, uint32_t layer, const float* x, uint32_t T, const float* cos_t,
+                           const float* sin_t, float* out, void* stream) {
+    HY_TRY(check_layer(c, layer, true));
     if (!x || !out) return fail(HY_ERR_INVALID, "null x/out");
     if (T == 0 || T > (uint32_t)c->Tm) return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%d", T, c->Tm);
     if ((cos_t == nullptr) != (sin_t == nullptr)) return fail(HY_ERR_INVALID, "give both rotary tables or neither");
-    if ((uint64_t)c->cache_len + T > (uint64_t)c->Lc)
-        return fail(HY_ERR_INVALID, "cache overflow: %u cached + %u new > max_cache %d", c->cache_len, T, c->Lc);
+    AttnLayer& L = c->layers[layer];
+    if ((uint64_t)L.cache_len + T > (uint64_t)c->Lc)
+        return fail(HY_ERR_INVALID, "cache overflow: %u cached + %u new > max_cache %d", L.cache_len, T, c->Lc);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int pos0 = (int)c->cache_len;
-    HY_TRY(run(c, x, (int)T, cos_t ? hy::ROPE_TABLE : hy::ROPE_NONE, nullptr, cos_t, sin_t, 1, c->kc, c->vc, c->Lc,
+    const int pos0 = (int)L.cache_len;
+    HY_TRY(run(c, L, x, (int)T, cos_t ? hy::ROPE_TABLE : hy::ROPE_NONE, nullptr, cos_t, sin_t, 1, L.kc, L.vc, c->Lc,
                pos0, pos0 + (int)T, 0, out, s));
-    c->cache_len += T;
+    L.cache_len += T;
     return HY_OK;
 }
 
-int hy_attn_set_input_norm(hy_attn_ctx* c, const float* w) {
+int hy_attn_cache_reset(hy_attn_ctx* c) {
     if (!c) return fail(HY_ERR_INVALID, "null ctx");
-    if (!w) {
-        c->has_in_norm = false;
-        return HY_OK;
-    }
-    HIP_TRY(hipSetDevice(c->cfg.device));
-    HIP_TRY(hipMemcpy(c->in_norm, w, (size_t)c->H * 4, hipMemcpyHostToDevice));
-    c->has_in_norm = true;
+    for (auto& L : c->layers) L.cache_len = 0;
     return HY_OK;
 }
 
-int hy_decoder_layer_forward(hy_attn_ctx* c, hy_moe_ctx* moe, uint32_t moe_layer, const float* x, uint32_t T,
-                             const int32_t* positions, float* out, float* debug_h, void* stream) {
-    if (!c || !moe) return fail(HY_ERR_INVALID, "null context");
+int hy_attn_cache_len(const hy_attn_ctx* c, uint32_t layer, uint32_t* len) {
+    HY_TRY(check_layer(c, layer, false));
+    if (!len) return fail(HY_ERR_INVALID, "null len");
+    *len = c->layers[layer].cache_len;
+    return HY_OK;
+}
+
+int hy_decoder_layer_forward(hy_attn_ctx* c, uint32_t attn_layer, hy_moe_ctx* moe, uint32_t moe_layer,
+                             const float* x, uint32_t T, const int32_t* positions, float* out, float* debug_h,
+                             void* stream) {
+    HY_TRY(check_layer(c, attn_layer, true));
+    if (!moe) return fail(HY_ERR_INVALID, "null MoE context");
     if (hy::moe_hidden(moe) != c->H || hy::moe_device(moe) != c->cfg.device)
-        return fail(HY_ERR_INVALID, "the MoE context (hidden %d, device %d) does not match the attention context "
-                    "(hidden %d, device %d)", hy::moe_hidden(moe), hy::moe_device(moe), c->H, c->cfg.device);
-    if (!c->loaded) return fail(HY_ERR_STATE, "attention weights not uploaded");
+        return fail(HY_ERR_INVALID,
+                    "the MoE context (hidden %d, device %d) does not match the attention context (hidden %d, device %d)",
+                    hy::moe_hidden(moe), hy::moe_device(moe), c->H, c->cfg.device);
     if (!x || !out) return fail(HY_ERR_INVALID, "null x/out");
     if (T == 0 || T > (uint32_t)c->Tm) return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%d", T, c->Tm);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int iT = (int)T;
     const float eps = c->cfg.rms_norm_eps;
+    const AttnLayer& L = c->layers[attn_layer];
     // input_layernorm -> self-attention -> h = x + attention (in the output projection)
-    HIP_TRY(c->has_in_norm ? hy::launch_rms_norm_w(x, c->in_norm, iT, c->H, eps, c->xn, s)
-                           : hy::launch_rms_norm(x, iT, c->H, eps, c->xn, s));
-    HY_TRY(run(c, c->xn, iT, hy::ROPE_1D, positions, nullptr, nullptr, 0, c->kf, c->vf, c->Tm, 0, iT, 1, c->hres, s,
-               x));
+    HIP_TRY(L.has_in_norm ? hy::launch_rms_norm_w(x, L.in_norm, iT, c->H, eps, c->xn, s)
+                          : hy::launch_rms_norm(x, iT, c->H, eps, c->xn, s));
+    HY_TRY(run(c, L, c->xn, iT, hy::ROPE_1D, positions, nullptr, nullptr, 0, c->kf, c->vf, c->Tm, 0, iT, 1, c->hres,
+               s, x));
     if (debug_h) HIP_TRY(hipMemcpyAsync(debug_h, c->hres, (size_t)T * c->H * 4, hipMemcpyDeviceToDevice, s));
     // post_attention_layernorm -> MoE -> out = h + MoE (the MoE context's layer and norm)
     return hy_moe_stack_forward(moe, moe_layer, 1, c->hres, T, eps, out, stream);
-}
-
-int hy_attn_cache_reset(hy_attn_ctx* c) {
-    if (!c) return fail(HY_ERR_INVALID, "null ctx");
-    c->cache_len = 0;
-    return HY_OK;
-}
-
-int hy_attn_cache_len(const hy_attn_ctx* c, uint32_t* len) {
-    if (!c || !len) return fail(HY_ERR_INVALID, "null argument");
-    *len = c->cache_len;
-    return HY_OK;
 }
 
 int hy_build_2d_rope(uint32_t seq, uint32_t n_elem, uint32_t text_len, uint32_t img_h, uint32_t img_w, float base,
@@ -332,6 +463,151 @@ int hy_attn_prof_read(hy_attn_ctx* c, uint32_t kid, uint64_t* n, double* ms) {
     HY_TRY(drain_prof(c));
     *n = c->prof_n[kid];
     *ms = c->prof_ms[kid];
+    return HY_OK;
+}
+
+// ------------------------------------------------------------------ the backbone
+
+int hy_model_create(const hy_model_config* cfg, hy_model_ctx** out) {
+    if (!out) return fail(HY_ERR_INVALID, "null out");
+    *out = nullptr;
+    if (!cfg) return fail(HY_ERR_INVALID, "null config");
+    if (cfg->moe.hidden != cfg->attn.hidden || cfg->moe.num_layers != cfg->attn.num_layers ||
+        cfg->moe.max_tokens != cfg->attn.max_tokens || cfg->moe.device != cfg->attn.device)
+        return fail(HY_ERR_INVALID, "the MoE and attention configs must agree on hidden, num_layers, max_tokens "
+                                    "and device");
+    if (cfg->vocab == 0 || cfg->vocab > (1u << 22)) return fail(HY_ERR_INVALID, "vocab=%u out of range", cfg->vocab);
+    if (cfg->attn.hidden % 4) return fail(HY_ERR_INVALID, "hidden must be a multiple of 4");
+    hy_model_ctx* m = new hy_model_ctx();
+    m->cfg = *cfg;
+    int rc = hy_attn_create(&cfg->attn, &m->attn);
+    if (rc == HY_OK) rc = hy_moe_create(&cfg->moe, &m->moe);
+    if (rc != HY_OK) {
+        hy_attn_destroy(m->attn);
+        delete m;
+        return rc;
+    }
+    m->H = (int)cfg->attn.hidden;
+    m->V = (int)cfg->vocab;
+    m->Tm = (int)cfg->attn.max_tokens;
+    m->L = (int)cfg->attn.num_layers;
+    const size_t H = m->H, V = m->V, Tm = m->Tm;
+    struct Part {
+        float** p;
+        size_t n;
+    } parts[] = {{&m->embed, V * H}, {&m->fnorm, H}, {&m->lm_head, V * H},
+                 {&m->ha, Tm * H},   {&m->hb, Tm * H}, {&m->normed, Tm * H}};
+    size_t total = 0;
+    for (auto& p : parts) total += al256(p.n * 4);
+    if (hipMalloc(&m->arena, total) != hipSuccess) {
+        hy_moe_destroy(m->moe);
+        hy_attn_destroy(m->attn);
+        delete m;
+        return fail(HY_ERR_NOMEM, "hipMalloc of %zu bytes for the model's global weights failed", total);
+    }
+    size_t o = 0;
+    for (auto& p : parts) {
+        *p.p = reinterpret_cast<float*>(static_cast<uint8_t*>(m->arena) + o);
+        o += al256(p.n * 4);
+    }
+    if (hy::launch_fill_f32(m->fnorm, H, 1.0f, nullptr) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hy_model_destroy(m);
+        return fail(HY_ERR_HIP, "initialising the final norm failed");
+    }
+    *out = m;
+    return HY_OK;
+}
+
+int hy_model_destroy(hy_model_ctx* m) {
+    if (!m) return HY_OK;
+    (void)hipSetDevice(m->cfg.attn.device);
+    (void)hipDeviceSynchronize();
+    hy_attn_destroy(m->attn);
+    hy_moe_destroy(m->moe);
+    if (m->arena) (void)hipFree(m->arena);
+    delete m;
+    return HY_OK;
+}
+
+hy_attn_ctx* hy_model_attn(hy_model_ctx* m) { return m ? m->attn : nullptr; }
+hy_moe_ctx* hy_model_moe(hy_model_ctx* m) { return m ? m->moe : nullptr; }
+
+int hy_model_upload_globals(hy_model_ctx* m, const float* embedding, const float* final_norm, const float* lm_head) {
+    if (!m) return fail(HY_ERR_INVALID, "null ctx");
+    HIP_TRY(hipSetDevice(m->cfg.attn.device));
+    const size_t VH = (size_t)m->V * m->H;
+    if (embedding) HIP_TRY(hipMemcpy(m->embed, embedding, VH * 4, hipMemcpyHostToDevice));
+    if (final_norm) HIP_TRY(hipMemcpy(m->fnorm, final_norm, (size_t)m->H * 4, hipMemcpyHostToDevice));
+    if (lm_head) HIP_TRY(hipMemcpy(m->lm_head, lm_head, VH * 4, hipMemcpyHostToDevice));
+    return HY_OK;
+}
+
+int hy_model_upload_globals_gguf(hy_model_ctx* m, const hy_gguf* g) {
+    if (!m || !g) return fail(HY_ERR_INVALID, "null argument");
+    const hy::GgufFile& f = hy::gguf_file(g);
+    std::vector<float> emb, fn, lm;
+    HY_TRY(gguf_f32(f, "token_embd.weight", (uint64_t)m->H, (uint64_t)m->V, false, emb, nullptr));
+    HY_TRY(gguf_f32(f, "output_norm.weight", (uint64_t)m->H, 1, false, fn, nullptr));
+    HY_TRY(gguf_f32(f, "output.weight", (uint64_t)m->H, (uint64_t)m->V, false, lm, nullptr));
+    return hy_model_upload_globals(m, emb.data(), fn.data(), lm.data());
+}
+
+int hy_model_synth_globals(hy_model_ctx* m, uint64_t seed, float std) {
+    if (!m) return fail(HY_ERR_INVALID, "null ctx");
+    HIP_TRY(hipSetDevice(m->cfg.attn.device));
+    const size_t VH = (size_t)m->V * m->H;
+    const float scale = std * hy::NORM_SCALE;
+    HIP_TRY(hy::launch_synth_fill(m->embed, VH, hy::stream_key(seed, 0, hy::TENSOR_EMBED, 0), scale, nullptr));
+    HIP_TRY(hy::launch_synth_fill(m->lm_head, VH, hy::stream_key(seed, 0, hy::TENSOR_LM_HEAD, 0), scale, nullptr));
+    HIP_TRY(hy::launch_fill_f32(m->fnorm, (size_t)m->H, 1.0f, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    return HY_OK;
+}
+
+}  // extern "C"
+
+namespace {
+// layers 0..n-1 from `in` (not modified); *result is the buffer holding the output
+int run_layers(hy_model_ctx* m, const float* in, uint32_t T, const int32_t* positions, uint32_t n, hipStream_t s,
+               const float** result) {
+    const float* cur = in;
+    for (uint32_t l = 0; l < n; l++) {
+        float* dst = (cur == m->ha) ? m->hb : m->ha;
+        HY_TRY(hy_decoder_layer_forward(m->attn, l, m->moe, l, cur, T, positions, dst, nullptr, s));
+        cur = dst;
+    }
+    *result = cur;
+    return HY_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int hy_model_forward(hy_model_ctx* m, const int32_t* ids, uint32_t T, const int32_t* positions, float* logits,
+                     void* stream) {
+    if (!m) return fail(HY_ERR_INVALID, "null ctx");
+    if (!ids || !logits) return fail(HY_ERR_INVALID, "null ids/logits");
+    if (T == 0 || T > (uint32_t)m->Tm) return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%d", T, m->Tm);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    HIP_TRY(hy::launch_embed(ids, m->embed, (int)T, m->H, m->V, m->hb, s));
+    const float* h = nullptr;
+    HY_TRY(run_layers(m, m->hb, T, positions, (uint32_t)m->L, s, &h));
+    HIP_TRY(hy::launch_rms_norm_w(h, m->fnorm, (int)T, m->H, m->cfg.attn.rms_norm_eps, m->normed, s));
+    HIP_TRY(hy::launch_gemm_nt_f32(m->normed, m->lm_head, nullptr, logits, (int)T, m->V, m->H, s));
+    return HY_OK;
+}
+
+int hy_model_forward_hidden(hy_model_ctx* m, const float* embeds, uint32_t T, const int32_t* positions,
+                            uint32_t n_layers, float* hidden, void* stream) {
+    if (!m) return fail(HY_ERR_INVALID, "null ctx");
+    if (!embeds || !hidden) return fail(HY_ERR_INVALID, "null embeds/hidden");
+    if (T == 0 || T > (uint32_t)m->Tm) return fail(HY_ERR_INVALID, "T=%u must be in 1..max_tokens=%d", T, m->Tm);
+    if (n_layers > (uint32_t)m->L) return fail(HY_ERR_INVALID, "n_layers=%u > %d layers", n_layers, m->L);
+    const uint32_t n = n_layers ? n_layers : (uint32_t)m->L;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const float* h = nullptr;
+    HY_TRY(run_layers(m, embeds, T, positions, n, s, &h));
+    HIP_TRY(hipMemcpyAsync(hidden, h, (size_t)T * m->H * 4, hipMemcpyDeviceToDevice, s));
     return HY_OK;
 }
 

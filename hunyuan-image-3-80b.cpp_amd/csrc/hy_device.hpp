@@ -53,7 +53,10 @@ __device__ __forceinline__ float synth_normal(uint64_t key, uint64_t idx, float 
 }
 
 // tensor ids of the generator streams
-enum { TENSOR_X = 0, TENSOR_ROUTER = 1, TENSOR_GU = 2, TENSOR_DN = 3 };
+enum {
+    TENSOR_X = 0, TENSOR_ROUTER = 1, TENSOR_GU = 2, TENSOR_DN = 3,
+    TENSOR_QKV = 4, TENSOR_O = 5, TENSOR_EMBED = 6, TENSOR_LM_HEAD = 7
+};
 
 // ---------------------------------------------------------------- wave helpers
 

@@ -130,5 +130,7 @@ hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s);
 hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,
                                float* sin_out, hipStream_t s);
 hipError_t launch_gather_kv(const float* src, int nkv, int L, int pos0, int T, int hd, float* dst, hipStream_t s);
+hipError_t launch_embed(const int* ids, const float* table, int T, int H, int vocab, float* out, hipStream_t s);
+hipError_t launch_fill_f32(float* out, size_t n, float v, hipStream_t s);
 
 }  // namespace hy

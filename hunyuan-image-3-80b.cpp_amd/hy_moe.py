@@ -40,9 +40,13 @@ class Config(C.Structure):
 class AttnConfig(C.Structure):
     _fields_ = [
         ("hidden", C.c_uint32), ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
-        ("max_tokens", C.c_uint32), ("max_cache", C.c_uint32), ("rms_norm_eps", C.c_float),
-        ("rope_theta", C.c_float), ("device", C.c_int32),
+        ("num_layers", C.c_uint32), ("max_tokens", C.c_uint32), ("max_cache", C.c_uint32),
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("device", C.c_int32),
     ]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("moe", Config), ("attn", AttnConfig), ("vocab", C.c_uint32)]
 
 
 _vp = C.c_void_p
@@ -57,14 +61,25 @@ _SIGS = {
     "hy_moe_set_ffn_norm": (C.c_int, [_vp, _u32, _vp]),
     "hy_attn_create": (C.c_int, [C.POINTER(AttnConfig), C.POINTER(_vp)]),
     "hy_attn_destroy": (C.c_int, [_vp]),
-    "hy_attn_upload": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
-    "hy_attn_forward": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "hy_attn_forward_cached": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "hy_attn_upload": (C.c_int, [_vp, _u32, _vp, _vp, _vp, _vp]),
+    "hy_attn_upload_gguf": (C.c_int, [_vp, _u32, _vp, _u32]),
+    "hy_attn_synth_layer": (C.c_int, [_vp, _u32, _u64, _f]),
+    "hy_attn_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hy_attn_forward_cached": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
     "hy_attn_cache_reset": (C.c_int, [_vp]),
-    "hy_attn_cache_len": (C.c_int, [_vp, C.POINTER(_u32)]),
+    "hy_attn_cache_len": (C.c_int, [_vp, _u32, C.POINTER(_u32)]),
+    "hy_model_create": (C.c_int, [C.POINTER(ModelConfig), C.POINTER(_vp)]),
+    "hy_model_destroy": (C.c_int, [_vp]),
+    "hy_model_attn": (_vp, [_vp]),
+    "hy_model_moe": (_vp, [_vp]),
+    "hy_model_upload_globals": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "hy_model_upload_globals_gguf": (C.c_int, [_vp, _vp]),
+    "hy_model_synth_globals": (C.c_int, [_vp, _u64, _f]),
+    "hy_model_forward": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp]),
+    "hy_model_forward_hidden": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp]),
     "hy_build_2d_rope": (C.c_int, [_u32, _u32, _u32, _u32, _u32, _f, _vp, _vp, _vp]),
-    "hy_attn_set_input_norm": (C.c_int, [_vp, _vp]),
-    "hy_decoder_layer_forward": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "hy_attn_set_input_norm": (C.c_int, [_vp, _u32, _vp]),
+    "hy_decoder_layer_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
     "hy_attn_prof_enable": (C.c_int, [_vp, _i32]),
     "hy_attn_prof_read": (C.c_int, [_vp, _u32, C.POINTER(_u64), C.POINTER(C.c_double)]),
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
@@ -217,9 +232,9 @@ class Moe:
         self.h = h.value
 
     def close(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and getattr(self, "owned", True):
             lib().hy_moe_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:
@@ -430,62 +445,74 @@ ATTN_KERNELS = ("qkv_proj", "rope_qknorm", "attention", "o_proj")
 
 
 class Attn:
-    """One resident attention layer (include/hy_attn.h): weights, key / value cache
-    and the fp32 kernels of attention_forward_cpu and the KV-cache branch."""
+    """Resident attention layers (include/hy_attn.h): weights, key / value caches and
+    the fp32 kernels of attention_forward_cpu and the KV-cache branch.  `layer`
+    arguments default to 0 (single-layer use)."""
 
-    def __init__(self, H, nh, nkv, hd, max_tokens, max_cache=0, eps=1e-5, theta=10000.0, device=0):
-        cfg = AttnConfig(H, nh, nkv, hd, max_tokens, max_cache, eps, theta, device)
+    def __init__(self, H, nh, nkv, hd, max_tokens, max_cache=0, eps=1e-5, theta=10000.0, device=0, num_layers=1,
+                 handle=None):
+        self.H, self.nh, self.nkv, self.hd = H, nh, nkv, hd
+        self.owned = handle is None
+        if handle is not None:
+            self.h = handle
+            return
+        cfg = AttnConfig(H, nh, nkv, hd, num_layers, max_tokens, max_cache, eps, theta, device)
         h = _vp()
         check(lib().hy_attn_create(C.byref(cfg), C.byref(h)))
         self.h = h
-        self.H, self.nh, self.nkv, self.hd = H, nh, nkv, hd
 
     def close(self):
-        if self.h:
+        if self.h and self.owned:
             check(lib().hy_attn_destroy(self.h))
-            self.h = None
+        self.h = None
 
-    def upload(self, qkv_w, o_w, q_norm, k_norm):
+    def upload(self, qkv_w, o_w, q_norm, k_norm, layer=0):
         arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (qkv_w, o_w, q_norm, k_norm)]
         nq, nk = self.nh * self.hd, self.nkv * self.hd
         want = [(nq + 2 * nk, self.H), (self.H, nq), (self.hd,), (self.hd,)]
         for a, w in zip(arrs, want):
             if a.shape != w:
                 raise ValueError(f"attention weight shape {a.shape}, want {w}")
-        check(lib().hy_attn_upload(self.h, *[a.ctypes.data for a in arrs]))
+        check(lib().hy_attn_upload(self.h, layer, *[a.ctypes.data for a in arrs]))
 
-    def forward(self, x: Buf, T, out: Buf, positions=None, dq=None, dk=None, dv=None, stream=None):
-        check(lib().hy_attn_forward(self.h, x.ptr, T, positions.ptr if positions is not None else None, out.ptr,
-                                    dq.ptr if dq is not None else None, dk.ptr if dk is not None else None,
+    def upload_gguf(self, layer, gguf, block):
+        check(lib().hy_attn_upload_gguf(self.h, layer, gguf.h, block))
+
+    def synth(self, layer=0, seed=42, std=0.02):
+        check(lib().hy_attn_synth_layer(self.h, layer, seed, std))
+
+    def forward(self, x: Buf, T, out: Buf, positions=None, dq=None, dk=None, dv=None, stream=None, layer=0):
+        check(lib().hy_attn_forward(self.h, layer, x.ptr, T, positions.ptr if positions is not None else None,
+                                    out.ptr, dq.ptr if dq is not None else None, dk.ptr if dk is not None else None,
                                     dv.ptr if dv is not None else None, stream))
 
-    def forward_cached(self, x: Buf, T, out: Buf, cos=None, sin=None, stream=None):
-        check(lib().hy_attn_forward_cached(self.h, x.ptr, T, cos.ptr if cos is not None else None,
+    def forward_cached(self, x: Buf, T, out: Buf, cos=None, sin=None, stream=None, layer=0):
+        check(lib().hy_attn_forward_cached(self.h, layer, x.ptr, T, cos.ptr if cos is not None else None,
                                            sin.ptr if sin is not None else None, out.ptr, stream))
 
-    def set_input_norm(self, w=None):
+    def set_input_norm(self, w=None, layer=0):
         """input_layernorm weight [H] (None: unit) for decoder_layer_forward."""
         if w is None:
-            check(lib().hy_attn_set_input_norm(self.h, None))
+            check(lib().hy_attn_set_input_norm(self.h, layer, None))
             return
         w = np.ascontiguousarray(w, dtype=np.float32)
         if w.shape != (self.H,):
             raise ValueError(f"input norm weight must have shape ({self.H},), got {w.shape}")
-        check(lib().hy_attn_set_input_norm(self.h, w.ctypes.data))
+        check(lib().hy_attn_set_input_norm(self.h, layer, w.ctypes.data))
 
     def decoder_layer_forward(self, moe, moe_layer, x: Buf, T, out: Buf, positions=None, debug_h=None,
-                              stream=None):
+                              stream=None, layer=0):
         """decoder_layer_forward_cpu: out = h + MoE(RMSNorm(h)), h = x + attention(RMSNorm(x))."""
-        check(lib().hy_decoder_layer_forward(self.h, moe.h, moe_layer, x.ptr, T,
+        check(lib().hy_decoder_layer_forward(self.h, layer, moe.h, moe_layer, x.ptr, T,
                                              positions.ptr if positions is not None else None, out.ptr,
                                              debug_h.ptr if debug_h is not None else None, stream))
 
     def cache_reset(self):
         check(lib().hy_attn_cache_reset(self.h))
 
-    def cache_len(self):
+    def cache_len(self, layer=0):
         n = _u32()
-        check(lib().hy_attn_cache_len(self.h, C.byref(n)))
+        check(lib().hy_attn_cache_len(self.h, layer, C.byref(n)))
         return n.value
 
     def prof_enable(self, on):
@@ -499,7 +526,7 @@ class Attn:
             out[name] = (n.value, ms.value)
         return out
 
-    def run(self, x, positions=None, debug=False):
+    def run(self, x, positions=None, debug=False, layer=0):
         """Host convenience: x [T][H] -> out (and q, k, v when debug)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         T = x.shape[0]
@@ -508,10 +535,51 @@ class Attn:
         dq = Buf.empty((T, self.nh, self.hd)) if debug else None
         dk = Buf.empty((T, self.nkv, self.hd)) if debug else None
         dv = Buf.empty((T, self.nkv, self.hd)) if debug else None
-        self.forward(xb, T, ob, pb, dq, dk, dv)
+        self.forward(xb, T, ob, pb, dq, dk, dv, layer=layer)
         if debug:
             return ob.numpy(), dq.numpy(), dk.numpy(), dv.numpy()
         return ob.numpy()
+
+
+class Model:
+    """The resident backbone (HunyuanFullModel): embedding -> decoder layers -> final
+    norm -> lm_head.  .attn / .moe are views of its two layer contexts."""
+
+    def __init__(self, H, I, E, K, wtype, nh, nkv, hd, vocab, num_layers, max_tokens, eps=1e-5, theta=10000.0,
+                 device=0, has_shared=True):
+        mc = Config(H, I, E, K, num_layers, max_tokens, wtype, 1 if has_shared else 0, 1, 1.0, 0, 0, 0, device)
+        ac = AttnConfig(H, nh, nkv, hd, num_layers, max_tokens, 0, eps, theta, device)
+        cfg = ModelConfig(mc, ac, vocab)
+        h = _vp()
+        check(lib().hy_model_create(C.byref(cfg), C.byref(h)))
+        self.h = h
+        self.H, self.V, self.L = H, vocab, num_layers
+        self.attn = Attn(H, nh, nkv, hd, max_tokens, handle=_vp(lib().hy_model_attn(h)))
+        self.moe = Moe.__new__(Moe)
+        self.moe.h = lib().hy_model_moe(h)
+        self.moe.H, self.moe.I, self.moe.E, self.moe.K, self.moe.wtype = H, I, E, K, wtype
+        self.moe.owned = False
+
+    def close(self):
+        if self.h:
+            check(lib().hy_model_destroy(self.h))
+            self.h = None
+
+    def upload_globals(self, embedding=None, final_norm=None, lm_head=None):
+        arrs = [None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+                for a in (embedding, final_norm, lm_head)]
+        check(lib().hy_model_upload_globals(self.h, *[None if a is None else a.ctypes.data for a in arrs]))
+
+    def synth_globals(self, seed=42, std=0.02):
+        check(lib().hy_model_synth_globals(self.h, seed, std))
+
+    def forward(self, ids: Buf, T, logits: Buf, positions=None, stream=None):
+        check(lib().hy_model_forward(self.h, ids.ptr, T, positions.ptr if positions is not None else None,
+                                     logits.ptr, stream))
+
+    def forward_hidden(self, embeds: Buf, T, hidden: Buf, n_layers=0, positions=None, stream=None):
+        check(lib().hy_model_forward_hidden(self.h, embeds.ptr, T, positions.ptr if positions is not None else None,
+                                            n_layers, hidden.ptr, stream))
 
 
 def build_2d_rope(seq, n_elem, text_len, img_h, img_w, base=10000.0):

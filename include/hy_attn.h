@@ -11,8 +11,8 @@
  * AttentionWeights / HunyuanConfig (src/hunyuan_model.h:13-40, 93-101), the KV-cache branch of
  * decoder_layer_extended_f32 (src/hunyuan_extended.cpp:52-176), rope_f32
  * (src/rms_norm.cpp:97-152) and build_2d_rope / apply_rope_2d_f32
- * (src/hunyuan_image_gen.cpp:11-117).  One context holds one layer's weights and
- * key / value cache, resident on the device.
+ * (src/hunyuan_image_gen.cpp:11-117).  One context holds num_layers layers' weights and
+ * key / value caches, resident on the device, and one work arena shared by them.
  */
 #ifndef HY_ATTN_H
 #define HY_ATTN_H
@@ -29,14 +29,15 @@ extern "C" {
  * num_attention_heads, num_key_value_heads, attention_head_dim, rms_norm_eps,
  * rope_theta.  The GPU kernels take head_dim 64 or 128 and 4 query heads per kv
  * head (HunyuanImage-3: 32 / 8); other shapes are HY_ERR_UNSUPPORTED.
- * max_tokens bounds T per call; max_cache the key / value cache length. */
+ * max_tokens bounds T per call; max_cache the key / value cache length per layer. */
 typedef struct {
     uint32_t hidden;      /* H */
     uint32_t n_heads;     /* query heads */
     uint32_t n_kv_heads;  /* key / value heads */
     uint32_t head_dim;    /* 64 or 128 */
+    uint32_t num_layers;  /* resident layers */
     uint32_t max_tokens;  /* 1..16384 */
-    uint32_t max_cache;   /* cache positions (0: no cache) */
+    uint32_t max_cache;   /* cache positions per layer (0: no cache) */
     float rms_norm_eps;
     float rope_theta;
     int32_t device;
@@ -47,12 +48,24 @@ typedef struct hy_attn_ctx hy_attn_ctx;
 int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out);
 int hy_attn_destroy(hy_attn_ctx* ctx);
 
-/* AttentionWeights (src/hunyuan_model.h:93-101), F32, host memory, reference layout:
- * qkv_weight [(n_heads + 2 n_kv_heads) head_dim][hidden] (query head rows, then key
- * heads, then value heads), o_weight [hidden][n_heads head_dim], q_norm_weight and
- * k_norm_weight [head_dim].  Uploaded once. */
-int hy_attn_upload(hy_attn_ctx* ctx, const float* qkv_weight_host, const float* o_weight_host,
+/* AttentionWeights (src/hunyuan_model.h:93-101) of one layer, F32, host memory,
+ * reference layout: qkv_weight [(n_heads + 2 n_kv_heads) head_dim][hidden] (query head
+ * rows, then key heads, then value heads), o_weight [hidden][n_heads head_dim],
+ * q_norm_weight and k_norm_weight [head_dim].  Uploaded once. */
+int hy_attn_upload(hy_attn_ctx* ctx, uint32_t layer, const float* qkv_weight_host, const float* o_weight_host,
                    const float* q_norm_host, const float* k_norm_host);
+
+/* The attention tensors of block `block` of a GGUF file into layer `layer`, as
+ * load_layer_weights reads them (src/hunyuan_gguf_loader.cpp:249-257):
+ * blk.N.attn_qkv.weight ne {H, (nh+2nkv) hd}, blk.N.attn_output.weight ne {nh hd, H},
+ * blk.N.attn_q_norm.weight / attn_k_norm.weight ne {hd}, and blk.N.attn_norm.weight
+ * ne {H} (input_layernorm; optional, absent: unit).  F32, F16 or BF16 (converted to
+ * F32 on upload).  Types and shapes are checked before anything is uploaded. */
+int hy_attn_upload_gguf(hy_attn_ctx* ctx, uint32_t layer, const hy_gguf* f, uint32_t block);
+
+/* One layer's weights from the counter-based synthetic generator (projections
+ * ~ N(0, std), norms 1), on the device. */
+int hy_attn_synth_layer(hy_attn_ctx* ctx, uint32_t layer, uint64_t seed, float std);
 
 /* attention_forward_cpu (src/attention.cpp:10-185): out = o_proj(causal GQA
  * attention of RMSNorm(RoPE(q)), RMSNorm(RoPE(k)), v) for T tokens of x [T][hidden].
@@ -60,8 +73,8 @@ int hy_attn_upload(hy_attn_ctx* ctx, const float* qkv_weight_host, const float* 
  * [T][n_heads][head_dim], debug_k_dev / debug_v_dev [T][n_kv_heads][head_dim]
  * (each may be NULL) receive q, k, v after RoPE and norm, as the reference's debug
  * outputs.  Does not touch the cache. */
-int hy_attn_forward(hy_attn_ctx* ctx, const float* x_dev, uint32_t T, const int32_t* positions_dev, float* out_dev,
-                    float* debug_q_dev, float* debug_k_dev, float* debug_v_dev, void* stream);
+int hy_attn_forward(hy_attn_ctx* ctx, uint32_t layer, const float* x_dev, uint32_t T, const int32_t* positions_dev,
+                    float* out_dev, float* debug_q_dev, float* debug_k_dev, float* debug_v_dev, void* stream);
 
 /* The KV-cache branch of decoder_layer_extended_f32 (src/hunyuan_extended.cpp:52-176):
  * project the T new tokens, rotate them by rows 0..T-1 of the 2D tables cos_dev /
@@ -69,11 +82,11 @@ int hy_attn_forward(hy_attn_ctx* ctx, const float* x_dev, uint32_t T, const int3
  * append k / v at the cache's current length, and let every new token attend to
  * all cached positions (no mask among the new tokens, as the reference).
  * HY_ERR_INVALID when the cache would overflow (the cache is left unchanged). */
-int hy_attn_forward_cached(hy_attn_ctx* ctx, const float* x_dev, uint32_t T, const float* cos_dev,
+int hy_attn_forward_cached(hy_attn_ctx* ctx, uint32_t layer, const float* x_dev, uint32_t T, const float* cos_dev,
                            const float* sin_dev, float* out_dev, void* stream);
-/* KVCache::reset / current_len (src/hunyuan_image_gen.h:179-193), for this layer. */
+/* KVCache::reset (every layer) / current_len (one layer) (src/hunyuan_image_gen.h:179-193). */
 int hy_attn_cache_reset(hy_attn_ctx* ctx);
-int hy_attn_cache_len(const hy_attn_ctx* ctx, uint32_t* len);
+int hy_attn_cache_len(const hy_attn_ctx* ctx, uint32_t layer, uint32_t* len);
 
 /* build_2d_rope (src/hunyuan_image_gen.cpp:11-69) on the device: cos_dev / sin_dev
  * [seq][n_elem] for text_len text positions followed by an img_h x img_w grid. */
@@ -89,9 +102,48 @@ int hy_build_2d_rope(uint32_t seq, uint32_t n_elem, uint32_t text_len, uint32_t 
  * unit); w_post: the MoE layer's hy_moe_set_ffn_norm.  The contexts must share
  * hidden size and device; eps is this context's rms_norm_eps.  debug_h_dev
  * (nullable) receives h [T][hidden]. */
-int hy_attn_set_input_norm(hy_attn_ctx* ctx, const float* w_host);
-int hy_decoder_layer_forward(hy_attn_ctx* attn, hy_moe_ctx* moe, uint32_t moe_layer, const float* x_dev, uint32_t T,
-                             const int32_t* positions_dev, float* out_dev, float* debug_h_dev, void* stream);
+int hy_attn_set_input_norm(hy_attn_ctx* ctx, uint32_t layer, const float* w_host);
+int hy_decoder_layer_forward(hy_attn_ctx* attn, uint32_t attn_layer, hy_moe_ctx* moe, uint32_t moe_layer,
+                             const float* x_dev, uint32_t T, const int32_t* positions_dev, float* out_dev,
+                             float* debug_h_dev, void* stream);
+
+/* ---- the resident backbone ---------------------------------------------------
+ * HunyuanFullModel (src/hunyuan_full_model.h, .cpp:173-318): embedding lookup ->
+ * num_layers decoder layers -> final RMSNorm -> lm_head, every weight resident (the
+ * reference loads and frees each layer per forward).  The model owns an attention
+ * context and a MoE context of num_layers layers each; their layers are uploaded
+ * through hy_attn_* / hy_moe_* on the handles hy_model_attn / hy_model_moe give. */
+typedef struct {
+    hy_moe_config moe;    /* num_layers, max_tokens and device must match attn's */
+    hy_attn_config attn;
+    uint32_t vocab;       /* vocab_size */
+} hy_model_config;
+
+typedef struct hy_model_ctx hy_model_ctx;
+
+int hy_model_create(const hy_model_config* cfg, hy_model_ctx** out);
+int hy_model_destroy(hy_model_ctx* ctx);
+hy_attn_ctx* hy_model_attn(hy_model_ctx* ctx);
+hy_moe_ctx* hy_model_moe(hy_model_ctx* ctx);
+/* Global weights, F32 host arrays: token_embd.weight [vocab][hidden],
+ * output_norm.weight [hidden], output.weight (lm_head) [vocab][hidden]; any may be
+ * NULL to leave it as it is. */
+int hy_model_upload_globals(hy_model_ctx* ctx, const float* embedding_host, const float* final_norm_host,
+                            const float* lm_head_host);
+/* The same three tensors from a GGUF file (F32, F16 or BF16). */
+int hy_model_upload_globals_gguf(hy_model_ctx* ctx, const hy_gguf* f);
+/* Synthetic global weights (embedding and lm_head ~ N(0, std), final norm 1). */
+int hy_model_synth_globals(hy_model_ctx* ctx, uint64_t seed, float std);
+/* HunyuanFullModel::forward (src/hunyuan_full_model.cpp:173-216): input_ids_dev int32
+ * [T] (ids >= vocab give zero rows), positions_dev int32 [T] or NULL (0..T-1),
+ * logits_dev f32 [T][vocab]. */
+int hy_model_forward(hy_model_ctx* ctx, const int32_t* input_ids_dev, uint32_t T, const int32_t* positions_dev,
+                     float* logits_dev, void* stream);
+/* HunyuanFullModel::forward_hidden / forward_debug (src/hunyuan_full_model.cpp:218-269):
+ * inputs_embeds_dev [T][hidden] through layers 0..n_layers-1 (n_layers 0: all) into
+ * hidden_dev [T][hidden]. */
+int hy_model_forward_hidden(hy_model_ctx* ctx, const float* inputs_embeds_dev, uint32_t T,
+                            const int32_t* positions_dev, uint32_t n_layers, float* hidden_dev, void* stream);
 
 /* Per-kernel timing of this context's launches (as hy_moe_prof_*): kernel ids
  * 0 = qkv_proj, 1 = rope_qknorm, 2 = attention, 3 = o_proj. */
