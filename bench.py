@@ -15,6 +15,7 @@ c4 Q4_0 T=4096 Zipf-skewed routing, c5 32-layer Q8_0 stack T=4096.
     python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
     python bench.py --gguf-load /tmp/l.gguf [--config c2]   # layer load from a GGUF file
     python bench.py --attn [--tokens 4096]   # attention half of a decoder layer (fp32)
+    python bench.py --model [--tokens 512]   # resident backbone: embedding, 32 layers, lm_head
 
 roofline.traffic (HBM bytes per launch of the dominant kernel) is read from
 profiles/hbm_traffic.md, the table made from rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -271,6 +272,78 @@ def attn_main(a, hy):
     m.close()
 
 
+VOCAB = 133120
+
+
+def model_main(a, hy):
+    """The resident backbone (HunyuanFullModel::forward): token ids -> embedding ->
+    32 decoder layers (fp32 attention + Q8_0 MoE) -> final norm -> lm_head logits,
+    every weight synthetic and resident (~94 GB)."""
+    T = a.tokens or 512
+    nl = 32
+    m = hy.Model(H, I, E, K, 8, ATTN["nh"], ATTN["nkv"], ATTN["hd"], VOCAB, nl, T)
+    t0 = time.perf_counter()
+    m.synth_globals(seed=a.seed, std=0.02)
+    for l in range(nl):
+        m.attn.synth(l, seed=a.seed, std=0.02)
+        m.moe.synth(l, seed=a.seed, std=0.02)
+        if l % 8 == 7:
+            print(f"backbone: {l + 1}/{nl} layers synthesized", file=sys.stderr, flush=True)
+    setup_s = time.perf_counter() - t0
+    ids = hy.Buf.from_array(np.random.default_rng(a.seed).integers(0, VOCAB, size=T).astype(np.int32))
+    logits = hy.Buf.empty((T, VOCAB))
+    for _ in range(a.warmup):
+        m.forward(ids, T, logits)
+    hy.sync()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    t1 = time.perf_counter()
+    hy.check(hy.lib().hy_event_record(ev0, None))
+    for _ in range(a.steps):
+        m.forward(ids, T, logits)
+    hy.check(hy.lib().hy_event_record(ev1, None))
+    hy.sync()
+    wall = time.perf_counter() - t1
+    ms = hy.C.c_float()
+    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+    ms_per_step = ms.value / a.steps
+    # per-kernel times of the two layer contexts (profiled pass)
+    m.moe.prof_enable(True)
+    m.attn.prof_enable(True)
+    m.forward(ids, T, logits)
+    hy.sync()
+    prof = {k: v for k, v in {**m.moe.prof_read(), **m.attn.prof_read()}.items() if v[0] > 0}
+    m.moe.prof_enable(False)
+    m.attn.prof_enable(False)
+    dom = max(prof, key=lambda k: prof[k][1])
+    n_l, t_l = prof[dom]
+    avg_s = t_l / n_l / 1e3
+    if dom in ("qkv_proj", "o_proj", "attention"):
+        fl = attn_flops(dom, T)
+        roof = {"bound": "mfma", "kernel": dom, "achieved": fl / avg_s / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
+                "unit": "TFLOP/s", "frac": fl / avg_s / PEAK_FP32_MFMA, "traffic": None, "avg_launch_ms": avg_s * 1e3}
+    else:
+        tr = kernel_traffic(dom, 8, T, E)
+        roof = {"bound": "hbm", "kernel": dom, "achieved": tr / avg_s / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                "frac": tr / avg_s / PEAK_HBM, "traffic": None, "avg_launch_ms": avg_s * 1e3}
+    per_forward = {k: round(t, 4) for k, (n, t) in prof.items()}
+    res = {
+        "metric": "backbone tokens/sec (HunyuanFullModel forward, 32 layers + lm_head), 1 MI355X",
+        "value": T / (ms_per_step / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 attention / int8 MoE", "data": "synthetic",
+        "config": {"workload": f"backbone32_q8_0_t{T}", "hidden": H, "layers": nl, "vocab": VOCAB, "tokens": T,
+                   "moe_weights": "Q8_0", "attention_weights": "F32"},
+        "roofline": roof,
+        "kernel_ms_per_forward": per_forward,
+        "lm_head_and_rest_ms": ms_per_step - sum(t for _, t in prof.values()),
+        "setup_s": setup_s, "wall_s": wall,
+    }
+    print(json.dumps(res), flush=True)
+    m.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -283,6 +356,7 @@ def main():
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     ap.add_argument("--attn", action="store_true", help="time the attention half instead of the MoE layer")
+    ap.add_argument("--model", action="store_true", help="time the resident 32-layer backbone with lm_head")
     ap.add_argument("--gguf-load", default=None, metavar="PATH",
                     help="time loading one real-shape layer from a GGUF file written at PATH")
     a = ap.parse_args()
@@ -302,6 +376,9 @@ def main():
         return
     if a.attn:
         attn_main(a, hy)
+        return
+    if a.model:
+        model_main(a, hy)
         return
     wl = dict(WORKLOADS[a.config])
     if a.tokens:

@@ -7,9 +7,10 @@
 // Kernels:
 //  * gemm_nt_f32_kernel: C[M][N] = (R[M][N] +) A[M][K] . W[N][K]^T on
 //    v_mfma_f32_32x32x2f32 (the QKV and output projections; R is the decoder layer's
-//    residual stream when the output projection adds it).  Work group 128 x 128, four waves of 64 x 64 (2 x 2
-//    MFMA tiles), K in steps of 16 straight from global memory into registers (the
-//    next step's loads are in flight while the current one multiplies).
+//    residual stream when the output projection adds it).  Waves of 64 x 64 (2 x 2
+//    MFMA tiles), four per 128 x 128 work group (one per work group when that grid
+//    would be small), K in steps of 16 straight from global memory into registers
+//    (the next step's loads are in flight while the current one multiplies).
 //  * rope_qknorm_kernel: one wave per (token, head): rotary embedding (1D positions,
 //    2D tables or none), per-head RMSNorm, written to q [T][nh][hd] and, for key
 //    heads, k / v into a [nkv][L][hd] cache at row pos0 + t.
@@ -36,14 +37,16 @@ __device__ __forceinline__ v16f_t mfma_f32(float a, float b, v16f_t c) {
 }
 
 // ---------------------------------------------------------------- GEMM (NT)
-constexpr int GM_TILE = 128;
-
-__global__ __launch_bounds__(256, 2) void gemm_nt_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
-                                                             const float* __restrict__ R, float* __restrict__ C, int M,
-                                                             int N, int K) {
+// WM x WN waves per work group, each a 64 x 64 output tile: 2 x 2 (128 x 128) for
+// large grids; 1 x 1 when that grid would leave CUs idle (few tokens)
+template <int WM, int WN>
+__global__ __launch_bounds__(WAVE * WM * WN) void gemm_nt_f32_kernel(const float* __restrict__ A,
+                                                                    const float* __restrict__ W,
+                                                                    const float* __restrict__ R,
+                                                                    float* __restrict__ C, int M, int N, int K) {
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int lr = lane % 32, h = lane / 32;
-    const int m0 = blockIdx.y * GM_TILE + (wave / 2) * 64, n0 = blockIdx.x * GM_TILE + (wave % 2) * 64;
+    const int m0 = blockIdx.y * (64 * WM) + (wave / WN) * 64, n0 = blockIdx.x * (64 * WN) + (wave % WN) * 64;
     // operand rows of this lane (clamped for loads; the stores are guarded)
     const float* pa[2];
     const float* pb[2];
@@ -105,8 +108,14 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f32_kernel(const float* __rest
 
 hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
                               hipStream_t s) {
-    const dim3 grid((N + GM_TILE - 1) / GM_TILE, (M + GM_TILE - 1) / GM_TILE);
-    hipLaunchKernelGGL(gemm_nt_f32_kernel, grid, dim3(256), 0, s, A, W, R, C, M, N, K);
+    const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
+    if (big >= 512) {
+        const dim3 grid((N + 127) / 128, (M + 127) / 128);
+        hipLaunchKernelGGL((gemm_nt_f32_kernel<2, 2>), grid, dim3(256), 0, s, A, W, R, C, M, N, K);
+    } else {
+        const dim3 grid((N + 63) / 64, (M + 63) / 64);
+        hipLaunchKernelGGL((gemm_nt_f32_kernel<1, 1>), grid, dim3(64), 0, s, A, W, R, C, M, N, K);
+    }
     return hipGetLastError();
 }
 

@@ -445,6 +445,17 @@ int hy_build_2d_rope(uint32_t seq, uint32_t n_elem, uint32_t text_len, uint32_t 
     return HY_OK;
 }
 
+int hy_lm_head_f32(const float* x, const float* w, const float* resid, uint32_t T, uint32_t hidden, uint32_t vocab,
+                   float* out, void* stream) {
+    if (!x || !w || !out) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || vocab == 0 || hidden == 0 || hidden % 16)
+        return fail(HY_ERR_INVALID, "bad GEMM shape T=%u hidden=%u vocab=%u (hidden a multiple of 16)", T, hidden,
+                    vocab);
+    HIP_TRY(hy::launch_gemm_nt_f32(x, w, resid, out, (int)T, (int)vocab, (int)hidden,
+                                   static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
 int hy_attn_prof_enable(hy_attn_ctx* c, int32_t on) {
     if (!c) return fail(HY_ERR_INVALID, "null ctx");
     if (!on) HY_TRY(drain_prof(c));

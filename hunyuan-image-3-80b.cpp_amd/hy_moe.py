@@ -80,6 +80,7 @@ _SIGS = {
     "hy_build_2d_rope": (C.c_int, [_u32, _u32, _u32, _u32, _u32, _f, _vp, _vp, _vp]),
     "hy_attn_set_input_norm": (C.c_int, [_vp, _u32, _vp]),
     "hy_decoder_layer_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "hy_lm_head_f32": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "hy_attn_prof_enable": (C.c_int, [_vp, _i32]),
     "hy_attn_prof_read": (C.c_int, [_vp, _u32, C.POINTER(_u64), C.POINTER(C.c_double)]),
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
@@ -587,3 +588,14 @@ def build_2d_rope(seq, n_elem, text_len, img_h, img_w, base=10000.0):
     cos, sin = Buf.empty((seq, n_elem)), Buf.empty((seq, n_elem))
     check(lib().hy_build_2d_rope(seq, n_elem, text_len, img_h, img_w, base, cos.ptr, sin.ptr, None))
     return cos, sin
+
+
+def lm_head_f32(x, w, resid=None):
+    """Host convenience over hy_lm_head_f32: x [T][H] . w[V][H]^T (+ resid)."""
+    x, w = np.ascontiguousarray(x, dtype=np.float32), np.ascontiguousarray(w, dtype=np.float32)
+    T, Hd = x.shape
+    V = w.shape[0]
+    xb, wb, ob = Buf.from_array(x), Buf.from_array(w), Buf.empty((T, V))
+    rb = Buf.from_array(np.ascontiguousarray(resid, dtype=np.float32)) if resid is not None else None
+    check(lib().hy_lm_head_f32(xb.ptr, wb.ptr, rb.ptr if rb is not None else None, T, Hd, V, ob.ptr, None))
+    return ob.numpy()

@@ -145,6 +145,13 @@ int hy_model_forward(hy_model_ctx* ctx, const int32_t* input_ids_dev, uint32_t T
 int hy_model_forward_hidden(hy_model_ctx* ctx, const float* inputs_embeds_dev, uint32_t T,
                             const int32_t* positions_dev, uint32_t n_layers, float* hidden_dev, void* stream);
 
+/* lm_head_f32 (src/hunyuan_full_model.cpp:298-318) and the projections' GEMM:
+ * out[t][v] = sum_h x[t][h] * w[v][h] (+ resid[t][v] when resid_dev is not NULL),
+ * fp32 MFMA; x [T][hidden], w [vocab][hidden], all device memory; hidden a multiple
+ * of 16. */
+int hy_lm_head_f32(const float* x_dev, const float* w_dev, const float* resid_dev, uint32_t T, uint32_t hidden,
+                   uint32_t vocab, float* out_dev, void* stream);
+
 /* Per-kernel timing of this context's launches (as hy_moe_prof_*): kernel ids
  * 0 = qkv_proj, 1 = rope_qknorm, 2 = attention, 3 = o_proj. */
 int hy_attn_prof_enable(hy_attn_ctx* ctx, int32_t on);

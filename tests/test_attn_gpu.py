@@ -176,3 +176,17 @@ def test_decoder_layer_matches_oracle(gpu):
     other.close()
     moe.close()
     att.close()
+
+
+@pytest.mark.parametrize("M,N,Kd", [(7, 100, 48), (300, 512, 256), (2048, 4096, 512), (1111, 6144, 64)])
+def test_gemm_both_tilings(gpu, M, N, Kd):
+    """The projections' GEMM (hy_lm_head_f32) on its one-wave (small grids) and
+    four-wave (>= 512 tiles of 128 x 128) tilings, ragged M and N, with and without
+    the residual, against float64."""
+    rng = np.random.default_rng(M)
+    x = rng.standard_normal((M, Kd)).astype(np.float32)
+    w = rng.standard_normal((N, Kd)).astype(np.float32)
+    r = rng.standard_normal((M, N)).astype(np.float32)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    check(gpu.lm_head_f32(x, w), ref, f"gemm {M}x{N}x{Kd}")
+    check(gpu.lm_head_f32(x, w, r), ref + r, f"gemm+resid {M}x{N}x{Kd}")
