@@ -571,6 +571,9 @@ class Model:
                 for a in (embedding, final_norm, lm_head)]
         check(lib().hy_model_upload_globals(self.h, *[None if a is None else a.ctypes.data for a in arrs]))
 
+    def upload_globals_gguf(self, gguf):
+        check(lib().hy_model_upload_globals_gguf(self.h, gguf.h))
+
     def synth_globals(self, seed=42, std=0.02):
         check(lib().hy_model_synth_globals(self.h, seed, std))
 

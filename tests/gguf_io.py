@@ -14,7 +14,7 @@ import numpy as np
 
 (T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STR, T_ARR, T_U64, T_I64,
  T_F64) = range(13)
-GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_BF16 = 0, 1, 2, 8, 30
 
 _FMT = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32: "<i", T_F32: "<f",
         T_BOOL: "<?", T_U64: "<Q", T_I64: "<q", T_F64: "<d"}
@@ -90,3 +90,46 @@ def layer_meta(layer):
             ("hunyuan.num_experts", T_U32, layer.E),
             ("hunyuan.moe_topk", T_U32, layer.K),
             ("hunyuan.rms_norm_eps", T_F32, 1e-5)]
+
+
+def float_tensor(a, gtype):
+    """(bytes, values the reader gives back as f32) of a float array stored as F32,
+    F16 or BF16 (BF16: the upper 16 bits of each f32)."""
+    a = np.ascontiguousarray(a, np.float32)
+    if gtype == GGML_F32:
+        return a.tobytes(), a
+    if gtype == GGML_F16:
+        h = a.astype(np.float16)
+        return h.tobytes(), h.astype(np.float32)
+    if gtype == GGML_BF16:
+        b = (a.view(np.uint32) >> 16).astype(np.uint16)
+        return b.tobytes(), (b.astype(np.uint32) << 16).view(np.float32)
+    raise ValueError(gtype)
+
+
+def attn_tensors(w, block, gtype=GGML_F32, in_norm=None):
+    """blk.N.attn_* of an attention layer (oracle AttnWeights), as the reference loader
+    reads them; returns (tensors, the f32 values a reader recovers per name)."""
+    p = f"blk.{block}."
+    nq, H = w.nh * w.hd, w.H
+    items = [("attn_qkv.weight", w.qkv_w, [H, w.qkv_w.shape[0]]), ("attn_output.weight", w.o_w, [nq, H]),
+             ("attn_q_norm.weight", w.q_norm, [w.hd]), ("attn_k_norm.weight", w.k_norm, [w.hd])]
+    if in_norm is not None:
+        items.append(("attn_norm.weight", in_norm, [H]))
+    ts, vals = [], {}
+    for name, arr, ne in items:
+        data, back = float_tensor(arr, gtype)
+        ts.append((p + name, gtype, ne, data))
+        vals[name] = back.reshape(np.asarray(arr).shape)
+    return ts, vals
+
+
+def global_tensors(emb, final_norm, lm_head, gtype=GGML_F32):
+    V, H = emb.shape
+    ts, vals = [], {}
+    for name, arr, ne in (("token_embd.weight", emb, [H, V]), ("output_norm.weight", final_norm, [H]),
+                          ("output.weight", lm_head, [H, V])):
+        data, back = float_tensor(arr, gtype)
+        ts.append((name, gtype, ne, data))
+        vals[name] = back.reshape(np.asarray(arr).shape)
+    return ts, vals

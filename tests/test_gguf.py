@@ -205,3 +205,94 @@ def test_layer_from_gguf_mismatches_rejected(gpu, tmp_path):
         m.forward(0, xb, 2, ob)
     f.close()
     m.close()
+
+
+# ------------------------------------------------------------------ GPU: attention + globals
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_F16, G.GGML_BF16], ids=["f32", "f16", "bf16"])
+def test_attention_from_gguf(gpu, tmp_path, gtype):
+    """blk.N.attn_* (F32 / F16 / BF16) uploaded from a file compute exactly what the
+    same values uploaded directly compute; attn_norm.weight becomes the layer's input
+    norm."""
+    import hy_oracle_attn as A
+    H, nh, nkv, hd = 256, 8, 2, 64
+    w = A.synth_weights(H, nh, nkv, hd, seed=gtype, std=0.05, norm_jitter=0.2)
+    in_norm = (0.5 + np.random.default_rng(gtype).random(H)).astype(np.float32)
+    ts, vals = G.attn_tensors(w, 4, gtype, in_norm=in_norm)
+    f = gpu.Gguf(_write(tmp_path, "a.gguf", G.gguf_bytes([], ts)))
+    a = gpu.Attn(H, nh, nkv, hd, 32, num_layers=2)
+    a.upload_gguf(1, f, 4)
+    f.close()
+    a.upload(vals["attn_qkv.weight"], vals["attn_output.weight"], vals["attn_q_norm.weight"],
+             vals["attn_k_norm.weight"], layer=0)
+    a.set_input_norm(vals["attn_norm.weight"], layer=0)
+    x = np.random.default_rng(9).standard_normal((20, H)).astype(np.float32)
+    np.testing.assert_array_equal(a.run(x, layer=1), a.run(x, layer=0))
+    moe = gpu.Moe(H, 128, 16, 4, O.Q8_0, max_tokens=32)
+    moe.synth(0, seed=1, std=0.05)
+    xb = gpu.Buf.from_array(x)
+    o0, o1 = gpu.Buf.empty((20, H)), gpu.Buf.empty((20, H))
+    a.decoder_layer_forward(moe, 0, xb, 20, o0, layer=0)
+    a.decoder_layer_forward(moe, 0, xb, 20, o1, layer=1)
+    np.testing.assert_array_equal(o0.numpy(), o1.numpy())
+    moe.close()
+    a.close()
+
+
+@pytest.mark.gpu
+def test_attention_gguf_rejects_bad_tensors(gpu, tmp_path):
+    import hy_oracle_attn as A
+    H, nh, nkv, hd = 256, 8, 2, 64
+    w = A.synth_weights(H, nh, nkv, hd, seed=3)
+    good, _ = G.attn_tensors(w, 0)
+    a = gpu.Attn(H, nh, nkv, hd, 16)
+    cases = {
+        "missing k norm": [t for t in good if "attn_k_norm" not in t[0]],
+        "wrong shape": [(n, gt, [ne[0] // 2, ne[1]], d[: len(d) // 2]) if "attn_qkv" in n else (n, gt, ne, d)
+                        for n, gt, ne, d in good],
+        "quantized": [(n, G.GGML_Q8_0, ne, bytes(len(d) // 4 * 34 // 32)) if "attn_output" in n else (n, gt, ne, d)
+                      for n, gt, ne, d in good],
+    }
+    for case, ts in cases.items():
+        f = gpu.Gguf(_write(tmp_path, "bad.gguf", G.gguf_bytes([], ts)))
+        with pytest.raises(gpu.HyError):
+            a.upload_gguf(0, f, 0)
+        f.close()
+    a.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_BF16], ids=["f32", "bf16"])
+def test_model_globals_from_gguf(gpu, tmp_path, gtype):
+    """token_embd / output_norm / output from a file give the same logits as the same
+    values uploaded directly."""
+    import hy_oracle_attn as A
+    H, I, E, K, nh, nkv, hd, V, L = 256, 128, 16, 4, 8, 2, 64, 300, 1
+    rng = np.random.default_rng(5)
+    emb = rng.standard_normal((V, H)).astype(np.float32)
+    fn = (0.5 + rng.random(H)).astype(np.float32)
+    lm = (rng.standard_normal((V, H)) * 0.05).astype(np.float32)
+    ts, vals = G.global_tensors(emb, fn, lm, gtype)
+    path = _write(tmp_path, "g.gguf", G.gguf_bytes([], ts))
+    models = []
+    for from_file in (True, False):
+        m = gpu.Model(H, I, E, K, O.Q8_0, nh, nkv, hd, V, L, 16)
+        w = A.synth_weights(H, nh, nkv, hd, seed=7, std=0.05)
+        m.attn.upload(w.qkv_w, w.o_w, w.q_norm, w.k_norm)
+        m.moe.synth(0, seed=7, std=0.05)
+        if from_file:
+            f = gpu.Gguf(path)
+            m.upload_globals_gguf(f)
+            f.close()
+        else:
+            m.upload_globals(vals["token_embd.weight"], vals["output_norm.weight"], vals["output.weight"])
+        models.append(m)
+    ids = gpu.Buf.from_array(rng.integers(0, V, size=9).astype(np.int32))
+    outs = []
+    for m in models:
+        lb = gpu.Buf.empty((9, V))
+        m.forward(ids, 9, lb)
+        outs.append(lb.numpy())
+        m.close()
+    np.testing.assert_array_equal(outs[0], outs[1])
