@@ -368,6 +368,41 @@ hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// rope_f32 (src/rms_norm.cpp:97-152) / apply_rope_2d_f32 (src/hunyuan_image_gen.cpp:71-117)
+// in place on x [T][heads][hd]: one thread per interleaved pair
+__global__ void rope_apply_kernel(float* __restrict__ x, int T, int heads, int hd, int mode,
+                                  const int* __restrict__ positions, float theta, const float* __restrict__ cos_t,
+                                  const float* __restrict__ sin_t) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int np = hd / 2;
+    if (idx >= (size_t)T * heads * np) return;
+    const int d = (int)(idx % np);
+    const int t = (int)(idx / ((size_t)np * heads));
+    float c, sn;
+    if (mode == ROPE_1D) {
+        const float pos = positions ? (float)positions[t] : (float)t;
+        const float freq = 1.0f / powf(theta, (2.0f * (float)d) / (float)hd);
+        c = cosf(pos * freq);
+        sn = sinf(pos * freq);
+    } else {
+        c = cos_t[(size_t)t * hd + 2 * d];
+        sn = sin_t[(size_t)t * hd + 2 * d];
+    }
+    float* v = x + (idx / np) * hd + 2 * d;
+    const float x0 = v[0], x1 = v[1];
+    v[0] = x0 * c - x1 * sn;
+    v[1] = x0 * sn + x1 * c;
+}
+
+hipError_t launch_rope_apply(float* x, int T, int heads, int hd, int mode, const int* positions, float theta,
+                             const float* cos_t, const float* sin_t, hipStream_t s) {
+    const size_t n = (size_t)T * heads * (hd / 2);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_apply_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, T, heads, hd, mode,
+                       positions, theta, cos_t, sin_t);
+    return hipGetLastError();
+}
+
 // embedding_lookup_f32 (src/hunyuan_full_model.cpp:276-290): row ids[t] of the table;
 // an id outside the vocabulary gives a zero row instead of an out-of-bounds read
 __global__ void embed_kernel(const int* __restrict__ ids, const float* __restrict__ table, int T, int H, int vocab,

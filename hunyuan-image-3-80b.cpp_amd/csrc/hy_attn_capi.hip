@@ -456,6 +456,32 @@ int hy_lm_head_f32(const float* x, const float* w, const float* resid, uint32_t 
     return HY_OK;
 }
 
+int hy_rope_f32(float* x, uint32_t T, uint32_t heads, uint32_t hd, float theta, const int32_t* positions,
+                void* stream) {
+    if (!x) return fail(HY_ERR_INVALID, "null x");
+    if (hd == 0 || hd % 2) return fail(HY_ERR_INVALID, "head_dim=%u must be even", hd);
+    HIP_TRY(hy::launch_rope_apply(x, (int)T, (int)heads, (int)hd, hy::ROPE_1D, positions, theta, nullptr, nullptr,
+                                  static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_rope_2d_f32(float* x, uint32_t T, uint32_t heads, uint32_t hd, const float* cos_t, const float* sin_t,
+                   void* stream) {
+    if (!x || !cos_t || !sin_t) return fail(HY_ERR_INVALID, "null pointer");
+    if (hd == 0 || hd % 2) return fail(HY_ERR_INVALID, "head_dim=%u must be even", hd);
+    HIP_TRY(hy::launch_rope_apply(x, (int)T, (int)heads, (int)hd, hy::ROPE_TABLE, nullptr, 0.0f, cos_t, sin_t,
+                                  static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_embedding_lookup_f32(const int32_t* ids, const float* table, uint32_t T, uint32_t hidden, uint32_t vocab,
+                            float* out, void* stream) {
+    if (!ids || !table || !out) return fail(HY_ERR_INVALID, "null pointer");
+    if (hidden == 0 || hidden % 4) return fail(HY_ERR_INVALID, "hidden=%u must be a multiple of 4", hidden);
+    HIP_TRY(hy::launch_embed(ids, table, (int)T, (int)hidden, (int)vocab, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
 int hy_attn_prof_enable(hy_attn_ctx* c, int32_t on) {
     if (!c) return fail(HY_ERR_INVALID, "null ctx");
     if (!on) HY_TRY(drain_prof(c));

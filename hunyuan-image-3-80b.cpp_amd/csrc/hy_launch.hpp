@@ -132,5 +132,7 @@ hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int
 hipError_t launch_gather_kv(const float* src, int nkv, int L, int pos0, int T, int hd, float* dst, hipStream_t s);
 hipError_t launch_embed(const int* ids, const float* table, int T, int H, int vocab, float* out, hipStream_t s);
 hipError_t launch_fill_f32(float* out, size_t n, float v, hipStream_t s);
+hipError_t launch_rope_apply(float* x, int T, int heads, int hd, int mode, const int* positions, float theta,
+                             const float* cos_t, const float* sin_t, hipStream_t s);
 
 }  // namespace hy

@@ -152,6 +152,19 @@ int hy_model_forward_hidden(hy_model_ctx* ctx, const float* inputs_embeds_dev, u
 int hy_lm_head_f32(const float* x_dev, const float* w_dev, const float* resid_dev, uint32_t T, uint32_t hidden,
                    uint32_t vocab, float* out_dev, void* stream);
 
+/* rope_f32 (src/rms_norm.cpp:97-152) in place on x_dev [T][heads][head_dim]
+ * (positions_dev int32 [T] or NULL: 0..T-1), and apply_rope_2d_f32
+ * (src/hunyuan_image_gen.cpp:71-117) with tables [T][head_dim]; the reference rotates
+ * q and k in one call, here each is one call. */
+int hy_rope_f32(float* x_dev, uint32_t T, uint32_t heads, uint32_t head_dim, float theta,
+                const int32_t* positions_dev, void* stream);
+int hy_rope_2d_f32(float* x_dev, uint32_t T, uint32_t heads, uint32_t head_dim, const float* cos_dev,
+                   const float* sin_dev, void* stream);
+/* embedding_lookup_f32 (src/hunyuan_full_model.cpp:276-290): out[t] = table[ids[t]];
+ * ids outside 0..vocab-1 give zero rows. */
+int hy_embedding_lookup_f32(const int32_t* ids_dev, const float* table_dev, uint32_t T, uint32_t hidden,
+                            uint32_t vocab, float* out_dev, void* stream);
+
 /* Per-kernel timing of this context's launches (as hy_moe_prof_*): kernel ids
  * 0 = qkv_proj, 1 = rope_qknorm, 2 = attention, 3 = o_proj. */
 int hy_attn_prof_enable(hy_attn_ctx* ctx, int32_t on);

@@ -8,9 +8,11 @@
 #include <string>
 #include <vector>
 
+#include "hunyuan_model_attn.h"
 #include "hunyuan_model_moe.h"
 #include "hunyuan_moe_full.h"
 #include "hy_oracle.h"
+#include "hy_oracle_attn.h"
 
 static int g_fail = 0;
 
@@ -213,6 +215,112 @@ int main() {
             threw = e.code == HY_ERR_INVALID;
         }
         report(threw, "moe_forward_full rejects a hidden size the kernels do not tile");
+    }
+    // ---------------------------------------------------------------- attention half, decoder layer, backbone helpers
+    {
+        HunyuanConfig cfg;
+        cfg.hidden_size = 256;
+        cfg.num_attention_heads = 8;
+        cfg.num_key_value_heads = 2;
+        cfg.attention_head_dim = 64;
+        cfg.moe_intermediate_size = 128;
+        cfg.moe_topk = 2;
+        cfg.compute_derived();
+        const uint32_t Ha = 256, nh = 8, nkv = 2, hd = 64, Ta = 9, Ea = 8;
+        const size_t nq = (size_t)nh * hd, nk = (size_t)nkv * hd;
+        AttentionWeights aw;
+        aw.qkv_weight = synth(30, 4, 0, (nq + 2 * nk) * Ha, 0.05f);
+        aw.o_weight = synth(31, 5, 0, Ha * nq, 0.05f);
+        aw.q_norm_weight = synth(32, 0, 0, hd, 0.2f);
+        aw.k_norm_weight = synth(33, 0, 0, hd, 0.2f);
+        for (auto& v : aw.q_norm_weight) v += 1.0f;
+        for (auto& v : aw.k_norm_weight) v += 1.0f;
+        std::vector<float> xa = synth(34, 0, 0, (size_t)Ta * Ha, 1.0f);
+        std::vector<int> pos(Ta);
+        for (uint32_t t = 0; t < Ta; t++) pos[t] = (int)(3 * t + 1);
+        std::vector<float> out((size_t)Ta * Ha), ref(out.size()), q(Ta * nq), qr(q.size()), k(Ta * nk), kr(k.size()),
+            v(Ta * nk), vr(v.size());
+        attention_forward_cpu(xa.data(), aw, Ta, cfg, pos.data(), out.data(), q.data(), k.data(), v.data());
+        hyo_attention_forward(xa.data(), aw.qkv_weight.data(), aw.o_weight.data(), aw.q_norm_weight.data(),
+                              aw.k_norm_weight.data(), Ta, Ha, nh, nkv, hd, 1e-5f, 10000.0f, pos.data(), ref.data(),
+                              qr.data(), kr.data(), vr.data());
+        report(rel_err(out.data(), ref.data(), out.size()) < 1e-4 && rel_err(q.data(), qr.data(), q.size()) < 1e-4 &&
+                   rel_err(k.data(), kr.data(), k.size()) < 1e-4 && rel_err(v.data(), vr.data(), v.size()) < 1e-4,
+               "attention_forward_cpu (output and debug q/k/v)", errs(out.data(), ref.data(), out.size()));
+
+        std::vector<float> rq = synth(35, 0, 0, Ta * nq, 1.0f), rk = synth(36, 0, 0, Ta * nk, 1.0f), oq = rq, ok = rk;
+        rope_f32(rq.data(), rk.data(), Ta, nh, nkv, hd, 10000.0f, pos.data());
+        hyo_rope_f32(oq.data(), ok.data(), Ta, nh, nkv, hd, 10000.0f, pos.data());
+        report(rel_err(rq.data(), oq.data(), rq.size()) < 1e-5 && rel_err(rk.data(), ok.data(), rk.size()) < 1e-5,
+               "rope_f32", errs(rq.data(), oq.data(), rq.size()));
+
+        const uint32_t text = 3, ih = 2, iw = 3, seq = text + ih * iw;
+        std::vector<float> cs(seq * hd), sn(seq * hd), csr(cs.size()), snr(sn.size());
+        build_2d_rope(seq, hd, text, ih, iw, 10000.0f, cs.data(), sn.data());
+        hyo_build_2d_rope(seq, hd, text, ih, iw, 10000.0f, csr.data(), snr.data());
+        double dmax = 0;
+        for (size_t i = 0; i < cs.size(); i++)
+            dmax = std::fmax(dmax, std::fmax(std::fabs(cs[i] - csr[i]), std::fabs(sn[i] - snr[i])));
+        report(dmax < 4e-6, "build_2d_rope", "max abs diff " + std::to_string(dmax));
+        std::vector<float> tq = synth(37, 0, 0, seq * nq, 1.0f), tk = synth(38, 0, 0, seq * nk, 1.0f), uq = tq, uk = tk;
+        apply_rope_2d_f32(tq.data(), tk.data(), csr.data(), snr.data(), seq, nh, nkv, hd);
+        hyo_apply_rope_2d_f32(uq.data(), uk.data(), csr.data(), snr.data(), seq, nh, nkv, hd);
+        report(rel_err(tq.data(), uq.data(), tq.size()) < 1e-6 && rel_err(tk.data(), uk.data(), tk.size()) < 1e-6,
+               "apply_rope_2d_f32", errs(tq.data(), uq.data(), tq.size()));
+
+        DecoderLayerWeights dw;
+        dw.attn = aw;
+        dw.input_ln_weight = synth(39, 0, 0, Ha, 0.2f);
+        dw.post_attn_ln_weight = synth(40, 0, 0, Ha, 0.2f);
+        for (auto& x : dw.input_ln_weight) x += 1.0f;
+        for (auto& x : dw.post_attn_ln_weight) x += 1.0f;
+        const uint32_t Ia = 128;
+        dw.moe.num_experts = Ea;
+        dw.moe.router_weight = synth(41, 1, 0, (size_t)Ea * Ha, 0.05f);
+        dw.moe.shared_gate_up = synth(42, 2, Ea, (size_t)2 * Ia * Ha, 0.05f);
+        dw.moe.shared_down = synth(43, 3, Ea, (size_t)Ha * Ia, 0.05f);
+        dw.moe.experts.resize(Ea);
+        std::vector<float> gua, dna;
+        for (uint32_t e = 0; e < Ea; e++) {
+            dw.moe.experts[e].gate_up = synth(44, 2, e, (size_t)2 * Ia * Ha, 0.05f);
+            dw.moe.experts[e].down = synth(45, 3, e, (size_t)Ha * Ia, 0.05f);
+            gua.insert(gua.end(), dw.moe.experts[e].gate_up.begin(), dw.moe.experts[e].gate_up.end());
+            dna.insert(dna.end(), dw.moe.experts[e].down.begin(), dw.moe.experts[e].down.end());
+        }
+        cfg.num_experts = Ea;
+        std::vector<float> dout((size_t)Ta * Ha), xn(dout.size()), att(dout.size()), hres(dout.size()), hn(dout.size()),
+            moe(dout.size()), dref(dout.size());
+        decoder_layer_forward_cpu(xa.data(), dw, Ta, cfg, pos.data(), dout.data());
+        hyo_rms_norm_f32(xa.data(), dw.input_ln_weight.data(), xn.data(), Ta, Ha, 1e-5f);
+        hyo_attention_forward(xn.data(), aw.qkv_weight.data(), aw.o_weight.data(), aw.q_norm_weight.data(),
+                              aw.k_norm_weight.data(), Ta, Ha, nh, nkv, hd, 1e-5f, 10000.0f, pos.data(), att.data(),
+                              nullptr, nullptr, nullptr);
+        for (size_t i = 0; i < hres.size(); i++) hres[i] = xa[i] + att[i];
+        hyo_rms_norm_f32(hres.data(), dw.post_attn_ln_weight.data(), hn.data(), Ta, Ha, 1e-5f);
+        hyo_moe_forward_cpu(hn.data(), dw.moe.router_weight.data(), dw.moe.shared_gate_up.data(),
+                            dw.moe.shared_down.data(), gua.data(), dna.data(), Ta, Ha, Ea, Ia, 2, moe.data(), nullptr,
+                            nullptr, nullptr);
+        for (size_t i = 0; i < dref.size(); i++) dref[i] = hres[i] + moe[i];
+        report(rel_err(dout.data(), dref.data(), dout.size()) < 1e-4, "decoder_layer_forward_cpu",
+               errs(dout.data(), dref.data(), dout.size()));
+
+        const uint32_t Va = 40;
+        std::vector<float> table = synth(46, 6, 0, (size_t)Va * Ha, 1.0f), emb((size_t)Ta * Ha);
+        std::vector<int> ids(Ta);
+        for (uint32_t t = 0; t < Ta; t++) ids[t] = (int)((t * 7 + 3) % Va);
+        embedding_lookup_f32(ids.data(), table.data(), emb.data(), Ta, Ha);
+        bool eok = true;
+        for (uint32_t t = 0; t < Ta; t++) eok = eok && memcmp(&emb[(size_t)t * Ha], &table[(size_t)ids[t] * Ha], Ha * 4) == 0;
+        report(eok, "embedding_lookup_f32");
+        std::vector<float> lw = synth(47, 7, 0, (size_t)Va * Ha, 0.05f), lo((size_t)Ta * Va), lr(lo.size());
+        lm_head_f32(xa.data(), lw.data(), lo.data(), Ta, Ha, Va);
+        for (uint32_t t = 0; t < Ta; t++)
+            for (uint32_t j = 0; j < Va; j++) {
+                double acc = 0;
+                for (uint32_t h = 0; h < Ha; h++) acc += (double)xa[(size_t)t * Ha + h] * lw[(size_t)j * Ha + h];
+                lr[(size_t)t * Va + j] = (float)acc;
+            }
+        report(rel_err(lo.data(), lr.data(), lo.size()) < 1e-5, "lm_head_f32", errs(lo.data(), lr.data(), lo.size()));
     }
     printf("%d failure(s)\n", g_fail);
     return g_fail;
