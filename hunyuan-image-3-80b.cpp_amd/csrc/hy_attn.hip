@@ -5,12 +5,13 @@
 // 2D rotary tables (src/hunyuan_image_gen.cpp:11-117).
 //
 // Kernels:
-//  * gemm_nt_f32_kernel: C[M][N] = (R[M][N] +) A[M][K] . W[N][K]^T on
-//    v_mfma_f32_32x32x2f32 (the QKV and output projections; R is the decoder layer's
-//    residual stream when the output projection adds it).  Waves of 64 x 64 (2 x 2
-//    MFMA tiles), four per 128 x 128 work group (one per work group when that grid
-//    would be small), K in steps of 16 straight from global memory into registers
-//    (the next step's loads are in flight while the current one multiplies).
+//  * gemm_nt_f32_lds_kernel / gemm_nt_f32_kernel: C[M][N] = (R[M][N] +) A[M][K] .
+//    W[N][K]^T on v_mfma_f32_32x32x2f32 (the QKV and output projections; R is the
+//    decoder layer's residual stream when the output projection adds it).  Waves of
+//    64 x 64 (2 x 2 MFMA tiles).  Large grids: four waves per 128 x 128 work group,
+//    K in stages of 32 (16) floats DMA-copied into a swizzled LDS ring.  Small grids:
+//    one wave per work group, K in steps of 16 straight from global memory into
+//    registers (the next step's loads in flight while the current one multiplies).
 //  * rope_qknorm_kernel: one wave per (token, head): rotary embedding (1D positions,
 //    2D tables or none), per-head RMSNorm, written to q [T][nh][hd] and, for key
 //    heads, k / v into a [nkv][L][hd] cache at row pos0 + t.
@@ -27,6 +28,7 @@
 // at step j of a 16-wide chunk, so each lane reads 8 consecutive floats.
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
+#include "hy_lds.hpp"
 
 namespace hy {
 
@@ -37,8 +39,8 @@ __device__ __forceinline__ v16f_t mfma_f32(float a, float b, v16f_t c) {
 }
 
 // ---------------------------------------------------------------- GEMM (NT)
-// WM x WN waves per work group, each a 64 x 64 output tile: 2 x 2 (128 x 128) for
-// large grids; 1 x 1 when that grid would leave CUs idle (few tokens)
+// WM x WN waves per work group, each a 64 x 64 output tile (launched as 1 x 1: the
+// grids too small for the LDS-staged kernel below)
 template <int WM, int WN>
 __global__ __launch_bounds__(WAVE * WM * WN) void gemm_nt_f32_kernel(const float* __restrict__ A,
                                                                     const float* __restrict__ W,
@@ -106,12 +108,162 @@ __global__ __launch_bounds__(WAVE * WM * WN) void gemm_nt_f32_kernel(const float
         }
 }
 
+// LDS-staged GEMM for large grids: a 128 x 128 tile per work group of 4 waves (2 x 2,
+// 64 x 64 each).  K advances in stages of KC floats: each wave DMA-copies 32 rows of
+// A and 32 rows of W (KC floats each) global -> LDS into a RING-deep ring, so every
+// operand element is fetched once per work group (the register kernel above fetches
+// it once per wave) and no VGPRs hold copies in flight.  Rows sit in LDS as 16-byte
+// chunks whose position is XOR-swizzled by the row (gemm_swz), so the ds_read_b128
+// of 32 consecutive rows at one logical chunk spreads over all banks.
+template <int KC>
+struct GemmLds {
+    static constexpr int ROWB = KC * 4;                // bytes of one operand row in a stage
+    static constexpr int OPB = 128 * ROWB;             // one operand tile
+    static constexpr int BYTES = 2 * OPB;              // A tile, then W tile
+    static constexpr int CPO = 32 * ROWB / 1024;       // 1 KB copies per wave and operand
+    static constexpr int LOADS = 2 * CPO;              // copies per wave and stage
+    static_assert(KC == 16 || KC == 32, "stages of 16 or 32 floats");
+};
+
+// chunk swizzle of LDS row r: chunk c sits at position c ^ gemm_swz(r).  Any 8 (and
+// any 16) consecutive rows read at one logical chunk land in distinct 16-byte bank
+// groups of the 128-byte (256-byte) window.
+template <int KC>
+__device__ __forceinline__ int gemm_swz(int r) {
+    if constexpr (KC == 16)
+        return (((r >> 2) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1);
+    else
+        return (((r >> 2) & 1) << 2) | (((r >> 1) & 1) << 1) | ((r ^ (r >> 3)) & 1);
+}
+
+template <int KC, int RING, int WG_PER_CU>
+__global__ __launch_bounds__(256, WG_PER_CU) void gemm_nt_f32_lds_kernel(const float* __restrict__ A,
+                                                                        const float* __restrict__ W,
+                                                                        const float* __restrict__ R,
+                                                                        float* __restrict__ C, int M, int N, int K) {
+    using G = GemmLds<KC>;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[RING][G::BYTES];
+    const int tid = threadIdx.x, lane = tid % WAVE;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int lr = lane % 32, h = lane / 32;
+    const int mt = blockIdx.y * 128, nt = blockIdx.x * 128;
+
+    // copy sources: lane l of copy i lands at byte 16 l of the wave's 1 KB piece i,
+    // i.e. row 32 wv + (1024 i + 16 l) / ROWB, position p = l % (ROWB / 16), and
+    // fetches the chunk stored there, p ^ gemm_swz(row).  Rows past M / N re-read
+    // the last row (in bounds; their results are never stored).
+    const float* a_base = A + (size_t)mt * K;
+    const float* w_base = W + (size_t)nt * K;
+    uint32_t a_off[G::CPO], w_off[G::CPO];
+#pragma unroll
+    for (int i = 0; i < G::CPO; i++) {
+        const int o = 1024 * i + 16 * lane;
+        const int r = 32 * wv + o / G::ROWB;
+        const int c = (o % G::ROWB) / 16 ^ gemm_swz<KC>(r);
+        a_off[i] = (uint32_t)((min(mt + r, M - 1) - mt) * K + 4 * c) * 4u;
+        w_off[i] = (uint32_t)((min(nt + r, N - 1) - nt) * K + 4 * c) * 4u;
+    }
+    auto issue = [&](int s) {
+        uint8_t* st = ring[s % RING];
+        const uint8_t* ab = reinterpret_cast<const uint8_t*>(a_base + (size_t)s * KC);
+        const uint8_t* wb = reinterpret_cast<const uint8_t*>(w_base + (size_t)s * KC);
+#pragma unroll
+        for (int i = 0; i < G::CPO; i++) {
+            g2l16(ab + a_off[i], st + 32 * wv * G::ROWB + 1024 * i);
+            g2l16(wb + w_off[i], st + G::OPB + 32 * wv * G::ROWB + 1024 * i);
+        }
+    };
+
+    // operand reads: A rows 64 wm + 32 ti + lr, W rows 64 wn + 32 tj + lr; sub-step u
+    // (16 floats) takes floats 16 u + 8 h .. + 7 of the row as two chunks
+    const int wm = wv / 2, wn = wv % 2;
+    const int sw = gemm_swz<KC>(lr);  // rows 32 t + lr share the swizzle of lr
+    uint32_t ra[KC / 16][2], rw[KC / 16][2];
+#pragma unroll
+    for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int pos = 16 * ((4 * u + 2 * h + t) ^ sw);
+            ra[u][t] = (uint32_t)((64 * wm + lr) * G::ROWB + pos);
+            rw[u][t] = (uint32_t)(G::OPB + (64 * wn + lr) * G::ROWB + pos);
+        }
+    const uint32_t ring0 = lds_off(ring[0]);
+
+    v16f_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
+
+    const int nstage = K / KC;
+#pragma unroll
+    for (int s = 0; s < RING - 1; s++)
+        if (s < nstage) issue(s);
+    for (int s = 0; s < nstage; s++) {
+        wait_copies<G::LOADS, RING - 2>(nstage - 1 - s);
+        __syncthreads();
+        if (s + RING - 1 < nstage) issue(s + RING - 1);  // refills the slot read at s - 1
+        const uint32_t st = ring0 + (uint32_t)((s % RING) * G::BYTES);
+        v4i_t a[KC / 16][2][2], b[KC / 16][2][2];  // [u][tile][chunk]
+#pragma unroll
+        for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                a[u][0][t] = lds_b128_at<0>(st + ra[u][t]);
+                a[u][1][t] = lds_b128_at<32 * G::ROWB>(st + ra[u][t]);
+                b[u][0][t] = lds_b128_at<0>(st + rw[u][t]);
+                b[u][1][t] = lds_b128_at<32 * G::ROWB>(st + rw[u][t]);
+            }
+        lds_wait();
+#pragma unroll
+        for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    lds_pin(a[u][i][t]);
+                    lds_pin(b[u][i][t]);
+                }
+#pragma unroll
+        for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                    for (int tj = 0; tj < 2; tj++)
+                        // (__int_as_float: this hipcc miscompiles __builtin_bit_cast of a
+                        // vector element into a read of element 0)
+                        acc[ti][tj] = mfma_f32(__int_as_float(a[u][ti][j / 4][j % 4]),
+                                               __int_as_float(b[u][tj][j / 4][j % 4]), acc[ti][tj]);
+    }
+
+    const int m0 = mt + 64 * wm, n0 = nt + 64 * wn;
+#pragma unroll
+    for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+        for (int tj = 0; tj < 2; tj++) {
+            const int col = n0 + 32 * tj + lr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = m0 + 32 * ti + 8 * (v / 4) + 4 * h + v % 4;
+                if (row >= M) continue;
+                const size_t o = (size_t)row * N + col;
+                C[o] = R ? R[o] + acc[ti][tj][v] : acc[ti][tj][v];  // optional residual: R + A.W^T
+            }
+        }
+}
+
 hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
                               hipStream_t s) {
     const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
     if (big >= 512) {
         const dim3 grid((N + 127) / 128, (M + 127) / 128);
-        hipLaunchKernelGGL((gemm_nt_f32_kernel<2, 2>), grid, dim3(256), 0, s, A, W, R, C, M, N, K);
+        if (K % 32 == 0)
+            hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<32, 2, 2>), grid, dim3(256), 0, s, A, W, R, C, M, N, K);
+        else
+            hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<16, 3, 3>), grid, dim3(256), 0, s, A, W, R, C, M, N, K);
     } else {
         const dim3 grid((N + 63) / 64, (M + 63) / 64);
         hipLaunchKernelGGL((gemm_nt_f32_kernel<1, 1>), grid, dim3(64), 0, s, A, W, R, C, M, N, K);

@@ -16,6 +16,22 @@ __device__ __forceinline__ void g2l16(const void* g, void* lds_wave_base) {
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
 #define MM_WAIT_VM_LGKM(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (((N) >> 4) << 14))
 
+// vmcnt wait for the ring stage about to be consumed: the R stages issued after it
+// may stay in flight (R = min(RING - 2, stages left after it), LOADS copies per stage
+// and wave; copies complete in issue order)
+template <int LOADS, int R>
+__device__ __forceinline__ void wait_copies(int left) {
+    if constexpr (R == 0) {
+        MM_WAIT_VM_LGKM(0);
+    } else {
+        if (left >= R) {
+            MM_WAIT_VM_LGKM(R * LOADS);
+        } else {
+            wait_copies<LOADS, R - 1>(left);
+        }
+    }
+}
+
 // LDS reads of the ring are issued as plain ds_read instructions: the compiler does
 // not associate them with the in-flight global->LDS copies (it would otherwise wait
 // for every outstanding copy, including the stages being prefetched).  Their

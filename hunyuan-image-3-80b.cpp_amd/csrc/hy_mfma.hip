@@ -124,20 +124,6 @@ __device__ __forceinline__ v16f_t scale_outer(_Float16 dw, _Float16 dx, int lg) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, zero, 0, 0, 0);
 }
 
-// vmcnt wait for the stage being consumed: the R stages issued after it may stay in
-// flight (R = min(RING - 2, stages left after it), LOADS copies per stage and wave)
-template <int LOADS, int R>
-__device__ __forceinline__ void wait_stage(int left) {
-    if constexpr (R == 0) {
-        MM_WAIT_VM_LGKM(0);
-    } else {
-        if (left >= R) {
-            MM_WAIT_VM_LGKM(R * LOADS);
-        } else {
-            wait_stage<LOADS, R - 1>(left);
-        }
-    }
-}
 
 template <int WT, int MODE, class SH>
 __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(MmArgs a) {
@@ -331,7 +317,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         if (i < nstage) issue(i);
     for (int s = 0; s < nstage; s++) {
         // stage s landed (this wave's loads), and every wave's (barrier)
-        wait_stage<LOADS, MM_RING - 2>(nstage - 1 - s);
+        wait_copies<LOADS, MM_RING - 2>(nstage - 1 - s);
         __builtin_amdgcn_s_barrier();
         // refill: slot (s + RING - 1) % RING was last read in iteration s-1, finished
         // by every wave before this barrier -- issue it now so that RING - 1 stages are

@@ -178,11 +178,13 @@ def test_decoder_layer_matches_oracle(gpu):
     att.close()
 
 
-@pytest.mark.parametrize("M,N,Kd", [(7, 100, 48), (300, 512, 256), (2048, 4096, 512), (1111, 6144, 64)])
+@pytest.mark.parametrize("M,N,Kd", [(7, 100, 48), (300, 512, 256), (2048, 4096, 512), (1111, 6144, 64),
+                                    (1300, 6200, 80), (1290, 6150, 4096)])
 def test_gemm_both_tilings(gpu, M, N, Kd):
-    """The projections' GEMM (hy_lm_head_f32) on its one-wave (small grids) and
-    four-wave (>= 512 tiles of 128 x 128) tilings, ragged M and N, with and without
-    the residual, against float64."""
+    """The projections' GEMM (hy_lm_head_f32) on its one-wave register kernel (small
+    grids) and its LDS-staged kernel (>= 512 tiles of 128 x 128; stages of 32 floats
+    when K % 32 == 0, else 16), ragged M and N, with and without the residual,
+    against float64."""
     rng = np.random.default_rng(M)
     x = rng.standard_normal((M, Kd)).astype(np.float32)
     w = rng.standard_normal((N, Kd)).astype(np.float32)
