@@ -52,7 +52,9 @@ __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, fl
 // four waves take consecutive items, experts varying fastest so they share the
 // token rows in L1.  Small batches use <8,1> (64 experts -> 64 waves even at T=1),
 // large ones <4,8> (each Wr float4 feeds 4 tokens, 32 accumulators per lane).  The
-// h loop is unrolled so a lane's loads are issued together; the per-lane
+// h loop is software-pipelined: the loads of the next D - 1 chunks of 256 elements
+// are in flight while a chunk is accumulated (a large batch has about one wave per
+// SIMD, so the wave itself must cover the memory latency).  The per-lane
 // accumulation order is unchanged.
 template <int TPW, int EPW>
 __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
@@ -67,39 +69,71 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
     for (int t = 0; t < TPW; t++)
 #pragma unroll
         for (int e = 0; e < EPW; e++) acc[t][e] = 0.0f;
-    // small work items issue several chunks' loads at once; the 4x8 item keeps one
-    // chunk in flight (its 12 float4 loads per chunk already overlap)
-    constexpr int UNR = TPW * EPW <= 8 ? 4 : 1;
-#pragma unroll UNR
-    for (int h0 = 4 * lane; h0 < H; h0 += 4 * WAVE) {
-        float4 xv[TPW], wv[EPW];
+    // chunks in flight: about 144 VGPRs of staged operands
+    constexpr int PER = 4 * (TPW + EPW);
+    constexpr int D = 144 / PER >= 8 ? 8 : (144 / PER < 2 ? 2 : 144 / PER);
+    const int nch = (H + 4 * WAVE - 1) / (4 * WAVE);
+    float4 xb[D][TPW], wb[D][EPW];
+    // chunk i of this lane: elements h0 = 4 lane + 256 i .. + 3 (H % 4 == 0: a lane's
+    // 4 elements are all in range or all out).  The loads are unconditional, from
+    // clamped rows / offsets (always in bounds): tokens past T and experts past E
+    // accumulate a copy that is never stored, chunks past the lane's end are skipped
+    // in the accumulation.  (Zero-filling loads under a condition would make the
+    // compiler wait for every load at the branch join, serialising the pipeline.)
+    const float* xrow[TPW];
+    const float* wrow[EPW];
 #pragma unroll
-        for (int t = 0; t < TPW; t++)
-            xv[t] = (t0 + t < T) ? *reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * H + h0)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = 0; t < TPW; t++) xrow[t] = x + (size_t)min(t0 + t, T - 1) * H;
 #pragma unroll
-        for (int e = 0; e < EPW; e++)
-            wv[e] = (e0 + e < E) ? *reinterpret_cast<const float4*>(wr + (size_t)(e0 + e) * H + h0)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int e = 0; e < EPW; e++) wrow[e] = wr + (size_t)min(e0 + e, E - 1) * H;
+    auto load = [&](int i, float4* xd, float4* wd) {
+        const int h0 = min(4 * lane + 4 * WAVE * i, H - 4);
 #pragma unroll
-        for (int t = 0; t < TPW; t++)
+        for (int t = 0; t < TPW; t++) xd[t] = *reinterpret_cast<const float4*>(xrow[t] + h0);
 #pragma unroll
-            for (int e = 0; e < EPW; e++) {
-                float a = acc[t][e];
-                a = fmaf(xv[t].x, wv[e].x, a);
-                a = fmaf(xv[t].y, wv[e].y, a);
-                a = fmaf(xv[t].z, wv[e].z, a);
-                a = fmaf(xv[t].w, wv[e].w, a);
-                acc[t][e] = a;
-            }
-    }
+        for (int e = 0; e < EPW; e++) wd[e] = *reinterpret_cast<const float4*>(wrow[e] + h0);
+    };
 #pragma unroll
-    for (int t = 0; t < TPW; t++)
+    for (int d = 0; d < D - 1; d++) load(d, xb[d], wb[d]);
+    for (int i0 = 0; i0 < nch; i0 += D) {
 #pragma unroll
-        for (int e = 0; e < EPW; e++) {
-            const float v = tree_sum64(acc[t][e]);
-            if (lane == 0 && t0 + t < T && e0 + e < E) logits[(size_t)(t0 + t) * E + e0 + e] = v;
+        for (int d = 0; d < D; d++) {
+            const int i = i0 + d;
+            // refill the slot of chunk i - 1 with chunk i + D - 1
+            load(i + D - 1, xb[(d + D - 1) % D], wb[(d + D - 1) % D]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the refill ahead of the math
+            // chunk past the lane's end: the accumulators keep their values (a select,
+            // not a branch, so no wait is forced on the loads in flight)
+            const bool ok = i < nch && 4 * lane + 4 * WAVE * i < H;
+#pragma unroll
+            for (int t = 0; t < TPW; t++)
+#pragma unroll
+                for (int e = 0; e < EPW; e++) {
+                    const float4 xv = xb[d][t], wv = wb[d][e];
+                    float a = acc[t][e];
+                    a = fmaf(xv.x, wv.x, a);
+                    a = fmaf(xv.y, wv.y, a);
+                    a = fmaf(xv.z, wv.z, a);
+                    a = fmaf(xv.w, wv.w, a);
+                    acc[t][e] = ok ? a : acc[t][e];
+                }
         }
+    }
+    // the 64-lane tree p[l] += p[l + s], s = 32..1, one level at a time over all the
+    // accumulators, so each level's shuffles are in flight together
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1)
+#pragma unroll
+        for (int t = 0; t < TPW; t++)
+#pragma unroll
+            for (int e = 0; e < EPW; e++) acc[t][e] += shfl_down(acc[t][e], sh);
+    if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < TPW; t++)
+#pragma unroll
+            for (int e = 0; e < EPW; e++)
+                if (t0 + t < T && e0 + e < E) logits[(size_t)(t0 + t) * E + e0 + e] = acc[t][e];
+    }
 }
 
 // Top-k + weights per token (one wave each), optionally quantizing the token's
