@@ -9,9 +9,11 @@
 //    W[N][K]^T on v_mfma_f32_32x32x2f32 (the QKV and output projections; R is the
 //    decoder layer's residual stream when the output projection adds it).  Waves of
 //    64 x 64 (2 x 2 MFMA tiles).  Large grids: four waves per 128 x 128 work group,
-//    K in stages of 32 (16) floats DMA-copied into a swizzled LDS ring.  Small grids:
-//    one wave per work group, K in steps of 16 straight from global memory into
-//    registers (the next step's loads in flight while the current one multiplies).
+//    K in stages of 32 (16) floats DMA-copied into a swizzled LDS ring.  Mid-size
+//    grids (64..1023 tiles): the same kernel as 512 stream-K work groups that split
+//    the tiles' K stages evenly, and gemm_fixup_kernel summing the cut tiles' pieces
+//    in K order.  Small grids: one wave per work group, K in steps of 16 straight
+//    from global memory into registers.
 //  * rope_qknorm_kernel: one wave per (token, head): rotary embedding (1D positions,
 //    2D tables or none), per-head RMSNorm, written to q [T][nh][hd] and, for key
 //    heads, k / v into a [nkv][L][hd] cache at row pos0 + t.
@@ -136,44 +138,52 @@ __device__ __forceinline__ int gemm_swz(int r) {
         return (((r >> 2) & 1) << 2) | (((r >> 1) & 1) << 1) | ((r ^ (r >> 3)) & 1);
 }
 
+struct GemmArgs {
+    const float* A;
+    const float* W;
+    const float* R;  // optional residual (C = R + A.W^T)
+    float* C;
+    int M, N, K;
+    int mtiles;      // 128-row tiles of M
+    int tiles;
+    int G;           // 0: one tile per work group; else the stream-K work-group count
+    float* part;     // stream-K partial tiles: 2 G slots of 128 x 128 floats
+};
+
+// first row / column of tile t: N varies fastest, so consecutive work groups share
+// the A rows of one row of tiles (measured ~3 % faster than M-fastest at 4096 tokens)
+__device__ __forceinline__ int tile_m0(const GemmArgs& p, int t) { return 128 * (t / (p.tiles / p.mtiles)); }
+__device__ __forceinline__ int tile_n0(const GemmArgs& p, int t) { return 128 * (t % (p.tiles / p.mtiles)); }
+
+// Stream-K split: the tiles x (K / KC) stage units are cut into G equal contiguous
+// ranges, work group g taking units [g U / G, (g + 1) U / G).  A tile whose units all
+// fall in one range is written directly; the pieces of a tile cut between ranges are
+// written to partial slots (slot 2 g for the range's first piece, 2 g + 1 for its
+// last) and summed in K order by gemm_fixup_kernel.
+__device__ __forceinline__ long sk_lo(long g, long U, int G) { return g * U / G; }
+__device__ __forceinline__ int sk_owner(long u, long U, int G) { return (int)(((u + 1) * G - 1) / U); }
+
 template <int KC, int RING, int WG_PER_CU>
-__global__ __launch_bounds__(256, WG_PER_CU) void gemm_nt_f32_lds_kernel(const float* __restrict__ A,
-                                                                        const float* __restrict__ W,
-                                                                        const float* __restrict__ R,
-                                                                        float* __restrict__ C, int M, int N, int K) {
+__global__ __launch_bounds__(256, WG_PER_CU) void gemm_nt_f32_lds_kernel(GemmArgs p) {
     using G = GemmLds<KC>;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[RING][G::BYTES];
     const int tid = threadIdx.x, lane = tid % WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int lr = lane % 32, h = lane / 32;
-    const int mt = blockIdx.y * 128, nt = blockIdx.x * 128;
+    const int M = p.M, N = p.N, K = p.K;
+    const int nstage = K / KC;
 
-    // copy sources: lane l of copy i lands at byte 16 l of the wave's 1 KB piece i,
-    // i.e. row 32 wv + (1024 i + 16 l) / ROWB, position p = l % (ROWB / 16), and
-    // fetches the chunk stored there, p ^ gemm_swz(row).  Rows past M / N re-read
-    // the last row (in bounds; their results are never stored).
-    const float* a_base = A + (size_t)mt * K;
-    const float* w_base = W + (size_t)nt * K;
-    uint32_t a_off[G::CPO], w_off[G::CPO];
+    // copy lanes: lane l of copy i lands at byte 16 l of the wave's 1 KB piece i, i.e.
+    // row 32 wv + (1024 i + 16 l) / ROWB, position q = l % (ROWB / 16), and fetches
+    // the chunk stored there, q ^ gemm_swz(row).  Rows past M / N re-read the last
+    // row (in bounds; their results are never stored).
+    int crow[G::CPO], ccol[G::CPO];
 #pragma unroll
     for (int i = 0; i < G::CPO; i++) {
         const int o = 1024 * i + 16 * lane;
-        const int r = 32 * wv + o / G::ROWB;
-        const int c = (o % G::ROWB) / 16 ^ gemm_swz<KC>(r);
-        a_off[i] = (uint32_t)((min(mt + r, M - 1) - mt) * K + 4 * c) * 4u;
-        w_off[i] = (uint32_t)((min(nt + r, N - 1) - nt) * K + 4 * c) * 4u;
+        crow[i] = 32 * wv + o / G::ROWB;
+        ccol[i] = 4 * ((o % G::ROWB) / 16 ^ gemm_swz<KC>(crow[i]));
     }
-    auto issue = [&](int s) {
-        uint8_t* st = ring[s % RING];
-        const uint8_t* ab = reinterpret_cast<const uint8_t*>(a_base + (size_t)s * KC);
-        const uint8_t* wb = reinterpret_cast<const uint8_t*>(w_base + (size_t)s * KC);
-#pragma unroll
-        for (int i = 0; i < G::CPO; i++) {
-            g2l16(ab + a_off[i], st + 32 * wv * G::ROWB + 1024 * i);
-            g2l16(wb + w_off[i], st + G::OPB + 32 * wv * G::ROWB + 1024 * i);
-        }
-    };
-
     // operand reads: A rows 64 wm + 32 ti + lr, W rows 64 wn + 32 tj + lr; sub-step u
     // (16 floats) takes floats 16 u + 8 h .. + 7 of the row as two chunks
     const int wm = wv / 2, wn = wv % 2;
@@ -189,81 +199,184 @@ __global__ __launch_bounds__(256, WG_PER_CU) void gemm_nt_f32_lds_kernel(const f
         }
     const uint32_t ring0 = lds_off(ring[0]);
 
-    v16f_t acc[2][2];
+    // stages [s0, s1) of tile t into acc
+    auto segment = [&](int t, int s0, int s1, v16f_t (&acc)[2][2]) {
+        const int mt = tile_m0(p, t), nt = tile_n0(p, t);
+        const float* a_base = p.A + (size_t)mt * K;
+        const float* w_base = p.W + (size_t)nt * K;
+        uint32_t a_off[G::CPO], w_off[G::CPO];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
-
-    const int nstage = K / KC;
-#pragma unroll
-    for (int s = 0; s < RING - 1; s++)
-        if (s < nstage) issue(s);
-    for (int s = 0; s < nstage; s++) {
-        wait_copies<G::LOADS, RING - 2>(nstage - 1 - s);
-        __syncthreads();
-        if (s + RING - 1 < nstage) issue(s + RING - 1);  // refills the slot read at s - 1
-        const uint32_t st = ring0 + (uint32_t)((s % RING) * G::BYTES);
-        v4i_t a[KC / 16][2][2], b[KC / 16][2][2];  // [u][tile][chunk]
-#pragma unroll
-        for (int u = 0; u < KC / 16; u++)
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                a[u][0][t] = lds_b128_at<0>(st + ra[u][t]);
-                a[u][1][t] = lds_b128_at<32 * G::ROWB>(st + ra[u][t]);
-                b[u][0][t] = lds_b128_at<0>(st + rw[u][t]);
-                b[u][1][t] = lds_b128_at<32 * G::ROWB>(st + rw[u][t]);
-            }
-        lds_wait();
-#pragma unroll
-        for (int u = 0; u < KC / 16; u++)
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    lds_pin(a[u][i][t]);
-                    lds_pin(b[u][i][t]);
-                }
-#pragma unroll
-        for (int u = 0; u < KC / 16; u++)
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-#pragma unroll
-                for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-                    for (int tj = 0; tj < 2; tj++)
-                        // (__int_as_float: this hipcc miscompiles __builtin_bit_cast of a
-                        // vector element into a read of element 0)
-                        acc[ti][tj] = mfma_f32(__int_as_float(a[u][ti][j / 4][j % 4]),
-                                               __int_as_float(b[u][tj][j / 4][j % 4]), acc[ti][tj]);
-    }
-
-    const int m0 = mt + 64 * wm, n0 = nt + 64 * wn;
-#pragma unroll
-    for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-        for (int tj = 0; tj < 2; tj++) {
-            const int col = n0 + 32 * tj + lr;
-            if (col >= N) continue;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int row = m0 + 32 * ti + 8 * (v / 4) + 4 * h + v % 4;
-                if (row >= M) continue;
-                const size_t o = (size_t)row * N + col;
-                C[o] = R ? R[o] + acc[ti][tj][v] : acc[ti][tj][v];  // optional residual: R + A.W^T
-            }
+        for (int i = 0; i < G::CPO; i++) {
+            a_off[i] = (uint32_t)((min(mt + crow[i], M - 1) - mt) * K + ccol[i]) * 4u;
+            w_off[i] = (uint32_t)((min(nt + crow[i], N - 1) - nt) * K + ccol[i]) * 4u;
         }
+        auto issue = [&](int s) {
+            uint8_t* st = ring[(s - s0) % RING];
+            const uint8_t* ab = reinterpret_cast<const uint8_t*>(a_base + (size_t)s * KC);
+            const uint8_t* wb = reinterpret_cast<const uint8_t*>(w_base + (size_t)s * KC);
+#pragma unroll
+            for (int i = 0; i < G::CPO; i++) {
+                g2l16(ab + a_off[i], st + 32 * wv * G::ROWB + 1024 * i);
+                g2l16(wb + w_off[i], st + G::OPB + 32 * wv * G::ROWB + 1024 * i);
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
+#pragma unroll
+        for (int s = 0; s < RING - 1; s++)
+            if (s0 + s < s1) issue(s0 + s);
+        for (int s = s0; s < s1; s++) {
+            wait_copies<G::LOADS, RING - 2>(s1 - 1 - s);
+            __syncthreads();
+            if (s + RING - 1 < s1) issue(s + RING - 1);  // refills the slot read at s - 1
+            const uint32_t st = ring0 + (uint32_t)(((s - s0) % RING) * G::BYTES);
+            v4i_t a[KC / 16][2][2], b[KC / 16][2][2];  // [u][tile][chunk]
+#pragma unroll
+            for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    a[u][0][q] = lds_b128_at<0>(st + ra[u][q]);
+                    a[u][1][q] = lds_b128_at<32 * G::ROWB>(st + ra[u][q]);
+                    b[u][0][q] = lds_b128_at<0>(st + rw[u][q]);
+                    b[u][1][q] = lds_b128_at<32 * G::ROWB>(st + rw[u][q]);
+                }
+            lds_wait();
+#pragma unroll
+            for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int q = 0; q < 2; q++) {
+                        lds_pin(a[u][i][q]);
+                        lds_pin(b[u][i][q]);
+                    }
+#pragma unroll
+            for (int u = 0; u < KC / 16; u++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                        for (int tj = 0; tj < 2; tj++)
+                            // (__int_as_float: this hipcc miscompiles __builtin_bit_cast of
+                            // a vector element into a read of element 0)
+                            acc[ti][tj] = mfma_f32(__int_as_float(a[u][ti][j / 4][j % 4]),
+                                                   __int_as_float(b[u][tj][j / 4][j % 4]), acc[ti][tj]);
+        }
+        __syncthreads();  // every wave is done with the ring before it is refilled
+    };
+    auto store = [&](int t, const v16f_t (&acc)[2][2]) {
+        const int m0 = tile_m0(p, t) + 64 * wm, n0 = tile_n0(p, t) + 64 * wn;
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int tj = 0; tj < 2; tj++) {
+                const int col = n0 + 32 * tj + lr;
+                if (col >= N) continue;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int row = m0 + 32 * ti + 8 * (v / 4) + 4 * h + v % 4;
+                    if (row >= M) continue;
+                    const size_t o = (size_t)row * N + col;
+                    p.C[o] = p.R ? p.R[o] + acc[ti][tj][v] : acc[ti][tj][v];  // R + A.W^T
+                }
+            }
+    };
+
+    v16f_t acc[2][2];
+    if (p.G == 0) {
+        segment(blockIdx.x, 0, nstage, acc);
+        store(blockIdx.x, acc);
+        return;
+    }
+    const long U = (long)p.tiles * nstage;
+    const int g = blockIdx.x;
+    const long lo = sk_lo(g, U, p.G), hi = sk_lo(g + 1, U, p.G);
+    for (long u = lo; u < hi;) {
+        const int t = (int)(u / nstage);
+        const int s0 = (int)(u - (long)t * nstage);
+        const int s1 = (int)min((long)nstage, s0 + (hi - u));
+        segment(t, s0, s1, acc);
+        if (s0 == 0 && s1 == nstage) {
+            store(t, acc);
+        } else {
+            float* slot = p.part + (size_t)(2 * g + (u == lo ? 0 : 1)) * (128 * 128) + wv * 4096 + lane;
+#pragma unroll
+            for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) slot[((ti * 2 + tj) * 16 + v) * 64] = acc[ti][tj][v];
+        }
+        u += s1 - s0;
+    }
+}
+
+// Sum of the stream-K pieces of every cut tile, in K order (+ R): work group (t, y)
+// takes values 4 y .. 4 y + 3 of every thread of tile t (tiles written directly return
+// at once).  Thread layout and slot layout are the GEMM's: wave w, lane l, value
+// q = (2 ti + tj) 16 + v at slot + 4096 w + 64 q + l.
+constexpr int FIX_Q = 4;
+__global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs p, int nstage) {
+    const int t = blockIdx.x;
+    const long U = (long)p.tiles * nstage;
+    const long u0 = (long)t * nstage, u1 = u0 + nstage - 1;
+    const int g0 = sk_owner(u0, U, p.G), g1 = sk_owner(u1, U, p.G);
+    if (g0 == g1) return;
+    const int tid = threadIdx.x, wv = tid / WAVE, lane = tid % WAVE;
+    const int lr = lane % 32, h = lane / 32, wm = wv / 2, wn = wv % 2;
+    const int m0 = tile_m0(p, t) + 64 * wm, n0 = tile_n0(p, t) + 64 * wn;
+    // the first piece is g0's last one unless g0's range starts at this tile
+    const int slot0 = 2 * g0 + (sk_lo(g0, U, p.G) == u0 ? 0 : 1);
+    const float* __restrict__ part = p.part;
+    const size_t base = (size_t)wv * 4096 + (size_t)blockIdx.y * FIX_Q * 64 + lane;
+    float sum[FIX_Q];
+#pragma unroll
+    for (int j = 0; j < FIX_Q; j++) sum[j] = part[(size_t)slot0 * (128 * 128) + base + 64 * j];
+    for (int g = g0 + 1; g <= g1; g++) {
+        float x[FIX_Q];
+#pragma unroll
+        for (int j = 0; j < FIX_Q; j++) x[j] = part[(size_t)(2 * g) * (128 * 128) + base + 64 * j];
+#pragma unroll
+        for (int j = 0; j < FIX_Q; j++) sum[j] += x[j];
+    }
+#pragma unroll
+    for (int j = 0; j < FIX_Q; j++) {
+        const int q = blockIdx.y * FIX_Q + j, ti = q / 32, tj = (q / 16) % 2, v = q % 16;
+        const int col = n0 + 32 * tj + lr, row = m0 + 32 * ti + 8 * (v / 4) + 4 * h + v % 4;
+        if (col < p.N && row < p.M) {
+            const size_t o = (size_t)row * p.N + col;
+            p.C[o] = p.R ? p.R[o] + sum[j] : sum[j];
+        }
+    }
+}
+
+size_t gemm_nt_f32_ws_bytes() { return (size_t)2 * GEMM_SK_GROUPS * 128 * 128 * 4; }
+
+// fewer 128 x 128 tiles than two full rounds of resident work groups (but enough to
+// split): stream-K over all of them, two 64 KB-LDS work groups per CU
+bool gemm_nt_f32_uses_ws(int M, int N, int K) {
+    const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+    return K % 32 == 0 && tiles >= 64 && tiles < 2 * GEMM_SK_GROUPS && tiles * (K / 32) >= 4 * GEMM_SK_GROUPS;
 }
 
 hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
-                              hipStream_t s) {
-    const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
-    if (big >= 512) {
-        const dim3 grid((N + 127) / 128, (M + 127) / 128);
+                              hipStream_t s, float* ws) {
+    const int mtiles = (M + 127) / 128, tiles = mtiles * ((N + 127) / 128);
+    GemmArgs p{A, W, R, C, M, N, K, mtiles, tiles, 0, ws};
+    if (ws && gemm_nt_f32_uses_ws(M, N, K)) {
+        p.G = GEMM_SK_GROUPS;
+        hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<32, 2, 2>), dim3(p.G), dim3(256), 0, s, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(gemm_fixup_kernel, dim3(tiles, 64 / FIX_Q), dim3(256), 0, s, p, K / 32);
+    } else if (tiles >= 512) {
         if (K % 32 == 0)
-            hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<32, 2, 2>), grid, dim3(256), 0, s, A, W, R, C, M, N, K);
+            hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<32, 2, 2>), dim3(tiles), dim3(256), 0, s, p);
         else
-            hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<16, 3, 3>), grid, dim3(256), 0, s, A, W, R, C, M, N, K);
+            hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<16, 3, 3>), dim3(tiles), dim3(256), 0, s, p);
     } else {
         const dim3 grid((N + 63) / 64, (M + 63) / 64);
         hipLaunchKernelGGL((gemm_nt_f32_kernel<1, 1>), grid, dim3(64), 0, s, A, W, R, C, M, N, K);

@@ -81,6 +81,7 @@ struct hy_attn_ctx {
     float* kf = nullptr;       // [nkv][Tm][hd] (forward without cache)
     float* vf = nullptr;
     float* merged = nullptr;   // [Tm][nh*hd]
+    float* gemm_ws = nullptr;  // stream-K partial tiles of the projections' GEMM
     float* xn = nullptr;       // decoder layer: normed input [Tm][H]
     float* hres = nullptr;     // decoder layer: x + attention [Tm][H]
     bool prof = false;
@@ -182,7 +183,7 @@ int run(hy_attn_ctx* c, const AttnLayer& W, const float* x, int T, int mode, con
         const float* cos_t, const float* sin_t, int norm_assoc, float* k, float* v, int Lrows, int pos0, int kv_len,
         int causal, float* out, hipStream_t s, const float* resid = nullptr) {
     HY_TRY(timed(c, AK_QKV, s,
-                 [&] { return hy::launch_gemm_nt_f32(x, W.qkv_w, nullptr, c->qkv, T, c->nqkv, c->H, s); }));
+                 [&] { return hy::launch_gemm_nt_f32(x, W.qkv_w, nullptr, c->qkv, T, c->nqkv, c->H, s, c->gemm_ws); }));
     hy::RopeNormArgs r{c->qkv, T, c->nh, c->nkv, c->hd, c->nqkv, mode, positions, c->cfg.rope_theta, cos_t, sin_t,
                        W.q_norm, W.k_norm, c->cfg.rms_norm_eps, norm_assoc, c->q, k, v, Lrows, pos0};
     HY_TRY(timed(c, AK_ROPE, s, [&] { return hy::launch_rope_qknorm(r, s); }));
@@ -190,7 +191,10 @@ int run(hy_attn_ctx* c, const AttnLayer& W, const float* x, int T, int mode, con
                     1.0f / sqrtf((float)c->hd)};
     HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s); }));
     HY_TRY(timed(c, AK_OPROJ, s,
-                 [&] { return hy::launch_gemm_nt_f32(c->merged, W.o_w, resid, out, T, c->H, c->nh * c->hd, s); }));
+                 [&] {
+                     return hy::launch_gemm_nt_f32(c->merged, W.o_w, resid, out, T, c->H, c->nh * c->hd, s,
+                                                   c->gemm_ws);
+                 }));
     return HY_OK;
 }
 
@@ -264,7 +268,8 @@ int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out) {
         float** p;
         size_t n;
     } parts[] = {{&c->qkv, Tm * c->nqkv}, {&c->q, Tm * nq},  {&c->kf, Tm * nk},   {&c->vf, Tm * nk},
-                 {&c->merged, Tm * nq},   {&c->xn, Tm * H}, {&c->hres, Tm * H}};
+                 {&c->merged, Tm * nq},   {&c->xn, Tm * H}, {&c->hres, Tm * H},
+                 {&c->gemm_ws, hy::gemm_nt_f32_ws_bytes() / 4}};
     size_t total = 0;
     for (auto& p : parts) total += al256(p.n * 4);
     if (hipMalloc(&c->arena, total) != hipSuccess) {
@@ -451,8 +456,16 @@ int hy_lm_head_f32(const float* x, const float* w, const float* resid, uint32_t 
     if (T == 0 || vocab == 0 || hidden == 0 || hidden % 16)
         return fail(HY_ERR_INVALID, "bad GEMM shape T=%u hidden=%u vocab=%u (hidden a multiple of 16)", T, hidden,
                     vocab);
-    HIP_TRY(hy::launch_gemm_nt_f32(x, w, resid, out, (int)T, (int)vocab, (int)hidden,
-                                   static_cast<hipStream_t>(stream)));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // mid-size grids take the stream-K split, which needs a scratch of partial tiles:
+    // stream-ordered, freed after the launch
+    float* ws = nullptr;
+    if (hy::gemm_nt_f32_uses_ws((int)T, (int)vocab, (int)hidden) &&
+        hipMallocAsync(reinterpret_cast<void**>(&ws), hy::gemm_nt_f32_ws_bytes(), s) != hipSuccess)
+        return fail(HY_ERR_NOMEM, "GEMM scratch allocation failed");
+    const hipError_t e = hy::launch_gemm_nt_f32(x, w, resid, out, (int)T, (int)vocab, (int)hidden, s, ws);
+    if (ws) (void)hipFreeAsync(ws, s);
+    HIP_TRY(e);
     return HY_OK;
 }
 
@@ -630,7 +643,7 @@ int hy_model_forward(hy_model_ctx* m, const int32_t* ids, uint32_t T, const int3
     const float* h = nullptr;
     HY_TRY(run_layers(m, m->hb, T, positions, (uint32_t)m->L, s, &h));
     HIP_TRY(hy::launch_rms_norm_w(h, m->fnorm, (int)T, m->H, m->cfg.attn.rms_norm_eps, m->normed, s));
-    HIP_TRY(hy::launch_gemm_nt_f32(m->normed, m->lm_head, nullptr, logits, (int)T, m->V, m->H, s));
+    HIP_TRY(hy::launch_gemm_nt_f32(m->normed, m->lm_head, nullptr, logits, (int)T, m->V, m->H, s, m->attn->gemm_ws));
     return HY_OK;
 }
 

@@ -122,9 +122,14 @@ struct FlashArgs {
     int causal;
     float scale;
 };
-// C = A . W^T, plus R elementwise when R is not null (R may alias nothing written here)
+// C = A . W^T, plus R elementwise when R is not null (R may alias nothing written here).
+// ws: gemm_nt_f32_ws_bytes() of device scratch for the stream-K split of mid-size grids
+// (gemm_nt_f32_uses_ws); without it those grids run one tile per work group.
+constexpr int GEMM_SK_GROUPS = 512;  // stream-K work groups: two per CU
+size_t gemm_nt_f32_ws_bytes();
+bool gemm_nt_f32_uses_ws(int M, int N, int K);
 hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
-                              hipStream_t s);
+                              hipStream_t s, float* ws = nullptr);
 hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s);
 hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s);
 hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,

@@ -179,12 +179,15 @@ def test_decoder_layer_matches_oracle(gpu):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(7, 100, 48), (300, 512, 256), (2048, 4096, 512), (1111, 6144, 64),
-                                    (1300, 6200, 80), (1290, 6150, 4096)])
+                                    (1300, 6200, 80), (1290, 6150, 4096), (2100, 8200, 64), (520, 6150, 1024)])
 def test_gemm_both_tilings(gpu, M, N, Kd):
-    """The projections' GEMM (hy_lm_head_f32) on its one-wave register kernel (small
-    grids) and its LDS-staged kernel (>= 512 tiles of 128 x 128; stages of 32 floats
-    when K % 32 == 0, else 16), ragged M and N, with and without the residual,
-    against float64."""
+    """The projections' GEMM (hy_lm_head_f32) on each of its paths, ragged M and N, with
+    and without the residual, against float64:
+      * one-wave register kernel: small grids (300x512, 1111x6144 with K=64);
+      * LDS-staged, one 128 x 128 tile per work group: >= 1024 tiles (2100x8200), or
+        K % 32 != 0 with >= 512 tiles (1300x6200x80, stages of 16 floats);
+      * LDS-staged stream-K + fix-up: 64..1023 tiles with K % 32 == 0 (2048x4096x512,
+        1290x6150x4096, 520x6150x1024)."""
     rng = np.random.default_rng(M)
     x = rng.standard_normal((M, Kd)).astype(np.float32)
     w = rng.standard_normal((N, Kd)).astype(np.float32)
