@@ -227,17 +227,18 @@ def attn_main(a, hy):
     m.upload(w.qkv_w, w.o_w, w.q_norm, w.k_norm)
     x = hy.Buf.from_array(np.random.default_rng(a.seed).standard_normal((T, ATTN["H"])).astype(np.float32))
     out = hy.Buf.empty((T, ATTN["H"]))
+    st = hy.Stream()
     for _ in range(a.warmup):
-        m.forward(x, T, out)
+        m.forward(x, T, out, stream=st.h)
     hy.sync()
     ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
     t0 = time.perf_counter()
-    hy.check(hy.lib().hy_event_record(ev0, None))
+    hy.check(hy.lib().hy_event_record(ev0, st.h))
     for _ in range(a.steps):
-        m.forward(x, T, out)
-    hy.check(hy.lib().hy_event_record(ev1, None))
+        m.forward(x, T, out, stream=st.h)
+    hy.check(hy.lib().hy_event_record(ev1, st.h))
     hy.sync()
     wall = time.perf_counter() - t0
     ms = hy.C.c_float()
@@ -245,7 +246,7 @@ def attn_main(a, hy):
     ms_per_step = ms.value / a.steps
     m.prof_enable(True)
     for _ in range(a.steps):
-        m.forward(x, T, out)
+        m.forward(x, T, out, stream=st.h)
     hy.sync()
     prof = {k: v for k, v in m.prof_read().items() if v[0] > 0}
     m.prof_enable(False)
@@ -292,17 +293,18 @@ def model_main(a, hy):
     setup_s = time.perf_counter() - t0
     ids = hy.Buf.from_array(np.random.default_rng(a.seed).integers(0, VOCAB, size=T).astype(np.int32))
     logits = hy.Buf.empty((T, VOCAB))
+    st = hy.Stream()
     for _ in range(a.warmup):
-        m.forward(ids, T, logits)
+        m.forward(ids, T, logits, stream=st.h)
     hy.sync()
     ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
     t1 = time.perf_counter()
-    hy.check(hy.lib().hy_event_record(ev0, None))
+    hy.check(hy.lib().hy_event_record(ev0, st.h))
     for _ in range(a.steps):
-        m.forward(ids, T, logits)
-    hy.check(hy.lib().hy_event_record(ev1, None))
+        m.forward(ids, T, logits, stream=st.h)
+    hy.check(hy.lib().hy_event_record(ev1, st.h))
     hy.sync()
     wall = time.perf_counter() - t1
     ms = hy.C.c_float()
@@ -311,7 +313,7 @@ def model_main(a, hy):
     # per-kernel times of the two layer contexts (profiled pass)
     m.moe.prof_enable(True)
     m.attn.prof_enable(True)
-    m.forward(ids, T, logits)
+    m.forward(ids, T, logits, stream=st.h)
     hy.sync()
     prof = {k: v for k, v in {**m.moe.prof_read(), **m.attn.prof_read()}.items() if v[0] > 0}
     m.moe.prof_enable(False)
@@ -352,6 +354,7 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="replay the step as a captured hipGraph")
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
@@ -398,13 +401,28 @@ def main():
         xh[:, 0] = 1.0
         x = hy.Buf.from_array(xh)
     out = hy.Buf.empty((T, H))
-    stream = None
+    st = hy.Stream()
+    stream = st.h
 
-    def step(i):
+    def eager_step(i):
         if wl.get("stack"):
             m.stack_forward(0, nl, x, T, 1e-5, out, stream)
         else:
             m.forward(i % rot, x, T, out, stream)
+
+    for i in range(a.warmup):
+        eager_step(i)
+    hy.sync()
+    # kernels are launched from the host on a created stream (measured faster than the
+    # null stream); --graph replays the layer forward captured once per resident weight
+    # set instead (hipGraph; on this stack no faster than the eager launches)
+    graphs = [hy.Graph(st, lambda l=l: eager_step(l)) for l in range(rot)] if a.graph else []
+
+    def step(i):
+        if graphs:
+            graphs[i % rot].launch()
+        else:
+            eager_step(i)
 
     for i in range(a.warmup):
         step(i)
@@ -426,10 +444,10 @@ def main():
     tokens_per_s = T / (ms_per_step / 1e3)
 
     D, counts = m.last_routing()
-    # per-kernel durations on the launch stream (separate, profiled pass)
+    # per-kernel durations on the launch stream (separate, profiled pass, eager launches)
     m.prof_enable(True)
     for i in range(a.steps):
-        step(i)
+        eager_step(i)
     hy.sync()
     prof = m.prof_read()
     m.prof_enable(False)
@@ -468,11 +486,15 @@ def main():
         "layer_int8_util": layer_ops / t_layer / PEAK_INT8,
         "roofline": roof,
         "kernels_ms": {k: round(t / n, 5) for k, (n, t) in kern.items()},
+        "launch": "hip_graph" if a.graph else "eager",
         "wall_s": wall,
     }
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(wl, a.seed)
     print(json.dumps(res), flush=True)
+    for g in graphs:
+        g.close()
+    st.close()
     m.close()
 
 

@@ -801,6 +801,31 @@ int hy_event_record(void* ev, void* s) {
     HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(s)));
     return HY_OK;
 }
+int hy_graph_begin(void* s) {
+    if (!s) return fail(HY_ERR_INVALID, "capture needs a created stream (not the null stream)");
+    HIP_TRY(hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeThreadLocal));
+    return HY_OK;
+}
+int hy_graph_end(void* s, void** exec) {
+    if (!s || !exec) return fail(HY_ERR_INVALID, "null stream/exec");
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(static_cast<hipStream_t>(s), &g));
+    hipGraphExec_t x = nullptr;
+    const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_TRY(e);
+    *exec = x;
+    return HY_OK;
+}
+int hy_graph_launch(void* exec, void* s) {
+    if (!exec) return fail(HY_ERR_INVALID, "null graph");
+    HIP_TRY(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(s)));
+    return HY_OK;
+}
+int hy_graph_destroy(void* exec) {
+    if (exec) HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)));
+    return HY_OK;
+}
 int hy_event_elapsed_ms(void* a, void* b, float* ms) {
     HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(b)));
     HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)));

@@ -119,6 +119,10 @@ _SIGS = {
     "hy_event_destroy": (C.c_int, [_vp]),
     "hy_event_record": (C.c_int, [_vp, _vp]),
     "hy_event_elapsed_ms": (C.c_int, [_vp, _vp, C.POINTER(C.c_float)]),
+    "hy_graph_begin": (C.c_int, [_vp]),
+    "hy_graph_end": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "hy_graph_launch": (C.c_int, [_vp, _vp]),
+    "hy_graph_destroy": (C.c_int, [_vp]),
     "hy_synth_fill": (C.c_int, [_vp, C.c_size_t, _u64, _u32, _u32, _u32, _f, _vp]),
     "hy_moe_prof_enable": (C.c_int, [_vp, _i32]),
     "hy_moe_prof_read": (C.c_int, [_vp, _i32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]),
@@ -207,6 +211,49 @@ class Buf:
 
 def sync():
     check(lib().hy_device_synchronize())
+
+
+class Stream:
+    """A created HIP stream (hy_stream_create); .h is passed as the stream argument."""
+
+    def __init__(self):
+        self.h = C.c_void_p()
+        check(lib().hy_stream_create(C.byref(self.h)))
+
+    def synchronize(self):
+        check(lib().hy_stream_synchronize(self.h))
+
+    def close(self):
+        if self.h:
+            check(lib().hy_stream_destroy(self.h))
+            self.h = C.c_void_p()
+
+
+class Graph:
+    """Work issued on `stream` by fn() captured once (hy_graph_begin / hy_graph_end) and
+    replayed with launch()."""
+
+    def __init__(self, stream: Stream, fn):
+        self.stream = stream
+        self.h = C.c_void_p()
+        check(lib().hy_graph_begin(stream.h))
+        try:
+            fn()
+        except Exception:
+            g = C.c_void_p()
+            lib().hy_graph_end(stream.h, C.byref(g))   # end the capture; keep the first error
+            if g:
+                lib().hy_graph_destroy(g)
+            raise
+        check(lib().hy_graph_end(stream.h, C.byref(self.h)))
+
+    def launch(self):
+        check(lib().hy_graph_launch(self.h, self.stream.h))
+
+    def close(self):
+        if self.h:
+            check(lib().hy_graph_destroy(self.h))
+            self.h = C.c_void_p()
 
 
 # ------------------------------------------------------------------ context

@@ -259,6 +259,18 @@ int hy_event_create(void** ev);
 int hy_event_destroy(void* ev);
 int hy_event_record(void* ev, void* stream);
 int hy_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Capture of stream work into a replayable graph: begin / end (instantiate) / launch /
+ * destroy.  No counterpart in the reference (its layer runs on the CPU); for callers
+ * that replay a fixed-shape step (decode) without per-kernel launch costs.
+ * hy_moe_forward and hy_moe_stack_forward allocate nothing, read nothing back to the
+ * host and record no memset, so they can be captured, with profiling off; a replay
+ * equals the eager call bit for bit.  A replay reads the pointers and sizes of the
+ * captured calls.  The stream must be a created stream (hy_stream_create), not the
+ * null stream. */
+int hy_graph_begin(void* stream);
+int hy_graph_end(void* stream, void** graph_exec);
+int hy_graph_launch(void* graph_exec, void* stream);
+int hy_graph_destroy(void* graph_exec);
 /* Fill f32 [n] with the synthetic N(0,std) stream (seed, layer, tensor, expert). */
 int hy_synth_fill(float* dev, size_t n, uint64_t seed, uint32_t layer, uint32_t tensor,
                   uint32_t expert, float std, void* stream);
