@@ -113,7 +113,9 @@ int get_event(hy_attn_ctx* c, hipEvent_t* ev) {
         c->free_events.pop_back();
         return HY_OK;
     }
-    HIP_TRY(hipEventCreate(ev));
+    // timing-only events: no system-scope fence (cache writeback / invalidate) when
+    // they are recorded, which would otherwise be counted in the kernel's time
+    HIP_TRY(hipEventCreateWithFlags(ev, hipEventDisableSystemFence));
     return HY_OK;
 }
 
