@@ -506,9 +506,11 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int lr = lane % 32, h = lane / 32;
     const int n_qt = (a.T + 31) / 32;
-    // longest (causal) query tiles first
-    const int qt = n_qt - 1 - (int)(blockIdx.x / a.nkv);
-    const int g = (int)(blockIdx.x % a.nkv);
+    // chunk-major, and inside a chunk the longest (causal) query tiles first
+    const int per_chunk = n_qt * a.nkv;
+    const int chunk = (int)blockIdx.x / per_chunk, rem = (int)blockIdx.x % per_chunk;
+    const int qt = n_qt - 1 - rem / a.nkv;
+    const int g = rem % a.nkv;
     const int q0 = qt * 32;
     const int head = g * 4 + wave;  // 4 query heads per kv group
     const int qrow = min(q0 + lr, a.T - 1);
@@ -529,6 +531,10 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     const int last_q = min(q0 + 31, a.T - 1);
     const int key_end = a.causal ? min(a.kv_len, a.q_pos0 + last_q + 1) : a.kv_len;
     const int nblk = (key_end + 31) / 32;
+    // this work group's key blocks: all of them, or chunk `chunk` of cb blocks
+    const int nc = a.cb ? (nblk + a.cb - 1) / a.cb : 1;
+    if (chunk >= nc) return;  // whole work group: the tile has fewer chunks
+    const int kb0 = a.cb ? chunk * a.cb : 0, kb1 = a.cb ? min(nblk, kb0 + a.cb) : nblk;
 
     const float* kg = a.k + (size_t)g * a.L * HD;
     const float* vg = a.v + (size_t)g * a.L * HD;
@@ -558,11 +564,11 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     float m_run = -INFINITY, l_run = 0.0f;
     const int my_q = a.q_pos0 + q0 + lr;  // key index of this lane's query (causal bound)
 
-    fetch(0);
-    for (int kb = 0; kb < nblk; kb++) {
+    fetch(kb0);
+    for (int kb = kb0; kb < kb1; kb++) {
         __syncthreads();  // the previous block's LDS reads are done
         stash();
-        if (kb + 1 < nblk) fetch(kb + 1);
+        if (kb + 1 < kb1) fetch(kb + 1);
         __syncthreads();
         // S^T[key][q] = sum_d K[key][d] Q[q][d]
         v16f_t s = v16f_t{};
@@ -609,6 +615,17 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
                 o[c] = mfma_f32(vs[key * S::VP + 32 * c + lr], s[v], o[c]);
             }
     }
+    if (nc > 1) {
+        // partial result of this chunk: unnormalised O^T, running max and sum
+        float* pp = a.part + ((size_t)((qt * a.nch + chunk) * a.nkv + g) * 4 + wave) * (HD * 32 + 128);
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) pp[(c * 16 + v) * 64 + lane] = o[c][v];
+        pp[HD * 32 + lane] = m_run;
+        pp[HD * 32 + 64 + lane] = l_run;
+        return;
+    }
     if (q0 + lr >= a.T) return;
     const float inv = 1.0f / l_run;
     float* op = a.out + ((size_t)(q0 + lr) * a.nh + head) * HD;
@@ -622,14 +639,113 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
         }
 }
 
-hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s) {
-    const dim3 grid((unsigned)(((a.T + 31) / 32) * a.nkv));
+// Join the chunks of every split query tile: work group (tile x kv group, piece y)
+// takes 4 of the output values of every thread of the attention kernel's layout
+// (y = 4 cc + v4: dims 32 cc + 8 v4 + 4 h .. + 3 of query lr).  With M = max_c m_c,
+// O = sum_c e^(m_c - M) O_c and l = sum_c e^(m_c - M) l_c in chunk order; out = O / l.
+template <int HD>
+__global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs a) {
+    const int qt = (int)blockIdx.x / a.nkv, g = (int)blockIdx.x % a.nkv;
+    const int q0 = qt * 32;
+    const int last_q = min(q0 + 31, a.T - 1);
+    const int key_end = a.causal ? min(a.kv_len, a.q_pos0 + last_q + 1) : a.kv_len;
+    const int nblk = (key_end + 31) / 32;
+    const int nc = (nblk + a.cb - 1) / a.cb;
+    if (nc <= 1) return;  // written directly by the attention kernel
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int lr = lane % 32, h = lane / 32;
+    if (q0 + lr >= a.T) return;
+    const int head = g * 4 + wave;
+    const int cc = (int)blockIdx.y / 4, v4 = (int)blockIdx.y % 4;
+    const float* __restrict__ base = a.part + ((size_t)(qt * a.nch * a.nkv + g) * 4 + wave) * (HD * 32 + 128);
+    const size_t cstride = (size_t)a.nkv * 4 * (HD * 32 + 128);  // chunk c + 1 of the same tile
+    float mx = -INFINITY;
+    for (int c = 0; c < nc; c++) mx = fmaxf(mx, base[c * cstride + HD * 32 + lane]);
+    float l = 0.0f, r0 = 0.0f, r1 = 0.0f, r2 = 0.0f, r3 = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        const float* pp = base + c * cstride;
+        const float mc = pp[HD * 32 + lane], lc = pp[HD * 32 + 64 + lane];
+        const float* ov = pp + (cc * 16 + 4 * v4) * 64 + lane;
+        const float o0 = ov[0], o1 = ov[64], o2 = ov[128], o3 = ov[192];
+        const float wgt = mc == -INFINITY ? 0.0f : expf(mc - mx);
+        l += wgt * lc;
+        r0 += wgt * o0;
+        r1 += wgt * o1;
+        r2 += wgt * o2;
+        r3 += wgt * o3;
+    }
+    const float inv = 1.0f / l;
+    const int d = 32 * cc + 8 * v4 + 4 * h;
+    *reinterpret_cast<float4*>(a.out + ((size_t)(q0 + lr) * a.nh + head) * HD + d) =
+        make_float4(r0 * inv, r1 * inv, r2 * inv, r3 * inv);
+}
+
+int flash_attn_ws_slots(int max_tokens, int max_keys, int nkv) {
+    const long n = (long)((max_tokens + 31) / 32) * ((max_keys + 31) / 32) * nkv;
+    return (int)min(n, (long)FA_SPLIT_SLOTS);
+}
+size_t flash_attn_ws_floats(int hd, int slots) { return (size_t)slots * 4 * (hd * 32 + 128); }
+
+hipError_t launch_flash_attn(const FlashArgs& a_in, hipStream_t s, float* ws, int ws_slots) {
+    FlashArgs a = a_in;
+    const int n_qt = (a.T + 31) / 32, base = n_qt * a.nkv;
+    const int max_keys = a.causal ? min(a.kv_len, a.q_pos0 + a.T) : a.kv_len;
+    const int max_nblk = (max_keys + 31) / 32;
+    a.part = nullptr;
+    a.cb = 0;
+    a.nch = 1;
+    // Split the keys of each query tile into chunks of cb blocks when that shortens the
+    // launch.  Cost model, in units of one key block of one work group (~6.8 us at two
+    // work groups per CU):
+    //   whole tiles (longest first):  max(longest tile, all blocks / resident groups) + 1
+    //   chunks of cb:                 rounds x (cb + 1) + partial-tile traffic
+    // (+1: the ramp of a round; the partials are written and read back by the merge at
+    // ~5 TB/s, ~34 MB per unit of time).  Short prompts, causal tiles of very different
+    // lengths and decode against a long cache split; long prompts fill the chip with
+    // whole tiles.
+    const int slots = 256 * (a.hd == 128 ? 2 : 3);  // resident work groups (occupancy)
+    if (ws && max_nblk >= 2) {
+        auto tile_blocks = [&](int t) {
+            const int kend = a.causal ? min(a.kv_len, a.q_pos0 + min(32 * t + 31, a.T - 1) + 1) : a.kv_len;
+            return (kend + 31) / 32;
+        };
+        long total = 0;
+        for (int t = 0; t < n_qt; t++) total += tile_blocks(t);
+        total *= a.nkv;
+        const double part_units = 2.0 * 4 * (a.hd * 32 + 128) * 4 / 34e6;  // per split unit
+        double best = (double)max((long)max_nblk, (total + slots - 1) / slots) + 1;
+        int best_cb = 0;
+        for (int cb = 1; cb < max_nblk; cb++) {
+            const int nch = (max_nblk + cb - 1) / cb;
+            if ((long)n_qt * nch * a.nkv > ws_slots) continue;
+            long units = 0;
+            for (int t = 0; t < n_qt; t++) units += (tile_blocks(t) + cb - 1) / cb;
+            units *= a.nkv;
+            const double cost = (double)((units + slots - 1) / slots) * (cb + 1) + units * part_units;
+            if (cost < best) {
+                best = cost;
+                best_cb = cb;
+            }
+        }
+        if (best_cb) {
+            a.cb = best_cb;
+            a.nch = (max_nblk + best_cb - 1) / best_cb;
+            a.part = ws;
+        }
+    }
+    const dim3 grid((unsigned)(base * a.nch));
     if (a.hd == 128)
         hipLaunchKernelGGL(flash_attn_kernel<128>, grid, dim3(256), 0, s, a);
     else if (a.hd == 64)
         hipLaunchKernelGGL(flash_attn_kernel<64>, grid, dim3(256), 0, s, a);
     else
         return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !a.cb) return e;
+    if (a.hd == 128)
+        hipLaunchKernelGGL(flash_merge_kernel<128>, dim3((unsigned)base, 128 / 8), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(flash_merge_kernel<64>, dim3((unsigned)base, 64 / 8), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

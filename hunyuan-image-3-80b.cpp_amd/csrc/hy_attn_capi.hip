@@ -82,6 +82,8 @@ struct hy_attn_ctx {
     float* vf = nullptr;
     float* merged = nullptr;   // [Tm][nh*hd]
     float* gemm_ws = nullptr;  // stream-K partial tiles of the projections' GEMM
+    float* fa_ws = nullptr;    // partial tiles of the attention split over the keys
+    int fa_slots = 0;
     float* xn = nullptr;       // decoder layer: normed input [Tm][H]
     float* hres = nullptr;     // decoder layer: x + attention [Tm][H]
     bool prof = false;
@@ -191,7 +193,7 @@ int run(hy_attn_ctx* c, const AttnLayer& W, const float* x, int T, int mode, con
     HY_TRY(timed(c, AK_ROPE, s, [&] { return hy::launch_rope_qknorm(r, s); }));
     hy::FlashArgs f{c->q, k, v, c->merged, T, c->nh, c->nkv, c->hd, Lrows, kv_len, pos0, causal,
                     1.0f / sqrtf((float)c->hd)};
-    HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s); }));
+    HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s, c->fa_ws, c->fa_slots); }));
     HY_TRY(timed(c, AK_OPROJ, s,
                  [&] {
                      return hy::launch_gemm_nt_f32(c->merged, W.o_w, resid, out, T, c->H, c->nh * c->hd, s,
@@ -266,12 +268,14 @@ int hy_attn_create(const hy_attn_config* cfg, hy_attn_ctx** out) {
     c->Lc = (int)cfg->max_cache;
     c->layers.resize(cfg->num_layers);
     const size_t H = c->H, nq = (size_t)c->nh * c->hd, nk = (size_t)c->nkv * c->hd, Tm = c->Tm;
+    c->fa_slots = hy::flash_attn_ws_slots(c->Tm, c->Tm > c->Lc ? c->Tm : c->Lc, c->nkv);
     struct Part {
         float** p;
         size_t n;
     } parts[] = {{&c->qkv, Tm * c->nqkv}, {&c->q, Tm * nq},  {&c->kf, Tm * nk},   {&c->vf, Tm * nk},
                  {&c->merged, Tm * nq},   {&c->xn, Tm * H}, {&c->hres, Tm * H},
-                 {&c->gemm_ws, hy::gemm_nt_f32_ws_bytes() / 4}};
+                 {&c->gemm_ws, hy::gemm_nt_f32_ws_bytes() / 4},
+                 {&c->fa_ws, hy::flash_attn_ws_floats(c->hd, c->fa_slots)}};
     size_t total = 0;
     for (auto& p : parts) total += al256(p.n * 4);
     if (hipMalloc(&c->arena, total) != hipSuccess) {

@@ -121,7 +121,17 @@ struct FlashArgs {
     int q_pos0;               // key index of query 0 (causal bound: key <= q_pos0 + t)
     int causal;
     float scale;
+    // split over the keys (set by launch_flash_attn): chunks of cb key blocks, at most
+    // nch per query tile, partial results in part (flash_attn_ws_floats)
+    float* part = nullptr;
+    int cb = 0, nch = 1;
 };
+// scratch of the split attention: partial tiles (at most FA_SPLIT_SLOTS) for head_dim
+// hd; flash_attn_ws_slots: the slots a context of max_tokens queries and max_keys
+// keys can use
+constexpr int FA_SPLIT_SLOTS = 4096;
+int flash_attn_ws_slots(int max_tokens, int max_keys, int nkv);
+size_t flash_attn_ws_floats(int hd, int slots);
 // C = A . W^T, plus R elementwise when R is not null (R may alias nothing written here).
 // ws: gemm_nt_f32_ws_bytes() of device scratch for the stream-K split of mid-size grids
 // (gemm_nt_f32_uses_ws); without it those grids run one tile per work group.
@@ -131,7 +141,9 @@ bool gemm_nt_f32_uses_ws(int M, int N, int K);
 hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, float* C, int M, int N, int K,
                               hipStream_t s, float* ws = nullptr);
 hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s);
-hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s);
+// ws: flash_attn_ws_floats(hd, ws_slots) of device scratch, or nullptr (no split over
+// the keys)
+hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s, float* ws = nullptr, int ws_slots = 0);
 hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,
                                float* sin_out, hipStream_t s);
 hipError_t launch_gather_kv(const float* src, int nkv, int L, int pos0, int T, int hd, float* dst, hipStream_t s);

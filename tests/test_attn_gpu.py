@@ -61,6 +61,54 @@ def test_forward_full_head_shape(gpu):
     m.close()
 
 
+def _attn64(q, k, v, nh, nkv, causal=True, q_pos0=0):
+    """float64 GQA attention of given q [T][nh][hd], k / v [L][nkv][hd] -> [T][nh*hd]."""
+    T, _, hd = q.shape
+    L = k.shape[0]
+    out = np.empty((T, nh, hd))
+    for hh in range(nh):
+        g = hh // (nh // nkv)
+        s = q[:, hh, :].astype(np.float64) @ k[:, g, :].astype(np.float64).T / np.sqrt(hd)
+        if causal:
+            s = np.where(np.arange(L)[None, :] <= q_pos0 + np.arange(T)[:, None], s, -np.inf)
+        s = np.exp(s - s.max(1, keepdims=True))
+        out[:, hh, :] = (s / s.sum(1, keepdims=True)) @ v[:, g, :].astype(np.float64)
+    return out.reshape(T, nh * hd)
+
+
+@pytest.mark.parametrize("T", [1024, 2048])
+def test_flash_split_and_whole_tiles(gpu, T):
+    """32 query / 8 kv heads: T=1024 runs the split over the keys (chunks of 8 key
+    blocks per query tile, merged in chunk order); T=2048 fills 512 work groups and
+    runs whole tiles.  The output against float64 attention of the device's own q / k /
+    v followed by the output projection."""
+    shp = dict(H=256, nh=32, nkv=8, hd=64)
+    m, w = _ctx(gpu, shp, max_tokens=T, seed=T)
+    x = np.random.default_rng(T).standard_normal((T, shp["H"])).astype(np.float32)
+    out, dq, dk, dv = m.run(x, debug=True)
+    q = dq.reshape(T, 32, 64)
+    k, v = dk.reshape(T, 8, 64), dv.reshape(T, 8, 64)
+    ref = _attn64(q, k, v, 32, 8) @ w.o_w.astype(np.float64).T
+    check(out, ref, f"flash T={T}")
+    m.close()
+
+
+def test_cached_decode_long_cache(gpu):
+    """Decode against a long cache (one query tile per kv group: the keys are split
+    into chunks of one block): 2 900 cached positions, then chunks of 1 and 4 tokens."""
+    shp = SHAPES[0]
+    m, w = _ctx(gpu, shp, max_tokens=2900, max_cache=2910, seed=5)
+    cache = A.KVCache(shp["nkv"], shp["hd"], max_len=2910)
+    rng = np.random.default_rng(5)
+    for n in (2900, 1, 4):
+        x = rng.standard_normal((n, shp["H"])).astype(np.float32)
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((n, shp["H"]))
+        m.forward_cached(xb, n, ob)
+        ref = A.attention_cached(w, x, cache)
+        check(ob.numpy(), ref, f"cached +{n} at {cache.cur_len - n}")
+    m.close()
+
+
 def test_forward_is_causal(gpu):
     shp = SHAPES[0]
     m, _ = _ctx(gpu, shp)
