@@ -28,6 +28,8 @@
 // C[8*(v/4) + 4*(l/32) + v%4][l%32].  Operand k-slots can be any permutation of the
 // reduction index as long as A and B use the same one: lane half h takes k = 8h + j
 // at step j of a 16-wide chunk, so each lane reads 8 consecutive floats.
+#include <utility>
+
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_lds.hpp"
@@ -35,6 +37,7 @@
 namespace hy {
 
 typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v16f_t mfma_f32(float a, float b, v16f_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -490,20 +493,32 @@ hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int
 // 64 banks: 16 consecutive rows hit 16 distinct bank quads); V rows 4 B per lane by
 // two rows 4 apart per instruction (pitch = 8 mod 16: the two half-waves land on
 // opposite bank halves).
+// K / V blocks of 32 keys reach LDS by DMA (global_load_lds_dwordx4) into a 2-deep
+// ring: the next block's copies are in flight during a block's math, no registers
+// hold them, and one barrier per block suffices.  Rows are HD floats (HD / 4 16-byte
+// chunks), unpadded; chunk c of K row r sits at position c ^ (r & 15) and chunk c of V
+// row r at c ^ 8 ((r >> 2) & 1).  Then the K reads of 16 consecutive rows at one
+// logical chunk (QK^T) and the V reads of rows key and key + 4 by the two half-waves
+// (PV) fall on distinct bank groups.  Each lane of a copy fetches the chunk that
+// belongs at its position.
 template <int HD>
 struct FaShape {
-    static constexpr int KP = HD + 4, VP = HD + 8;
-    static constexpr int KV_F4 = 32 * HD / 4;        // float4 per K (or V) block
-    static constexpr int PER_THREAD = 2 * KV_F4 / 256;
-    static_assert((2 * KV_F4) % 256 == 0, "K and V blocks split evenly over the work group");
+    static constexpr int ROWB = HD * 4;         // bytes per row
+    static constexpr int BLK = 32 * ROWB;       // one K (or V) block
+    static constexpr int BUF = 2 * BLK;         // K block, then V block
+    static constexpr int CPW = BLK / 1024 / 4;  // 1 KB copies per wave for K (and for V)
+    static constexpr int RPC = 1024 / ROWB;     // rows per copy
+    static_assert(CPW >= 1 && HD / 4 >= 16, "head_dim 64 or 128");
 };
+__device__ __forceinline__ int fa_swz_k(int r) { return r & 15; }
+__device__ __forceinline__ int fa_swz_v(int r) { return 8 * ((r >> 2) & 1); }
 
 template <int HD>
 __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     using S = FaShape<HD>;
-    __shared__ __align__(16) float ks[32 * S::KP];
-    __shared__ __align__(16) float vs[32 * S::VP];
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[2][S::BUF];
+    const int tid = threadIdx.x, lane = tid % WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int lr = lane % 32, h = lane / 32;
     const int n_qt = (a.T + 31) / 32;
     // chunk-major, and inside a chunk the longest (causal) query tiles first
@@ -515,18 +530,6 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     const int head = g * 4 + wave;  // 4 query heads per kv group
     const int qrow = min(q0 + lr, a.T - 1);
 
-    // Q resident: lane (query lr, half h) holds Q[q][16c + 8h + j]
-    float qv[HD / 2];
-    {
-        const float* qp = a.q + ((size_t)qrow * a.nh + head) * HD + 8 * h;
-#pragma unroll
-        for (int c = 0; c < HD / 16; c++) {
-            const float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * c);
-            const float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
-            qv[8 * c + 0] = x0.x; qv[8 * c + 1] = x0.y; qv[8 * c + 2] = x0.z; qv[8 * c + 3] = x0.w;
-            qv[8 * c + 4] = x1.x; qv[8 * c + 5] = x1.y; qv[8 * c + 6] = x1.z; qv[8 * c + 7] = x1.w;
-        }
-    }
     // visible keys: all kv_len, or (causal) keys <= q_pos0 + q
     const int last_q = min(q0 + 31, a.T - 1);
     const int key_end = a.causal ? min(a.kv_len, a.q_pos0 + last_q + 1) : a.kv_len;
@@ -536,27 +539,55 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     if (chunk >= nc) return;  // whole work group: the tile has fewer chunks
     const int kb0 = a.cb ? chunk * a.cb : 0, kb1 = a.cb ? min(nblk, kb0 + a.cb) : nblk;
 
+    // copies: copy q of this wave moves rows (wave CPW + q) RPC .. + RPC - 1 of the
+    // block; lane l lands at byte 16 l of it: row + l / (ROWB / 16), position
+    // l % (ROWB / 16), fetching the chunk stored there
     const float* kg = a.k + (size_t)g * a.L * HD;
     const float* vg = a.v + (size_t)g * a.L * HD;
-    float4 pre[S::PER_THREAD];
-    auto fetch = [&](int kb) {
+    int crow[S::CPW], kchunk[S::CPW], vchunk[S::CPW];
 #pragma unroll
-        for (int i = 0; i < S::PER_THREAD; i++) {
-            const int f = tid + 256 * i;                   // float4 index over [K block | V block]
-            const int which = f / S::KV_F4, r = (f % S::KV_F4) / (HD / 4), c4 = f % (HD / 4);
-            const int key = min(kb * 32 + r, a.kv_len - 1);
-            pre[i] = *reinterpret_cast<const float4*>((which ? vg : kg) + (size_t)key * HD + 4 * c4);
+    for (int q = 0; q < S::CPW; q++) {
+        crow[q] = (wave * S::CPW + q) * S::RPC + lane / (S::ROWB / 16);
+        const int pos = lane % (S::ROWB / 16);
+        kchunk[q] = 4 * (pos ^ fa_swz_k(crow[q]));
+        vchunk[q] = 4 * (pos ^ fa_swz_v(crow[q]));
+    }
+    auto issue = [&](int kb) {
+        uint8_t* buf = ring[(kb - kb0) & 1];
+#pragma unroll
+        for (int q = 0; q < S::CPW; q++) {
+            const size_t row = (size_t)min(kb * 32 + crow[q], a.kv_len - 1) * HD;  // in bounds
+            g2l16(kg + row + kchunk[q], buf + (wave * S::CPW + q) * 1024);
+            g2l16(vg + row + vchunk[q], buf + S::BLK + (wave * S::CPW + q) * 1024);
         }
     };
-    auto stash = [&]() {
+    issue(kb0);
+
+    // Q resident: lane (query lr, half h) holds Q[q][16c + 8h + j], pre-multiplied by
+    // scale * log2(e): the scores come out in the base-2 domain, where the softmax uses
+    // the hardware 2^x (v_exp_f32; 2^-inf = 0 serves the masked keys)
+    const float qscale = a.scale * 1.4426950408889634f;
+    float qv[HD / 2];
+    {
+        const float* qp = a.q + ((size_t)qrow * a.nh + head) * HD + 8 * h;
 #pragma unroll
-        for (int i = 0; i < S::PER_THREAD; i++) {
-            const int f = tid + 256 * i;
-            const int which = f / S::KV_F4, r = (f % S::KV_F4) / (HD / 4), c4 = f % (HD / 4);
-            float* dst = which ? vs + r * S::VP + 4 * c4 : ks + r * S::KP + 4 * c4;
-            *reinterpret_cast<float4*>(dst) = pre[i];
+        for (int c = 0; c < HD / 16; c++) {
+            const v4f_t x0 = *reinterpret_cast<const v4f_t*>(qp + 16 * c);
+            const v4f_t x1 = *reinterpret_cast<const v4f_t*>(qp + 16 * c + 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                qv[8 * c + j] = x0[j] * qscale;
+                qv[8 * c + 4 + j] = x1[j] * qscale;
+            }
         }
-    };
+    }
+    // LDS read offsets inside a buffer: K row lr at logical chunk 4c + 2h + t; V rows
+    // 8 i + 4 h + j at float 32 c + lr (the row part 8 i + j is an immediate)
+    const int swk = fa_swz_k(lr);
+    uint32_t voff[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) voff[c] = (uint32_t)(S::BLK + 4 * h * S::ROWB + 128 * (c ^ h) + 4 * lr);
+    const uint32_t ring0 = lds_off(ring[0]);
 
     v16f_t o[HD / 32];
 #pragma unroll
@@ -564,56 +595,86 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
     float m_run = -INFINITY, l_run = 0.0f;
     const int my_q = a.q_pos0 + q0 + lr;  // key index of this lane's query (causal bound)
 
-    fetch(kb0);
     for (int kb = kb0; kb < kb1; kb++) {
-        __syncthreads();  // the previous block's LDS reads are done
-        stash();
-        if (kb + 1 < kb1) fetch(kb + 1);
-        __syncthreads();
-        // S^T[key][q] = sum_d K[key][d] Q[q][d]
+        MM_WAIT_VM_LGKM(0);  // this wave's copies of block kb have landed
+        __syncthreads();     // everyone's have, and block kb - 1's buffer is free
+        if (kb + 1 < kb1) issue(kb + 1);
+        const uint32_t base = ring0 + (uint32_t)(((kb - kb0) & 1) * S::BUF);
+        // S^T[key][q] = sum_d K[key][d] Q[q][d]: all K reads of the block in flight,
+        // consumed in order
+        const uint32_t krow = base + (uint32_t)(lr * S::ROWB);
+        v4i_t kr[HD / 16][2];
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) kr[c][t] = lds_b128_at<0>(krow + 16u * (uint32_t)((4 * c + 2 * h + t) ^ swk));
         v16f_t s = v16f_t{};
+        [&]<int... C>(std::integer_sequence<int, C...>) {
+            (
+                [&] {
+                    lds_wait_upto<HD / 8 - 2 - 2 * C>();
+                    lds_pin(kr[C][0]);
+                    lds_pin(kr[C][1]);
 #pragma unroll
-        for (int c = 0; c < HD / 16; c++) {
-            const float* kr = ks + lr * S::KP + 16 * c + 8 * h;
-            const float4 k0 = *reinterpret_cast<const float4*>(kr);
-            const float4 k1 = *reinterpret_cast<const float4*>(kr + 4);
-            const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                    for (int j = 0; j < 8; j++)
+                        s = mfma_f32(__int_as_float(kr[C][j / 4][j % 4]), qv[8 * C + j], s);
+                }(),
+                ...);
+        }(std::make_integer_sequence<int, HD / 16>{});
+        // mask (only blocks that reach past the tile's first query or past kv_len),
+        // online softmax over this lane pair's 32 keys
+        const bool need_mask = kb * 32 + 31 >= a.kv_len || (a.causal && kb * 32 + 31 > a.q_pos0 + q0);
+        if (need_mask) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) s = mfma_f32(kk[j], qv[8 * c + j], s);
+            for (int v = 0; v < 16; v++) {
+                const int key = kb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+                if (key >= a.kv_len || (a.causal && key > my_q)) s[v] = -INFINITY;
+            }
         }
-        // scale, mask, online softmax over this lane pair's 32 keys
-        float mloc = -INFINITY;
+        float mloc = s[0];
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int key = kb * 32 + 8 * (v / 4) + 4 * h + v % 4;
-            float x = s[v] * a.scale;
-            if (key >= a.kv_len || (a.causal && key > my_q)) x = -INFINITY;
-            s[v] = x;
-            mloc = fmaxf(mloc, x);
-        }
+        for (int v = 1; v < 16; v++) mloc = fmaxf(mloc, s[v]);
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, WAVE));
+        // every processed block leaves at least one visible key per query, so m_new is
+        // finite
         const float m_new = fmaxf(m_run, mloc);
-        const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 for the first block
         float psum = 0.0f;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const float p = s[v] == -INFINITY ? 0.0f : expf(s[v] - m_new);
+            const float p = __builtin_amdgcn_exp2f(s[v] - m_new);
             s[v] = p;
             psum += p;
         }
         psum += __shfl_xor(psum, 32, WAVE);
         l_run = l_run * alpha + psum;
         m_run = m_new;
+        if (__ballot(alpha != 1.0f)) {  // the running max moved for some query
 #pragma unroll
-        for (int c = 0; c < HD / 32; c++) o[c] *= alpha;
-        // O^T[d][q] += sum_key V[key][d] P^T[key][q]
+            for (int c = 0; c < HD / 32; c++) o[c] *= alpha;
+        }
+        // O^T[d][q] += sum_key V[key][d] P^T[key][q]: per 32 dims, the 16 key values
+        // of the lane in two groups of 8 reads
 #pragma unroll
-        for (int c = 0; c < HD / 32; c++)
+        for (int c = 0; c < HD / 32; c++) {
+            const uint32_t vb = base + voff[c];
+            uint32_t vv[16];
+            [&]<int... V>(std::integer_sequence<int, V...>) {
+                ((vv[V] = lds_b32_at<(8 * (V / 4) + V % 4) * S::ROWB>(vb)), ...);
+            }(std::make_integer_sequence<int, 16>{});
+            lds_wait_upto<8>();
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int key = 8 * (v / 4) + 4 * h + v % 4;
-                o[c] = mfma_f32(vs[key * S::VP + 32 * c + lr], s[v], o[c]);
+            for (int v = 0; v < 8; v++) {
+                lds_pin(vv[v]);
+                o[c] = mfma_f32(__uint_as_float(vv[v]), s[v], o[c]);
             }
+            lds_wait_upto<0>();
+#pragma unroll
+            for (int v = 8; v < 16; v++) {
+                lds_pin(vv[v]);
+                o[c] = mfma_f32(__uint_as_float(vv[v]), s[v], o[c]);
+            }
+        }
     }
     if (nc > 1) {
         // partial result of this chunk: unnormalised O^T, running max and sum
@@ -642,7 +703,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(FlashArgs a) {
 // Join the chunks of every split query tile: work group (tile x kv group, piece y)
 // takes 4 of the output values of every thread of the attention kernel's layout
 // (y = 4 cc + v4: dims 32 cc + 8 v4 + 4 h .. + 3 of query lr).  With M = max_c m_c,
-// O = sum_c e^(m_c - M) O_c and l = sum_c e^(m_c - M) l_c in chunk order; out = O / l.
+// O = sum_c 2^(m_c - M) O_c and l = sum_c 2^(m_c - M) l_c in chunk order; out = O / l.
 template <int HD>
 __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs a) {
     const int qt = (int)blockIdx.x / a.nkv, g = (int)blockIdx.x % a.nkv;
@@ -659,6 +720,7 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs a) {
     const int cc = (int)blockIdx.y / 4, v4 = (int)blockIdx.y % 4;
     const float* __restrict__ base = a.part + ((size_t)(qt * a.nch * a.nkv + g) * 4 + wave) * (HD * 32 + 128);
     const size_t cstride = (size_t)a.nkv * 4 * (HD * 32 + 128);  // chunk c + 1 of the same tile
+    // the chunks' running maxima are in the base-2 domain of the attention kernel
     float mx = -INFINITY;
     for (int c = 0; c < nc; c++) mx = fmaxf(mx, base[c * cstride + HD * 32 + lane]);
     float l = 0.0f, r0 = 0.0f, r1 = 0.0f, r2 = 0.0f, r3 = 0.0f;
@@ -667,7 +729,7 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs a) {
         const float mc = pp[HD * 32 + lane], lc = pp[HD * 32 + 64 + lane];
         const float* ov = pp + (cc * 16 + 4 * v4) * 64 + lane;
         const float o0 = ov[0], o1 = ov[64], o2 = ov[128], o3 = ov[192];
-        const float wgt = mc == -INFINITY ? 0.0f : expf(mc - mx);
+        const float wgt = __builtin_amdgcn_exp2f(mc - mx);
         l += wgt * lc;
         r0 += wgt * o0;
         r1 += wgt * o1;

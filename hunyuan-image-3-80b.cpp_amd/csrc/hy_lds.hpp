@@ -58,6 +58,13 @@ __device__ __forceinline__ void lds_st128(void* p, v4i_t v) {
     asm volatile("ds_write_b128 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
 }
 __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// wait until at most N of this wave's LDS reads are outstanding (they complete in
+// order); pin each consumed result afterwards (lds_pin)
+template <int N>
+__device__ __forceinline__ void lds_wait_upto() {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt is 4 bits");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+}
 // After a bare lds_wait(): pin a ds_read result so none of its uses is scheduled above
 // the wait (volatile asm statements keep their program order).
 __device__ __forceinline__ void lds_pin(v4i_t& v) { asm volatile("" : "+v"(v)); }
