@@ -388,68 +388,88 @@ hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, fl
 }
 
 // ---------------------------------------------------------------- RoPE + QK-norm
+// One wave per (token, group of RQ_HEADS heads): the rotation angles depend on
+// (token, pair) only, so each wave computes them once for its group.  Lane l owns
+// pairs l and l + 64 (head_dim <= 256) and moves them as float2.  Key heads also copy
+// their value row.
+constexpr int RQ_HEADS = 4;
 __global__ __launch_bounds__(256) void rope_qknorm_kernel(RopeNormArgs a) {
-    const int wid = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int heads = a.nh + a.nkv;
-    if (wid >= a.T * heads) return;
-    const int t = wid / heads, hh = wid % heads;
-    const bool is_q = hh < a.nh;
+    const int groups = (heads + RQ_HEADS - 1) / RQ_HEADS;
+    const int wid = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (wid >= a.T * groups) return;
+    const int t = wid / groups, h0 = (wid % groups) * RQ_HEADS;
     const int hd = a.hd, npair = hd / 2;
-    const float* src = a.qkv + (size_t)t * a.nqkv + (size_t)hh * hd;  // q heads, then k heads
     const float pos = a.positions ? (float)a.positions[t] : (float)t;
     constexpr int MAXP = 2;  // pairs per lane: hd <= 256
-    float r0[MAXP], r1[MAXP];
-    float ss = 0.0f;
+    float cs[MAXP], sn[MAXP];
 #pragma unroll
     for (int i = 0; i < MAXP; i++) {
         const int d = lane + WAVE * i;
-        r0[i] = r1[i] = 0.0f;
+        cs[i] = 1.0f;
+        sn[i] = 0.0f;
         if (d >= npair) continue;
-        const float x0 = src[2 * d], x1 = src[2 * d + 1];
-        float c = 1.0f, sn = 0.0f;
-        bool rot = true;
         if (a.mode == ROPE_1D) {
             const float freq = 1.0f / powf(a.theta, (2.0f * (float)d) / (float)hd);
-            c = cosf(pos * freq);
-            sn = sinf(pos * freq);
+            cs[i] = cosf(pos * freq);
+            sn[i] = sinf(pos * freq);
         } else if (a.mode == ROPE_TABLE) {
-            c = a.cos_t[(size_t)t * hd + 2 * d];
-            sn = a.sin_t[(size_t)t * hd + 2 * d];
-        } else {
-            rot = false;
+            cs[i] = a.cos_t[(size_t)t * hd + 2 * d];
+            sn[i] = a.sin_t[(size_t)t * hd + 2 * d];
         }
-        if (rot) {
-            r0[i] = x0 * c - x1 * sn;
-            r1[i] = x0 * sn + x1 * c;
-        } else {
-            r0[i] = x0;
-            r1[i] = x1;
-        }
-        ss += r0[i] * r0[i];
-        ss += r1[i] * r1[i];
     }
-    ss = wave_sum(ss);
-    const float rms = 1.0f / sqrtf(ss / (float)hd + a.eps);
-    const float* w = is_q ? a.q_norm : a.k_norm;
-    float* dst = is_q ? a.q + ((size_t)t * a.nh + hh) * hd : a.k + ((size_t)(hh - a.nh) * a.L + a.pos0 + t) * hd;
+    const bool rot = a.mode != ROPE_NONE;
+    // the group's rows, loaded together
+    float2 x[RQ_HEADS][MAXP];
 #pragma unroll
-    for (int i = 0; i < MAXP; i++) {
-        const int d = lane + WAVE * i;
-        if (d >= npair) continue;
-        const float w0 = w[2 * d], w1 = w[2 * d + 1];
-        // (x * rms) * w as attention_forward_cpu; x * (rms * w) as the cache branch
-        dst[2 * d] = a.norm_assoc ? r0[i] * (rms * w0) : r0[i] * rms * w0;
-        dst[2 * d + 1] = a.norm_assoc ? r1[i] * (rms * w1) : r1[i] * rms * w1;
-    }
-    if (!is_q) {  // the value row of this kv head, unchanged
-        const float* vs = a.qkv + (size_t)t * a.nqkv + (size_t)(a.nh + a.nkv) * hd + (size_t)(hh - a.nh) * hd;
-        float* vd = a.v + ((size_t)(hh - a.nh) * a.L + a.pos0 + t) * hd;
-        for (int d = lane; d < hd; d += WAVE) vd[d] = vs[d];
+    for (int j = 0; j < RQ_HEADS; j++)
+#pragma unroll
+        for (int i = 0; i < MAXP; i++) {
+            const int d = lane + WAVE * i, hh = h0 + j;
+            x[j][i] = (d < npair && hh < heads)
+                          ? *reinterpret_cast<const float2*>(a.qkv + (size_t)t * a.nqkv + (size_t)hh * hd + 2 * d)
+                          : make_float2(0.0f, 0.0f);
+        }
+#pragma unroll
+    for (int j = 0; j < RQ_HEADS; j++) {
+        const int hh = h0 + j;
+        if (hh >= heads) break;  // wave-uniform
+        const bool is_q = hh < a.nh;
+        float r0[MAXP], r1[MAXP];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MAXP; i++) {
+            const float x0 = x[j][i].x, x1 = x[j][i].y;
+            r0[i] = rot ? x0 * cs[i] - x1 * sn[i] : x0;
+            r1[i] = rot ? x0 * sn[i] + x1 * cs[i] : x1;
+            ss += r0[i] * r0[i];
+            ss += r1[i] * r1[i];
+        }
+        ss = wave_sum(ss);
+        const float rms = 1.0f / sqrtf(ss / (float)hd + a.eps);
+        const float* w = is_q ? a.q_norm : a.k_norm;
+        float* dst = is_q ? a.q + ((size_t)t * a.nh + hh) * hd : a.k + ((size_t)(hh - a.nh) * a.L + a.pos0 + t) * hd;
+#pragma unroll
+        for (int i = 0; i < MAXP; i++) {
+            const int d = lane + WAVE * i;
+            if (d >= npair) continue;
+            const float2 wv = *reinterpret_cast<const float2*>(w + 2 * d);
+            // (x * rms) * w as attention_forward_cpu; x * (rms * w) as the cache branch
+            const float o0 = a.norm_assoc ? r0[i] * (rms * wv.x) : r0[i] * rms * wv.x;
+            const float o1 = a.norm_assoc ? r1[i] * (rms * wv.y) : r1[i] * rms * wv.y;
+            *reinterpret_cast<float2*>(dst + 2 * d) = make_float2(o0, o1);
+        }
+        if (!is_q) {  // the value row of this kv head, unchanged
+            const float* vs = a.qkv + (size_t)t * a.nqkv + (size_t)(a.nh + a.nkv) * hd + (size_t)(hh - a.nh) * hd;
+            float* vd = a.v + ((size_t)(hh - a.nh) * a.L + a.pos0 + t) * hd;
+            for (int d = 2 * lane; d < hd; d += 2 * WAVE)
+                *reinterpret_cast<float2*>(vd + d) = *reinterpret_cast<const float2*>(vs + d);
+        }
     }
 }
 
 hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s) {
-    const int waves = a.T * (a.nh + a.nkv);
+    const int waves = a.T * ((a.nh + a.nkv + RQ_HEADS - 1) / RQ_HEADS);
     hipLaunchKernelGGL(rope_qknorm_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
