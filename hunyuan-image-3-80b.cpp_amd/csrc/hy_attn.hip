@@ -356,6 +356,83 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs p, int nstage)
     }
 }
 
+// Decode-sized products (M <= 16 rows of A): C = (R +) A . W^T is a stream over W.
+// One wave owns GV_RPW consecutive W rows; lane l takes floats 4 l + 256 c .. + 3 of
+// every row (chunk c), so each W load is a contiguous 1 KB per wave and each A float4
+// (the same for all waves: L1 hits) feeds GV_RPW rows.  Loads are unconditional from
+// clamped addresses and software-pipelined GV_D chunks deep; a chunk past K is masked
+// by a select.  The 64 lane partials of every output fold level by level at the end.
+constexpr int GV_RPW = 4;
+template <int MB, int GV_D>
+__global__ __launch_bounds__(256) void gemv_nt_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
+                                                         const float* __restrict__ R, float* __restrict__ C, int M,
+                                                         int N, int K) {
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int n0 = (blockIdx.x * 4 + wave) * GV_RPW;
+    if (n0 >= N) return;
+    const int nch = (K + 4 * WAVE - 1) / (4 * WAVE);
+    const float* wrow[GV_RPW];
+    const float* arow[MB];
+#pragma unroll
+    for (int r = 0; r < GV_RPW; r++) wrow[r] = W + (size_t)min(n0 + r, N - 1) * K;
+#pragma unroll
+    for (int m = 0; m < MB; m++) arow[m] = A + (size_t)min(m, M - 1) * K;
+    float acc[GV_RPW][MB];
+#pragma unroll
+    for (int r = 0; r < GV_RPW; r++)
+#pragma unroll
+        for (int m = 0; m < MB; m++) acc[r][m] = 0.0f;
+    v4f_t wb[GV_D][GV_RPW], ab[GV_D][MB];
+    auto load = [&](int c, v4f_t* wd, v4f_t* ad) {
+        const int k = min(4 * lane + 4 * WAVE * c, K - 4);  // in bounds (K % 4 == 0)
+#pragma unroll
+        for (int r = 0; r < GV_RPW; r++) wd[r] = *reinterpret_cast<const v4f_t*>(wrow[r] + k);
+#pragma unroll
+        for (int m = 0; m < MB; m++) ad[m] = *reinterpret_cast<const v4f_t*>(arow[m] + k);
+    };
+#pragma unroll
+    for (int d = 0; d < GV_D - 1; d++) load(d, wb[d], ab[d]);
+    for (int c0 = 0; c0 < nch; c0 += GV_D) {
+#pragma unroll
+        for (int d = 0; d < GV_D; d++) {
+            const int c = c0 + d;
+            load(c + GV_D - 1, wb[(d + GV_D - 1) % GV_D], ab[(d + GV_D - 1) % GV_D]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the refill ahead of the math
+            const bool ok = c < nch && 4 * lane + 4 * WAVE * c < K;
+#pragma unroll
+            for (int r = 0; r < GV_RPW; r++)
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    const v4f_t w = wb[d][r], x = ab[d][m];
+                    float s = acc[r][m];
+                    s = fmaf(w[0], x[0], s);
+                    s = fmaf(w[1], x[1], s);
+                    s = fmaf(w[2], x[2], s);
+                    s = fmaf(w[3], x[3], s);
+                    acc[r][m] = ok ? s : acc[r][m];
+                }
+        }
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1)
+#pragma unroll
+        for (int r = 0; r < GV_RPW; r++)
+#pragma unroll
+            for (int m = 0; m < MB; m++) acc[r][m] += shfl_down(acc[r][m], sh);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < GV_RPW; r++)
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const int n = n0 + r;
+                if (n < N && m < M) {
+                    const size_t o = (size_t)m * N + n;
+                    C[o] = R ? R[o] + acc[r][m] : acc[r][m];
+                }
+            }
+    }
+}
+
 size_t gemm_nt_f32_ws_bytes() { return (size_t)2 * GEMM_SK_GROUPS * 128 * 128 * 4; }
 
 // fewer 128 x 128 tiles than two full rounds of resident work groups (but enough to
@@ -369,6 +446,25 @@ hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, fl
                               hipStream_t s, float* ws) {
     const int mtiles = (M + 127) / 128, tiles = mtiles * ((N + 127) / 128);
     GemmArgs p{A, W, R, C, M, N, K, mtiles, tiles, 0, ws};
+    if (M <= 16) {
+        const dim3 grid((unsigned)((N + 4 * GV_RPW - 1) / (4 * GV_RPW)));
+        // rows 8.. go through a second pass over W (M <= 16 keeps it at two)
+        for (int m0 = 0; m0 < M; m0 += 8) {
+            const int mb = min(M - m0, 8);
+            const float* a = A + (size_t)m0 * K;
+            const float* r = R ? R + (size_t)m0 * N : nullptr;
+            float* c = C + (size_t)m0 * N;
+            if (mb == 1)
+                hipLaunchKernelGGL((gemv_nt_f32_kernel<1, 4>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
+            else if (mb == 2)
+                hipLaunchKernelGGL((gemv_nt_f32_kernel<2, 4>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
+            else if (mb <= 4)
+                hipLaunchKernelGGL((gemv_nt_f32_kernel<4, 3>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
+            else
+                hipLaunchKernelGGL((gemv_nt_f32_kernel<8, 2>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
+        }
+        return hipGetLastError();
+    }
     if (ws && gemm_nt_f32_uses_ws(M, N, K)) {
         p.G = GEMM_SK_GROUPS;
         hipLaunchKernelGGL((gemm_nt_f32_lds_kernel<32, 2, 2>), dim3(p.G), dim3(256), 0, s, p);

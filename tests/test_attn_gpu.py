@@ -226,12 +226,16 @@ def test_decoder_layer_matches_oracle(gpu):
     att.close()
 
 
-@pytest.mark.parametrize("M,N,Kd", [(7, 100, 48), (300, 512, 256), (2048, 4096, 512), (1111, 6144, 64),
+@pytest.mark.parametrize("M,N,Kd", [(1, 6150, 4096), (2, 100, 48), (3, 1031, 272), (5, 4099, 1040),
+                                    (8, 6144, 4096), (9, 517, 4096), (16, 4097, 336), (17, 100, 48),
+                                    (300, 512, 256), (2048, 4096, 512), (1111, 6144, 64),
                                     (1300, 6200, 80), (1290, 6150, 4096), (2100, 8200, 64), (520, 6150, 1024)])
 def test_gemm_both_tilings(gpu, M, N, Kd):
     """The projections' GEMM (hy_lm_head_f32) on each of its paths, ragged M and N, with
     and without the residual, against float64:
-      * one-wave register kernel: small grids (300x512, 1111x6144 with K=64);
+      * decode-sized GEMV, M <= 16 (one or two passes over W, ragged N, K not a multiple
+        of the 256-float chunk a wave loads);
+      * one-wave register kernel: small grids (17x100, 300x512, 1111x6144 with K=64);
       * LDS-staged, one 128 x 128 tile per work group: >= 1024 tiles (2100x8200), or
         K % 32 != 0 with >= 512 tiles (1300x6200x80, stages of 16 floats);
       * LDS-staged stream-K + fix-up: 64..1023 tiles with K % 32 == 0 (2048x4096x512,
