@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs p, int nstage)
 // (the same for all waves: L1 hits) feeds GV_RPW rows.  Loads are unconditional from
 // clamped addresses and software-pipelined GV_D chunks deep; a chunk past K is masked
 // by a select.  The 64 lane partials of every output fold level by level at the end.
-constexpr int GV_RPW = 4;
+constexpr int GV_RPW = 2;  // two rows per wave: 4 KB in flight per wave at depth 4 (swept 1..8)
 template <int MB, int GV_D>
 __global__ __launch_bounds__(256) void gemv_nt_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
                                                          const float* __restrict__ R, float* __restrict__ C, int M,
@@ -459,9 +459,9 @@ hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, fl
             else if (mb == 2)
                 hipLaunchKernelGGL((gemv_nt_f32_kernel<2, 4>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
             else if (mb <= 4)
-                hipLaunchKernelGGL((gemv_nt_f32_kernel<4, 3>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
+                hipLaunchKernelGGL((gemv_nt_f32_kernel<4, 4>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
             else
-                hipLaunchKernelGGL((gemv_nt_f32_kernel<8, 2>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
+                hipLaunchKernelGGL((gemv_nt_f32_kernel<8, 3>), grid, dim3(256), 0, s, a, W, r, c, mb, N, K);
         }
         return hipGetLastError();
     }
@@ -858,13 +858,216 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs a) {
         make_float4(r0 * inv, r1 * inv, r2 * inv, r3 * inv);
 }
 
+// ---------------------------------------------------------------- decode (T <= 8)
+// A few new tokens against a long cache: the 4 query heads of a kv group times the T
+// tokens pack into one 32-row tile (row r: token r / 4, head 4 g + r % 4), so a single
+// wave covers the whole group for a block of keys, and the keys spread over as many
+// waves as the chip holds.  Every wave is a work group of its own and takes cb
+// consecutive key blocks of one group: K and V of a block reach its own LDS buffer by
+// DMA, in the prompt kernel's swizzled layout, read by the same MFMA steps.  The wave
+// writes unnormalised O, running max and sum of its 4T live rows;
+// flash_decode_merge_kernel joins the waves of a group.
+template <int HD>
+__global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
+    using S = FaShape<HD>;
+    constexpr int NCP = S::BLK / 1024;  // 1 KB copies per block of K (and of V)
+    __shared__ __attribute__((aligned(1024))) uint8_t buf[S::BUF];
+    const int lane = threadIdx.x, lr = lane % 32, h = lane / 32;
+    const int g = (int)blockIdx.x / a.nch, w = (int)blockIdx.x % a.nch;
+    const int t = min(lr / 4, a.T - 1), head = g * 4 + lr % 4;
+    const int key_end = a.causal ? min(a.kv_len, a.q_pos0 + a.T) : a.kv_len;
+    const int nblk = (key_end + 31) / 32;
+    const int kb0 = w * a.cb, kb1 = min(nblk, kb0 + a.cb);  // kb0 < nblk: nch = ceil(nblk / cb)
+
+    const float* kg = a.k + (size_t)g * a.L * HD;
+    const float* vg = a.v + (size_t)g * a.L * HD;
+    const int pos = lane % (S::ROWB / 16);
+    auto issue = [&](int kb) {
+#pragma unroll
+        for (int q = 0; q < NCP; q++) {
+            const int r = q * S::RPC + lane / (S::ROWB / 16);
+            const size_t row = (size_t)min(kb * 32 + r, a.kv_len - 1) * HD;  // in bounds
+            g2l16(kg + row + 4 * (pos ^ fa_swz_k(r)), buf + q * 1024);
+            g2l16(vg + row + 4 * (pos ^ fa_swz_v(r)), buf + S::BLK + q * 1024);
+        }
+    };
+    issue(kb0);
+
+    const float qscale = a.scale * 1.4426950408889634f;
+    float qv[HD / 2];
+    {
+        const float* qp = a.q + ((size_t)t * a.nh + head) * HD + 8 * h;
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++) {
+            const v4f_t x0 = *reinterpret_cast<const v4f_t*>(qp + 16 * c);
+            const v4f_t x1 = *reinterpret_cast<const v4f_t*>(qp + 16 * c + 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                qv[8 * c + j] = x0[j] * qscale;
+                qv[8 * c + 4 + j] = x1[j] * qscale;
+            }
+        }
+    }
+    const int swk = fa_swz_k(lr);
+    uint32_t voff[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) voff[c] = (uint32_t)(S::BLK + 4 * h * S::ROWB + 128 * (c ^ h) + 4 * lr);
+    const uint32_t base = lds_off(buf);
+
+    v16f_t o[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) o[c] = v16f_t{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int my_q = a.q_pos0 + t;
+
+    for (int kb = kb0; kb < kb1; kb++) {
+        MM_WAIT_VM_LGKM(0);  // block kb is in LDS
+        const uint32_t krow = base + (uint32_t)(lr * S::ROWB);
+        v4i_t kr[HD / 16][2];
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) kr[c][u] = lds_b128_at<0>(krow + 16u * (uint32_t)((4 * c + 2 * h + u) ^ swk));
+        v16f_t s = v16f_t{};
+        [&]<int... C>(std::integer_sequence<int, C...>) {
+            (
+                [&] {
+                    lds_wait_upto<HD / 8 - 2 - 2 * C>();
+                    lds_pin(kr[C][0]);
+                    lds_pin(kr[C][1]);
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        s = mfma_f32(__int_as_float(kr[C][j / 4][j % 4]), qv[8 * C + j], s);
+                }(),
+                ...);
+        }(std::make_integer_sequence<int, HD / 16>{});
+        const bool need_mask = kb * 32 + 31 >= a.kv_len || (a.causal && kb * 32 + 31 > a.q_pos0);
+        if (need_mask) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int key = kb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+                if (key >= a.kv_len || (a.causal && key > my_q)) s[v] = -INFINITY;
+            }
+        }
+        float mloc = s[0];
+#pragma unroll
+        for (int v = 1; v < 16; v++) mloc = fmaxf(mloc, s[v]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, WAVE));
+        // a wave's blocks may hide every key from a causal row (the cache's last block
+        // against an earlier new token): its max stays -inf, its weights 0
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float psum = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float p = __builtin_amdgcn_exp2f(s[v] - m_use);
+            s[v] = p;
+            psum += p;
+        }
+        psum += __shfl_xor(psum, 32, WAVE);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int c = 0; c < HD / 32; c++) o[c] *= alpha;
+        }
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++) {
+            const uint32_t vb = base + voff[c];
+            uint32_t vv[16];
+            [&]<int... V>(std::integer_sequence<int, V...>) {
+                ((vv[V] = lds_b32_at<(8 * (V / 4) + V % 4) * S::ROWB>(vb)), ...);
+            }(std::make_integer_sequence<int, 16>{});
+            lds_wait_upto<8>();
+#pragma unroll
+            for (int v = 0; v < 8; v++) {
+                lds_pin(vv[v]);
+                o[c] = mfma_f32(__uint_as_float(vv[v]), s[v], o[c]);
+            }
+            lds_wait_upto<0>();
+#pragma unroll
+            for (int v = 8; v < 16; v++) {
+                lds_pin(vv[v]);
+                o[c] = mfma_f32(__uint_as_float(vv[v]), s[v], o[c]);
+            }
+        }
+        // every LDS read of the block has returned (lgkmcnt 0): the buffer is free
+        if (kb + 1 < kb1) issue(kb + 1);
+    }
+    if (lr >= 4 * a.T) return;
+    // partial of wave w of group g: O rows [32][HD], then m [32], l [32]
+    float* pp = a.part + (size_t)blockIdx.x * (32 * HD + 64);
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; v4++) {
+            const int d = 32 * c + 8 * v4 + 4 * h;
+            *reinterpret_cast<v4f_t*>(pp + lr * HD + d) =
+                v4f_t{o[c][4 * v4], o[c][4 * v4 + 1], o[c][4 * v4 + 2], o[c][4 * v4 + 3]};
+        }
+    if (h == 0) {
+        pp[32 * HD + lr] = m_run;
+        pp[32 * HD + 32 + lr] = l_run;
+    }
+}
+
+// Join the nch waves of a group for one row (work group = group x row): M = max_w m_w,
+// O = sum_w 2^(m_w - M) O_w and l likewise; out = O / l.  The work group's 256 threads
+// form 256 / (HD / 4) teams of HD / 4 (one float4 of the row each); team j takes waves
+// j, j + teams, ..., and the teams' sums are added in team order.
+template <int HD>
+__global__ __launch_bounds__(256) void flash_decode_merge_kernel(FlashArgs a) {
+    constexpr int TPR = HD / 4, TEAMS = 256 / TPR;
+    constexpr size_t STRIDE = 32 * HD + 64;
+    __shared__ float red[256 / WAVE];
+    __shared__ v4f_t team_o[TEAMS][TPR];
+    __shared__ float team_l[TEAMS];
+    const int rows = 4 * a.T;
+    const int g = (int)blockIdx.x / rows, r = (int)blockIdx.x % rows;
+    const float* __restrict__ base = a.part + (size_t)g * a.nch * STRIDE;
+    const int tid = threadIdx.x;
+    float mx = -INFINITY;
+    for (int w = tid; w < a.nch; w += 256) mx = fmaxf(mx, base[w * STRIDE + 32 * HD + r]);
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, WAVE));
+    if (tid % WAVE == 0) red[tid / WAVE] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));  // finite: key 0 is visible to every row
+    const int j = tid / TPR, d4 = tid % TPR;
+    v4f_t acc = v4f_t{};
+    float l = 0.0f;
+#pragma unroll 4
+    for (int w = j; w < a.nch; w += TEAMS) {
+        const float* pp = base + w * STRIDE;
+        const float wgt = __builtin_amdgcn_exp2f(pp[32 * HD + r] - mx);
+        const v4f_t ov = *reinterpret_cast<const v4f_t*>(pp + r * HD + 4 * d4);
+        acc += wgt * ov;
+        l += wgt * pp[32 * HD + 32 + r];
+    }
+    team_o[j][d4] = acc;
+    if (d4 == 0) team_l[j] = l;
+    __syncthreads();
+    if (j != 0) return;
+    v4f_t sum = team_o[0][d4];
+    float lsum = team_l[0];
+#pragma unroll
+    for (int u = 1; u < TEAMS; u++) {
+        sum += team_o[u][d4];
+        lsum += team_l[u];
+    }
+    const float inv = 1.0f / lsum;
+    const int tok = r / 4, head = g * 4 + r % 4;
+    *reinterpret_cast<v4f_t*>(a.out + ((size_t)tok * a.nh + head) * HD + 4 * d4) = sum * inv;
+}
+
 int flash_attn_ws_slots(int max_tokens, int max_keys, int nkv) {
     const long n = (long)((max_tokens + 31) / 32) * ((max_keys + 31) / 32) * nkv;
     return (int)min(n, (long)FA_SPLIT_SLOTS);
 }
 size_t flash_attn_ws_floats(int hd, int slots) { return (size_t)slots * 4 * (hd * 32 + 128); }
 
-hipError_t launch_flash_attn(const FlashArgs& a_in, hipStream_t s, float* ws, int ws_slots) {
+hipError_t launch_flash_attn(const FlashArgs& a_in, hipStream_t s, float* ws, int ws_slots, int max_waves) {
     FlashArgs a = a_in;
     const int n_qt = (a.T + 31) / 32, base = n_qt * a.nkv;
     const int max_keys = a.causal ? min(a.kv_len, a.q_pos0 + a.T) : a.kv_len;
@@ -881,6 +1084,31 @@ hipError_t launch_flash_attn(const FlashArgs& a_in, hipStream_t s, float* ws, in
     // ~5 TB/s, ~34 MB per unit of time).  Short prompts, causal tiles of very different
     // lengths and decode against a long cache split; long prompts fill the chip with
     // whole tiles.
+    if (a.T <= 8 && ws && max_nblk >= 2) {
+        // decode: one wave per cb key blocks of a group, as many waves as are resident
+        // (LDS: 32 KB a wave at head_dim 128, 5 a CU; 16 KB at 64, 10 a CU) unless the
+        // caller caps them
+        const int resident = 256 * (a.hd == 128 ? 5 : 10);
+        const int target = max_waves > 0 ? min(max_waves, resident) : resident;
+        int cb = (int)max(1L, ((long)max_nblk * a.nkv + target - 1) / target);
+        int nw = (max_nblk + cb - 1) / cb;
+        const size_t cap = flash_attn_ws_floats(a.hd, ws_slots);
+        while (nw > 1 && (size_t)a.nkv * nw * (32 * a.hd + 64) > cap) nw = (max_nblk + ++cb - 1) / cb;
+        a.cb = cb;
+        a.nch = nw;
+        a.part = ws;
+        const dim3 grid((unsigned)(a.nkv * nw)), mgrid((unsigned)(a.nkv * 4 * a.T));
+        if (a.hd == 128) {
+            hipLaunchKernelGGL(flash_decode_kernel<128>, grid, dim3(64), 0, s, a);
+            hipLaunchKernelGGL(flash_decode_merge_kernel<128>, mgrid, dim3(256), 0, s, a);
+        } else if (a.hd == 64) {
+            hipLaunchKernelGGL(flash_decode_kernel<64>, grid, dim3(64), 0, s, a);
+            hipLaunchKernelGGL(flash_decode_merge_kernel<64>, mgrid, dim3(256), 0, s, a);
+        } else {
+            return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     const int slots = 256 * (a.hd == 128 ? 2 : 3);  // resident work groups (occupancy)
     if (ws && max_nblk >= 2) {
         auto tile_blocks = [&](int t) {

@@ -84,6 +84,7 @@ struct hy_attn_ctx {
     float* gemm_ws = nullptr;  // stream-K partial tiles of the projections' GEMM
     float* fa_ws = nullptr;    // partial tiles of the attention split over the keys
     int fa_slots = 0;
+    int decode_waves = 0;      // cap on the decode attention's waves (0: resident count)
     float* xn = nullptr;       // decoder layer: normed input [Tm][H]
     float* hres = nullptr;     // decoder layer: x + attention [Tm][H]
     bool prof = false;
@@ -193,7 +194,7 @@ int run(hy_attn_ctx* c, const AttnLayer& W, const float* x, int T, int mode, con
     HY_TRY(timed(c, AK_ROPE, s, [&] { return hy::launch_rope_qknorm(r, s); }));
     hy::FlashArgs f{c->q, k, v, c->merged, T, c->nh, c->nkv, c->hd, Lrows, kv_len, pos0, causal,
                     1.0f / sqrtf((float)c->hd)};
-    HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s, c->fa_ws, c->fa_slots); }));
+    HY_TRY(timed(c, AK_ATTN, s, [&] { return hy::launch_flash_attn(f, s, c->fa_ws, c->fa_slots, c->decode_waves); }));
     HY_TRY(timed(c, AK_OPROJ, s,
                  [&] {
                      return hy::launch_gemm_nt_f32(c->merged, W.o_w, resid, out, T, c->H, c->nh * c->hd, s,
@@ -498,6 +499,13 @@ int hy_embedding_lookup_f32(const int32_t* ids, const float* table, uint32_t T, 
     if (!ids || !table || !out) return fail(HY_ERR_INVALID, "null pointer");
     if (hidden == 0 || hidden % 4) return fail(HY_ERR_INVALID, "hidden=%u must be a multiple of 4", hidden);
     HIP_TRY(hy::launch_embed(ids, table, (int)T, (int)hidden, (int)vocab, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
+int hy_attn_set_decode_waves(hy_attn_ctx* c, uint32_t max_waves) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (max_waves > (1u << 20)) return fail(HY_ERR_INVALID, "max_waves=%u out of range", max_waves);
+    c->decode_waves = (int)max_waves;
     return HY_OK;
 }
 

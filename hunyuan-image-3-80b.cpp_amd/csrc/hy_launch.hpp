@@ -143,7 +143,10 @@ hipError_t launch_gemm_nt_f32(const float* A, const float* W, const float* R, fl
 hipError_t launch_rope_qknorm(const RopeNormArgs& a, hipStream_t s);
 // ws: flash_attn_ws_floats(hd, ws_slots) of device scratch, or nullptr (no split over
 // the keys)
-hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s, float* ws = nullptr, int ws_slots = 0);
+// T <= 8 (decode) with ws: the row-packed decode kernel on at most max_waves waves
+// (0: as many as the chip holds)
+hipError_t launch_flash_attn(const FlashArgs& a, hipStream_t s, float* ws = nullptr, int ws_slots = 0,
+                             int max_waves = 0);
 hipError_t launch_rope2d_table(int seq, int n_elem, int text_len, int img_h, int img_w, float base, float* cos_out,
                                float* sin_out, hipStream_t s);
 hipError_t launch_gather_kv(const float* src, int nkv, int L, int pos0, int T, int hd, float* dst, hipStream_t s);

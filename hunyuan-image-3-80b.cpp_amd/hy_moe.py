@@ -81,6 +81,7 @@ _SIGS = {
     "hy_attn_set_input_norm": (C.c_int, [_vp, _u32, _vp]),
     "hy_decoder_layer_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
     "hy_lm_head_f32": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
+    "hy_attn_set_decode_waves": (C.c_int, [_vp, _u32]),
     "hy_attn_prof_enable": (C.c_int, [_vp, _i32]),
     "hy_attn_prof_read": (C.c_int, [_vp, _u32, C.POINTER(_u64), C.POINTER(C.c_double)]),
     "hy_moe_forward": (C.c_int, [_vp, _u32, _vp, _u32, _vp, _vp]),
@@ -562,6 +563,9 @@ class Attn:
         n = _u32()
         check(lib().hy_attn_cache_len(self.h, layer, C.byref(n)))
         return n.value
+
+    def set_decode_waves(self, max_waves):
+        check(lib().hy_attn_set_decode_waves(self.h, max_waves))
 
     def prof_enable(self, on):
         check(lib().hy_attn_prof_enable(self.h, 1 if on else 0))

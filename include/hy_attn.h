@@ -165,6 +165,13 @@ int hy_rope_2d_f32(float* x_dev, uint32_t T, uint32_t heads, uint32_t head_dim, 
 int hy_embedding_lookup_f32(const int32_t* ids_dev, const float* table_dev, uint32_t T, uint32_t hidden,
                             uint32_t vocab, float* out_dev, void* stream);
 
+/* Decode (T <= 8 new tokens): the attention spreads the cached keys over up to
+ * max_waves waves, each taking whole 32-key blocks of one kv head, and joins the waves'
+ * partial results afterwards.  0 (the default) = as many waves as the GPU keeps
+ * resident; a smaller cap gives each wave more blocks.  No counterpart in the
+ * reference (its CPU attention loops over the cache); a tuning and testing knob. */
+int hy_attn_set_decode_waves(hy_attn_ctx* ctx, uint32_t max_waves);
+
 /* Per-kernel timing of this context's launches (as hy_moe_prof_*): kernel ids
  * 0 = qkv_proj, 1 = rope_qknorm, 2 = attention, 3 = o_proj. */
 int hy_attn_prof_enable(hy_attn_ctx* ctx, int32_t on);

@@ -109,6 +109,26 @@ def test_cached_decode_long_cache(gpu):
     m.close()
 
 
+@pytest.mark.parametrize("shp", SHAPES, ids=["hd64", "hd128"])
+@pytest.mark.parametrize("waves", [0, 7, 1])
+def test_cached_decode_waves(gpu, shp, waves):
+    """Decode (1..8 new tokens: the row-packed decode kernel and its merge) against a
+    cache of 700 positions, with the waves uncapped (one 32-key block each), capped at 7
+    (several blocks a wave, the last wave's range ragged) and at 1 (the whole cache in
+    one wave, nothing to join)."""
+    m, w = _ctx(gpu, shp, max_tokens=700, max_cache=760, seed=7)
+    m.set_decode_waves(waves)
+    cache = A.KVCache(shp["nkv"], shp["hd"], max_len=760)
+    rng = np.random.default_rng(7)
+    for n in (700, 1, 2, 3, 8, 5):
+        x = rng.standard_normal((n, shp["H"])).astype(np.float32)
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((n, shp["H"]))
+        m.forward_cached(xb, n, ob)
+        ref = A.attention_cached(w, x, cache)
+        check(ob.numpy(), ref, f"cached +{n} at {cache.cur_len - n} waves={waves}")
+    m.close()
+
+
 def test_forward_is_causal(gpu):
     shp = SHAPES[0]
     m, _ = _ctx(gpu, shp)
