@@ -882,17 +882,17 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
     const float* kg = a.k + (size_t)g * a.L * HD;
     const float* vg = a.v + (size_t)g * a.L * HD;
     const int pos = lane % (S::ROWB / 16);
-    auto issue = [&](int kb) {
+    // K copies of a block, then its V copies (copies complete in issue order): QK^T
+    // starts once K has landed, while V is still on its way
+    auto issue = [&](int kb, const float* src, int (*swz)(int), int off) {
 #pragma unroll
         for (int q = 0; q < NCP; q++) {
             const int r = q * S::RPC + lane / (S::ROWB / 16);
             const size_t row = (size_t)min(kb * 32 + r, a.kv_len - 1) * HD;  // in bounds
-            g2l16(kg + row + 4 * (pos ^ fa_swz_k(r)), buf + q * 1024);
-            g2l16(vg + row + 4 * (pos ^ fa_swz_v(r)), buf + S::BLK + q * 1024);
+            g2l16(src + row + 4 * (pos ^ swz(r)), buf + off + q * 1024);
         }
     };
-    issue(kb0);
-
+    // Q first: its loads then complete ahead of the block copies issued after them
     const float qscale = a.scale * 1.4426950408889634f;
     float qv[HD / 2];
     {
@@ -908,6 +908,10 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
             }
         }
     }
+    issue(kb0, kg, fa_swz_k, 0);
+    issue(kb0, vg, fa_swz_v, S::BLK);
+    MM_WAIT_VM_LGKM(2 * NCP);  // Q has landed (older than the copies): nothing of it is pending in the loop
+
     const int swk = fa_swz_k(lr);
     uint32_t voff[HD / 32];
 #pragma unroll
@@ -921,7 +925,7 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
     const int my_q = a.q_pos0 + t;
 
     for (int kb = kb0; kb < kb1; kb++) {
-        MM_WAIT_VM_LGKM(0);  // block kb is in LDS
+        MM_WAIT_VM_LGKM(NCP);  // K of block kb is in LDS
         const uint32_t krow = base + (uint32_t)(lr * S::ROWB);
         v4i_t kr[HD / 16][2];
 #pragma unroll
@@ -941,6 +945,9 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
                 }(),
                 ...);
         }(std::make_integer_sequence<int, HD / 16>{});
+        // every K read has returned: the K half of the buffer takes the next block's K
+        const bool more = kb + 1 < kb1;
+        if (more) issue(kb + 1, kg, fa_swz_k, 0);
         const bool need_mask = kb * 32 + 31 >= a.kv_len || (a.causal && kb * 32 + 31 > a.q_pos0);
         if (need_mask) {
 #pragma unroll
@@ -972,6 +979,10 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
 #pragma unroll
             for (int c = 0; c < HD / 32; c++) o[c] *= alpha;
         }
+        if (more)  // V of block kb landed; the next block's K may still be in flight
+            MM_WAIT_VM_LGKM(NCP);
+        else
+            MM_WAIT_VM_LGKM(0);
 #pragma unroll
         for (int c = 0; c < HD / 32; c++) {
             const uint32_t vb = base + voff[c];
@@ -992,8 +1003,8 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
                 o[c] = mfma_f32(__uint_as_float(vv[v]), s[v], o[c]);
             }
         }
-        // every LDS read of the block has returned (lgkmcnt 0): the buffer is free
-        if (kb + 1 < kb1) issue(kb + 1);
+        // every V read has returned (lgkmcnt 0): the V half takes the next block's V
+        if (more) issue(kb + 1, vg, fa_swz_v, S::BLK);
     }
     if (lr >= 4 * a.T) return;
     // partial of wave w of group g: O rows [32][HD], then m [32], l [32]
@@ -1012,49 +1023,225 @@ __global__ __launch_bounds__(64) void flash_decode_kernel(FlashArgs a) {
     }
 }
 
-// Join the nch waves of a group for one row (work group = group x row): M = max_w m_w,
-// O = sum_w 2^(m_w - M) O_w and l likewise; out = O / l.  The work group's 256 threads
-// form 256 / (HD / 4) teams of HD / 4 (one float4 of the row each); team j takes waves
-// j, j + teams, ..., and the teams' sums are added in team order.
+// The same for T <= 4 (16 live rows): 16 x 16 x 4 fp32 MFMA tiles, half the matrix
+// work of the 32-row tile.  Lane l: kq = l % 16, kk = l / 16.
+//   S^T[key][q] (two halves of 16 keys): step j takes d = (HD / 4) kk + j, lane
+//     supplying K[16 hf + kq][d] and Q[kq][d]; lane l ends with S of query l % 16 and
+//     keys 16 hf + 4 (l / 16) + v.
+//   O^T[d][q] (HD / 16 tiles of 16 dims): step j takes keys 16 (j / 4) + 4 kk + j % 4,
+//     lane supplying V[key][16 dt + kq] and its own P; lane l ends with O of query
+//     l % 16, dims 16 dt + 4 (l / 16) + v.
+// V sits at chunk position c ^ (8 ((r >> 2) & 1) + 4 ((r >> 3) & 1)): the four key rows
+// of one read (4 kk + const) fall on four different 16-chunk bank groups.
+__device__ __forceinline__ int fa_swz_vd(int r) { return 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1); }
+
 template <int HD>
-__global__ __launch_bounds__(256) void flash_decode_merge_kernel(FlashArgs a) {
-    constexpr int TPR = HD / 4, TEAMS = 256 / TPR;
+__global__ __launch_bounds__(64) void flash_decode16_kernel(FlashArgs a) {
+    using S = FaShape<HD>;
+    constexpr int NCP = S::BLK / 1024;
+    constexpr int KR = HD / 16;  // 16-byte K reads per half
+    __shared__ __attribute__((aligned(1024))) uint8_t buf[S::BUF];
+    const int lane = threadIdx.x, kq = lane % 16, kk = lane / 16;
+    const int g = (int)blockIdx.x / a.nch, w = (int)blockIdx.x % a.nch;
+    const int key_end = a.causal ? min(a.kv_len, a.q_pos0 + a.T) : a.kv_len;
+    const int nblk = (key_end + 31) / 32;
+    const int kb0 = w * a.cb, kb1 = min(nblk, kb0 + a.cb);
+
+    const float* kg = a.k + (size_t)g * a.L * HD;
+    const float* vg = a.v + (size_t)g * a.L * HD;
+    const int pos = lane % (S::ROWB / 16);
+    auto issue = [&](int kb, const float* src, int (*swz)(int), int off) {
+#pragma unroll
+        for (int q = 0; q < NCP; q++) {
+            const int r = q * S::RPC + lane / (S::ROWB / 16);
+            const size_t row = (size_t)min(kb * 32 + r, a.kv_len - 1) * HD;  // in bounds
+            g2l16(src + row + 4 * (pos ^ swz(r)), buf + off + q * 1024);
+        }
+    };
+    // Q first: its loads then complete ahead of the block copies issued after them
+    const float qscale = a.scale * 1.4426950408889634f;
+    float qv[HD / 4];
+    {
+        const int t = min(kq / 4, a.T - 1), head = g * 4 + kq % 4;
+        const float* qp = a.q + ((size_t)t * a.nh + head) * HD + (HD / 4) * kk;
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++) {
+            const v4f_t x = *reinterpret_cast<const v4f_t*>(qp + 4 * c);
+#pragma unroll
+            for (int j = 0; j < 4; j++) qv[4 * c + j] = x[j] * qscale;
+        }
+    }
+    issue(kb0, kg, fa_swz_k, 0);
+    issue(kb0, vg, fa_swz_vd, S::BLK);
+    MM_WAIT_VM_LGKM(2 * NCP);  // Q has landed (older than the copies): nothing of it is pending in the loop
+
+    const uint32_t base = lds_off(buf);
+    // K: row 16 hf + kq, logical chunks (HD / 16) kk + m at position ^ kq
+    const uint32_t krow = base + (uint32_t)(kq * S::ROWB);
+    // V: rows 4 kk (+ 16 hf + v, immediate), logical chunk 4 dt + kq / 4 at position
+    // 4 (dt ^ sv) + kq / 4 with sv = the row's swizzle / 4 (dt = 4 dh + dl: dh immediate)
+    const int sv = fa_swz_vd(4 * kk) / 4;
+    uint32_t voff[4];
+#pragma unroll
+    for (int dl = 0; dl < 4; dl++)
+        voff[dl] = base + (uint32_t)(S::BLK + 4 * kk * S::ROWB + 64 * (dl ^ sv) + 4 * kq);
+
+    v4f_t o[HD / 16];
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) o[dt] = v4f_t{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int my_q = a.q_pos0 + min(kq / 4, a.T - 1);  // lane's query: l % 16
+
+    for (int kb = kb0; kb < kb1; kb++) {
+        MM_WAIT_VM_LGKM(NCP);  // K of block kb is in LDS
+        v4i_t kr[2][KR];
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+            for (int m = 0; m < KR; m++)
+                kr[hf][m] = lds_b128_at<0>(krow + (uint32_t)(16 * hf * S::ROWB) +
+                                           16u * (uint32_t)(((HD / 16) * kk + m) ^ kq));
+        v4f_t sc[2] = {v4f_t{}, v4f_t{}};
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+            (
+                [&] {
+                    constexpr int hf = I / KR, m = I % KR;
+                    lds_wait_upto<2 * KR - 1 - I>();
+                    lds_pin(kr[hf][m]);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        sc[hf] = __builtin_amdgcn_mfma_f32_16x16x4f32(__int_as_float(kr[hf][m][j]), qv[4 * m + j],
+                                                                    sc[hf], 0, 0, 0);
+                }(),
+                ...);
+        }(std::make_integer_sequence<int, 2 * KR>{});
+        const bool more = kb + 1 < kb1;
+        if (more) issue(kb + 1, kg, fa_swz_k, 0);
+        const bool need_mask = kb * 32 + 31 >= a.kv_len || (a.causal && kb * 32 + 31 > a.q_pos0);
+        if (need_mask) {
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int key = kb * 32 + 16 * hf + 4 * kk + v;
+                    if (key >= a.kv_len || (a.causal && key > my_q)) sc[hf][v] = -INFINITY;
+                }
+        }
+        float mloc = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                           fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, WAVE));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, WAVE));
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float psum = 0.0f;
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float p = __builtin_amdgcn_exp2f(sc[hf][v] - m_use);
+                sc[hf][v] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 16, WAVE);
+        psum += __shfl_xor(psum, 32, WAVE);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < HD / 16; dt++) o[dt] *= alpha;
+        }
+        if (more)
+            MM_WAIT_VM_LGKM(NCP);
+        else
+            MM_WAIT_VM_LGKM(0);
+        // two dim tiles at a time: 16 reads in flight, consumed 8 and 8
+        [&]<int... DP>(std::integer_sequence<int, DP...>) {
+            (
+                [&] {
+                    constexpr int dt = 2 * DP;
+                    uint32_t vv[2][8];
+                    [&]<int... V>(std::integer_sequence<int, V...>) {
+                        ((vv[V / 8][V % 8] = lds_b32_at<(16 * ((V % 8) / 4) + (V % 8) % 4) * S::ROWB +
+                                                        256 * ((dt + V / 8) / 4)>(voff[(dt + V / 8) % 4])),
+                         ...);
+                    }(std::make_integer_sequence<int, 16>{});
+                    lds_wait_upto<8>();
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        lds_pin(vv[0][j]);
+                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vv[0][j]), sc[j / 4][j % 4],
+                                                                     o[dt], 0, 0, 0);
+                    }
+                    lds_wait_upto<0>();
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        lds_pin(vv[1][j]);
+                        o[dt + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vv[1][j]), sc[j / 4][j % 4],
+                                                                         o[dt + 1], 0, 0, 0);
+                    }
+                }(),
+                ...);
+        }(std::make_integer_sequence<int, HD / 32>{});
+        if (more) issue(kb + 1, vg, fa_swz_vd, S::BLK);
+    }
+    if (kq >= 4 * a.T) return;
+    float* pp = a.part + (size_t)blockIdx.x * (32 * HD + 64);
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) *reinterpret_cast<v4f_t*>(pp + kq * HD + 16 * dt + 4 * kk) = o[dt];
+    if (kk == 0) {
+        pp[32 * HD + kq] = m_run;
+        pp[32 * HD + 32 + kq] = l_run;
+    }
+}
+
+// Join the nch waves of a group for one row (work group = group x row): with
+// M = max_w m_w, O = sum_w 2^(m_w - M) O_w and l likewise; out = O / l.  The work
+// group's 1024 threads form 1024 / (HD / 4) teams of HD / 4 (one float4 of the row
+// each); team j folds waves j, j + teams, ... in one pass with a running max, and the
+// teams' results are joined in team order.
+constexpr int FDM_THREADS = 1024;
+template <int HD>
+__global__ __launch_bounds__(FDM_THREADS) void flash_decode_merge_kernel(FlashArgs a) {
+    constexpr int TPR = HD / 4, TEAMS = FDM_THREADS / TPR;
     constexpr size_t STRIDE = 32 * HD + 64;
-    __shared__ float red[256 / WAVE];
     __shared__ v4f_t team_o[TEAMS][TPR];
-    __shared__ float team_l[TEAMS];
+    __shared__ float team_m[TEAMS], team_l[TEAMS];
     const int rows = 4 * a.T;
     const int g = (int)blockIdx.x / rows, r = (int)blockIdx.x % rows;
     const float* __restrict__ base = a.part + (size_t)g * a.nch * STRIDE;
-    const int tid = threadIdx.x;
-    float mx = -INFINITY;
-    for (int w = tid; w < a.nch; w += 256) mx = fmaxf(mx, base[w * STRIDE + 32 * HD + r]);
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, WAVE));
-    if (tid % WAVE == 0) red[tid / WAVE] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));  // finite: key 0 is visible to every row
-    const int j = tid / TPR, d4 = tid % TPR;
+    const int j = (int)threadIdx.x / TPR, d4 = (int)threadIdx.x % TPR;
     v4f_t acc = v4f_t{};
-    float l = 0.0f;
-#pragma unroll 4
+    float mt = -INFINITY, lt = 0.0f;
+#pragma unroll 2
     for (int w = j; w < a.nch; w += TEAMS) {
         const float* pp = base + w * STRIDE;
-        const float wgt = __builtin_amdgcn_exp2f(pp[32 * HD + r] - mx);
+        const float mw = pp[32 * HD + r], lw = pp[32 * HD + 32 + r];
         const v4f_t ov = *reinterpret_cast<const v4f_t*>(pp + r * HD + 4 * d4);
-        acc += wgt * ov;
-        l += wgt * pp[32 * HD + 32 + r];
+        const float m_new = fmaxf(mt, mw);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a wave may see no key of this row
+        const float a0 = __builtin_amdgcn_exp2f(mt - m_use), a1 = __builtin_amdgcn_exp2f(mw - m_use);
+        acc = acc * a0 + ov * a1;
+        lt = lt * a0 + lw * a1;
+        mt = m_new;
     }
     team_o[j][d4] = acc;
-    if (d4 == 0) team_l[j] = l;
+    if (d4 == 0) {
+        team_m[j] = mt;
+        team_l[j] = lt;
+    }
     __syncthreads();
     if (j != 0) return;
-    v4f_t sum = team_o[0][d4];
-    float lsum = team_l[0];
+    float mx = team_m[0];
 #pragma unroll
-    for (int u = 1; u < TEAMS; u++) {
-        sum += team_o[u][d4];
-        lsum += team_l[u];
+    for (int u = 1; u < TEAMS; u++) mx = fmaxf(mx, team_m[u]);  // finite: key 0 is visible to every row
+    v4f_t sum = v4f_t{};
+    float lsum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < TEAMS; u++) {
+        const float wgt = __builtin_amdgcn_exp2f(team_m[u] - mx);  // 0 for a team without waves
+        sum += team_o[u][d4] * wgt;
+        lsum += team_l[u] * wgt;
     }
     const float inv = 1.0f / lsum;
     const int tok = r / 4, head = g * 4 + r % 4;
@@ -1098,12 +1285,25 @@ hipError_t launch_flash_attn(const FlashArgs& a_in, hipStream_t s, float* ws, in
         a.nch = nw;
         a.part = ws;
         const dim3 grid((unsigned)(a.nkv * nw)), mgrid((unsigned)(a.nkv * 4 * a.T));
-        if (a.hd == 128) {
+        if (a.T <= 4) {
+            if (a.hd == 128)
+                hipLaunchKernelGGL(flash_decode16_kernel<128>, grid, dim3(64), 0, s, a);
+            else if (a.hd == 64)
+                hipLaunchKernelGGL(flash_decode16_kernel<64>, grid, dim3(64), 0, s, a);
+            else
+                return hipErrorInvalidValue;
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            if (a.hd == 128)
+                hipLaunchKernelGGL(flash_decode_merge_kernel<128>, mgrid, dim3(FDM_THREADS), 0, s, a);
+            else
+                hipLaunchKernelGGL(flash_decode_merge_kernel<64>, mgrid, dim3(FDM_THREADS), 0, s, a);
+        } else if (a.hd == 128) {
             hipLaunchKernelGGL(flash_decode_kernel<128>, grid, dim3(64), 0, s, a);
-            hipLaunchKernelGGL(flash_decode_merge_kernel<128>, mgrid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL(flash_decode_merge_kernel<128>, mgrid, dim3(FDM_THREADS), 0, s, a);
         } else if (a.hd == 64) {
             hipLaunchKernelGGL(flash_decode_kernel<64>, grid, dim3(64), 0, s, a);
-            hipLaunchKernelGGL(flash_decode_merge_kernel<64>, mgrid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL(flash_decode_merge_kernel<64>, mgrid, dim3(FDM_THREADS), 0, s, a);
         } else {
             return hipErrorInvalidValue;
         }
