@@ -483,7 +483,10 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 
 // combine: out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e y_e[t] ), the
 // shared expert's output at slot T*K + t when has_shared.  One thread per 4 outputs
-// (16-byte loads of the y rows); each output keeps the scalar fmaf order.
+// (16-byte loads of the y rows); each output keeps the scalar fmaf order.  The token's
+// KMAX list entries (indices clamped to K - 1) and then its y rows are all loaded
+// before the first fmaf, so a thread waits for two rounds of loads, not 2 K.
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __restrict__ y, int T, int H, int K,
                                                       int has_shared, const float* __restrict__ resid,
                                                       float* __restrict__ out) {
@@ -491,16 +494,27 @@ __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __
     const int H4 = H / 4;
     if (idx >= (size_t)T * H4) return;
     const int t = (int)(idx / H4), r4 = (int)(idx % H4);
-    float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < K; k++) {
-        const float w = R.comb_w[t * K + k];
-        const float4 v = reinterpret_cast<const float4*>(y + (size_t)R.comb_pos[t * K + k] * H)[r4];
-        c = make_float4(fmaf(w, v.x, c.x), fmaf(w, v.y, c.y), fmaf(w, v.z, c.z), fmaf(w, v.w, c.w));
+    int pos[KMAX];
+    float w[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+        const int kk = min(k, K - 1);
+        pos[k] = R.comb_pos[t * K + kk];
+        w[k] = R.comb_w[t * K + kk];
     }
+    float4 v[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) v[k] = reinterpret_cast<const float4*>(y + (size_t)pos[k] * H)[r4];
+    float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < KMAX; k++)
+        if (k < K)
+            c = make_float4(fmaf(w[k], v[k].x, c.x), fmaf(w[k], v[k].y, c.y), fmaf(w[k], v[k].z, c.z),
+                            fmaf(w[k], v[k].w, c.w));
     float4 o = c;
     if (has_shared) {
-        const float4 v = reinterpret_cast<const float4*>(y + ((size_t)T * K + t) * H)[r4];
-        o = make_float4(v.x + c.x, v.y + c.y, v.z + c.z, v.w + c.w);
+        const float4 u = reinterpret_cast<const float4*>(y + ((size_t)T * K + t) * H)[r4];
+        o = make_float4(u.x + c.x, u.y + c.y, u.z + c.z, u.w + c.w);
     }
     if (resid) {
         const float4 q = reinterpret_cast<const float4*>(resid + (size_t)t * H)[r4];
@@ -577,8 +591,13 @@ hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatVie
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,
                           float* out, hipStream_t s) {
     const size_t n = (size_t)T * (H / 4);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, y, T, H, K, has_shared,
-                       resid, out);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (K <= 4)
+        hipLaunchKernelGGL(combine_kernel<4>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
+    else if (K <= 8)
+        hipLaunchKernelGGL(combine_kernel<8>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
+    else
+        hipLaunchKernelGGL(combine_kernel<MAX_K>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
     return hipGetLastError();
 }
 
