@@ -204,6 +204,91 @@ def attn_flops(kname, T):
     return 0.0
 
 
+def attn_decode_bytes(kname, T, L):
+    """Algorithmic HBM bytes of one launch of the cached (decode) attention at T new
+    tokens against L cached positions: the weights each projection streams, the keys
+    and values the attention reads, q / k / v / out rows."""
+    Hh, nh, nkv, hd = ATTN["H"], ATTN["nh"], ATTN["nkv"], ATTN["hd"]
+    nqkv = (nh + 2 * nkv) * hd
+    if kname == "qkv_proj":
+        return 4.0 * (nqkv * Hh + T * Hh + T * nqkv)
+    if kname == "o_proj":
+        return 4.0 * (Hh * nh * hd + T * nh * hd + 2 * T * Hh)
+    if kname == "attention":
+        return 4.0 * (2 * (L + T) * nkv * hd + 2 * T * nh * hd)
+    if kname == "rope_qknorm":
+        return 4.0 * 2 * T * nqkv
+    return 0.0
+
+
+def attn_decode_main(a, hy):
+    """The KV-cache branch at decode: T new tokens (default 1) against a cache of
+    a.cache positions, fp32, weights N(0, 0.02) resident.  Each timed step appends its
+    T tokens, so the cache grows by T per step (50 steps: +1 % at 4096)."""
+    import hy_oracle_attn as A
+    T, L = a.tokens or 1, a.cache
+    steps_all = a.warmup + 2 * a.steps
+    w = A.synth_weights(ATTN["H"], ATTN["nh"], ATTN["nkv"], ATTN["hd"], seed=a.seed, std=0.02)
+    m = hy.Attn(ATTN["H"], ATTN["nh"], ATTN["nkv"], ATTN["hd"], max(T, min(L, 4096)),
+                max_cache=L + T * steps_all)
+    m.upload(w.qkv_w, w.o_w, w.q_norm, w.k_norm)
+    st = hy.Stream()
+    rng = np.random.default_rng(a.seed)
+    chunk = min(L, 4096)
+    xf = hy.Buf.from_array(rng.standard_normal((chunk, ATTN["H"])).astype(np.float32))
+    of = hy.Buf.empty((chunk, ATTN["H"]))
+    filled = 0
+    while filled < L:  # fill the cache in prompt chunks
+        n = min(chunk, L - filled)
+        m.forward_cached(xf, n, of, stream=st.h)
+        filled += n
+    x = hy.Buf.from_array(rng.standard_normal((T, ATTN["H"])).astype(np.float32))
+    out = hy.Buf.empty((T, ATTN["H"]))
+    for _ in range(a.warmup):
+        m.forward_cached(x, T, out, stream=st.h)
+    st.synchronize()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    L0 = m.cache_len()
+    t0 = time.perf_counter()
+    hy.check(hy.lib().hy_event_record(ev0, st.h))
+    for _ in range(a.steps):
+        m.forward_cached(x, T, out, stream=st.h)
+    hy.check(hy.lib().hy_event_record(ev1, st.h))
+    st.synchronize()
+    wall = time.perf_counter() - t0
+    ms = hy.C.c_float()
+    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+    ms_per_step = ms.value / a.steps
+    Lmid = L0 + T * a.steps // 2  # mean cache length over the timed steps
+    m.prof_enable(True)
+    for _ in range(a.steps):
+        m.forward_cached(x, T, out, stream=st.h)
+    st.synchronize()
+    prof = {k: v for k, v in m.prof_read().items() if v[0] > 0}
+    m.prof_enable(False)
+    Lp = L0 + T * a.steps + T * a.steps // 2
+    dom = max(prof, key=lambda k: prof[k][1])
+    avg_s = prof[dom][1] / prof[dom][0] / 1e3
+    by = attn_decode_bytes(dom, T, Lp)
+    res = {
+        "metric": "attention decode tokens/sec (fp32 KV cache), 1 MI355X", "value": T / (ms_per_step / 1e3),
+        "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"attention_decode_f32_t{T}_cache{L}", "hidden": ATTN["H"], "heads": ATTN["nh"],
+                   "kv_heads": ATTN["nkv"], "head_dim": ATTN["hd"], "tokens": T, "cache_len_mean": Lmid},
+        "step_hbm_gbs": sum(attn_decode_bytes(k, T, Lmid) for k in prof) / (ms_per_step / 1e3) / 1e9,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": by / avg_s / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": by / avg_s / PEAK_HBM, "traffic": None,
+                     "algorithmic_bytes_per_launch": by, "avg_launch_ms": avg_s * 1e3},
+        "kernels_ms": {k: round(t / n, 5) for k, (n, t) in prof.items()},
+        "wall_s": wall,
+    }
+    print(json.dumps(res), flush=True)
+    m.close()
+
+
 def attn_cpu_baseline(w, T_sample=192):
     """attention_forward_cpu restated (the oracle, one thread, the reference's scalar
     fp32 loops) on a T_sample-token sequence of the same shape."""
@@ -359,6 +444,8 @@ def main():
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     ap.add_argument("--attn", action="store_true", help="time the attention half instead of the MoE layer")
+    ap.add_argument("--cache", type=int, default=0, metavar="L",
+                    help="with --attn: decode T (--tokens, default 1) new tokens against L cached positions")
     ap.add_argument("--model", action="store_true", help="time the resident 32-layer backbone with lm_head")
     ap.add_argument("--gguf-load", default=None, metavar="PATH",
                     help="time loading one real-shape layer from a GGUF file written at PATH")
@@ -378,7 +465,7 @@ def main():
         gguf_load(hy, WORKLOADS[a.config]["wtype"], a.gguf_load, a.seed)
         return
     if a.attn:
-        attn_main(a, hy)
+        (attn_decode_main if a.cache else attn_main)(a, hy)
         return
     if a.model:
         model_main(a, hy)

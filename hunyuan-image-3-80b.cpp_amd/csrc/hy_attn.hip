@@ -1272,11 +1272,13 @@ hipError_t launch_flash_attn(const FlashArgs& a_in, hipStream_t s, float* ws, in
     // lengths and decode against a long cache split; long prompts fill the chip with
     // whole tiles.
     if (a.T <= 8 && ws && max_nblk >= 2) {
-        // decode: one wave per cb key blocks of a group, as many waves as are resident
-        // (LDS: 32 KB a wave at head_dim 128, 5 a CU; 16 KB at 64, 10 a CU) unless the
-        // caller caps them
+        // decode: one wave per cb key blocks of a group, at most half as many waves as
+        // are resident (LDS: 32 KB a wave at head_dim 128, 5 a CU; 16 KB at 64, 10 a
+        // CU), or the caller's cap.  Two blocks a wave beat one (T=1 against 4,116
+        // positions: 15.3-15.9 us for 520 waves, 18.9 us for 1,032): the second
+        // block's K copy overlaps the first block's PV, and half the partials remain.
         const int resident = 256 * (a.hd == 128 ? 5 : 10);
-        const int target = max_waves > 0 ? min(max_waves, resident) : resident;
+        const int target = max_waves > 0 ? min(max_waves, resident) : resident / 2;
         int cb = (int)max(1L, ((long)max_nblk * a.nkv + target - 1) / target);
         int nw = (max_nblk + cb - 1) / cb;
         const size_t cap = flash_attn_ws_floats(a.hd, ws_slots);

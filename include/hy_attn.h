@@ -167,8 +167,9 @@ int hy_embedding_lookup_f32(const int32_t* ids_dev, const float* table_dev, uint
 
 /* Decode (T <= 8 new tokens): the attention spreads the cached keys over up to
  * max_waves waves, each taking whole 32-key blocks of one kv head, and joins the waves'
- * partial results afterwards.  0 (the default) = as many waves as the GPU keeps
- * resident; a smaller cap gives each wave more blocks.  No counterpart in the
+ * partial results afterwards.  0 (the default) = half as many waves as the GPU
+ * keeps resident (up to the resident count may be asked for); a smaller cap gives
+ * each wave more blocks.  No counterpart in the
  * reference (its CPU attention loops over the cache); a tuning and testing knob. */
 int hy_attn_set_decode_waves(hy_attn_ctx* ctx, uint32_t max_waves);
 
