@@ -272,15 +272,20 @@ def attn_decode_main(a, hy):
     dom = max(prof, key=lambda k: prof[k][1])
     avg_s = prof[dom][1] / prof[dom][0] / 1e3
     by = attn_decode_bytes(dom, T, Lp)
+    workload = f"attention_decode_f32_t{T}_cache{L}"
+    traffic = measured_traffic(workload, dom)
+    if traffic is not None and dom == "attention":  # the decode kernel and its merge
+        merge = measured_traffic(workload, "attention (merge)")
+        traffic = traffic + merge if merge is not None else None
     res = {
         "metric": "attention decode tokens/sec (fp32 KV cache), 1 MI355X", "value": T / (ms_per_step / 1e3),
         "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"attention_decode_f32_t{T}_cache{L}", "hidden": ATTN["H"], "heads": ATTN["nh"],
+        "config": {"workload": workload, "hidden": ATTN["H"], "heads": ATTN["nh"],
                    "kv_heads": ATTN["nkv"], "head_dim": ATTN["hd"], "tokens": T, "cache_len_mean": Lmid},
         "step_hbm_gbs": sum(attn_decode_bytes(k, T, Lmid) for k in prof) / (ms_per_step / 1e3) / 1e9,
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": by / avg_s / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": by / avg_s / PEAK_HBM, "traffic": None,
+                     "unit": "GB/s", "frac": by / avg_s / PEAK_HBM, "traffic": traffic,
                      "algorithmic_bytes_per_launch": by, "avg_launch_ms": avg_s * 1e3},
         "kernels_ms": {k: round(t / n, 5) for k, (n, t) in prof.items()},
         "wall_s": wall,
