@@ -37,7 +37,6 @@
 namespace hy {
 
 typedef float v16f_t __attribute__((ext_vector_type(16)));
-typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v16f_t mfma_f32(float a, float b, v16f_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);

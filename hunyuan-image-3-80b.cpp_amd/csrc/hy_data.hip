@@ -54,8 +54,8 @@ __global__ void synth_matrix_kernel(int wtype, uint64_t key, float scale, int ro
     for (int j = 0; j < QK; j++) v[j] = synth_normal(key, (uint64_t)r * cols + (uint64_t)b * QK + j, scale);
     uint8_t* dq = qs + il_q_offset(pr, b, nb, block_bytes(wtype));
     if (wtype == HY_TYPE_F32) {
-        float* dst = reinterpret_cast<float*>(dq);
-        for (int j = 0; j < QK; j++) dst[j] = v[j];
+        float* dst = reinterpret_cast<float*>(qs);
+        for (int j = 0; j < QK; j++) dst[il_f32_offset(pr, b, nb, j)] = v[j];
     } else if (wtype == HY_TYPE_Q8_0) {
         quant_block_q8_0(v, reinterpret_cast<int8_t*>(dq), sc + il_s_offset(pr, b, nb));
     } else {
@@ -94,8 +94,8 @@ __global__ void repack_kernel(int wtype, const uint8_t* __restrict__ src, int ro
     uint8_t* dq = qs + il_q_offset(pr, b, nb, block_bytes(wtype));
     if (wtype == HY_TYPE_F32) {
         const float* s = reinterpret_cast<const float*>(src) + (size_t)r * cols + (size_t)b * QK;
-        float* d = reinterpret_cast<float*>(dq);
-        for (int j = 0; j < QK; j++) d[j] = s[j];
+        float* d = reinterpret_cast<float*>(qs);
+        for (int j = 0; j < QK; j++) d[il_f32_offset(pr, b, nb, j)] = s[j];
     } else if (wtype == HY_TYPE_Q8_0) {
         const uint8_t* blk = src + ((size_t)r * nb + b) * 34;
         sc[il_s_offset(pr, b, nb)] = (uint16_t)(blk[0] | (blk[1] << 8));

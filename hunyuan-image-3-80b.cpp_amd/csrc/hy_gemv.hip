@@ -140,13 +140,17 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     for (int i = 0; i < NT; i++) acc[i] = 0.0f;
 
     if (WT == HY_TYPE_F32) {
+        // quad-major blocks: quad c of this lane's row at c * 256 + 4 lane floats; the
+        // next block's 8 loads are in flight while this block is consumed
         const float* wbase = reinterpret_cast<const float*>(a.W.qs + (size_t)e * a.W.qs_stride) +
-                             ((size_t)G * nb * 64 + lane) * QK;
-        for (int b = 0; b < nb; b++) {
-            const float4* wv = reinterpret_cast<const float4*>(wbase + (size_t)b * 64 * QK);
-            float4 w[8];
+                             (size_t)G * nb * 64 * QK + 4 * lane;
+        v4f_t w[2][8];
+        auto load = [&](int set, int b) {
+            const float* p = wbase + (size_t)min(b, nb - 1) * 64 * QK;  // in bounds
 #pragma unroll
-            for (int c = 0; c < 8; c++) w[c] = wv[c];
+            for (int c = 0; c < 8; c++) w[set][c] = *reinterpret_cast<const v4f_t*>(p + c * 256);
+        };
+        auto consume = [&](int set, int b) {
 #pragma unroll
             for (int i = 0; i < NT; i++) {
                 if (i < n) {
@@ -156,14 +160,22 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 #pragma unroll
                     for (int c = 0; c < 8; c++) {
                         const float4 xx = xv[c];
-                        s = fmaf(w[c].x, xx.x, s);
-                        s = fmaf(w[c].y, xx.y, s);
-                        s = fmaf(w[c].z, xx.z, s);
-                        s = fmaf(w[c].w, xx.w, s);
+                        s = fmaf(w[set][c][0], xx.x, s);
+                        s = fmaf(w[set][c][1], xx.y, s);
+                        s = fmaf(w[set][c][2], xx.z, s);
+                        s = fmaf(w[set][c][3], xx.w, s);
                     }
                     acc[i] = s;
                 }
             }
+        };
+        load(0, 0);
+        for (int b = 0; b < nb; b += 2) {
+            load(1, b + 1);
+            consume(0, b);
+            if (b + 1 >= nb) break;
+            load(0, b + 2);
+            consume(1, b + 1);
         }
     } else {
         constexpr int BPB = WT == HY_TYPE_Q8_0 ? 32 : 16;

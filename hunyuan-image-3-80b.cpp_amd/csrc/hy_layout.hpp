@@ -9,6 +9,9 @@
 //   scale plane: [E+1][rows/64][cols/32][64 rows] fp16 (none for F32)
 // A wave whose lane l owns row l of a group reads one contiguous 64*bpb chunk per
 // block (the decode GEMV), and an MFMA row block stages 64-row x block chunks.
+// F32 blocks (8 KB) are stored quad-major inside: floats 4q..4q+3 of the 64 rows
+// form 1 KB, [8 quads][64 rows][4 floats], so each 16-byte load of the wave (lane =
+// row, one quad) reads 1 KB contiguous.
 // gate_up rows are packed so each 64-row group holds 32 SiLU rows then the
 // matching 32 linear rows: packed row 64g+r is gate row 32g+r for r < 32 and up
 // row I+32g+(r-32) for r >= 32.  Down rows keep their natural order.
@@ -37,6 +40,10 @@ __host__ __device__ inline int gu_packed_row(int orig, int I) {
 // byte offset of block b of row r in an interleaved quant plane (bpb bytes per block)
 __host__ __device__ inline size_t il_q_offset(int r, int b, int nb, int bpb) {
     return (((size_t)(r / 64) * nb + b) * 64 + (r % 64)) * (size_t)bpb;
+}
+// float offset of element j (0..31) of block b of row r in an F32 plane
+__host__ __device__ inline size_t il_f32_offset(int r, int b, int nb, int j) {
+    return ((size_t)(r / 64) * nb + b) * 64 * 32 + (size_t)(j / 4) * 256 + (r % 64) * 4 + j % 4;
 }
 // element offset of the scale of block b of row r
 __host__ __device__ inline size_t il_s_offset(int r, int b, int nb) {

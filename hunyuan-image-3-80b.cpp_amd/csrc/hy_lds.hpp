@@ -7,6 +7,7 @@
 namespace hy {
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 // 16-byte global -> LDS copy (global_load_lds_dwordx4): lane i of the wave writes
 // lds_wave_base + 16*i.  The wave's loads are tracked by vmcnt, not by barriers.
