@@ -129,6 +129,23 @@ def test_cached_decode_waves(gpu, shp, waves):
     m.close()
 
 
+def test_cached_decode_full_head_shape(gpu):
+    """Decode at HunyuanImage-3's head shape (32 query / 8 kv heads of 128; hidden 256
+    keeps the oracle's projections short): 1, 4, 5 and 8 new tokens (both decode tiles)
+    against 520 cached positions, each kv group's keys over many waves."""
+    shp = dict(H=256, nh=32, nkv=8, hd=128)
+    m, w = _ctx(gpu, shp, max_tokens=520, max_cache=560, seed=9)
+    cache = A.KVCache(shp["nkv"], shp["hd"], max_len=560)
+    rng = np.random.default_rng(9)
+    for n in (520, 1, 4, 5, 8):
+        x = rng.standard_normal((n, shp["H"])).astype(np.float32)
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((n, shp["H"]))
+        m.forward_cached(xb, n, ob)
+        ref = A.attention_cached(w, x, cache)
+        check(ob.numpy(), ref, f"cached +{n} at {cache.cur_len - n}")
+    m.close()
+
+
 def test_forward_is_causal(gpu):
     shp = SHAPES[0]
     m, _ = _ctx(gpu, shp)
