@@ -290,6 +290,8 @@ def attn_decode_main(a, hy):
         "kernels_ms": {k: round(t / n, 5) for k, (n, t) in prof.items()},
         "wall_s": wall,
     }
+    if not a.no_cpu:
+        res["cpu_baseline"] = attn_decode_cpu_baseline(w, L, T)
     print(json.dumps(res), flush=True)
     m.close()
 
@@ -305,6 +307,28 @@ def attn_cpu_baseline(w, T_sample=192):
     return {"value": T_sample / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": f"one {T_sample}-token causal sequence through the oracle's attention_forward_cpu "
                       f"restatement (scalar fp32, 1 thread), {dt:.1f} s"}
+
+
+def attn_decode_cpu_baseline(w, L, T, n_steps=150):
+    """The KV-cache branch restated (the oracle, one thread): n_steps calls of T new
+    tokens against a cache of L positions.  The cache rows are filled with N(0, 1)
+    values directly, since prefilling L positions through the oracle would take
+    minutes; the work per decode call (projections, attention over the whole cache,
+    o_proj) is the same."""
+    import hy_oracle_attn as A
+    rng = np.random.default_rng(7)
+    cache = A.KVCache(ATTN["nkv"], ATTN["hd"], max_len=L + T * n_steps)
+    cache.k[:, :L] = rng.standard_normal((ATTN["nkv"], L, ATTN["hd"])).astype(np.float32)
+    cache.v[:, :L] = rng.standard_normal((ATTN["nkv"], L, ATTN["hd"])).astype(np.float32)
+    cache.c.cur_len = L
+    x = rng.standard_normal((T, ATTN["H"])).astype(np.float32)
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        A.attention_cached(w, x, cache)
+    dt = time.perf_counter() - t0
+    return {"value": n_steps * T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n_steps} calls of {T} new token(s) against {L} cached positions (random cache rows) "
+                      f"through the oracle's KV-cache branch (scalar fp32, 1 thread), {dt:.1f} s"}
 
 
 def attn_main(a, hy):
