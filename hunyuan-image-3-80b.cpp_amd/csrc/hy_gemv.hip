@@ -288,9 +288,13 @@ constexpr int GQ_U = 8;       // blocks per step
 constexpr int GQ_WAVES = 1;   // one wave per work group: work groups spread over every CU
 constexpr int GQ_THREADS = GQ_WAVES * WAVE;
 
+// Ring depth: Q4_0 3 steps (31 KB of LDS, 5 waves a CU), Q8_0 2 (37 KB, 4 a CU); copies
+// in flight <= 36 < 64 (vmcnt).  A launch with more waves than the deeper ring leaves
+// resident takes 2 steps for Q4_0 (21 KB, 7 a CU): one round of waves instead of a
+// second, short one (T=2: 15 tiles x 96 row groups = 1,440 waves for 1,280 slots).
 template <int WT>
 struct GqSteps {
-    static constexpr int value = WT == HY_TYPE_Q4_0 ? 3 : 2;  // copies in flight <= 36 < 64 (vmcnt)
+    static constexpr int value = WT == HY_TYPE_Q4_0 ? 3 : 2;
 };
 
 template <int WT, int NT>
@@ -317,12 +321,11 @@ __device__ __forceinline__ void gemv_tail(F& step, int base) {
     }
 }
 
-template <int WT, int NT, int MODE>
+template <int WT, int NT, int MODE, int NSTEP>
 __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     static_assert(MODE == 0 || MODE == 1, "routed/shared products only (the combine runs separately)");
     using SL = GqSlot<WT, NT>;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
-    constexpr int NSTEP = GqSteps<WT>::value;
     constexpr int BPB = SL::BPB;
     constexpr int WBYTES = 64 * BPB;  // one block of a 64-row group
     extern __shared__ __align__(16) uint8_t ring[];
@@ -545,8 +548,8 @@ size_t gemv_smem(int wtype, int Kd) {
 
 // LDS of gemv_q_kernel: a ring of NSTEP steps
 template <int WT>
-static size_t gemv_q_smem() {
-    return (size_t)GqSteps<WT>::value * GqSlot<WT, GEMV_NT>::BYTES;
+static size_t gemv_q_smem(int nstep) {
+    return (size_t)nstep * GqSlot<WT, GEMV_NT>::BYTES;
 }
 
 template <int WT>
@@ -554,6 +557,9 @@ static bool gemv_q_fits(int Kd) {
     const int nb = Kd / QK;
     return nb % GQ_U == 0 && nb / GQ_U >= GqSteps<WT>::value;
 }
+
+// resident one-wave work groups per CU at this LDS footprint (160 KB of LDS a CU)
+static int gemv_q_slots(size_t smem) { return 256 * (int)((160u * 1024u) / smem); }
 
 template <int MODE>
 static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
@@ -564,19 +570,26 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     switch (wtype) {
     case HY_TYPE_Q8_0:
         if (MODE != 2 && gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
-            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, QM>), grid_q, dim3(GQ_THREADS),
-                               gemv_q_smem<HY_TYPE_Q8_0>(), s, a);
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, QM, 2>), grid_q, dim3(GQ_THREADS),
+                               gemv_q_smem<HY_TYPE_Q8_0>(2), s, a);
         else
             hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);
         break;
     case HY_TYPE_Q4_0:
-        if (MODE != 2 && gemv_q_fits<HY_TYPE_Q4_0>(a.Kd))
-            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM>), grid_q, dim3(GQ_THREADS),
-                               gemv_q_smem<HY_TYPE_Q4_0>(), s, a);
-        else
+        if (MODE != 2 && gemv_q_fits<HY_TYPE_Q4_0>(a.Kd)) {
+            // tiles is the host's bound on the routed + shared tiles: the deeper ring
+            // when every launched wave is resident at once
+            if ((long)tiles * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3)))
+                hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM, 3>), grid_q, dim3(GQ_THREADS),
+                                   gemv_q_smem<HY_TYPE_Q4_0>(3), s, a);
+            else
+                hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM, 2>), grid_q, dim3(GQ_THREADS),
+                                   gemv_q_smem<HY_TYPE_Q4_0>(2), s, a);
+        } else {
             hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);
+        }
         break;
     default:
         hipLaunchKernelGGL((gemv_kernel<HY_TYPE_F32, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
