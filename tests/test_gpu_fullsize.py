@@ -32,6 +32,8 @@ def ctxs(gpu, full_layers):
 
 @pytest.mark.parametrize("T", [1, 2, 4, 8])
 def test_decode_q4_0_full_shape(gpu, full_layers, ctxs, T):
+    """Bit-exact decode; T=1 runs the up GEMV with the 3-step ring (864 waves), T >= 2
+    with the 2-step ring (more waves than the 3-step ring keeps resident)."""
     x = O.synth(100 + T, 0, O.T_X, 0, (T, H), 1.0)
     out, lg, w, idx = ctxs[O.Q4_0].run(0, x, debug=True)
     ref, rlg, rw, ridx = O.moe_forward_q(full_layers[O.Q4_0], x, debug=True, nthreads=16)
