@@ -178,6 +178,12 @@ int tile_bound_routed(int T, int K, int E, int NT) {
     return b < pairs ? b : pairs;
 }
 
+// Renormalise the selected weights?  HY_NORM_TOPK follows topkgating_full
+// (src/hunyuan_moe_full.cpp:230: `norm_topk_prob && K > 1`, so one expert keeps
+// p * routed_scaling_factor); HY_NORM_ALWAYS follows topkgating_easy and
+// moe_forward_cpu (src/attention.cpp:268-275), which renormalise at every K.
+int renorm_rule(int32_t norm, uint32_t K) { return (norm == HY_NORM_ALWAYS || (norm != HY_NORM_OFF && K > 1)) ? 1 : 0; }
+
 // largest batch the decode GEMV takes in AUTO mode; above it the MFMA grouped GEMM
 constexpr uint32_t kGemvMaxTokens = 16;
 
@@ -249,6 +255,7 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int H = c->H, I = c->I, E = c->E, K = c->K, wt = c->cfg.wtype;
     const int iT = (int)T;
     const int has_shared = c->cfg.has_shared ? 1 : 0;
+    const int renorm = renorm_rule(c->cfg.norm_topk_prob, c->cfg.topk);
     // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode
     const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) &&
                       (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
@@ -257,7 +264,7 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     if (!mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
         // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
-            return hy::launch_route_decode(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob,
+            return hy::launch_route_decode(x, L.router, iT, H, E, K, renorm,
                                            c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi,
                                            prequant ? nullptr : c->xq, c->xd, c->xs, NT, has_shared, c->cnt, c->off, c->srt_tok, c->pair_pos,
                                            c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n, c->meta, s);
@@ -271,7 +278,7 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
                 return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
             }));
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
-            return hy::launch_router_q(x, L.router, iT, H, E, K, c->cfg.norm_topk_prob,
+            return hy::launch_router_q(x, L.router, iT, H, E, K, renorm,
                                        c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi,
                                        fuse_quant ? c->xq : nullptr, c->xd, c->xs, s);
         }));
@@ -619,7 +626,7 @@ int hy_router_topk(const float* x, const float* wr, uint32_t T, uint32_t H, uint
     if (!x || !wr || !lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
     if (T == 0 || H == 0 || H % 4 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
         return fail(HY_ERR_INVALID, "bad router shape T=%u H=%u E=%u K=%u", T, H, E, K);
-    HIP_TRY(hy::launch_router(x, wr, (int)T, (int)H, (int)E, (int)K, norm, scale, lg, w, idx,
+    HIP_TRY(hy::launch_router(x, wr, (int)T, (int)H, (int)E, (int)K, renorm_rule(norm, K), scale, lg, w, idx,
                               static_cast<hipStream_t>(stream)));
     return HY_OK;
 }
@@ -628,6 +635,7 @@ int hy_topkgating_easy(const float* lg, uint32_t T, uint32_t E, uint32_t K, floa
     if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
     if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
         return fail(HY_ERR_INVALID, "bad gating shape");
+    // topkgating_easy renormalises at every K (src/hunyuan_moe_full.cpp:104-108)
     HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, 1, 1.0f, w, idx, static_cast<hipStream_t>(stream)));
     return HY_OK;
 }
@@ -637,7 +645,7 @@ int hy_route_logits(const float* lg, uint32_t T, uint32_t E, uint32_t K, int32_t
     if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
     if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
         return fail(HY_ERR_INVALID, "bad routing shape");
-    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, norm, scale, w, idx,
+    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, renorm_rule(norm, K), scale, w, idx,
                                         static_cast<hipStream_t>(stream)));
     return HY_OK;
 }

@@ -54,7 +54,10 @@ hy_moe_config layer_config(uint32_t H, uint32_t I, uint32_t E, uint32_t K, uint3
     c.max_tokens = std::max<uint32_t>(1, std::min<uint32_t>(T, 16384));
     c.wtype = wtype;
     c.has_shared = shared ? 1 : 0;
-    c.norm_topk_prob = rc ? (rc->norm_topk_prob ? 1 : 0) : 1;
+    // with a MoERoutingConfig: topkgating_full's rule (renormalise only when K > 1,
+    // src/hunyuan_moe_full.cpp:230); without one (moe_forward_cpu, swiglu_ffn_f32):
+    // renormalise at every K as src/attention.cpp:268-275 does
+    c.norm_topk_prob = rc ? (rc->norm_topk_prob ? HY_NORM_TOPK : HY_NORM_OFF) : HY_NORM_ALWAYS;
     c.routed_scaling_factor = rc ? rc->routed_scaling_factor : 1.0f;
     c.device = 0;
     return c;
@@ -152,7 +155,7 @@ void topkgating_full(const float* logits, uint32_t T, const MoERoutingConfig& cf
         off((size_t)(E + 1) * 4), pos(pairs * 4);
     l.up(logits, (size_t)T * E * 4);
     p.up(logits, (size_t)T * E * 4);
-    check(hy_route_logits(l.as<float>(), T, E, K, cfg.norm_topk_prob ? 1 : 0, cfg.routed_scaling_factor,
+    check(hy_route_logits(l.as<float>(), T, E, K, cfg.norm_topk_prob ? HY_NORM_TOPK : HY_NORM_OFF, cfg.routed_scaling_factor,
                           wd.as<float>(), id.as<int32_t>(), nullptr));
     check(hy_dispatch_pairs(id.as<int32_t>(), wd.as<float>(), T, K, E, cnt.as<int32_t>(), off.as<int32_t>(),
                             pos.as<int32_t>(), nullptr));

@@ -264,6 +264,9 @@ class Moe:
 
     def __init__(self, H, I, E, K, wtype, num_layers=1, max_tokens=64, has_shared=True, norm_topk_prob=True,
                  routed_scaling_factor=1.0, device=0, **unsupported):
+        extra = set(unsupported) - {"group_limited_greedy", "drop_tokens", "compute_aux_loss"}
+        if extra:
+            raise TypeError(f"Moe: unknown arguments {sorted(extra)}")
         c = Config()
         c.hidden, c.intermediate, c.num_experts, c.topk = H, I, E, K
         c.num_layers, c.max_tokens, c.wtype = num_layers, max_tokens, wtype

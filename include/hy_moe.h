@@ -35,6 +35,15 @@ typedef enum {
 /* ggml_type values accepted as weight formats (ggml.h numbering). */
 enum { HY_TYPE_F32 = 0, HY_TYPE_Q4_0 = 2, HY_TYPE_Q8_0 = 8 };
 
+/* Values of norm_topk_prob (config field and routing calls).
+ *   HY_NORM_OFF    w_k = p_k * routed_scaling_factor
+ *   HY_NORM_TOPK   w_k = p_k / max(sum_k p_k, 1e-8) when K > 1, else p * routed_scaling_factor:
+ *                  topkgating_full, src/hunyuan_moe_full.cpp:230 (`norm_topk_prob && K > 1`),
+ *                  the rule moe_forward_full routes with.  Any other nonzero value means this.
+ *   HY_NORM_ALWAYS renormalise at every K: topkgating_easy (src/hunyuan_moe_full.cpp:104-108)
+ *                  and moe_forward_cpu (src/attention.cpp:268-275); one expert gets weight 1. */
+enum { HY_NORM_OFF = 0, HY_NORM_TOPK = 1, HY_NORM_ALWAYS = 2 };
+
 /* Shapes and routing of one resident MoE stack.  The routing fields mirror
  * MoERoutingConfig (src/hunyuan_moe_full.h:25-47); the GPU runs the default
  * subset (softmax -> top-k -> renormalise or scale), and hy_moe_create rejects
@@ -48,7 +57,7 @@ typedef struct {
     uint32_t max_tokens;    /* largest T per call, 1..16384; sizes the work arena */
     int32_t  wtype;         /* HY_TYPE_F32 / HY_TYPE_Q8_0 / HY_TYPE_Q4_0 */
     int32_t  has_shared;    /* 1: one shared expert (num_shared_expert = 1) */
-    int32_t  norm_topk_prob;
+    int32_t  norm_topk_prob;       /* HY_NORM_*: moe_forward_full routes with HY_NORM_TOPK */
     float    routed_scaling_factor;
     int32_t  group_limited_greedy; /* must be 0 */
     int32_t  drop_tokens;          /* must be 0 */
@@ -174,7 +183,8 @@ int hy_moe_set_path(hy_moe_ctx* ctx, int32_t path);
  * index winning ties, weights = softmax at the selection renormalised (or scaled).
  * logits_dev [T][E] is required (it is the intermediate of the two passes).
  * Replaces the router GEMV of src/hunyuan_moe_full.cpp:414-423 plus
- * topkgating_easy (src/hunyuan_moe_full.h:83-89). */
+ * topkgating_easy (src/hunyuan_moe_full.h:83-89).  norm_topk_prob is a HY_NORM_* value
+ * (topkgating_easy itself is HY_NORM_ALWAYS). */
 int hy_router_topk(const float* x_dev, const float* wr_dev, uint32_t T, uint32_t H, uint32_t E,
                    uint32_t K, int32_t norm_topk_prob, float routed_scaling_factor,
                    float* logits_dev, float* weights_dev, int32_t* indices_dev, void* stream);
@@ -184,8 +194,8 @@ int hy_topkgating_easy(const float* logits_dev, uint32_t T, uint32_t E, uint32_t
                        float* weights_dev, int32_t* indices_dev, void* stream);
 
 /* Top-k selection and weights from precomputed logits with the routing options of
- * topkgating_full (src/hunyuan_moe_full.cpp:229-243): renormalise when norm_topk_prob,
- * else scale by routed_scaling_factor. */
+ * topkgating_full (src/hunyuan_moe_full.cpp:229-243): norm_topk_prob is a HY_NORM_*
+ * value (HY_NORM_TOPK: renormalise when K > 1, else scale by routed_scaling_factor). */
 int hy_route_logits(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K, int32_t norm_topk_prob,
                     float routed_scaling_factor, float* weights_dev, int32_t* indices_dev, void* stream);
 

@@ -813,7 +813,11 @@ static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, floa
         ps += p[k];
     }
     if (ps < 1e-8f) ps = 1e-8f;
-    for (uint32_t k = 0; k < K; k++) w[k] = norm ? p[k] / ps : p[k] * scale;
+    /* norm 1 renormalises only when K > 1 (src/hunyuan_moe_full.cpp:230, the rule of
+     * topkgating_full and so of moe_forward_full); norm 2 at every K
+     * (src/attention.cpp:268-275, moe_forward_cpu; topkgating_easy :104-108) */
+    const int rn = norm == 2 || (norm != 0 && K > 1);
+    for (uint32_t k = 0; k < K; k++) w[k] = rn ? p[k] / ps : p[k] * scale;
 }
 
 void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm,

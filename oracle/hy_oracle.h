@@ -146,8 +146,10 @@ float hyo_expf(float x);
 void hyo_router_logits_blocked(const float* x, const float* wr, uint32_t T, uint32_t H,
                                uint32_t E, float* logits);
 /* top-K on logits, descending, equal logits keep the lower expert index; weights are
- * softmax(logits) at the selected experts renormalised by max(sum, 1e-8) when norm,
- * else multiplied by scale. */
+ * softmax(logits) at the selected experts renormalised by max(sum, 1e-8), else
+ * multiplied by scale.  norm 1 renormalises only when K > 1 (topkgating_full,
+ * src/hunyuan_moe_full.cpp:230), norm 2 at every K (moe_forward_cpu,
+ * src/attention.cpp:268-275), norm 0 never. */
 void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm,
                     float scale, float* w, int32_t* idx);
 
@@ -157,7 +159,7 @@ void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int
 typedef struct {
     uint32_t H, I, E, K;
     int      wtype;
-    int      norm_topk_prob;
+    int      norm_topk_prob;  /* 0, 1 or 2 as hyo_route_topk's norm */
     float    routed_scaling_factor;
     const float* router;      /* [E,H] f32 */
     const void*  shared_gu;

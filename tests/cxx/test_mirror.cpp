@@ -200,6 +200,86 @@ int main() {
                "moe_forward_cpu debug router outputs");
         report(rel_err(out.data(), ref.data(), out.size()) < 1e-4, "moe_forward_cpu", errs(out.data(), ref.data(), out.size()));
     }
+    // ---------------------------------------------------------------- one expert per token (K = 1)
+    // topkgating_full keeps p * routed_scaling_factor (src/hunyuan_moe_full.cpp:230 `norm_topk_prob
+    // && K > 1`), so moe_forward_full does too; topkgating_easy and moe_forward_cpu renormalise to 1.
+    for (float scale : {1.0f, 2.5f}) {
+        MoERoutingConfig c1;
+        c1.num_experts = E;
+        c1.moe_topk = 1;
+        c1.routed_scaling_factor = scale;
+        MoEGateOutput g;
+        topkgating_full(lg.data(), T, c1, g);
+        hyo_routing_cfg rc;
+        hyo_routing_cfg_default(&rc);
+        rc.num_experts = E;
+        rc.moe_topk = 1;
+        rc.routed_scaling_factor = scale;
+        hyo_gate_full ref;
+        hyo_topkgating_full(lg.data(), T, &rc, &ref);
+        const size_t n = (size_t)T * E * ref.capacity;
+        bool ok = g.expert_capacity == ref.capacity && memcmp(g.exp_counts, ref.exp_counts, E * 4) == 0;
+        for (size_t i = 0; ok && i < n; i++) ok = (g.dispatch_mask[i] ? 1 : 0) == ref.dispatch_mask[i];
+        report(ok && rel_err(g.combine_weights, ref.combine_weights, n) < 2e-6,
+               scale == 1.0f ? "topkgating_full K=1 keeps p (no renormalisation)"
+                             : "topkgating_full K=1 keeps p * routed_scaling_factor",
+               "cw " + errs(g.combine_weights, ref.combine_weights, n));
+        hyo_gate_full_free(&ref);
+    }
+    {
+        std::vector<float> w(T), wr(T);
+        std::vector<int32_t> i(T), ir(T);
+        topkgating_easy(lg.data(), T, E, 1, w.data(), i.data());
+        hyo_topkgating_easy(lg.data(), T, E, 1, wr.data(), ir.data());
+        bool ones = true;
+        for (float v : w) ones = ones && v == 1.0f;
+        report(i == ir && ones && bits_equal(w.data(), wr.data(), T), "topkgating_easy K=1 weights are exactly 1");
+    }
+    {
+        MoERoutingConfig c1;
+        c1.num_experts = Ex;
+        c1.moe_topk = 1;
+        c1.routed_scaling_factor = 1.5f;
+        std::vector<float> out((size_t)Tl * H), ref(out.size()), q(out.size());
+        moe_forward_full(x.data(), Tl, H, wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data(), Ex, I, c1,
+                         out.data());
+        hyo_routing_cfg rc;
+        hyo_routing_cfg_default(&rc);
+        rc.num_experts = Ex;
+        rc.moe_topk = 1;
+        rc.routed_scaling_factor = 1.5f;
+        hyo_moe_forward_full(x.data(), Tl, H, wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data(), Ex, I, &rc,
+                             ref.data());
+        hyo_qlayer L{H, I, Ex, 1, HYO_F32, 1, 1.5f, wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data()};
+        hyo_moe_forward_q(&L, x.data(), Tl, q.data(), nullptr, nullptr, nullptr, 1);
+        report(bits_equal(out.data(), q.data(), out.size()) && rel_err(out.data(), ref.data(), out.size()) < 1e-4,
+               "moe_forward_full K=1 (p * scale) vs reference semantics", errs(out.data(), ref.data(), out.size()));
+
+        MoEWeights w;
+        w.num_experts = Ex;
+        w.router_weight = wr;
+        w.shared_gate_up = sgu;
+        w.shared_down = sdn;
+        w.experts.resize(Ex);
+        for (uint32_t e = 0; e < Ex; e++) {
+            w.experts[e].gate_up.assign(gu.begin() + (size_t)e * 2 * I * H, gu.begin() + (size_t)(e + 1) * 2 * I * H);
+            w.experts[e].down.assign(dn.begin() + (size_t)e * H * I, dn.begin() + (size_t)(e + 1) * H * I);
+        }
+        HunyuanConfig cfg;
+        cfg.hidden_size = H;
+        cfg.moe_intermediate_size = I;
+        cfg.moe_topk = 1;
+        std::vector<float> oc(out.size()), rcpu(out.size()), dw(Tl), dwr(Tl);
+        std::vector<int32_t> di(Tl), dir(Tl);
+        moe_forward_cpu(x.data(), w, Tl, cfg, oc.data(), nullptr, dw.data(), di.data());
+        hyo_moe_forward_cpu(x.data(), wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data(), Tl, H, Ex, I, 1,
+                            rcpu.data(), nullptr, dwr.data(), dir.data());
+        bool ones = true;
+        for (float v : dw) ones = ones && v == 1.0f;
+        report(di == dir && ones && bits_equal(dw.data(), dwr.data(), Tl) &&
+                   rel_err(oc.data(), rcpu.data(), oc.size()) < 1e-4,
+               "moe_forward_cpu K=1 renormalises to weight 1", errs(oc.data(), rcpu.data(), oc.size()));
+    }
     {
         std::vector<float> w = synth(7, 0, 0, H, 1.0f), out((size_t)Tl * H), ref(out.size());
         rms_norm_f32(x.data(), w.data(), out.data(), Tl, H, 1e-5f);

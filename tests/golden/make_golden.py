@@ -41,6 +41,8 @@ MOE_CASES = [
     # name, T, H, I, E, K, seed
     ("a", 5, 64, 32, 8, 2, 7),
     ("b", 9, 128, 64, 16, 4, 8),
+    # K = 1: topkgating_full keeps p * routed_scaling_factor (no renormalisation)
+    ("c", 6, 64, 32, 8, 1, 9),
 ]
 
 
@@ -61,6 +63,11 @@ GATING_CASES = [
     ("group_t9_e16_k4", 9, 16, 4, dict(group_limited_greedy=1, n_group=4, topk_group=2)),
     ("nonorm_t6_e8_k2", 6, 8, 2, dict(norm_topk_prob=0, routed_scaling_factor=2.5)),
     ("aux_t12_e8_k3", 12, 8, 3, dict(compute_aux_loss=1)),
+    # K = 1: easy gating renormalises (weight 1), full gating keeps p * scale
+    # (src/hunyuan_moe_full.cpp:230 `norm_topk_prob && K > 1`)
+    ("default_t11_e16_k1", 11, 16, 1, {}),
+    ("scaled_t7_e8_k1", 7, 8, 1, dict(routed_scaling_factor=2.5)),
+    ("nonorm_t5_e64_k1", 5, 64, 1, dict(norm_topk_prob=0, routed_scaling_factor=0.75)),
 ]
 
 

@@ -117,6 +117,46 @@ def test_router_scaling_without_norm(gpu):
     np.testing.assert_array_equal(w.view(np.uint32), ref_w.view(np.uint32))
 
 
+@pytest.mark.parametrize("norm", [0, 1, 2])
+def test_router_single_expert_rules(gpu, norm):
+    """K = 1: rule 1 (topkgating_full's `norm_topk_prob && K > 1`) keeps p * scale,
+    rule 2 (moe_forward_cpu) gives exactly 1, rule 0 scales."""
+    T, H, E = 21, 256, 16
+    x = O.synth(5, 0, O.T_X, 0, (T, H), 1.0)
+    wr = O.synth(5, 0, O.T_ROUTER, 0, (E, H), 0.1)
+    lg, w, idx = gpu.router_topk(x, wr, 1, norm=norm, scale=2.5)
+    ref_w, ref_idx = O.route_topk(O.router_logits_blocked(x, wr), 1, norm=norm, scale=2.5)
+    np.testing.assert_array_equal(idx, ref_idx)
+    np.testing.assert_array_equal(w.view(np.uint32), ref_w.view(np.uint32))
+    if norm == 2:
+        assert np.all(w == 1.0)
+    else:
+        assert np.all(w < 2.5) and np.all(w > 0)
+    ew, eidx = gpu.topkgating_easy(lg, 1)
+    np.testing.assert_array_equal(eidx, ref_idx)
+    assert np.all(ew == 1.0)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+@pytest.mark.parametrize("T", [1, 5, 40, 300])
+def test_layer_single_expert(gpu, wtype, T):
+    """A layer with K = 1 routes with p * routed_scaling_factor (moe_forward_full's
+    rule) on the decode and the grouped-GEMM paths."""
+    H, I, E = 256, 128, 16
+    layer = O.synth_layer(H, I, E, 1, wtype, seed=13, std=0.05)
+    layer.routed_scaling_factor = 1.5
+    m = gpu.Moe(H, I, E, 1, wtype, max_tokens=512, routed_scaling_factor=1.5)
+    m.upload(0, layer)
+    x = O.synth(70 + T, 0, O.T_X, 0, (T, H), 1.0)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+    assert np.all(w < 1.5)
+    assert_exact(out, ref, f"K=1 wtype={wtype} T={T}")
+    m.close()
+
+
 def test_topkgating_easy_from_logits(gpu):
     """topkgating_easy (reference semantics: glibc expf, sequential softmax sum): the
     GPU selects on logits, so indices match exactly and weights to float rounding."""

@@ -298,6 +298,37 @@ def test_route_topk_known_answers():
         np.testing.assert_allclose(w[0], p[order] / p[order].sum(), rtol=2e-6)
 
 
+def test_route_topk_single_expert_rules():
+    """K = 1.  Rule 1 (topkgating_full, src/hunyuan_moe_full.cpp:230: `norm_topk_prob &&
+    K > 1`) keeps the softmax probability times the scale; rule 2 (moe_forward_cpu,
+    src/attention.cpp:268-275) renormalises it to exactly 1; rule 0 scales.  The
+    probabilities are checked against float64 softmax, the index against argmax with
+    the lower index winning ties."""
+    rng = np.random.default_rng(11)
+    for E in (1, 8, 64):
+        lg = (rng.standard_normal((40, E)) * 1.5).astype(np.float32)
+        lg[:5] = np.round(lg[:5])               # ties for the top slot
+        order = np.argmax(lg, axis=1)          # first (lowest) index of the maximum
+        p = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True))
+        p = p[np.arange(40), order] / p.sum(axis=1)
+        for scale in (1.0, 2.5):
+            w1, i1 = O.route_topk(lg, 1, norm=1, scale=scale)
+            w0, i0 = O.route_topk(lg, 1, norm=0, scale=scale)
+            np.testing.assert_array_equal(i1[:, 0], order)
+            np.testing.assert_array_equal(i0, i1)
+            np.testing.assert_array_equal(w1.view(np.uint32), w0.view(np.uint32))
+            np.testing.assert_allclose(w1[:, 0], scale * p, rtol=2e-6)
+        w2, i2 = O.route_topk(lg, 1, norm=2, scale=2.5)
+        np.testing.assert_array_equal(i2[:, 0], order)
+        assert np.all(w2 == 1.0)
+    # K > 1: rules 1 and 2 agree
+    lg = (rng.standard_normal((20, 16)) * 1.5).astype(np.float32)
+    a = O.route_topk(lg, 4, norm=1)
+    b = O.route_topk(lg, 4, norm=2)
+    np.testing.assert_array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
+    np.testing.assert_array_equal(a[1], b[1])
+
+
 # ------------------------------------------------------------------ SwiGLU / RMSNorm
 
 def test_swiglu_closed_form():

@@ -74,6 +74,32 @@ def test_golden_routing(oracle):
     assert n_checked == 2 * len(mg.GATING_CASES)
 
 
+def test_golden_single_expert_q_semantics(oracle):
+    """K = 1 fixtures: the q-semantics router (the GPU's rule) selects the reference's
+    expert and, under rule 1, gives the reference topkgating_full's weight p * scale
+    to float rounding (the reference sums the softmax sequentially, the q-semantics
+    router in a 64-lane tree); topkgating_easy's weight is exactly 1 under rule 2."""
+    mg = _cases()
+    data = np.load(os.path.join(GOLD, "ref_routing.npz"))
+    cases = [c for c in mg.GATING_CASES if c[3] == 1]
+    assert len(cases) >= 3
+    for name, T, E, K, kw in cases:
+        cfg = O.default_cfg(E, K, **kw)
+        for kind in ("gauss", "ties"):
+            key = f"{name}_{kind}"
+            lg = data[f"{key}/logits"]
+            norm = 1 if cfg.norm_topk_prob else 0
+            w, idx = O.route_topk(lg, 1, norm=norm, scale=cfg.routed_scaling_factor)
+            mask, cw = data[f"{key}/full_mask"], data[f"{key}/full_cw"]
+            e_ref = mask.any(axis=2).argmax(axis=1)
+            np.testing.assert_array_equal(idx[:, 0], e_ref, err_msg=key)
+            w_ref = cw.sum(axis=2)[np.arange(T), e_ref]
+            np.testing.assert_allclose(w[:, 0], w_ref, rtol=2e-6, err_msg=key)
+            w2, _ = O.route_topk(lg, 1, norm=2)
+            np.testing.assert_array_equal(w2.view(np.uint32), data[f"{key}/easy_w"].view(np.uint32))
+            np.testing.assert_array_equal(data[f"{key}/easy_idx"][:, 0], e_ref)
+
+
 def test_golden_test_components(oracle):
     """The reference's own component-test inputs (src/test_components.cpp:88-115)."""
     d = np.load(os.path.join(GOLD, "ref_test_components.npz"))
@@ -165,7 +191,7 @@ def test_live_topk_all_k(refimpl):
                 np.testing.assert_array_equal(v, v_r)
 
 
-@pytest.mark.parametrize("dims", [(3, 64, 32, 8, 2), (16, 96, 64, 16, 4), (12, 64, 32, 64, 8)])
+@pytest.mark.parametrize("dims", [(3, 64, 32, 8, 2), (16, 96, 64, 16, 4), (12, 64, 32, 64, 8), (7, 64, 32, 16, 1)])
 def test_live_moe_forward_full_vs_reference(refimpl, dims):
     T, H, I, E, K = dims
     seed = 11 + T
