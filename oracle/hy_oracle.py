@@ -264,12 +264,25 @@ def synth_layer(H, I, E, K, wtype, seed=42, layer=0, std=0.02, router_bias=None,
     if router_bias is not None:
         router[:, 0] = np.asarray(router_bias, dtype=np.float32)
 
-    def mk(tensor, expert, rows, cols):
-        w = synth(seed, layer, tensor, expert, (rows, cols), std)
-        return w if wtype == F32 else quantize(w, wtype)
+    def mk(tensor, expert, rows, cols, out=None):
+        if wtype == F32:   # generated in place: a real-shape F32 layer is ~10 GB
+            w = np.empty((rows, cols), np.float32) if out is None else out
+            lib().hyo_synth_fill(lib().hyo_stream_key(seed, layer, tensor, expert), 0, w.size, std, fp(w))
+            return w
+        w = quantize(synth(seed, layer, tensor, expert, (rows, cols), std), wtype)
+        if out is not None:
+            out[...] = w
+        return w
 
-    gu = np.stack([mk(T_GU, e, 2 * I, H) for e in range(E)])
-    dn = np.stack([mk(T_DN, e, H, I) for e in range(E)])
+    def stacked(tensor, rows, cols):
+        a = np.empty((E, rows, row_bytes(wtype, cols) // (4 if wtype == F32 else 1)),
+                     np.float32 if wtype == F32 else np.uint8)
+        for e in range(E):
+            mk(tensor, e, rows, cols, out=a[e])
+        return a
+
+    gu = stacked(T_GU, 2 * I, H)
+    dn = stacked(T_DN, H, I)
     sgu = mk(T_GU, E, 2 * I, H) if shared else None
     sdn = mk(T_DN, E, H, I) if shared else None
     return Layer(H, I, E, K, wtype, router, sgu, sdn, gu, dn)

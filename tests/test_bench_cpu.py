@@ -11,6 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
 
 import bench  # noqa: E402
+import hy_oracle as O  # noqa: E402
 import hy_oracle_attn as A  # noqa: E402
 
 
@@ -53,3 +54,26 @@ def test_traffic_table_lookup():
     assert bench.measured_traffic("no_such_workload", "ffn_up", path) is None
     assert bench.measured_traffic("x", "y", path=os.path.join(ROOT, "no_such_file.md")) is None
     assert np.isfinite(got)
+
+
+def zipf_routing_counts(T=4096, seed=42):
+    """Pairs per expert of the skewed T=4096 workload, routed by the oracle's router
+    (the GPU's logits order, so the GPU routes these inputs identically)."""
+    x = O.synth(seed + 1000, 0, O.T_X, 0, (T, bench.H), 1.0)
+    x[:, 0] = 1.0
+    wr = O.synth(seed, 0, O.T_ROUTER, 0, (bench.E, bench.H), 0.02)
+    wr[:, 0] = bench.zipf_bias(seed)
+    _, idx = O.route_topk(O.router_logits_blocked(x, wr), bench.K)
+    return np.bincount(idx.ravel(), minlength=bench.E)
+
+
+def test_zipf_workload_is_calibrated():
+    """The Zipf(1.1) bias puts 63 % of the pairs on the eight most popular experts (the
+    top-8 mass of Zipf(1.1) over 64 experts) and one expert on nearly every token."""
+    p = np.arange(1, 65, dtype=np.float64) ** -1.1
+    assert abs(p[:8].sum() / p.sum() - 0.63) < 0.005
+    cnt = np.sort(zipf_routing_counts())[::-1]
+    assert cnt.sum() == 4096 * bench.K
+    share8 = cnt[:8].sum() / cnt.sum()
+    assert 0.625 <= share8 <= 0.635, share8
+    assert cnt[0] > 3900 and cnt[-1] < 100
