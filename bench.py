@@ -38,6 +38,11 @@ H, I, E, K = 4096, 3072, 64, 8
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_INT8 = 5.0e15         # ops/s, dense int8 MFMA
 PEAK_FP32_MFMA = 157.3e12  # FLOP/s, dense fp32 MFMA
+# Ceiling of a grouped int8 GEMM that keeps ggml's per-block fp32 rescale: every 32-MAC
+# block partial costs one int->float conversion and one fma on the vector ALUs, so the
+# rate is bounded by the VALU issue rate, not the matrix cores (measured with the
+# compute-only probe of the kernels' per-block instruction mix, bench.py --mfma-probe)
+RESCALE_CEILING = 1.62e15
 ATTN = dict(H=4096, nh=32, nkv=8, hd=128)   # HunyuanImage-3 attention shape
 PARAMS_PER_EXPERT = 3 * H * I
 BYTES = {0: 4.0, 8: 34.0 / 32.0, 2: 18.0 / 32.0}   # bytes per weight element
@@ -174,30 +179,6 @@ def gguf_load(hy, wtype, path, seed=42):
     os.remove(path)
     print(json.dumps({"probe": "gguf_load", "weights": {0: "F32", 2: "Q4_0", 8: "Q8_0"}[wtype], "file_bytes": size,
                       "seconds": dt, "GBps": size / dt / 1e9, "forward_bit_exact": same}), flush=True)
-
-
-def cpu_baseline(wl, seed, budget_s=15.0):
-    """The oracle's q-semantics layer (int8 block dots, OpenMP over all host
-    threads) on a bounded token sample of the same workload."""
-    import hy_oracle as O
-    nthreads = os.cpu_count() or 1
-    wtype = wl["wtype"]
-    layer = O.synth_layer(H, I, E, K, wtype, seed=seed, layer=0, std=0.02)
-    T = wl["T"]
-    x = O.synth(seed + 1000, 0, O.T_X, 0, (T, H), 1.0)
-    n = min(T, max(8, nthreads))
-    rows = np.arange(n) % T
-    t0 = time.perf_counter()
-    O.moe_forward_q_rows(layer, x, rows, nthreads=nthreads)
-    dt = time.perf_counter() - t0
-    n2 = int(min(T * 4, max(n, n * budget_s / max(dt, 1e-6))))
-    rows = np.arange(n2) % T
-    t0 = time.perf_counter()
-    O.moe_forward_q_rows(layer, x, rows, nthreads=nthreads)
-    dt = time.perf_counter() - t0
-    return {"value": n2 / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
-            "sample": f"{n2} tokens of the {wl['name']} workload through the oracle's int8 (ggml-semantics) "
-                      f"layer, {nthreads} OpenMP threads, {dt:.1f} s"}
 
 
 def attn_flops(kname, T):
@@ -468,14 +449,227 @@ def model_main(a, hy):
     m.close()
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def ref_cpu_baseline(wl, seed, budget_s=10.0):
+    """The reference's own arithmetic: moe_forward_full restated operation for operation
+    (scalar fp32, one thread, one sequential accumulator per dot product,
+    src/hunyuan_moe_full.cpp:405-516), on layer 0's weights dequantized to F32 as the
+    reference's loader does (src/hunyuan_gguf_loader.cpp:212-216), over a token sample."""
+    import ctypes as C
+    import hy_oracle as O
+    wtype, T = wl["wtype"], wl["T"]
+    layer = O.synth_layer(H, I, E, K, wtype, seed=seed, layer=0, std=0.02)
+
+    def f32(q, rows, cols):
+        return q if wtype == 0 else O.dequantize(q, wtype, cols).reshape(rows, cols)
+
+    gu = np.empty((E, 2 * I, H), np.float32)
+    dn = np.empty((E, H, I), np.float32)
+    for e in range(E):
+        gu[e] = f32(layer.gu[e], 2 * I, H)
+        dn[e] = f32(layer.dn[e], H, I)
+    sgu, sdn = f32(layer.shared_gu, 2 * I, H), f32(layer.shared_dn, H, I)
+    router = layer.router
+    del layer
+    x = O.synth(seed + 1000, 0, O.T_X, 0, (min(T, 64), H), 1.0)
+    cfg = O.default_cfg(E, K)
+
+    def run(n):
+        out = np.empty((n, H), np.float32)
+        t0 = time.perf_counter()
+        rc = O.lib().hyo_moe_forward_full(O.fp(x[:n].copy()), n, H, O.fp(router), O.fp(sgu), O.fp(sdn),
+                                          O.fp(gu), O.fp(dn), E, I, C.byref(cfg), O.fp(out))
+        assert rc == 0
+        return time.perf_counter() - t0
+
+    dt = run(1)
+    n = int(max(1, min(16, min(T, 64), budget_s / max(dt, 1e-3))))
+    if n > 1:
+        dt = run(n)
+    per_layer = n / dt
+    nl = wl["layers"]
+    return {"value": per_layer / nl, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "extrapolated": T > n or nl > 1,
+            "sample": f"{n} of the {T} tokens through one layer of reference arithmetic (moe_forward_full "
+                      f"restated: scalar fp32, 1 thread, weights dequantized to F32), {dt:.1f} s"
+                      + (f"; the per-layer rate divided by {nl} layers" if nl > 1 else "")}
+
+
+def cpu_baseline(wl, seed, budget_s=15.0):
+    """The oracle's q-semantics layer (the int8 block dots of ggml's CPU vec_dot, OpenMP
+    over all host threads; ggml itself is not in the reference tree) on a bounded token
+    sample of the same workload, plus the reference-arithmetic leg."""
+    import hy_oracle as O
+    nthreads = os.cpu_count() or 1
+    wtype = wl["wtype"]
+    layer = O.synth_layer(H, I, E, K, wtype, seed=seed, layer=0, std=0.02)
+    T = wl["T"]
+    x = O.synth(seed + 1000, 0, O.T_X, 0, (T, H), 1.0)
+    n = min(T, max(8, nthreads))
+    rows = np.arange(n) % T
+    t0 = time.perf_counter()
+    O.moe_forward_q_rows(layer, x, rows, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    n2 = int(min(T * 4, max(n, n * budget_s / max(dt, 1e-6))))
+    rows = np.arange(n2) % T
+    t0 = time.perf_counter()
+    O.moe_forward_q_rows(layer, x, rows, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    del layer
+    nl = wl["layers"]
+    res = {"value": n2 / dt / nl, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+           "extrapolated": nl > 1 or n2 < T, "cpu_model": cpu_model(),
+           "sample": f"{n2} tokens of the {wl['name']} workload through one layer of the oracle's int8 "
+                     f"(ggml-semantics) path, {nthreads} OpenMP threads, {dt:.1f} s"
+                     + (f"; the per-layer rate divided by {nl} layers" if nl > 1 else "")}
+    if wtype != 0:
+        res["reference_arithmetic"] = ref_cpu_baseline(wl, seed)
+    return res
+
+
+def run_moe(hy, wl, steps, warmup, seed, graph=False, tokens=None):
+    """Times `steps` steps of one MoE workload (after `warmup`) and profiles the
+    kernels in a second pass; returns the result fields of its JSON line."""
+    wl = dict(wl)
+    if tokens:
+        wl["T"] = tokens
+    T, wtype, nl = wl["T"], wl["wtype"], wl["layers"]
+    rot = wl["rot"] if not wl.get("stack") else 1
+    n_layers = nl * rot
+    bias = zipf_bias(seed) if wl.get("zipf") else None
+
+    m = hy.Moe(H, I, E, K, wtype, num_layers=n_layers, max_tokens=T)
+    for l in range(n_layers):
+        m.synth(l, seed=seed, std=0.02, router_bias=bias)
+    x = hy.Buf.empty((T, H))
+    hy.check(hy.lib().hy_synth_fill(x.ptr, T * H, seed + 1000, 0, 0, 0, 1.0, None))
+    if bias is not None:   # feature 0 carries the per-expert bias
+        xh = x.numpy()
+        xh[:, 0] = 1.0
+        x = hy.Buf.from_array(xh)
+    out = hy.Buf.empty((T, H))
+    st = hy.Stream()
+    stream = st.h
+
+    def eager_step(i):
+        if wl.get("stack"):
+            m.stack_forward(0, nl, x, T, 1e-5, out, stream)
+        else:
+            m.forward(i % rot, x, T, out, stream)
+
+    for i in range(warmup):
+        eager_step(i)
+    hy.sync()
+    # kernels are launched from the host on a created stream (measured faster than the
+    # null stream); --graph replays the layer forward captured once per resident weight
+    # set instead (hipGraph; on this stack no faster than the eager launches)
+    graphs = [hy.Graph(st, lambda l=l: eager_step(l)) for l in range(rot)] if graph else []
+
+    def step(i):
+        if graphs:
+            graphs[i % rot].launch()
+        else:
+            eager_step(i)
+
+    for i in range(warmup):
+        step(i)
+    hy.sync()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    hy.sync()
+    t0 = time.perf_counter()
+    hy.check(hy.lib().hy_event_record(ev0, stream))
+    for i in range(steps):
+        step(i)
+    hy.check(hy.lib().hy_event_record(ev1, stream))
+    hy.sync()
+    wall = time.perf_counter() - t0
+    ms = hy.C.c_float()
+    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+    ms_per_step = ms.value / steps
+    tokens_per_s = T / (ms_per_step / 1e3)
+
+    D, counts = m.last_routing()
+    # per-kernel durations on the launch stream (separate, profiled pass, eager launches)
+    m.prof_enable(True)
+    for i in range(steps):
+        eager_step(i)
+    hy.sync()
+    prof = m.prof_read()
+    m.prof_enable(False)
+    kern = {k: (n, t) for k, (n, t) in prof.items() if n > 0}
+    dom = max(kern, key=lambda k: kern[k][1])
+    n_l, t_l = kern[dom]
+    avg_s = t_l / n_l / 1e3
+    n_layer_launch = nl if wl.get("stack") else 1
+    traffic = kernel_traffic(dom, wtype, T, D)
+    hbm_measured = measured_traffic(wl["name"] if not tokens else f"{wl['name']}_t{T}", dom)
+    ops = kernel_ops(dom, T)
+    layer_bytes = (D + 1) * expert_bytes(wtype) + E * H * 4 + 2 * T * H * 4
+    layer_ops = 2.0 * T * (K + 1) * PARAMS_PER_EXPERT
+    t_layer = ms_per_step / 1e3 / n_layer_launch
+    # bound: HBM when the layer's bytes take longer at peak than its ops at int8 peak
+    bound = "hbm" if layer_bytes / PEAK_HBM >= layer_ops / PEAK_INT8 else "mfma"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "kernel": dom, "achieved": traffic / avg_s / 1e9, "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": traffic / avg_s / PEAK_HBM, "traffic": hbm_measured,
+                "algorithmic_bytes_per_launch": traffic, "avg_launch_ms": avg_s * 1e3}
+    else:
+        roof = {"bound": "mfma", "kernel": dom, "achieved": ops / avg_s / 1e12, "peak": PEAK_INT8 / 1e12,
+                "unit": "TFLOP/s", "frac": ops / avg_s / PEAK_INT8, "traffic": hbm_measured,
+                "algorithmic_ops_per_launch": ops, "avg_launch_ms": avg_s * 1e3,
+                "rescale_ceiling": {"peak": RESCALE_CEILING / 1e12, "unit": "TOP/s",
+                                    "frac": ops / avg_s / RESCALE_CEILING}}
+    top8 = float(np.sort(counts)[::-1][:8].sum() / max(1, counts.sum()))
+    res = {
+        "value": tokens_per_s, "ms_per_step": ms_per_step,
+        "config": {"workload": wl["name"], "hidden": H, "intermediate": I, "experts": E, "shared_experts": 1,
+                   "topk": K, "tokens": T, "weights": {0: "F32", 2: "Q4_0", 8: "Q8_0"}[wtype],
+                   "layers": nl, "resident_weight_sets": n_layers, "distinct_experts_last_step": int(D)},
+        "layer_hbm_gbps": layer_bytes / t_layer / 1e9,
+        "layer_hbm_frac": layer_bytes / t_layer / PEAK_HBM,
+        "layer_int8_util": layer_ops / t_layer / PEAK_INT8,
+        "roofline": roof,
+        "kernels_ms": {k: round(t / n, 5) for k, (n, t) in kern.items()},
+        "launch": "hip_graph" if graph else "eager",
+        "wall_s": wall,
+    }
+    if wl.get("zipf"):
+        res["routing"] = {"zipf_s": 1.1, "zipf_beta": ZIPF_BETA, "top8_pair_share": top8,
+                          "hottest_expert_tokens": int(counts.max()), "pairs_per_expert_sorted":
+                          [int(c) for c in np.sort(counts)[::-1]]}
+    for g in graphs:
+        g.close()
+    st.close()
+    m.close()
+    return res
+
+
+# extra workloads timed after the headline in the same run: the decode and skewed
+# image-token targets (name, workload, tokens, steps multiplier)
+EXTRAS = (("decode_t1", "c3", 1, 10), ("decode_t8", "c3", 8, 10), ("zipf_t4096", "c4", None, 1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--config", default="c5", choices=sorted(WORKLOADS))
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="time only the --config workload")
     ap.add_argument("--graph", action="store_true", help="replay the step as a captured hipGraph")
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
@@ -507,119 +701,31 @@ def main():
     if a.model:
         model_main(a, hy)
         return
-    wl = dict(WORKLOADS[a.config])
-    if a.tokens:
-        wl["T"] = a.tokens
-    T, wtype, nl = wl["T"], wl["wtype"], wl["layers"]
-    rot = wl["rot"] if not wl.get("stack") else 1
-    n_layers = nl * rot
-    bias = zipf_bias(a.seed) if wl.get("zipf") else None
-
-    m = hy.Moe(H, I, E, K, wtype, num_layers=n_layers, max_tokens=T)
-    for l in range(n_layers):
-        m.synth(l, seed=a.seed, std=0.02, router_bias=bias)
-    x = hy.Buf.empty((T, H))
-    hy.check(hy.lib().hy_synth_fill(x.ptr, T * H, a.seed + 1000, 0, 0, 0, 1.0, None))
-    if bias is not None:   # feature 0 carries the per-expert bias
-        xh = x.numpy()
-        xh[:, 0] = 1.0
-        x = hy.Buf.from_array(xh)
-    out = hy.Buf.empty((T, H))
-    st = hy.Stream()
-    stream = st.h
-
-    def eager_step(i):
-        if wl.get("stack"):
-            m.stack_forward(0, nl, x, T, 1e-5, out, stream)
-        else:
-            m.forward(i % rot, x, T, out, stream)
-
-    for i in range(a.warmup):
-        eager_step(i)
-    hy.sync()
-    # kernels are launched from the host on a created stream (measured faster than the
-    # null stream); --graph replays the layer forward captured once per resident weight
-    # set instead (hipGraph; on this stack no faster than the eager launches)
-    graphs = [hy.Graph(st, lambda l=l: eager_step(l)) for l in range(rot)] if a.graph else []
-
-    def step(i):
-        if graphs:
-            graphs[i % rot].launch()
-        else:
-            eager_step(i)
-
-    for i in range(a.warmup):
-        step(i)
-    hy.sync()
-    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
-    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
-    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
-    hy.sync()
-    t0 = time.perf_counter()
-    hy.check(hy.lib().hy_event_record(ev0, stream))
-    for i in range(a.steps):
-        step(i)
-    hy.check(hy.lib().hy_event_record(ev1, stream))
-    hy.sync()
-    wall = time.perf_counter() - t0
-    ms = hy.C.c_float()
-    hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
-    ms_per_step = ms.value / a.steps
-    tokens_per_s = T / (ms_per_step / 1e3)
-
-    D, counts = m.last_routing()
-    # per-kernel durations on the launch stream (separate, profiled pass, eager launches)
-    m.prof_enable(True)
-    for i in range(a.steps):
-        eager_step(i)
-    hy.sync()
-    prof = m.prof_read()
-    m.prof_enable(False)
-    kern = {k: (n, t) for k, (n, t) in prof.items() if n > 0}
-    dom = max(kern, key=lambda k: kern[k][1])
-    n_l, t_l = kern[dom]
-    avg_s = t_l / n_l / 1e3
-    n_layer_launch = nl if wl.get("stack") else 1
-    traffic = kernel_traffic(dom, wtype, T, D)
-    hbm_measured = measured_traffic(wl["name"] if not a.tokens else f"{wl['name']}_t{T}", dom)
-    ops = kernel_ops(dom, T)
-    layer_bytes = (D + 1) * expert_bytes(wtype) + E * H * 4 + 2 * T * H * 4
-    layer_ops = 2.0 * T * (K + 1) * PARAMS_PER_EXPERT
-    t_layer = ms_per_step / 1e3 / n_layer_launch
-    # bound: HBM when the layer's bytes take longer at peak than its ops at int8 peak
-    bound = "hbm" if layer_bytes / PEAK_HBM >= layer_ops / PEAK_INT8 else "mfma"
-    if bound == "hbm":
-        roof = {"bound": "hbm", "kernel": dom, "achieved": traffic / avg_s / 1e9, "peak": PEAK_HBM / 1e9,
-                "unit": "GB/s", "frac": traffic / avg_s / PEAK_HBM, "traffic": hbm_measured,
-                "algorithmic_bytes_per_launch": traffic, "avg_launch_ms": avg_s * 1e3}
-    else:
-        roof = {"bound": "mfma", "kernel": dom, "achieved": ops / avg_s / 1e12, "peak": PEAK_INT8 / 1e12,
-                "unit": "TFLOP/s", "frac": ops / avg_s / PEAK_INT8, "traffic": hbm_measured,
-                "algorithmic_ops_per_launch": ops, "avg_launch_ms": avg_s * 1e3}
-
-    res = {
-        "metric": "MoE-layer tokens/sec + achieved HBM GB/s / int8 MFMA util, 1 MI355X",
-        "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8" if wtype != 0 else "f32", "data": "synthetic",
-        "config": {"workload": wl["name"], "hidden": H, "intermediate": I, "experts": E, "shared_experts": 1,
-                   "topk": K, "tokens": T, "weights": {0: "F32", 2: "Q4_0", 8: "Q8_0"}[wtype],
-                   "layers": nl, "resident_weight_sets": n_layers, "distinct_experts_last_step": int(D)},
-        "layer_hbm_gbps": layer_bytes / t_layer / 1e9,
-        "layer_hbm_frac": layer_bytes / t_layer / PEAK_HBM,
-        "layer_int8_util": layer_ops / t_layer / PEAK_INT8,
-        "roofline": roof,
-        "kernels_ms": {k: round(t / n, 5) for k, (n, t) in kern.items()},
-        "launch": "hip_graph" if a.graph else "eager",
-        "wall_s": wall,
-    }
+    wl = WORKLOADS[a.config]
+    r = run_moe(hy, wl, a.steps, a.warmup, a.seed, graph=a.graph, tokens=a.tokens)
+    print(f"bench: {r['config']['workload']} {r['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
+    res = {"metric": "MoE-layer tokens/sec + achieved HBM GB/s / int8 MFMA util, 1 MI355X",
+           "value": r.pop("value"), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": r.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8" if wl["wtype"] != 0 else "f32", "data": "synthetic"}
+    res.update(r)
+    if not a.no_extras and a.config == "c5" and not a.tokens:
+        extras = {}
+        for name, cfg, toks, mult in EXTRAS:
+            e = run_moe(hy, WORKLOADS[cfg], a.steps * mult, a.warmup, a.seed, graph=a.graph, tokens=toks)
+            print(f"bench: {name} {e['ms_per_step']:.4f} ms/step", file=sys.stderr, flush=True)
+            extras[name] = {"workload": e["config"]["workload"], "tokens": e["config"]["tokens"],
+                            "value": e["value"], "unit": "tokens/s", "ms_per_step": e["ms_per_step"],
+                            "steps": a.steps * mult, "layer_hbm_frac": e["layer_hbm_frac"],
+                            "layer_int8_util": e["layer_int8_util"], "roofline": e["roofline"],
+                            "kernels_ms": e["kernels_ms"],
+                            "distinct_experts_last_step": e["config"]["distinct_experts_last_step"]}
+            if "routing" in e:
+                extras[name]["routing"] = e["routing"]
+        res["extras"] = extras
     if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(wl, a.seed)
+        res["cpu_baseline"] = cpu_baseline(wl if not a.tokens else dict(wl, T=a.tokens), a.seed)
     print(json.dumps(res), flush=True)
-    for g in graphs:
-        g.close()
-    st.close()
-    m.close()
 
 
 if __name__ == "__main__":
