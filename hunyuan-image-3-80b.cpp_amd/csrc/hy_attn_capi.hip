@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -47,6 +48,12 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 enum { AK_QKV = 0, AK_ROPE = 1, AK_ATTN = 2, AK_OPROJ = 3, AK_COUNT = 4 };
+
+// stream-K scratch of the stand-alone lm_head GEMM (one per device)
+struct LmScratch {
+    float* ws = nullptr;
+    hipEvent_t done = nullptr;
+};
 
 struct ProfRec {
     int kid;
@@ -203,7 +210,9 @@ int run(hy_attn_ctx* c, const AttnLayer& W, const float* x, int T, int mode, con
     return HY_OK;
 }
 
-// F32 / F16 / BF16 GGUF tensor -> f32 host copy (row-major as stored: ne0 innermost)
+// GGUF tensor -> f32 host copy (row-major as stored: ne0 innermost): F32, F16, BF16,
+// Q8_0 or Q4_0, as the reference loader's read_tensor_data takes every tensor
+// (src/hunyuan_gguf_loader.cpp:167-222)
 int gguf_f32(const hy::GgufFile& f, const std::string& name, uint64_t ne0, uint64_t ne1, bool optional,
              std::vector<float>& out, bool* present) {
     const hy::GgufTensor* t = f.find(name);
@@ -214,26 +223,10 @@ int gguf_f32(const hy::GgufFile& f, const std::string& name, uint64_t ne0, uint6
         return fail(HY_ERR_INVALID, "%s has shape [%llu, %llu], want [%llu, %llu]", name.c_str(),
                     (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)ne0,
                     (unsigned long long)ne1);
-    const size_t n = (size_t)ne0 * ne1;
-    out.resize(n);
-    if (t->type == hy::GGML_F32) {
-        std::memcpy(out.data(), t->data, n * 4);
-    } else if (t->type == hy::GGML_F16) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(t->data);
-        for (size_t i = 0; i < n; i++) {
-            _Float16 h;
-            std::memcpy(&h, src + i, 2);
-            out[i] = (float)h;
-        }
-    } else if (t->type == hy::GGML_BF16) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(t->data);
-        for (size_t i = 0; i < n; i++) {
-            const uint32_t b = (uint32_t)src[i] << 16;
-            std::memcpy(&out[i], &b, 4);
-        }
-    } else {
-        return fail(HY_ERR_UNSUPPORTED, "%s has ggml type %d; F32, F16 or BF16 expected", name.c_str(), t->type);
-    }
+    out.resize((size_t)ne0 * ne1);
+    if (!hy::tensor_to_f32(*t, out.data()))
+        return fail(HY_ERR_UNSUPPORTED, "%s has ggml type %d; F32, F16, BF16, Q8_0 or Q4_0 expected", name.c_str(),
+                    t->type);
     return HY_OK;
 }
 
@@ -464,15 +457,32 @@ int hy_lm_head_f32(const float* x, const float* w, const float* resid, uint32_t 
         return fail(HY_ERR_INVALID, "bad GEMM shape T=%u hidden=%u vocab=%u (hidden a multiple of 16)", T, hidden,
                     vocab);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!hy::gemm_nt_f32_uses_ws((int)T, (int)vocab, (int)hidden)) {
+        HIP_TRY(hy::launch_gemm_nt_f32(x, w, resid, out, (int)T, (int)vocab, (int)hidden, s, nullptr));
+        return HY_OK;
+    }
     // mid-size grids take the stream-K split, which needs a scratch of partial tiles:
-    // stream-ordered, freed after the launch
-    float* ws = nullptr;
-    if (hy::gemm_nt_f32_uses_ws((int)T, (int)vocab, (int)hidden) &&
-        hipMallocAsync(reinterpret_cast<void**>(&ws), hy::gemm_nt_f32_ws_bytes(), s) != hipSuccess)
-        return fail(HY_ERR_NOMEM, "GEMM scratch allocation failed");
-    const hipError_t e = hy::launch_gemm_nt_f32(x, w, resid, out, (int)T, (int)vocab, (int)hidden, s, ws);
-    if (ws) (void)hipFreeAsync(ws, s);
-    HIP_TRY(e);
+    // one per device, allocated on the first such call and kept for the process.  A
+    // call waits (on the device) for the previous call's use of it to finish, so calls
+    // on different streams stay ordered.
+    static std::mutex mu;
+    static std::vector<LmScratch> per_dev;
+    std::lock_guard<std::mutex> lock(mu);
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1);
+    LmScratch& sc = per_dev[dev];
+    if (!sc.ws) {
+        if (hipMalloc(reinterpret_cast<void**>(&sc.ws), hy::gemm_nt_f32_ws_bytes()) != hipSuccess) {
+            sc.ws = nullptr;
+            return fail(HY_ERR_NOMEM, "GEMM scratch allocation failed");
+        }
+        HIP_TRY(hipEventCreateWithFlags(&sc.done, hipEventDisableTiming));
+    } else {
+        HIP_TRY(hipStreamWaitEvent(s, sc.done, 0));
+    }
+    HIP_TRY(hy::launch_gemm_nt_f32(x, w, resid, out, (int)T, (int)vocab, (int)hidden, s, sc.ws));
+    HIP_TRY(hipEventRecord(sc.done, s));
     return HY_OK;
 }
 

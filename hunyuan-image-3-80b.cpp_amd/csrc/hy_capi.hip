@@ -503,40 +503,75 @@ int hy_moe_upload_layer_gguf(hy_moe_ctx* c, uint32_t layer, const hy_gguf* g, ui
                         m.want);
     }
     // every tensor first: nothing is uploaded from an incomplete or mismatched file
-    auto need = [&](const std::string& name, int type, uint64_t ne0, uint64_t ne1, const uint8_t** data) -> int {
+    auto find2 = [&](const std::string& name, uint64_t ne0, uint64_t ne1, const hy::GgufTensor** out) -> int {
         const hy::GgufTensor* t = f.find(name);
         if (!t) return fail(HY_ERR_INVALID, "GGUF file has no tensor %s", name.c_str());
-        if (t->type != type)
-            return fail(HY_ERR_INVALID, "%s has ggml type %d, the context wants %d", name.c_str(), t->type, type);
         if (t->n_dims != 2 || t->ne[0] != ne0 || t->ne[1] != ne1)
             return fail(HY_ERR_INVALID, "%s has shape [%llu, %llu], the context wants [%llu, %llu]", name.c_str(),
                         (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)ne0,
                         (unsigned long long)ne1);
-        *data = t->data;
+        *out = t;
         return HY_OK;
     };
+    auto convertible = [](int type) {
+        return type == hy::GGML_F32 || type == hy::GGML_F16 || type == hy::GGML_BF16 || type == hy::GGML_Q8_0 ||
+               type == hy::GGML_Q4_0;
+    };
+    // expert matrices: as stored when of the context's type; into an F32 context any
+    // convertible type becomes f32; Q4_0 into a Q8_0 context is re-encoded exactly
+    auto expert_ok = [&](const hy::GgufTensor* t) -> int {
+        if (t->type == wt || (wt == HY_TYPE_F32 && convertible(t->type)) ||
+            (wt == HY_TYPE_Q8_0 && t->type == hy::GGML_Q4_0))
+            return HY_OK;
+        if (!convertible(t->type))
+            return fail(HY_ERR_INVALID, "%s has ggml type %d, the context wants %d", t->name.c_str(), t->type, wt);
+        return fail(HY_ERR_UNSUPPORTED,
+                    "%s has ggml type %d: turning it into the context's type %d would change the weights "
+                    "(create the context with wtype F32, or use a file of type %d)",
+                    t->name.c_str(), t->type, wt, wt);
+    };
     const std::string pfx = "blk." + std::to_string(block) + ".";
-    const uint8_t* router = nullptr;
-    HY_TRY(need(pfx + "ffn_gate.weight", HY_TYPE_F32, (uint64_t)H, (uint64_t)E, &router));
-    std::vector<const uint8_t*> gus(c->X), dns(c->X);
+    const hy::GgufTensor* router_t = nullptr;
+    HY_TRY(find2(pfx + "ffn_gate.weight", (uint64_t)H, (uint64_t)E, &router_t));
+    if (!convertible(router_t->type))
+        return fail(HY_ERR_UNSUPPORTED, "%sffn_gate.weight has ggml type %d; F32, F16, BF16, Q8_0 or Q4_0 expected",
+                    pfx.c_str(), router_t->type);
+    std::vector<const hy::GgufTensor*> gus(c->X), dns(c->X);
     for (int e = 0; e < c->X; e++) {
         const std::string base = e < E ? pfx + "ffn_expert_" + std::to_string(e) + "_" : pfx + "ffn_shared_";
-        HY_TRY(need(base + "gate_up.weight", wt, (uint64_t)H, (uint64_t)2 * I, &gus[e]));
-        HY_TRY(need(base + "down.weight", wt, (uint64_t)I, (uint64_t)H, &dns[e]));
+        HY_TRY(find2(base + "gate_up.weight", (uint64_t)H, (uint64_t)2 * I, &gus[e]));
+        HY_TRY(expert_ok(gus[e]));
+        HY_TRY(find2(base + "down.weight", (uint64_t)I, (uint64_t)H, &dns[e]));
+        HY_TRY(expert_ok(dns[e]));
     }
-    // the post-attention RMSNorm weight (post_attention_layernorm -> ffn_norm), F32 [H];
+    // the post-attention RMSNorm weight (post_attention_layernorm -> ffn_norm), [H];
     // optional: a file without it leaves the layer at unit weight
-    const uint8_t* norm = nullptr;
-    if (const hy::GgufTensor* t = f.find(pfx + "ffn_norm.weight")) {
-        if (t->type != HY_TYPE_F32 || t->n_dims != 1 || t->ne[0] != (uint64_t)H)
-            return fail(HY_ERR_INVALID, "%sffn_norm.weight must be F32 [%d] (type %d, %u dims, ne0 %llu)", pfx.c_str(),
-                        H, t->type, t->n_dims, (unsigned long long)t->ne[0]);
-        norm = t->data;
-    }
+    const hy::GgufTensor* norm_t = f.find(pfx + "ffn_norm.weight");
+    if (norm_t && (!convertible(norm_t->type) || norm_t->n_dims != 1 || norm_t->ne[0] != (uint64_t)H))
+        return fail(HY_ERR_INVALID, "%sffn_norm.weight must be [%d] of F32/F16/BF16/Q8_0/Q4_0 (type %d, %u dims, ne0 %llu)",
+                    pfx.c_str(), H, norm_t->type, norm_t->n_dims, (unsigned long long)norm_t->ne[0]);
+    std::vector<float> router((size_t)E * H), norm(norm_t ? (size_t)H : 0);
+    hy::tensor_to_f32(*router_t, router.data());
+    if (norm_t) hy::tensor_to_f32(*norm_t, norm.data());
+    // one conversion buffer per matrix kind: upload_layer takes expert e's gate_up,
+    // then its down, before asking for expert e + 1
+    std::vector<uint8_t> gu_buf, dn_buf;
+    auto as_ctx = [&](const hy::GgufTensor* t, std::vector<uint8_t>& buf) -> const void* {
+        if (t->type == wt) return t->data;
+        const uint64_t n = t->ne[0] * t->ne[1];
+        if (wt == HY_TYPE_F32) {
+            buf.resize(n * 4);
+            hy::tensor_to_f32(*t, reinterpret_cast<float*>(buf.data()));
+        } else {  // Q4_0 -> Q8_0
+            buf.resize(n / 32 * 34);
+            hy::q4_0_to_q8_0(t->data, buf.data(), n / 32);
+        }
+        return buf.data();
+    };
     HY_TRY(upload_layer(
-        c, layer, reinterpret_cast<const float*>(router), [&](int e) -> const void* { return gus[e]; },
-        [&](int e) -> const void* { return dns[e]; }));
-    return hy_moe_set_ffn_norm(c, layer, reinterpret_cast<const float*>(norm));
+        c, layer, router.data(), [&](int e) -> const void* { return as_ctx(gus[e], gu_buf); },
+        [&](int e) -> const void* { return as_ctx(dns[e], dn_buf); }));
+    return hy_moe_set_ffn_norm(c, layer, norm_t ? norm.data() : nullptr);
 }
 
 int hy_moe_synth_layer(hy_moe_ctx* c, uint32_t layer, uint64_t seed, float std, const float* bias) {

@@ -32,6 +32,83 @@ uint64_t ggml_row_bytes(int32_t type, uint64_t n) {
     }
 }
 
+float fp16_bits_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0x1f) {
+        bits = sign | 0x7f800000u | (m << 13);   // inf / NaN
+    } else if (e != 0) {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    } else if (m == 0) {
+        bits = sign;
+    } else {  // subnormal: m * 2^-24, normalised
+        int sh = 0;
+        uint32_t mm = m;
+        while (!(mm & 0x400u)) {
+            mm <<= 1;
+            sh++;
+        }
+        bits = sign | ((uint32_t)(113 - sh) << 23) | ((mm & 0x3ffu) << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+float bf16_bits_to_f32(uint16_t b) {
+    const uint32_t bits = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+bool tensor_to_f32(const GgufTensor& t, float* out) {
+    if (!t.data) return false;
+    const uint64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    const uint8_t* p = t.data;
+    auto u16 = [](const uint8_t* q) { return (uint16_t)(q[0] | (q[1] << 8)); };
+    switch (t.type) {
+    case GGML_F32:
+        std::memcpy(out, p, n * 4);
+        return true;
+    case GGML_F16:
+        for (uint64_t i = 0; i < n; i++) out[i] = fp16_bits_to_f32(u16(p + 2 * i));
+        return true;
+    case GGML_BF16:
+        for (uint64_t i = 0; i < n; i++) out[i] = bf16_bits_to_f32(u16(p + 2 * i));
+        return true;
+    case GGML_Q8_0:
+        for (uint64_t b = 0; b < n / 32; b++, p += 34) {
+            const float d = fp16_bits_to_f32(u16(p));
+            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)(int8_t)p[2 + j];
+        }
+        return true;
+    case GGML_Q4_0:
+        for (uint64_t b = 0; b < n / 32; b++, p += 18) {
+            const float d = fp16_bits_to_f32(u16(p));
+            for (int j = 0; j < 16; j++) {
+                out[32 * b + j] = d * (float)((int)(p[2 + j] & 0x0f) - 8);
+                out[32 * b + 16 + j] = d * (float)((int)(p[2 + j] >> 4) - 8);
+            }
+        }
+        return true;
+    default:
+        return false;
+    }
+}
+
+void q4_0_to_q8_0(const uint8_t* src, uint8_t* dst, uint64_t n_blocks) {
+    for (uint64_t b = 0; b < n_blocks; b++, src += 18, dst += 34) {
+        dst[0] = src[0];
+        dst[1] = src[1];
+        for (int j = 0; j < 16; j++) {
+            dst[2 + j] = (uint8_t)(int8_t)((int)(src[2 + j] & 0x0f) - 8);
+            dst[2 + 16 + j] = (uint8_t)(int8_t)((int)(src[2 + j] >> 4) - 8);
+        }
+    }
+}
+
 GgufFile::~GgufFile() {
     if (map_) munmap(const_cast<uint8_t*>(map_), size);
     if (fd_ >= 0) close(fd_);
@@ -289,6 +366,21 @@ int hy_gguf_tensor(const hy_gguf* g, const char* name, int32_t* type, uint32_t* 
         for (int d = 0; d < 4; d++) ne[d] = t->ne[d];
     if (nbytes) *nbytes = t->nbytes;
     if (data) *data = t->data;
+    return HY_OK;
+}
+
+int hy_gguf_tensor_f32(const hy_gguf* g, const char* name, float* out, uint64_t n) {
+    if (!g || !name || !out) return hy::set_last_error(HY_ERR_INVALID, "null argument");
+    const hy::GgufTensor* t = g->f.find(name);
+    if (!t) return hy::set_last_error(HY_ERR_INVALID, std::string("no tensor ") + name);
+    const uint64_t count = t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3];
+    if (n != count)
+        return hy::set_last_error(HY_ERR_INVALID, std::string("tensor ") + name + " has " + std::to_string(count) +
+                                                      " elements, the buffer " + std::to_string(n));
+    if (!hy::tensor_to_f32(*t, out))
+        return hy::set_last_error(HY_ERR_UNSUPPORTED, std::string("tensor ") + name + " has ggml type " +
+                                                          std::to_string(t->type) +
+                                                          "; F32, F16, BF16, Q8_0 or Q4_0 expected");
     return HY_OK;
 }
 

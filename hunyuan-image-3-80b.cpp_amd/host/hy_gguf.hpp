@@ -34,6 +34,26 @@ enum GgmlType : int32_t {
 // not a whole number of blocks
 uint64_t ggml_row_bytes(int32_t type, uint64_t n);
 
+// IEEE binary16 / bfloat16 bit patterns to f32 (subnormals, infinities and NaNs kept)
+float fp16_bits_to_f32(uint16_t h);
+float bf16_bits_to_f32(uint16_t b);
+
+struct GgufTensor;
+
+// The tensor's values as f32, row-major as stored (ne0 innermost), for F32, F16,
+// BF16 and the GGUF block formats Q8_0 (fp16 d + 32 int8 q: d*q) and Q4_0 (fp16 d +
+// 16 bytes, element j in the low nibble of byte j and element j+16 in the high one:
+// d*(nibble-8)).  This is what the reference loader's read_tensor_data does for every
+// tensor it reads (src/hunyuan_gguf_loader.cpp:167-222), with two deliberate
+// differences: fp16 subnormal scales are kept rather than flushed to zero, and Q4_0
+// follows the GGUF nibble order (the reference's decoder reads element i from byte
+// i/2, which real GGUF files do not use).  Returns false for any other type.
+bool tensor_to_f32(const GgufTensor& t, float* out);
+
+// Q4_0 blocks re-encoded as Q8_0 blocks with the same scale: q = nibble - 8 is an
+// int8, so the values are unchanged.  n_blocks blocks of 18 bytes -> 34 bytes.
+void q4_0_to_q8_0(const uint8_t* src, uint8_t* dst, uint64_t n_blocks);
+
 struct GgufTensor {
     std::string name;
     int32_t type = 0;

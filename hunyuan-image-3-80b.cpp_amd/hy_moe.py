@@ -108,6 +108,7 @@ _SIGS = {
     "hy_gguf_n_tensors": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
     "hy_gguf_tensor": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int32), C.POINTER(C.c_uint32),
                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(_vp)]),
+    "hy_gguf_tensor_f32": (C.c_int, [_vp, C.c_char_p, _vp, C.c_uint64]),
     "hy_gguf_get_u32": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_uint32)]),
     "hy_gguf_get_f32": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_float)]),
     "hy_moe_upload_layer_gguf": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint32]),
@@ -470,6 +471,13 @@ class Gguf:
         check(lib().hy_gguf_tensor(self.h, name.encode(), C.byref(t), C.byref(nd), ne, C.byref(nb), C.byref(d)))
         data = C.string_at(d.value, nb.value) if d.value else None
         return t.value, nd.value, list(ne), nb.value, data
+
+    def tensor_f32(self, name):
+        """The tensor's values as f32, shape (ne[n_dims-1], ..., ne[0])."""
+        _, nd, ne, _, _ = self.tensor(name)
+        out = np.empty(int(np.prod(ne)), np.float32)
+        check(lib().hy_gguf_tensor_f32(self.h, name.encode(), out.ctypes.data, out.size))
+        return out.reshape(tuple(reversed(ne[:nd])))
 
     def get_u32(self, key):
         v = C.c_uint32()

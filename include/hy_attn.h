@@ -59,7 +59,7 @@ int hy_attn_upload(hy_attn_ctx* ctx, uint32_t layer, const float* qkv_weight_hos
  * load_layer_weights reads them (src/hunyuan_gguf_loader.cpp:249-257):
  * blk.N.attn_qkv.weight ne {H, (nh+2nkv) hd}, blk.N.attn_output.weight ne {nh hd, H},
  * blk.N.attn_q_norm.weight / attn_k_norm.weight ne {hd}, and blk.N.attn_norm.weight
- * ne {H} (input_layernorm; optional, absent: unit).  F32, F16 or BF16 (converted to
+ * ne {H} (input_layernorm; optional, absent: unit).  F32, F16, BF16, Q8_0 or Q4_0 (converted to
  * F32 on upload).  Types and shapes are checked before anything is uploaded. */
 int hy_attn_upload_gguf(hy_attn_ctx* ctx, uint32_t layer, const hy_gguf* f, uint32_t block);
 
@@ -130,7 +130,7 @@ hy_moe_ctx* hy_model_moe(hy_model_ctx* ctx);
  * NULL to leave it as it is. */
 int hy_model_upload_globals(hy_model_ctx* ctx, const float* embedding_host, const float* final_norm_host,
                             const float* lm_head_host);
-/* The same three tensors from a GGUF file (F32, F16 or BF16). */
+/* The same three tensors from a GGUF file (F32, F16, BF16, Q8_0 or Q4_0; converted to F32). */
 int hy_model_upload_globals_gguf(hy_model_ctx* ctx, const hy_gguf* f);
 /* Synthetic global weights (embedding and lm_head ~ N(0, std), final norm 1). */
 int hy_model_synth_globals(hy_model_ctx* ctx, uint64_t seed, float std);

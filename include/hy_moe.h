@@ -123,6 +123,12 @@ int hy_gguf_n_tensors(const hy_gguf* f, uint64_t* n);
  * not size).  Any output may be NULL. */
 int hy_gguf_tensor(const hy_gguf* f, const char* name, int32_t* ggml_type, uint32_t* n_dims, uint64_t* ne4,
                    uint64_t* nbytes, const void** data);
+/* A tensor's values as f32 (n = its element count), for F32, F16, BF16, Q8_0 and
+ * Q4_0 (GGUF block layouts): read_tensor_data / load_tensor
+ * (src/hunyuan_gguf_loader.cpp:160-222), which dequantizes whatever it reads.  Two
+ * deliberate differences: fp16 subnormal scales are kept (the reference flushes them
+ * to 0) and Q4_0 uses the GGUF nibble order (low nibble = element j, high = j+16). */
+int hy_gguf_tensor_f32(const hy_gguf* f, const char* name, float* out_host, uint64_t n);
 /* Metadata (HunyuanGGUFLoader::get_metadata_u32 / _f32, src/hunyuan_gguf_loader.cpp:286-297),
  * but a missing key or a value of another type is an error instead of a default. */
 int hy_gguf_get_u32(const hy_gguf* f, const char* key, uint32_t* out);
@@ -131,16 +137,23 @@ int hy_gguf_get_f32(const hy_gguf* f, const char* key, float* out);
 /* Upload layer `layer` of the context from block `block` of a GGUF file with the
  * tensor names the reference's converter writes and its loader reads
  * (scripts/convert_to_gguf.py:70-137, src/hunyuan_gguf_loader.cpp:229-280):
- *   blk.N.ffn_gate.weight                  f32    ne {H, E}   (router)
- *   blk.N.ffn_shared_gate_up.weight        wtype  ne {H, 2I}
- *   blk.N.ffn_shared_down.weight           wtype  ne {I, H}
- *   blk.N.ffn_expert_<e>_gate_up.weight    wtype  ne {H, 2I}, e = 0..E-1
- *   blk.N.ffn_expert_<e>_down.weight       wtype  ne {I, H}
- *   blk.N.ffn_norm.weight                  F32    ne {H}   (optional; absent: unit)
- * Types and shapes must match the context (else HY_ERR_INVALID naming the tensor);
- * hunyuan.hidden_size / moe_intermediate_size / num_experts / moe_topk, when present,
- * must agree with it too.  Replaces load_layer_weights + StackedExpertWeights
- * (src/hunyuan_extended.cpp:8-26): the blocks are repacked on the device once. */
+ *   blk.N.ffn_gate.weight                  any    ne {H, E}   (router)
+ *   blk.N.ffn_shared_gate_up.weight        expert ne {H, 2I}
+ *   blk.N.ffn_shared_down.weight           expert ne {I, H}
+ *   blk.N.ffn_expert_<e>_gate_up.weight    expert ne {H, 2I}, e = 0..E-1
+ *   blk.N.ffn_expert_<e>_down.weight       expert ne {I, H}
+ *   blk.N.ffn_norm.weight                  any    ne {H}   (optional; absent: unit)
+ * "any": F32, F16, BF16, Q8_0 or Q4_0, turned into f32 as hy_gguf_tensor_f32 does
+ * (the reference loader reads every tensor through read_tensor_data,
+ * src/hunyuan_gguf_loader.cpp:167-222, and its converter gives all tensors of a file
+ * one type, scripts/convert_to_gguf.py:196-200).  "expert": the context's wtype, used
+ * as stored; into an F32 context any type is turned into f32; Q4_0 into a Q8_0
+ * context is re-encoded exactly (same scales, q = nibble - 8).  Other combinations
+ * would change the weights and are HY_ERR_UNSUPPORTED.  Shapes must match the context
+ * (else HY_ERR_INVALID naming the tensor); hunyuan.hidden_size /
+ * moe_intermediate_size / num_experts / moe_topk, when present, must agree with it too.
+ * Replaces load_layer_weights + StackedExpertWeights (src/hunyuan_extended.cpp:8-26):
+ * the blocks are repacked on the device once. */
 int hy_moe_upload_layer_gguf(hy_moe_ctx* ctx, uint32_t layer, const hy_gguf* f, uint32_t block);
 
 /* ---- forward ------------------------------------------------------------- */

@@ -118,7 +118,7 @@ def attn_tensors(w, block, gtype=GGML_F32, in_norm=None):
         items.append(("attn_norm.weight", in_norm, [H]))
     ts, vals = [], {}
     for name, arr, ne in items:
-        data, back = float_tensor(arr, gtype)
+        data, back = typed_tensor(arr, gtype)
         ts.append((p + name, gtype, ne, data))
         vals[name] = back.reshape(np.asarray(arr).shape)
     return ts, vals
@@ -129,7 +129,51 @@ def global_tensors(emb, final_norm, lm_head, gtype=GGML_F32):
     ts, vals = [], {}
     for name, arr, ne in (("token_embd.weight", emb, [H, V]), ("output_norm.weight", final_norm, [H]),
                           ("output.weight", lm_head, [H, V])):
-        data, back = float_tensor(arr, gtype)
+        data, back = typed_tensor(arr, gtype)
         ts.append((name, gtype, ne, data))
         vals[name] = back.reshape(np.asarray(arr).shape)
     return ts, vals
+
+
+def typed_tensor(a, gtype):
+    """(bytes, the f32 values a reader gives back) of a float array stored as F32, F16,
+    BF16, Q8_0 or Q4_0 (blocks of 32 along the last axis, the oracle's quantizers)."""
+    if gtype in (GGML_F32, GGML_F16, GGML_BF16):
+        return float_tensor(a, gtype)
+    import hy_oracle as O
+    a = np.ascontiguousarray(a, np.float32)
+    q = O.quantize(a, gtype)
+    return q.tobytes(), O.dequantize(q, gtype, a.shape[-1])
+
+
+def typed_layer_tensors(router, gu, dn, sgu, sdn, block, gtype, ffn_norm=None):
+    """One MoE layer with every tensor in one ggml type, as the reference converter
+    writes a file (one --type for all tensors).  router [E][H], gu [E][2I][H],
+    dn [E][H][I], sgu / sdn the shared expert (or None), ffn_norm [H] or None.
+    Returns (tensors, {role: the f32 values a reader recovers})."""
+    E, H = router.shape
+    I = dn.shape[2]
+    p = f"blk.{block}."
+    ts, back = [], {}
+
+    def add(name, arr, ne, role):
+        data, vals = typed_tensor(arr, gtype)
+        ts.append((p + name, gtype, ne, data))
+        back[role] = vals
+        return data
+
+    add("ffn_gate.weight", router, [H, E], "router")
+    if ffn_norm is not None:
+        add("ffn_norm.weight", ffn_norm, [H], "ffn_norm")
+    raw = {"gu": [], "dn": []}
+    if sgu is not None:
+        raw["sgu"] = add("ffn_shared_gate_up.weight", sgu, [H, 2 * I], "sgu")
+        raw["sdn"] = add("ffn_shared_down.weight", sdn, [I, H], "sdn")
+    gus, dns = [], []
+    for e in range(E):
+        raw["gu"].append(add(f"ffn_expert_{e}_gate_up.weight", gu[e], [H, 2 * I], "gu"))
+        gus.append(back["gu"])
+        raw["dn"].append(add(f"ffn_expert_{e}_down.weight", dn[e], [I, H], "dn"))
+        dns.append(back["dn"])
+    back["gu"], back["dn"], back["raw"] = np.stack(gus), np.stack(dns), raw
+    return ts, back

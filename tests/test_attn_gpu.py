@@ -284,3 +284,26 @@ def test_gemm_both_tilings(gpu, M, N, Kd):
     ref = x.astype(np.float64) @ w.astype(np.float64).T
     check(gpu.lm_head_f32(x, w), ref, f"gemm {M}x{N}x{Kd}")
     check(gpu.lm_head_f32(x, w, r), ref + r, f"gemm+resid {M}x{N}x{Kd}")
+
+
+def test_gemm_stream_k_scratch_across_streams(gpu):
+    """The stand-alone GEMM keeps one stream-K scratch per device: calls queued on two
+    streams back to back (no host sync between them) are ordered on the device and
+    both give the right product."""
+    M, N, Kd = 1290, 6150, 1024   # a stream-K shape
+    rng = np.random.default_rng(3)
+    xs = [rng.standard_normal((M, Kd)).astype(np.float32) for _ in range(2)]
+    w = rng.standard_normal((N, Kd)).astype(np.float32)
+    wb = gpu.Buf.from_array(w)
+    xb = [gpu.Buf.from_array(x) for x in xs]
+    ob = [gpu.Buf.empty((M, N)) for _ in range(2)]
+    streams = [gpu.Stream(), gpu.Stream()]
+    for rep in range(3):
+        for i in range(2):
+            gpu.check(gpu.lib().hy_lm_head_f32(xb[i].ptr, wb.ptr, None, M, Kd, N, ob[i].ptr, streams[i].h))
+    for s in streams:
+        s.synchronize()
+    for i in range(2):
+        check(ob[i].numpy(), xs[i].astype(np.float64) @ w.astype(np.float64).T, f"stream {i}")
+    for s in streams:
+        s.close()

@@ -107,6 +107,58 @@ def test_missing_file(hy, tmp_path):
 
 # ------------------------------------------------------------------ GPU: layer upload
 
+def decode_blocks(data, gtype, n):
+    """GGUF Q8_0 / Q4_0 bytes -> f32 with numpy, written from the block layout
+    (fp16 scale, then 32 int8, or 16 bytes whose low nibbles are elements 0..15 and
+    high nibbles 16..31, value nibble - 8)."""
+    bb = 34 if gtype == G.GGML_Q8_0 else 18
+    b = np.frombuffer(data, np.uint8).reshape(-1, bb)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)
+    if gtype == G.GGML_Q8_0:
+        q = b[:, 2:].view(np.int8).astype(np.float32)
+    else:
+        q = np.concatenate([(b[:, 2:] & 15), (b[:, 2:] >> 4)], axis=1).astype(np.float32) - 8
+    return (d * q).reshape(-1)[:n]
+
+
+@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_F16, G.GGML_BF16, G.GGML_Q8_0, G.GGML_Q4_0],
+                         ids=["f32", "f16", "bf16", "q8_0", "q4_0"])
+def test_tensor_f32_every_loader_type(hy, tmp_path, gtype):
+    """hy_gguf_tensor_f32 (read_tensor_data) gives back every type the reference loader
+    reads: float types exactly, block types as d * q from an independent decoder,
+    including a block whose fp16 scale is subnormal (kept, not flushed)."""
+    rng = np.random.default_rng(gtype)
+    a = (rng.standard_normal((5, 96)) * 3).astype(np.float32)
+    a[2, :32] = rng.standard_normal(32) * 1e-4      # scale ~2e-6: an fp16 subnormal
+    data, back = G.typed_tensor(a, gtype)
+    f = hy.Gguf(_write(tmp_path, "t.gguf", G.gguf_bytes([], [("w", gtype, [96, 5], data)])))
+    got = f.tensor_f32("w")
+    assert got.shape == (5, 96)
+    np.testing.assert_array_equal(got.view(np.uint32), back.reshape(5, 96).view(np.uint32))
+    if gtype in (G.GGML_Q8_0, G.GGML_Q4_0):
+        ref = decode_blocks(data, gtype, a.size).reshape(5, 96)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+        d = np.frombuffer(data[(2 * 3) * (34 if gtype == G.GGML_Q8_0 else 18):][:2], np.float16)[0]
+        assert 0 < abs(float(d)) < 6.1e-5 and np.abs(got[2, :32]).max() > 0
+    elif gtype == G.GGML_F16:
+        np.testing.assert_array_equal(got, a.astype(np.float16).astype(np.float32))
+    f.close()
+
+
+def test_tensor_f32_rejects_other_types_and_sizes(hy, tmp_path):
+    q41 = bytes(20 * 3)   # Q4_1: 20 bytes per block, a type the loader does not read
+    ts = [("q41", 3, [96, 1], q41), ("f", G.GGML_F32, [8, 2], np.zeros(16, np.float32).tobytes())]
+    f = hy.Gguf(_write(tmp_path, "o.gguf", G.gguf_bytes([], ts)))
+    with pytest.raises(hy.HyError):
+        f.tensor_f32("q41")
+    out = np.empty(15, np.float32)
+    with pytest.raises(hy.HyError):
+        hy.check(hy.lib().hy_gguf_tensor_f32(f.h, b"f", out.ctypes.data, out.size))
+    with pytest.raises(hy.HyError):
+        f.tensor_f32("missing")
+    f.close()
+
+
 SHAPE = dict(H=256, I=128, E=16, K=4)
 
 
@@ -185,8 +237,12 @@ def test_layer_from_gguf_mismatches_rejected(gpu, tmp_path):
     good = G.layer_tensors(layer, 0)
     cases = {
         "missing expert": [t for t in good if "ffn_expert_5_down" not in t[0]],
-        "wrong type": [(n, G.GGML_Q4_0, ne, d[: len(d) * 18 // 34]) if "expert_2_gate_up" in n else (n, gt, ne, d)
-                       for n, gt, ne, d in good],
+        "type that would change the weights (F16 into Q8_0)":
+            [(n, G.GGML_F16, ne, bytes(ne[0] * ne[1] * 2)) if "expert_2_gate_up" in n else (n, gt, ne, d)
+             for n, gt, ne, d in good],
+        "type the loader does not read (Q4_1)":
+            [(n, 3, ne, bytes(ne[0] * ne[1] // 32 * 20)) if "expert_3_down" in n else (n, gt, ne, d)
+             for n, gt, ne, d in good],
         "wrong shape": [(n, gt, [ne[0], ne[1] // 2], d[: len(d) // 2]) if "shared_down" in n else (n, gt, ne, d)
                         for n, gt, ne, d in good],
     }
@@ -207,12 +263,71 @@ def test_layer_from_gguf_mismatches_rejected(gpu, tmp_path):
     m.close()
 
 
+def _f32_layer(seed, H, I, E):
+    r = O.synth(seed, 0, O.T_ROUTER, 0, (E, H), 0.05)
+    gu = O.synth(seed, 0, O.T_GU, 0, (E, 2 * I, H), 0.05)
+    dn = O.synth(seed, 0, O.T_DN, 0, (E, H, I), 0.05)
+    sgu = O.synth(seed, 0, O.T_GU, E, (2 * I, H), 0.05)
+    sdn = O.synth(seed, 0, O.T_DN, E, (H, I), 0.05)
+    w = (0.5 + np.random.default_rng(seed).random(H)).astype(np.float32)
+    return r, gu, dn, sgu, sdn, w
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ftype,wtype", [(G.GGML_Q8_0, O.Q8_0), (G.GGML_Q4_0, O.Q4_0), (G.GGML_F16, O.F32),
+                                         (G.GGML_BF16, O.F32), (G.GGML_Q8_0, O.F32), (G.GGML_Q4_0, O.Q8_0)],
+                         ids=["q8_0", "q4_0", "f16->f32", "bf16->f32", "q8_0->f32", "q4_0->q8_0"])
+def test_layer_from_single_type_file(gpu, tmp_path, ftype, wtype):
+    """A file with every tensor in one type, as the reference converter writes it:
+    router and ffn_norm are read as f32 whatever their type; expert matrices go as
+    stored, become f32 in an F32 context, or Q4_0 re-encodes exactly into Q8_0.  The
+    stack (RMSNorm -> MoE -> residual) equals the oracle on the values read back."""
+    H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
+    r, gu, dn, sgu, sdn, w = _f32_layer(40 + ftype, H, I, E)
+    ts, back = G.typed_layer_tensors(r, gu, dn, sgu, sdn, 1, ftype, ffn_norm=w)
+    f = gpu.Gguf(_write(tmp_path, "one.gguf", G.gguf_bytes([], ts)))
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=64)
+    m.upload_gguf(0, f, 1)
+    f.close()
+    if wtype == O.F32:
+        layer = O.Layer(H, I, E, K, O.F32, back["router"], back["sgu"], back["sdn"], back["gu"], back["dn"])
+    else:   # the oracle computes on the file's own blocks (Q4_0 values are Q8_0 values)
+        def blocks(b, rows, cols):
+            return np.frombuffer(b, np.uint8).reshape(rows, O.row_bytes(ftype, cols))
+        raw = back["raw"]
+        layer = O.Layer(H, I, E, K, ftype, back["router"], blocks(raw["sgu"], 2 * I, H), blocks(raw["sdn"], H, I),
+                        np.stack([blocks(b, 2 * I, H) for b in raw["gu"]]),
+                        np.stack([blocks(b, H, I) for b in raw["dn"]]))
+    for T in (3, 40):
+        x = O.synth(300 + T, 0, O.T_X, 0, (T, H), 1.0)
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((T, H))
+        m.stack_forward(0, 1, xb, T, 1e-5, ob)
+        ref = O.moe_stack_qw([layer], [back["ffn_norm"]], x, eps=1e-5)
+        np.testing.assert_array_equal(ob.numpy().view(np.uint32), ref.view(np.uint32), err_msg=f"T={T}")
+    m.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ftype,wtype", [(G.GGML_F16, O.Q8_0), (G.GGML_Q8_0, O.Q4_0), (G.GGML_F32, O.Q4_0)])
+def test_layer_file_type_that_would_change_weights_rejected(gpu, tmp_path, ftype, wtype):
+    H, I, E, K = SHAPE["H"], SHAPE["I"], SHAPE["E"], SHAPE["K"]
+    r, gu, dn, sgu, sdn, w = _f32_layer(50, H, I, E)
+    ts, _ = G.typed_layer_tensors(r, gu, dn, sgu, sdn, 0, ftype)
+    f = gpu.Gguf(_write(tmp_path, "x.gguf", G.gguf_bytes([], ts)))
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=8)
+    with pytest.raises(gpu.HyError, match="would change the weights"):
+        m.upload_gguf(0, f, 0)
+    f.close()
+    m.close()
+
+
 # ------------------------------------------------------------------ GPU: attention + globals
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_F16, G.GGML_BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_F16, G.GGML_BF16, G.GGML_Q8_0, G.GGML_Q4_0],
+                         ids=["f32", "f16", "bf16", "q8_0", "q4_0"])
 def test_attention_from_gguf(gpu, tmp_path, gtype):
-    """blk.N.attn_* (F32 / F16 / BF16) uploaded from a file compute exactly what the
+    """blk.N.attn_* (any type the reference loader reads) uploaded from a file compute exactly what the
     same values uploaded directly compute; attn_norm.weight becomes the layer's input
     norm."""
     import hy_oracle_attn as A
@@ -251,8 +366,8 @@ def test_attention_gguf_rejects_bad_tensors(gpu, tmp_path):
         "missing k norm": [t for t in good if "attn_k_norm" not in t[0]],
         "wrong shape": [(n, gt, [ne[0] // 2, ne[1]], d[: len(d) // 2]) if "attn_qkv" in n else (n, gt, ne, d)
                         for n, gt, ne, d in good],
-        "quantized": [(n, G.GGML_Q8_0, ne, bytes(len(d) // 4 * 34 // 32)) if "attn_output" in n else (n, gt, ne, d)
-                      for n, gt, ne, d in good],
+        "type the loader does not read (Q4_1)": [(n, 3, ne, bytes(len(d) // 4 * 20 // 32)) if "attn_output" in n
+                                                  else (n, gt, ne, d) for n, gt, ne, d in good],
     }
     for case, ts in cases.items():
         f = gpu.Gguf(_write(tmp_path, "bad.gguf", G.gguf_bytes([], ts)))
@@ -263,7 +378,7 @@ def test_attention_gguf_rejects_bad_tensors(gpu, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("gtype", [G.GGML_F32, G.GGML_BF16, G.GGML_Q8_0], ids=["f32", "bf16", "q8_0"])
 def test_model_globals_from_gguf(gpu, tmp_path, gtype):
     """token_embd / output_norm / output from a file give the same logits as the same
     values uploaded directly."""
