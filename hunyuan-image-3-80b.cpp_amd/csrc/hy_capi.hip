@@ -327,6 +327,71 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     return HY_OK;
 }
 
+// ---- token -> expert dispatch of caller-given top-k pairs (hy_dispatch_pairs*)
+
+int check_dispatch_args(const int32_t* topi, const float* topw, uint32_t T, uint32_t K, uint32_t E,
+                        const int32_t* counts, const int32_t* offsets, const int32_t* pos) {
+    if (!topi || !topw || !counts || !offsets || !pos) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || T > 16384 || K == 0 || K > (uint32_t)hy::MAX_K || E == 0 || E > (uint32_t)hy::MAX_E || K > E)
+        return fail(HY_ERR_INVALID, "bad dispatch shape T=%u K=%u E=%u", T, K, E);
+    return HY_OK;
+}
+
+int dispatch_max_tiles(uint32_t T, uint32_t K, uint32_t E) { return (int)(((size_t)T * K + E * 7) / 8 + 1); }
+
+// sorted tokens, combine positions and weights, three tile arrays, meta, per-block counts
+size_t dispatch_ws_bytes(uint32_t T, uint32_t K, uint32_t E) {
+    const size_t pairs = (size_t)T * K;
+    return pairs * 4 * 3 + (size_t)dispatch_max_tiles(T, K, E) * 4 * 3 + (size_t)hy::META_INTS * 4 +
+           hy::dispatch_scratch_bytes((int)T, (int)K, (int)E);
+}
+
+// The three dispatch kernels over a workspace of dispatch_ws_bytes: every word of it
+// they read was written earlier in the same call, so it needs no clearing.
+hipError_t launch_dispatch_ws(const int32_t* topi, const float* topw, uint32_t T, uint32_t K, uint32_t E,
+                              int32_t* counts, int32_t* offsets, int32_t* pos, void* ws, hipStream_t s) {
+    const size_t pairs = (size_t)T * K;
+    const int max_tiles = dispatch_max_tiles(T, K, E);
+    int* srt = static_cast<int*>(ws);
+    int* cpos = srt + pairs;
+    float* cw = reinterpret_cast<float*>(cpos + pairs);
+    int* te = reinterpret_cast<int*>(cw + pairs);
+    int* ts = te + max_tiles;
+    int* tn = ts + max_tiles;
+    int* meta = tn + max_tiles;
+    int* dscr = meta + hy::META_INTS;
+    return hy::launch_dispatch(topi, topw, (int)T, (int)K, (int)E, 8, 0, counts, offsets, srt, pos, cpos, cw, te, ts,
+                               tn, meta, dscr, s);
+}
+
+// Scratch of hy_dispatch_pairs_noalloc: a file-scope device array, one copy on every
+// GPU the library runs on, held until the process ends (4 MiB covers the largest
+// call the entry point accepts: T = 16384, K = 16, E = 64 needs about 3.6 MB).  Host
+// code never passes the array's name to a kernel: that name is a host-side stand-in,
+// not a device address.  The device address comes from hipGetSymbolAddress, taken
+// once per device with that device current.
+constexpr size_t kDispatchScratchMax = (size_t)4 << 20;
+__device__ __align__(256) uint8_t scratch[kDispatchScratchMax];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device ordinal
+
+int scratch_of_device(void** out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(HY_ERR_HIP, "hipGetSymbolAddress of the dispatch scratch failed: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return HY_OK;
+}
+
 }  // namespace
 
 namespace hy {
@@ -738,31 +803,29 @@ int hy_topk_rows(const float* x, uint32_t rows, uint32_t n, uint32_t k, float* v
 
 int hy_dispatch_pairs(const int32_t* topi, const float* topw, uint32_t T, uint32_t K, uint32_t E, int32_t* counts,
                       int32_t* offsets, int32_t* pos, void* stream) {
-    if (!topi || !topw || !counts || !offsets || !pos) return fail(HY_ERR_INVALID, "null pointer");
-    if (T == 0 || T > 16384 || K == 0 || K > (uint32_t)hy::MAX_K || E == 0 || E > (uint32_t)hy::MAX_E || K > E)
-        return fail(HY_ERR_INVALID, "bad dispatch shape T=%u K=%u E=%u", T, K, E);
+    HY_TRY(check_dispatch_args(topi, topw, T, K, E, counts, offsets, pos));
     hipStream_t s = static_cast<hipStream_t>(stream);
     // scratch for the lists the layer forward also builds
-    const size_t pairs = (size_t)T * K;
-    const int max_tiles = (int)((pairs + E * 7) / 8 + 1);
-    void* scratch = nullptr;
-    const size_t dsp = hy::dispatch_scratch_bytes((int)T, (int)K, (int)E);
-    const size_t bytes = pairs * 4 * 3 + (size_t)max_tiles * 4 * 3 + (size_t)hy::META_INTS * 4 + dsp;
-    if (hipMalloc(&scratch, bytes) != hipSuccess) return fail(HY_ERR_NOMEM, "dispatch scratch");
-    int* srt = static_cast<int*>(scratch);
-    int* cpos = srt + pairs;
-    float* cw = reinterpret_cast<float*>(cpos + pairs);
-    int* te = reinterpret_cast<int*>(cw + pairs);
-    int* ts = te + max_tiles;
-    int* tn = ts + max_tiles;
-    int* meta = tn + max_tiles;
-    int* dscr = meta + hy::META_INTS;
-    hipError_t e = hy::launch_dispatch(topi, topw, (int)T, (int)K, (int)E, 8, 0, counts, offsets, srt, pos, cpos, cw,
-                                       te, ts, tn, meta, dscr, s);
+    void* ws = nullptr;
+    if (hipMalloc(&ws, dispatch_ws_bytes(T, K, E)) != hipSuccess) return fail(HY_ERR_NOMEM, "dispatch scratch");
+    hipError_t e = launch_dispatch_ws(topi, topw, T, K, E, counts, offsets, pos, ws, s);
     hipError_t e2 = hipStreamSynchronize(s);
-    (void)hipFree(scratch);
+    (void)hipFree(ws);
     if (e != hipSuccess || e2 != hipSuccess)
         return fail(HY_ERR_HIP, "dispatch failed: %s", hipGetErrorString(e != hipSuccess ? e : e2));
+    return HY_OK;
+}
+
+int hy_dispatch_pairs_noalloc(const int32_t* topi, const float* topw, uint32_t T, uint32_t K, uint32_t E,
+                              int32_t* counts, int32_t* offsets, int32_t* pos, void* stream) {
+    HY_TRY(check_dispatch_args(topi, topw, T, K, E, counts, offsets, pos));
+    const size_t bytes = dispatch_ws_bytes(T, K, E);
+    if (bytes > kDispatchScratchMax)
+        return fail(HY_ERR_INVALID, "dispatch of T=%u K=%u E=%u needs %zu bytes of scratch, more than the %zu this "
+                    "entry point holds", T, K, E, bytes, kDispatchScratchMax);
+    void* ws = nullptr;
+    HY_TRY(scratch_of_device(&ws));
+    HIP_TRY(launch_dispatch_ws(topi, topw, T, K, E, counts, offsets, pos, ws, static_cast<hipStream_t>(stream)));
     return HY_OK;
 }
 

@@ -113,6 +113,7 @@ _SIGS = {
     "hy_gguf_get_f32": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_float)]),
     "hy_moe_upload_layer_gguf": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint32]),
     "hy_dispatch_pairs": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]),
+    "hy_dispatch_pairs_noalloc": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]),
     "hy_device_synchronize": (C.c_int, []),
     "hy_stream_create": (C.c_int, [C.POINTER(_vp)]),
     "hy_stream_destroy": (C.c_int, [_vp]),

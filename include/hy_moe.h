@@ -252,6 +252,19 @@ int hy_dispatch_pairs(const int32_t* indices_dev, const float* weights_dev, uint
                       uint32_t E, int32_t* counts_dev, int32_t* offsets_dev, int32_t* pos_dev,
                       void* stream);
 
+/* hy_dispatch_pairs without any allocation: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and results; the
+ * workspace is a fixed 4 MiB array in device memory that each GPU holds until the
+ * process ends, enough for every shape hy_dispatch_pairs accepts (larger needs are
+ * rejected with HY_ERR_INVALID).  Stream-ordered: it returns without waiting, the
+ * outputs are ready when the stream gets there.  All calls on one GPU share that
+ * array, so calls that overlap on one GPU (different streams, or different threads
+ * without ordering) race and must be ordered by the caller. */
+int hy_dispatch_pairs_noalloc(const int32_t* indices_dev, const float* weights_dev, uint32_t T,
+                              uint32_t K, uint32_t E, int32_t* counts_dev, int32_t* offsets_dev,
+                              int32_t* pos_dev, void* stream);
+
 /* einsum_dispatch (src/hunyuan_moe_full.h:95-102): out[e][c][:] = sum of x[t][:] over
  * t with mask[t][e][c] (mask: one byte per entry). */
 int hy_einsum_dispatch(const float* x_dev, uint32_t T, uint32_t H, const uint8_t* mask_dev,
