@@ -1,17 +1,20 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X MoE feed-forward block (HunyuanImage-3 shape).
 
-Default workload (what the one JSON line reports): one MoE layer, hidden 4096,
-64 routed experts + 1 shared, FFN width 3072, top-8, GGUF Q8_0 weights, T=512
-tokens per step (prefill batch), inputs resident in HBM.  A step is one full
-layer forward: Q8_0 activation quantization, router + top-8, dispatch, gate_up +
-SwiGLU, down + combine.  Weights are random-init N(0, 0.02) (synthetic, generated
-on the device), activations N(0, 1).
+Default workload (what the one JSON line reports): the 32-layer stack of the MoE block
+with GGUF Q8_0 weights, all resident in HBM (about 84 GB): per layer RMSNorm (eps 1e-5)
+-> MoE (hidden 4096, 64 routed + 1 shared experts of width 3072, top-8) -> residual
+add, T=4096 tokens per step, inputs resident in HBM.  A step is the whole stack;
+tokens/s = T / step time.  Weights are random-init N(0, 0.02) seeded by layer index
+(synthetic, generated on the device), activations N(0, 1).  The same line carries the
+decode (Q4_0, T=1 and T=8) and the Zipf-skewed image-token (Q4_0, T=4096) layers as
+`extras`, each timed in its own region.
 
-Other workloads (--config): c1 F32 T=16, c3 Q4_0 decode (--tokens 1/2/4/8),
-c4 Q4_0 T=4096 Zipf-skewed routing, c5 32-layer Q8_0 stack T=4096.
+Other workloads (--config): c1 F32 T=16, c2 Q8_0 T=512, c3 Q4_0 decode (--tokens
+1/2/4/8), c4 Q4_0 T=4096 Zipf-skewed routing, c5 the stack (default).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--no-cpu] [--no-extras]
+    python bench.py --mfma-probe          # the grouped GEMM's per-block instruction mix alone
     python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
     python bench.py --gguf-load /tmp/l.gguf [--config c2]   # layer load from a GGUF file
     python bench.py --attn [--tokens 4096]   # attention half of a decoder layer (fp32)
@@ -38,11 +41,11 @@ H, I, E, K = 4096, 3072, 64, 8
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_INT8 = 5.0e15         # ops/s, dense int8 MFMA
 PEAK_FP32_MFMA = 157.3e12  # FLOP/s, dense fp32 MFMA
-# Ceiling of a grouped int8 GEMM that keeps ggml's per-block fp32 rescale: every 32-MAC
-# block partial costs one int->float conversion and one fma on the vector ALUs, so the
-# rate is bounded by the VALU issue rate, not the matrix cores (measured with the
-# compute-only probe of the kernels' per-block instruction mix, bench.py --mfma-probe)
-RESCALE_CEILING = 1.62e15
+# The grouped int8 GEMM keeps ggml's per-block fp32 rescale: every 32-MAC block partial
+# costs an int->float conversion and an fma on the vector ALUs, and a rank-1 MFMA forms
+# the scale products.  Its ceiling is measured in the same run by a compute-only probe
+# of exactly that per-block instruction mix (hy_probe_block_mix, probe_block_mix below)
+PROBE_WGS, PROBE_ITERS = 512, 4000
 ATTN = dict(H=4096, nh=32, nkv=8, hd=128)   # HunyuanImage-3 attention shape
 PARAMS_PER_EXPERT = 3 * H * I
 BYTES = {0: 4.0, 8: 34.0 / 32.0, 2: 18.0 / 32.0}   # bytes per weight element
@@ -128,6 +131,32 @@ def measured_traffic(workload, kname, path=TRAFFIC_TABLE):
     except (OSError, ValueError):
         return None
     return None
+
+
+def probe_block_mix(hy, variant=0, reps=3):
+    """Rate (block-dot int8 ops/s) of the grouped GEMM's per-block instruction mix with
+    no memory traffic: the best of `reps` launches of hy_probe_block_mix (variant 0: the
+    whole mix; 1: its four MFMAs only; 2: its 64 vector ops only)."""
+    out = hy.Buf.empty((PROBE_WGS * 512,))
+    st = hy.Stream()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    hy.check(hy.lib().hy_probe_block_mix(variant, PROBE_WGS, 100, out.ptr, st.h))
+    best = None
+    for _ in range(reps):
+        hy.check(hy.lib().hy_event_record(ev0, st.h))
+        hy.check(hy.lib().hy_probe_block_mix(variant, PROBE_WGS, PROBE_ITERS, out.ptr, st.h))
+        hy.check(hy.lib().hy_event_record(ev1, st.h))
+        st.synchronize()
+        ms = hy.C.c_float()
+        hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+        best = ms.value if best is None else min(best, ms.value)
+    for e in (ev0, ev1):
+        hy.lib().hy_event_destroy(e)
+    st.close()
+    ops = PROBE_WGS * 8.0 * PROBE_ITERS * 2 * 32 * 32 * 32 * 2
+    return ops / (best / 1e3)
 
 
 def copy_probe(hy, mib, steps):
@@ -537,7 +566,7 @@ def cpu_baseline(wl, seed, budget_s=15.0):
     return res
 
 
-def run_moe(hy, wl, steps, warmup, seed, graph=False, tokens=None):
+def run_moe(hy, wl, steps, warmup, seed, graph=False, tokens=None, mix_ceiling=None):
     """Times `steps` steps of one MoE workload (after `warmup`) and profiles the
     kernels in a second pass; returns the result fields of its JSON line."""
     wl = dict(wl)
@@ -628,9 +657,11 @@ def run_moe(hy, wl, steps, warmup, seed, graph=False, tokens=None):
     else:
         roof = {"bound": "mfma", "kernel": dom, "achieved": ops / avg_s / 1e12, "peak": PEAK_INT8 / 1e12,
                 "unit": "TFLOP/s", "frac": ops / avg_s / PEAK_INT8, "traffic": hbm_measured,
-                "algorithmic_ops_per_launch": ops, "avg_launch_ms": avg_s * 1e3,
-                "rescale_ceiling": {"peak": RESCALE_CEILING / 1e12, "unit": "TOP/s",
-                                    "frac": ops / avg_s / RESCALE_CEILING}}
+                "algorithmic_ops_per_launch": ops, "avg_launch_ms": avg_s * 1e3}
+        if mix_ceiling:
+            roof["rescale_ceiling"] = {"peak": mix_ceiling / 1e12, "unit": "TOP/s",
+                                       "frac": ops / avg_s / mix_ceiling,
+                                       "source": "hy_probe_block_mix, the per-block mix alone, same run"}
     top8 = float(np.sort(counts)[::-1][:8].sum() / max(1, counts.sum()))
     res = {
         "value": tokens_per_s, "ms_per_step": ms_per_step,
@@ -674,6 +705,8 @@ def main():
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="rate of the grouped GEMM's per-block instruction mix alone (and of its halves)")
     ap.add_argument("--attn", action="store_true", help="time the attention half instead of the MoE layer")
     ap.add_argument("--cache", type=int, default=0, metavar="L",
                     help="with --attn: decode T (--tokens, default 1) new tokens against L cached positions")
@@ -701,8 +734,15 @@ def main():
     if a.model:
         model_main(a, hy)
         return
+    if a.mfma_probe:
+        rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"))}
+        print(json.dumps({"probe": "block_mix", "work_groups": PROBE_WGS, "iters_per_wave": PROBE_ITERS,
+                          "block_dot_ops_per_s": rates, "frac_of_dense_int8": rates["mix"] / PEAK_INT8}),
+              flush=True)
+        return
     wl = WORKLOADS[a.config]
-    r = run_moe(hy, wl, a.steps, a.warmup, a.seed, graph=a.graph, tokens=a.tokens)
+    mix = probe_block_mix(hy) if wl["wtype"] != 0 and wl["T"] > 16 else None
+    r = run_moe(hy, wl, a.steps, a.warmup, a.seed, graph=a.graph, tokens=a.tokens, mix_ceiling=mix)
     print(f"bench: {r['config']['workload']} {r['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
     res = {"metric": "MoE-layer tokens/sec + achieved HBM GB/s / int8 MFMA util, 1 MI355X",
            "value": r.pop("value"), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -712,7 +752,8 @@ def main():
     if not a.no_extras and a.config == "c5" and not a.tokens:
         extras = {}
         for name, cfg, toks, mult in EXTRAS:
-            e = run_moe(hy, WORKLOADS[cfg], a.steps * mult, a.warmup, a.seed, graph=a.graph, tokens=toks)
+            e = run_moe(hy, WORKLOADS[cfg], a.steps * mult, a.warmup, a.seed, graph=a.graph, tokens=toks,
+                        mix_ceiling=mix)
             print(f"bench: {name} {e['ms_per_step']:.4f} ms/step", file=sys.stderr, flush=True)
             extras[name] = {"workload": e["config"]["workload"], "tokens": e["config"]["tokens"],
                             "value": e["value"], "unit": "tokens/s", "ms_per_step": e["ms_per_step"],

@@ -1,0 +1,99 @@
+// hy_probe.hip -- compute-only probe of the grouped GEMM's per-block instruction mix.
+//
+// Each wave repeats, `iters` times, exactly the math the grouped int8 GEMM issues for
+// one 32-wide GGUF block of its two 32x32 output tiles (hy_mfma.hip):
+//   * two v_mfma_i32_32x32x32_i8: the exact int32 block dots of the two tiles;
+//   * two rank-1 v_mfma_f32_32x32x16_f16: the 32x32 scale products d_w * d_x;
+//   * 32 v_cvt_f32_i32 + 32 v_fmac_f32: acc = fmaf((float)S, C, acc) per output.
+// No memory traffic, no LDS, no barriers; launched at the GEMM's occupancy (8-wave
+// work groups, two per CU, at most 128 VGPRs: four waves per SIMD).  Its rate is the
+// ceiling the GEMM's instruction mix allows on this part; variants time the matrix
+// and vector halves alone.
+#include "hy_device.hpp"
+#include "hy_launch.hpp"
+
+namespace hy {
+
+namespace {
+
+typedef int v16i_p __attribute__((ext_vector_type(16)));
+typedef float v16f_p __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h_p __attribute__((ext_vector_type(8)));
+typedef int v4i_p __attribute__((ext_vector_type(4)));
+
+constexpr int PROBE_THREADS = 512;
+
+// VARIANT 0: the full per-block mix; 1: the four MFMAs only; 2: the 64 vector ops only
+template <int VARIANT>
+__global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, int seed, float* __restrict__ out) {
+    const int lane = threadIdx.x % WAVE;
+    float acc0[16], acc1[16];
+    for (int v = 0; v < 16; v++) {
+        acc0[v] = 0.0f;
+        acc1[v] = 0.0f;
+    }
+    v4i_p A0 = {lane, seed, 3, 4}, A1 = {5, 6, seed, 7}, B = {1, 2, seed, 5};
+    v8h_p xa = {}, xb = {};
+    xb[0] = (_Float16)(float)(seed & 7);
+    const v16i_p zi = {};
+    const v16f_p zf = {};
+    v16i_p S0 = zi, S1 = zi;
+    v16f_p C0 = zf, C1 = zf;
+    if (VARIANT == 2)
+        for (int v = 0; v < 16; v++) {
+            S0[v] = v * seed + lane;
+            S1[v] = v + seed;
+            C0[v] = 0.01f * (float)(v + seed);
+            C1[v] = 0.02f * (float)v;
+        }
+    for (int it = 0; it < iters; it++) {
+        xa[0] = (_Float16)(float)(it & 7);
+        A0.x += 1;
+        if (VARIANT == 0) {
+            S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zi, 0, 0, 0);
+            S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zi, 0, 0, 0);
+            C0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa, xb, zf, 0, 0, 0);
+            C1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xb, xa, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
+                acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
+            }
+        } else if (VARIANT == 1) {
+            // chained through the accumulators so that nothing is hoisted
+            S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, S0, 0, 0, 0);
+            S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, S1, 0, 0, 0);
+            C0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa, xb, C0, 0, 0, 0);
+            C1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xb, xa, C1, 0, 0, 0);
+        } else {
+            // the 64 vector ops; the integer sources change per iteration (32 more adds)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                S0[v] += 3;
+                S1[v] += 5;
+                acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
+                acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
+            }
+        }
+    }
+    float r = 0.0f;
+    for (int v = 0; v < 16; v++) r += acc0[v] + acc1[v] + (float)S0[v] + (float)S1[v] + C0[v] + C1[v];
+    out[(size_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = r;
+}
+
+}  // namespace
+
+size_t probe_block_mix_out_floats(int work_groups) { return (size_t)work_groups * PROBE_THREADS; }
+
+hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int seed, float* out, hipStream_t s) {
+    const dim3 grid((unsigned)work_groups), blk(PROBE_THREADS);
+    if (variant == 1)
+        hipLaunchKernelGGL(block_mix_kernel<1>, grid, blk, 0, s, iters, seed, out);
+    else if (variant == 2)
+        hipLaunchKernelGGL(block_mix_kernel<2>, grid, blk, 0, s, iters, seed, out);
+    else
+        hipLaunchKernelGGL(block_mix_kernel<0>, grid, blk, 0, s, iters, seed, out);
+    return hipGetLastError();
+}
+
+}  // namespace hy

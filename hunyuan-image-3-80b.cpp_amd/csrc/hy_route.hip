@@ -201,12 +201,10 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
         const int items = ((T + tpw - 1) / tpw) * ((E + epw - 1) / epw);
         return dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES);
     };
-    if (T == 1) {
+    if (T <= 16) {
+        // decode batches: one (token, expert) item per wave, T x E waves; a wave that
+        // covers several tokens serialises their dot products (9.3 vs 4.5 us at T=8)
         hipLaunchKernelGGL((router_logits_kernel<1, 1>), grid_for(1, 1), blk, 0, s, x, wr, T, H, E, logits);
-    } else if (T <= 2) {
-        hipLaunchKernelGGL((router_logits_kernel<2, 1>), grid_for(2, 1), blk, 0, s, x, wr, T, H, E, logits);
-    } else if (T <= 4) {
-        hipLaunchKernelGGL((router_logits_kernel<4, 1>), grid_for(4, 1), blk, 0, s, x, wr, T, H, E, logits);
     } else if (T <= 32) {
         hipLaunchKernelGGL((router_logits_kernel<8, 1>), grid_for(8, 1), blk, 0, s, x, wr, T, H, E, logits);
     } else {
