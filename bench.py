@@ -15,6 +15,7 @@ Other workloads (--config): c1 F32 T=16, c2 Q8_0 T=512, c3 Q4_0 decode (--tokens
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--no-cpu] [--no-extras]
     python bench.py --mfma-probe          # the grouped GEMM's per-block instruction mix alone
+    python bench.py --stream-probe 864    # HBM read rate of the decode GEMV's streams
     python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
     python bench.py --gguf-load /tmp/l.gguf [--config c2]   # layer load from a GGUF file
     python bench.py --attn [--tokens 4096]   # attention half of a decoder layer (fp32)
@@ -157,6 +158,40 @@ def probe_block_mix(hy, variant=0, reps=3):
     st.close()
     ops = PROBE_WGS * 8.0 * PROBE_ITERS * 2 * 32 * 32 * 32 * 2
     return ops / (best / 1e3)
+
+
+def stream_probe(hy, waves=864, kb_per_wave=144, sets=8, launches=40):
+    """HBM read rate of the decode GEMV's access pattern: `waves` single-wave streams of
+    kb_per_wave KB each (864 x 144 KB is the Q4_0 T=1 gate/up launch: 9 experts x 96
+    row groups of 64 rows x 4096 columns), rotating over `sets` separate buffers so the
+    256 MB Infinity Cache cannot serve a repeat; variant 1 reads the same bytes with a
+    grid-stride vector loop."""
+    per = waves * kb_per_wave * 1024
+    buf = hy.Buf(per * sets, np.uint8)
+    hy.check(hy.lib().hy_memset(buf.ptr, 1, per * sets))
+    out = hy.Buf.empty((waves * 64,))
+    st = hy.Stream()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    res = {}
+    for variant, name in ((0, "dma_streams"), (1, "vector_grid_stride")):
+        for i in range(sets):
+            hy.check(hy.lib().hy_probe_stream(variant, buf.ptr + i * per, per, waves, out.ptr, st.h))
+        hy.check(hy.lib().hy_event_record(ev0, st.h))
+        for i in range(launches):
+            hy.check(hy.lib().hy_probe_stream(variant, buf.ptr + (i % sets) * per, per, waves, out.ptr, st.h))
+        hy.check(hy.lib().hy_event_record(ev1, st.h))
+        st.synchronize()
+        ms = hy.C.c_float()
+        hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+        t = ms.value / launches / 1e3
+        res[name] = {"us_per_launch": t * 1e6, "GBps": per / t / 1e9, "frac_of_8TBps": per / t / PEAK_HBM}
+    for e in (ev0, ev1):
+        hy.lib().hy_event_destroy(e)
+    st.close()
+    print(json.dumps({"probe": "stream_read", "waves": waves, "bytes_per_wave": kb_per_wave * 1024,
+                      "bytes_per_launch": per, "rotating_sets": sets, "launches": launches, **res}), flush=True)
 
 
 def copy_probe(hy, mib, steps):
@@ -705,6 +740,8 @@ def main():
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
+    ap.add_argument("--stream-probe", type=int, default=0, metavar="WAVES",
+                    help="HBM read rate of WAVES single-wave 144 KB streams (864: the decode T=1 gate/up shape)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="rate of the grouped GEMM's per-block instruction mix alone (and of its halves)")
     ap.add_argument("--attn", action="store_true", help="time the attention half instead of the MoE layer")
@@ -733,6 +770,9 @@ def main():
         return
     if a.model:
         model_main(a, hy)
+        return
+    if a.stream_probe:
+        stream_probe(hy, waves=a.stream_probe)
         return
     if a.mfma_probe:
         rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"))}

@@ -1,4 +1,5 @@
-// hy_probe.hip -- compute-only probe of the grouped GEMM's per-block instruction mix.
+// hy_probe.hip -- measurement probes: the grouped GEMM's per-block instruction mix
+// (compute only) and the HBM read rate of the decode GEMV's access pattern.
 //
 // Each wave repeats, `iters` times, exactly the math the grouped int8 GEMM issues for
 // one 32-wide GGUF block of its two 32x32 output tiles (hy_mfma.hip):
@@ -11,6 +12,7 @@
 // and vector halves alone.
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
+#include "hy_lds.hpp"
 
 namespace hy {
 
@@ -81,7 +83,66 @@ __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, 
     out[(size_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = r;
 }
 
+// ---- read-rate probes (the decode GEMV's streams) ------------------------------
+// Variant 0: one wave per work group streams its own contiguous range with 16-byte
+// global->LDS copies into a private 3-step ring of 8 KB steps (8 copies of 1 KB per
+// step, two steps in flight), as the decode GEMV streams one 64-row group of an
+// expert; it reads back one word per step so every step is consumed.  Variant 1: a
+// grid-stride 16-byte vector read of the same bytes into registers.
+constexpr int STREAM_STEP = 8192, STREAM_RING = 3;
+
+__global__ __launch_bounds__(WAVE) void stream_dma_kernel(const uint8_t* __restrict__ base, uint32_t steps,
+                                                          float* __restrict__ out) {
+    __shared__ __align__(16) uint8_t ring[STREAM_RING][STREAM_STEP];
+    const int lane = threadIdx.x;
+    const uint8_t* src = base + (size_t)blockIdx.x * steps * STREAM_STEP + 16u * lane;
+    auto issue = [&](uint32_t st) {
+        uint8_t* dst = ring[st % STREAM_RING];
+#pragma unroll
+        for (int c = 0; c < STREAM_STEP / 1024; c++) g2l16(src + (size_t)st * STREAM_STEP + c * 1024, dst + c * 1024);
+    };
+    constexpr int LOADS = STREAM_STEP / 1024;
+    for (uint32_t i = 0; i < STREAM_RING - 1 && i < steps; i++) issue(i);
+    uint32_t acc = 0;
+    for (uint32_t st = 0; st < steps; st++) {
+        if (st + 1 < steps)
+            MM_WAIT_VM_LGKM(LOADS);   // step st landed, step st + 1 may stay in flight
+        else
+            MM_WAIT_VM_LGKM(0);
+        acc += lds_b32(ring[st % STREAM_RING] + 4 * lane);
+        lds_wait();
+        // every lane has read its word of slot st before the refill of that slot
+        if (st + STREAM_RING - 1 < steps) issue(st + STREAM_RING - 1);
+    }
+    out[(size_t)blockIdx.x * WAVE + lane] = (float)acc;
+}
+
+__global__ __launch_bounds__(256) void stream_vec_kernel(const int4* __restrict__ p, size_t n16,
+                                                         float* __restrict__ out) {
+    const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, nth = (size_t)gridDim.x * 256;
+    int a = 0;
+    for (size_t i = tid; i < n16; i += nth) {
+        const int4 v = p[i];
+        a ^= v.x + v.y + v.z + v.w;
+    }
+    out[tid] = (float)a;
+}
+
 }  // namespace
+
+size_t probe_stream_step_bytes() { return STREAM_STEP; }
+
+hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s) {
+    if (variant == 0) {
+        const uint32_t steps = (uint32_t)(bytes / ((size_t)waves * STREAM_STEP));
+        hipLaunchKernelGGL(stream_dma_kernel, dim3((unsigned)waves), dim3(WAVE), 0, s,
+                           static_cast<const uint8_t*>(buf), steps, out);
+    } else {
+        hipLaunchKernelGGL(stream_vec_kernel, dim3((unsigned)(waves * WAVE / 256)), dim3(256), 0, s,
+                           static_cast<const int4*>(buf), bytes / 16, out);
+    }
+    return hipGetLastError();
+}
 
 size_t probe_block_mix_out_floats(int work_groups) { return (size_t)work_groups * PROBE_THREADS; }
 

@@ -294,6 +294,14 @@ int hy_copy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
  * variant 1 runs only the four MFMAs, variant 2 only the 64 vector ops.  Each wave does
  * iters * 2 * 32*32*32 block-dot MACs; out_dev holds work_groups * 512 floats. */
 int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream);
+/* Measurement only, no counterpart in the reference: reads `bytes` of buf_dev as the
+ * decode GEMV streams its weights.  Variant 0: `waves` single-wave work groups, each
+ * streaming its own contiguous bytes / waves with 16-byte global->LDS copies through
+ * a private 3-step ring of 8 KB steps (bytes a multiple of waves x 8192); variant 1: a
+ * grid-stride 16-byte vector read by waves x 64 threads (waves a multiple of 4).
+ * out_dev holds waves x 64 floats. */
+int hy_probe_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev,
+                    void* stream);
 int hy_device_synchronize(void);
 int hy_stream_create(void** stream);
 int hy_stream_destroy(void* stream);

@@ -1,0 +1,40 @@
+"""The measurement probes bench.py reports ceilings from: they must do the work they
+claim.  The stream probe's per-lane checksum equals the bytes it read; the block-mix
+probe's variants run and give finite results; bad arguments are rejected."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_stream_probe_reads_every_step(gpu):
+    """Each wave's lane l adds word l of every 8 KB step it streamed: with the buffer set
+    to bytes of 1, every lane's sum is steps x 0x01010101, so a step read before its copy
+    landed (or skipped) would show."""
+    waves, steps = 96, 5
+    nbytes = waves * steps * 8192
+    buf = gpu.Buf(nbytes, np.uint8)
+    gpu.check(gpu.lib().hy_memset(buf.ptr, 1, nbytes))
+    out = gpu.Buf.empty((waves * 64,))
+    gpu.check(gpu.lib().hy_probe_stream(0, buf.ptr, nbytes, waves, out.ptr, None))
+    np.testing.assert_array_equal(out.numpy(), np.full(waves * 64, np.float32(steps * 0x01010101)))
+    gpu.check(gpu.lib().hy_probe_stream(1, buf.ptr, nbytes, waves, out.ptr, None))
+    assert np.all(np.isfinite(out.numpy()))
+
+
+def test_stream_probe_rejects_bad_sizes(gpu):
+    buf = gpu.Buf(8192 * 8, np.uint8)
+    out = gpu.Buf.empty((8 * 64,))
+    for variant, nbytes, waves in ((0, 8192 * 8 - 16, 8), (0, 8192 * 8, 0), (2, 8192 * 8, 8), (1, 8192 * 6, 6)):
+        with pytest.raises(gpu.HyError):
+            gpu.check(gpu.lib().hy_probe_stream(variant, buf.ptr, nbytes, waves, out.ptr, None))
+
+
+def test_block_mix_probe_variants(gpu):
+    wgs = 8
+    out = gpu.Buf.empty((wgs * 512,))
+    for variant in (0, 1, 2):
+        gpu.check(gpu.lib().hy_probe_block_mix(variant, wgs, 20, out.ptr, None))
+        assert np.all(np.isfinite(out.numpy()))
+    with pytest.raises(gpu.HyError):
+        gpu.check(gpu.lib().hy_probe_block_mix(3, wgs, 20, out.ptr, None))
