@@ -514,20 +514,40 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(Decod
     }
     if (tid < MAX_E) cnt_s[tid] = 0;
     __syncthreads();
-    // ---- dispatch: rank of each pair inside its expert, k-major then token: the
-    // pairs of earlier ranks (any token) plus those of the same rank and earlier tokens
+    // ---- dispatch: rank of each pair inside its expert in k-major order (all pairs of
+    // earlier ranks, then the same rank's earlier tokens).  Thread q takes the q-th pair
+    // of that order (token q % T, rank q / T); the pairs before it with the same expert
+    // are counted from each wave's ballots of the expert ids' six bits.
+    static_assert(MAX_E <= 64 && MAX_DECODE_PAIRS <= ROUTER_WAVES * WAVE, "six id bits, one pair per thread");
+    __shared__ unsigned long long bal_s[ROUTER_WAVES][7];
     const int P = T * K;
-    const int pt = tid / K, pk = tid - pt * K;  // this thread's pair (token, rank)
-    if (tid < P) {
-        const int e = sel_e[tid];
-        int rank = 0;
-        for (int kq = 0; kq < pk; kq++)
-            for (int tq = 0; tq < T; tq++) rank += sel_e[tq * K + kq] == e;
-        for (int tq = 0; tq < pt; tq++) rank += sel_e[tq * K + pk] == e;
-        rank_s[tid] = rank;
-        atomicAdd(&cnt_s[e], 1);
+    const bool qv = tid < P;
+    const int qt = tid % T, qk = tid / T;
+    const int qe = qv ? sel_e[qt * K + qk] : 0;
+    {
+        unsigned long long b[7];
+#pragma unroll
+        for (int i = 0; i < 6; i++) b[i] = __ballot(qv && ((qe >> i) & 1));
+        b[6] = __ballot(qv);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < 7; i++) bal_s[wave][i] = b[i];
     }
     __syncthreads();
+    if (qv) {
+        int rank = 0;
+        for (int w = 0; w <= wave; w++) {
+            unsigned long long m = bal_s[w][6];
+#pragma unroll
+            for (int i = 0; i < 6; i++) m &= ((qe >> i) & 1) ? bal_s[w][i] : ~bal_s[w][i];
+            if (w == wave) m &= (1ull << lane) - 1ull;
+            rank += __popcll(m);
+        }
+        rank_s[qt * K + qk] = rank;
+        atomicAdd(&cnt_s[qe], 1);
+    }
+    __syncthreads();
+    const int pt = tid / K;  // this thread's pair in token order (token pt, rank tid % K)
     const int NT = a.NT;
     if (wave == 0) {
         const int c = lane < E ? cnt_s[lane] : 0;
