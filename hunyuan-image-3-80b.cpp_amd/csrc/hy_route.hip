@@ -504,9 +504,20 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(Decod
     __shared__ float sel_w[MAX_DECODE_PAIRS];
     __shared__ int rank_s[MAX_DECODE_PAIRS], pos_s[MAX_DECODE_PAIRS];
     __shared__ int cnt_s[MAX_E], off_s[MAX_E + 1], toff_s[MAX_E + 2];
-    for (int t = wave; t < T; t += ROUTER_WAVES) {
-        const float v = lane < E ? a.logits[(size_t)t * E + lane] : 0.0f;
-        topk_wave(v, E, K, a.norm, a.scale, lane, sel_w + t * K, sel_e + t * K);
+    // a wave's tokens t = wave + 4i: all their logits rows are loaded before the first
+    // selection, so the loads' latency is paid once
+    constexpr int TPWV = (16 + ROUTER_WAVES - 1) / ROUTER_WAVES;  // decode batches: T <= 16
+    float lv[TPWV];
+#pragma unroll
+    for (int i = 0; i < TPWV; i++) {
+        const int t = wave + i * ROUTER_WAVES;
+        lv[i] = (t < T && lane < E) ? a.logits[(size_t)t * E + lane] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TPWV; i++) {
+        const int t = wave + i * ROUTER_WAVES;
+        if (t >= T) break;
+        topk_wave(lv[i], E, K, a.norm, a.scale, lane, sel_w + t * K, sel_e + t * K);
         if (lane < K) {
             a.topw[t * K + lane] = sel_w[t * K + lane];
             a.topi[t * K + lane] = sel_e[t * K + lane];
@@ -610,6 +621,8 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
                                float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, int NT,
                                int has_shared, int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos,
                                float* comb_w, int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s) {
+    // one work group selects and lists every pair: T <= 16 tokens (4 per wave), T*K <= 256 pairs
+    if (T < 1 || T > 16 || T * K > MAX_DECODE_PAIRS || E > MAX_E) return hipErrorInvalidValue;
     hipError_t e = launch_router_q(x, wr, T, H, E, K, norm, scale, logits, topw, topi, nullptr, nullptr, nullptr, s,
                                    /*logits_only=*/true);
     if (e != hipSuccess) return e;
