@@ -318,8 +318,8 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     // agent-scope release per work group, which writes back the XCD's L2: it made the
     // launch several times slower.)
     HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
-        return hy::launch_gemv_down(wt, routed_bound + shared_tiles, 0, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf,
-                                    iT, H, I, E, K, c->y, nullptr, nullptr, s);
+        return hy::launch_gemv_down(wt, routed_bound + shared_tiles, dn_view(c, L), R, c->hq, c->hd, c->hs, c->hf, iT,
+                                    H, I, E, K, c->y, s);
     }));
     HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {
         return hy::launch_combine(R, c->y, iT, H, K, has_shared, resid, out, s);

@@ -18,8 +18,7 @@
 // The down kernel's work item is (tile, 4 groups of 64 output rows); every tile
 // (routed and shared, one launch) writes y[slot][row], then the combine kernel forms
 //   out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e * y_e[t] )
-// (src/hunyuan_moe_full.cpp:503-515, einsum_combine order :387-397).  The fused
-// shared-tile combine (mode 2) stays available for callers that want one launch.
+// (src/hunyuan_moe_full.cpp:503-515, einsum_combine order :387-397).
 #include <utility>
 
 #include "hy_device.hpp"
@@ -77,17 +76,15 @@ struct GvArgs {
     float* hd;
     int* hs;
     float* hf;
-    float* y;           // mode 1 output / mode 2 input
-    const float* resid;
-    float* out;
+    float* y;           // mode 1 output
 };
 
 template <int WT, int NT, int MODE>
 __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int tok_s[NT], slot_s[NT];
-    // mode 1 covers every tile (routed and shared); mode 2 the shared tiles only
-    const int tile = (MODE == 2) ? a.R.meta[0] + (int)blockIdx.x : (int)blockIdx.x;
+    // mode 1 covers every tile, routed and shared
+    const int tile = (int)blockIdx.x;
     if (tile >= a.R.meta[1]) return;
     const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
@@ -254,16 +251,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (i >= n) break;
-            if (MODE == 1) {
-                a.y[(size_t)slot_s[i] * a.H + row] = acc[i];
-            } else {
-                const int t = tok_s[i];
-                float comb = 0.0f;
-                for (int k = 0; k < a.K; k++)
-                    comb = fmaf(a.R.comb_w[t * a.K + k], a.y[(size_t)a.R.comb_pos[t * a.K + k] * a.H + row], comb);
-                const float o = acc[i] + comb;
-                a.out[(size_t)t * a.H + row] = a.resid ? a.resid[(size_t)t * a.H + row] + o : o;
-            }
+            a.y[(size_t)slot_s[i] * a.H + row] = acc[i];
         }
     }
 }
@@ -566,25 +554,24 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     a.nx = a.T < GEMV_NT ? a.T : GEMV_NT;
     const dim3 grid_v(tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
     const dim3 grid_q(tiles, a.n_groups);
-    constexpr int QM = MODE == 2 ? 1 : MODE;  // mode 2 (fused shared combine) only in gemv_kernel
     switch (wtype) {
     case HY_TYPE_Q8_0:
-        if (MODE != 2 && gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
-            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, QM, 2>), grid_q, dim3(GQ_THREADS),
+        if (gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE, 2>), grid_q, dim3(GQ_THREADS),
                                gemv_q_smem<HY_TYPE_Q8_0>(2), s, a);
         else
             hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
                                gemv_smem(wtype, a.Kd), s, a);
         break;
     case HY_TYPE_Q4_0:
-        if (MODE != 2 && gemv_q_fits<HY_TYPE_Q4_0>(a.Kd)) {
+        if (gemv_q_fits<HY_TYPE_Q4_0>(a.Kd)) {
             // tiles is the host's bound on the routed + shared tiles: the deeper ring
             // when every launched wave is resident at once
             if ((long)tiles * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3)))
-                hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM, 3>), grid_q, dim3(GQ_THREADS),
+                hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE, 3>), grid_q, dim3(GQ_THREADS),
                                    gemv_q_smem<HY_TYPE_Q4_0>(3), s, a);
             else
-                hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, QM, 2>), grid_q, dim3(GQ_THREADS),
+                hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE, 2>), grid_q, dim3(GQ_THREADS),
                                    gemv_q_smem<HY_TYPE_Q4_0>(2), s, a);
         } else {
             hipLaunchKernelGGL((gemv_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE>), grid_v, dim3(GV_THREADS),
@@ -602,15 +589,15 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
 hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
                           int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
                           hipStream_t s) {
-    GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, 0, hq, hd, hs, hf, nullptr, nullptr, nullptr};
+    GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, 0, hq, hd, hs, hf, nullptr};
     return gemv_launch<0>(wtype, max_tiles, s, a);
 }
 
-hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
-                            const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
-                            int E, int K, float* y, const float* resid, float* out, hipStream_t s) {
-    GvArgs a{W, R, hq, hd, hs, hf, T, H, I, E, K, I, H / 64, 0, nullptr, nullptr, nullptr, nullptr, y, resid, out};
-    return mode == 0 ? gemv_launch<1>(wtype, n_tiles_bound, s, a) : gemv_launch<2>(wtype, n_tiles_bound, s, a);
+hipError_t launch_gemv_down(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const int8_t* hq,
+                            const float* hd, const int* hs, const float* hf, int T, int H, int I, int E, int K,
+                            float* y, hipStream_t s) {
+    GvArgs a{W, R, hq, hd, hs, hf, T, H, I, E, K, I, H / 64, 0, nullptr, nullptr, nullptr, nullptr, y};
+    return gemv_launch<1>(wtype, n_tiles_bound, s, a);
 }
 
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,

@@ -41,9 +41,9 @@ int gemv_tile_tokens();
 hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
                           int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
                           hipStream_t s);
-hipError_t launch_gemv_down(int wtype, int n_tiles_bound, int mode, const MatView& W, const Routing& R,
-                            const int8_t* hq, const float* hd, const int* hs, const float* hf, int T, int H, int I,
-                            int E, int K, float* y, const float* resid, float* out, hipStream_t s);
+hipError_t launch_gemv_down(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const int8_t* hq,
+                            const float* hd, const int* hs, const float* hf, int T, int H, int I, int E, int K,
+                            float* y, hipStream_t s);
 hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K, int has_shared, const float* resid,
                           float* out, hipStream_t s);
 hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
