@@ -66,7 +66,6 @@ hipError_t launch_ffn_down_mfma(int wtype, int shape, int n_tiles_bound, const M
 // residency (hy_data.hip)
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 // compute-only probe of the grouped GEMM's per-block mix (hy_probe.hip)
-size_t probe_block_mix_out_floats(int work_groups);
 hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int seed, float* out, hipStream_t s);
 size_t probe_stream_step_bytes();
 hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s);

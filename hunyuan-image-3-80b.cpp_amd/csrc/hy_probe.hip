@@ -25,7 +25,8 @@ typedef int v4i_p __attribute__((ext_vector_type(4)));
 
 constexpr int PROBE_THREADS = 512;
 
-// VARIANT 0: the full per-block mix; 1: the four MFMAs only; 2: the 64 vector ops only
+// VARIANT 0: the full per-block mix; 1: the four MFMAs only; 2: the 64 vector ops only, plus
+// 32 integer adds that vary their operands
 template <int VARIANT>
 __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, int seed, float* __restrict__ out) {
     const int lane = threadIdx.x % WAVE;
@@ -143,8 +144,6 @@ hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int w
     }
     return hipGetLastError();
 }
-
-size_t probe_block_mix_out_floats(int work_groups) { return (size_t)work_groups * PROBE_THREADS; }
 
 hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int seed, float* out, hipStream_t s) {
     const dim3 grid((unsigned)work_groups), blk(PROBE_THREADS);
