@@ -51,8 +51,10 @@ __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, fl
 // Router logits.  Work item of one wave = (TPW tokens) x (EPW experts); a block's
 // four waves take consecutive items, experts varying fastest so they share the
 // token rows in L1.  Decode batches (T <= 16) use <1,1> (one dot per wave), T <= 32
-// <8,1>, larger ones <8,8>: each loaded float4 of x or Wr feeds 8 dots, 64 accumulators
-// per lane (1.05 GB of L2 reads at T=4096 against 1.57 GB for <4,8>: 61 vs 78 us).  The
+// <8,1>, up to 2047 tokens <4,8> (each Wr float4 feeds 4 tokens, 32 accumulators per
+// lane), larger batches <8,8>: each loaded float4 feeds 8 dots, 64 accumulators per lane
+// (1.05 GB of L2 reads at T=4096 against 1.57 GB for <4,8>: 61 vs 78 us; at T=512 its
+// 512 waves are too few, 27 vs 23 us).  The
 // h loop is software-pipelined: the loads of the next D - 1 chunks of 256 elements
 // are in flight while a chunk is accumulated (a large batch has about one wave per
 // SIMD, so the wave itself must cover the memory latency).  The per-lane
@@ -209,9 +211,10 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
     } else if (T <= 32) {
         hipLaunchKernelGGL((router_logits_kernel<8, 1>), grid_for(8, 1), blk, 0, s, x, wr, T, H, E, logits);
     } else {
-        const int items = ((T + 7) / 8) * ((E + 7) / 8);
-        hipLaunchKernelGGL((router_logits_kernel<8, 8>), dim3((items + ROUTER_WAVES - 1) / ROUTER_WAVES),
-                           dim3(ROUTER_WAVES * WAVE), 0, s, x, wr, T, H, E, logits);
+        if (T >= 2048)
+            hipLaunchKernelGGL((router_logits_kernel<8, 8>), grid_for(8, 8), blk, 0, s, x, wr, T, H, E, logits);
+        else
+            hipLaunchKernelGGL((router_logits_kernel<4, 8>), grid_for(4, 8), blk, 0, s, x, wr, T, H, E, logits);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || logits_only) return e;
