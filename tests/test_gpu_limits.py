@@ -1,0 +1,77 @@
+"""GPU parity at the limits the C ABI accepts: the largest batch (max_tokens = 16384),
+the largest top-k (16), top-k equal to the number of experts, and a single expert.
+
+Each token's output depends only on its own row (default routing: no capacity, no
+drops), so the oracle runs on sampled rows and row-permutation invariance covers the
+rest (every output element is computed in a fixed order whatever tile a token lands
+in)."""
+import numpy as np
+import pytest
+
+import hy_oracle as O
+from test_gpu_parity import assert_exact
+from test_gpu_workloads import assert_permutes, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+def test_layer_at_max_tokens_and_topk(gpu, wtype):
+    """T = 16384 (the largest batch a context takes) and K = 16 (the largest top-k) over
+    64 experts: all 262,144 pairs dispatched, the routing of every row and sampled output
+    rows against the oracle, every row through permutation invariance."""
+    H, I, E, K, T = 256, 128, 64, 16, 16384
+    layer = O.synth_layer(H, I, E, K, wtype, seed=71, std=0.05)
+    x = O.synth(72, 0, O.T_X, 0, (T, H), 1.0)
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=T)
+    m.upload(0, layer)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    rows = sample_rows(T, n=40)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x[rows], debug=True)
+    np.testing.assert_array_equal(lg[rows].view(np.uint32), rlg.view(np.uint32))
+    np.testing.assert_array_equal(idx[rows], ridx)
+    np.testing.assert_array_equal(w[rows].view(np.uint32), rw.view(np.uint32))
+    assert_exact(out[rows], ref, f"T={T} K={K} wtype={wtype}")
+    # every row selects 16 distinct experts; the dispatch placed all of them
+    assert np.all(np.sort(idx, axis=1)[:, 1:] != np.sort(idx, axis=1)[:, :-1])
+    D, counts = m.last_routing()
+    assert counts.sum() == T * K and D == E
+    assert_permutes(lambda v: m.run(0, v), x, f"T={T} K={K}")
+    m.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_topk_equals_experts(gpu, wtype, T):
+    """K = E: every token routes to every expert (decode GEMV for T <= 16, grouped GEMM
+    above for the quantized types)."""
+    H, I, E = 256, 128, 8
+    layer = O.synth_layer(H, I, E, E, wtype, seed=80 + T, std=0.05)
+    x = O.synth(81 + T, 0, O.T_X, 0, (T, H), 1.0)
+    m = gpu.Moe(H, I, E, E, wtype, max_tokens=64)
+    m.upload(0, layer)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+    np.testing.assert_array_equal(idx, ridx)
+    assert np.all(np.sort(idx, axis=1) == np.arange(E))
+    assert_exact(out, ref, f"K=E={E} wtype={wtype} T={T}")
+    m.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("shared", [True, False])
+def test_single_expert(gpu, wtype, shared):
+    """E = 1, K = 1: routing is trivial (weight p * routed_scaling_factor, as the
+    reference's K = 1 rule gives); with and without the shared expert."""
+    H, I = 256, 128
+    layer = O.synth_layer(H, I, 1, 1, wtype, seed=90, std=0.05, shared=shared)
+    m = gpu.Moe(H, I, 1, 1, wtype, max_tokens=64, has_shared=shared)
+    m.upload(0, layer)
+    for T in (1, 3, 33):
+        x = O.synth(91 + T, 0, O.T_X, 0, (T, H), 1.0)
+        out, lg, w, idx = m.run(0, x, debug=True)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        assert np.all(idx == 0)
+        np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+        assert_exact(out, ref, f"E=1 wtype={wtype} shared={shared} T={T}")
+    m.close()
