@@ -766,9 +766,82 @@ __global__ __launch_bounds__(256) void rms_norm_quant_kernel(const float* __rest
     }
 }
 
+// The same RMSNorm + Q8_0 with the row read once: for H a multiple of 256 up to 4096 a
+// lane keeps its 4 H/256 elements (4 lane + 256 i .. +3, the sum-of-squares order)
+// in registers, and the 8 lanes holding one 32-wide block reduce its amax and sum.
+// Same values bit for bit.
+constexpr int RMSQ_MAX_CHUNKS = 16;
+__global__ __launch_bounds__(256) void rms_norm_quant_reg_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ w, int T, int H, float eps,
+                                                                 float* __restrict__ xn, int8_t* __restrict__ q,
+                                                                 float* __restrict__ d, int* __restrict__ qsum) {
+    const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (row >= T) return;  // whole waves: the shuffles below stay within live waves
+    const int nc = H / (4 * WAVE);
+    const float* xr = x + (size_t)row * H;
+    float4 v[RMSQ_MAX_CHUNKS];
+#pragma unroll
+    for (int i = 0; i < RMSQ_MAX_CHUNKS; i++)
+        if (i < nc) v[i] = *reinterpret_cast<const float4*>(xr + 4 * lane + 4 * WAVE * i);
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RMSQ_MAX_CHUNKS; i++)
+        if (i < nc) {
+            a = fmaf(v[i].x, v[i].x, a);
+            a = fmaf(v[i].y, v[i].y, a);
+            a = fmaf(v[i].z, v[i].z, a);
+            a = fmaf(v[i].w, v[i].w, a);
+        }
+    const float ss = __shfl(tree_sum64(a), 0, WAVE);
+    const float rms = 1.0f / sqrtf(ss / (float)H + eps);
+    const int nb = H / QK;
+#pragma unroll
+    for (int i = 0; i < RMSQ_MAX_CHUNKS; i++) {
+        if (i >= nc) continue;  // (uniform; keeps the loop unrolled and v[] in registers)
+        const int h = 4 * lane + 4 * WAVE * i;
+        float xs[4] = {v[i].x * rms, v[i].y * rms, v[i].z * rms, v[i].w * rms};
+        if (w) {
+            const float4 ww = *reinterpret_cast<const float4*>(w + h);
+            xs[0] *= ww.x;
+            xs[1] *= ww.y;
+            xs[2] *= ww.z;
+            xs[3] *= ww.w;
+        }
+        *reinterpret_cast<float4*>(xn + (size_t)row * H + h) = make_float4(xs[0], xs[1], xs[2], xs[3]);
+        float amax = fmaxf(fmaxf(fabsf(xs[0]), fabsf(xs[1])), fmaxf(fabsf(xs[2]), fabsf(xs[3])));
+        amax = fmaxf(amax, shfl_xor(amax, 1, 8));
+        amax = fmaxf(amax, shfl_xor(amax, 2, 8));
+        amax = fmaxf(amax, shfl_xor(amax, 4, 8));
+        const float dd = amax / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        int sum = 0;
+        uint32_t p = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int qv = (int)__builtin_roundf(xs[j] * id);
+            sum += qv;
+            p |= ((uint32_t)(qv & 0xff)) << (8 * j);
+        }
+        sum += shfl_xor(sum, 1, 8);
+        sum += shfl_xor(sum, 2, 8);
+        sum += shfl_xor(sum, 4, 8);
+        *reinterpret_cast<uint32_t*>(q + (size_t)row * H + h) = p;
+        if ((lane & 7) == 0) {
+            const size_t b = (size_t)row * nb + h / QK;
+            d[b] = h2f(f2h(dd));
+            qsum[b] = sum;
+        }
+    }
+}
+
 hipError_t launch_rms_norm_quant(const float* x, const float* w, int T, int H, float eps, float* xn, int8_t* q,
                                  float* d, int* qsum, hipStream_t s) {
-    hipLaunchKernelGGL(rms_norm_quant_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, T, H, eps, xn, q, d, qsum);
+    if (H % (4 * WAVE) == 0 && H <= 4 * WAVE * RMSQ_MAX_CHUNKS)
+        hipLaunchKernelGGL(rms_norm_quant_reg_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, T, H, eps, xn, q, d,
+                           qsum);
+    else
+        hipLaunchKernelGGL(rms_norm_quant_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, T, H, eps, xn, q, d,
+                           qsum);
     return hipGetLastError();
 }
 
