@@ -405,12 +405,18 @@ __global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E,
     const int tid = threadIdx.x, lane = tid % WAVE;
     const int nkb = K * nblk;
     if (tid < E) {
+        // 16 counts loaded before any base is stored, so the loads overlap
         int run = 0;
-        for (int kb = 0; kb < nkb; kb++) {
-            int* p = blk_cnt + (size_t)kb * E + tid;
-            const int c = *p;
-            *p = run;
-            run += c;
+        for (int kb0 = 0; kb0 < nkb; kb0 += 16) {
+            int c[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) c[j] = kb0 + j < nkb ? blk_cnt[(size_t)(kb0 + j) * E + tid] : 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (kb0 + j < nkb) {
+                    blk_cnt[(size_t)(kb0 + j) * E + tid] = run;
+                    run += c[j];
+                }
         }
         cnt_s[tid] = run;
     }
