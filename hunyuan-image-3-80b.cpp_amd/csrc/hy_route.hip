@@ -481,9 +481,9 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int* __rest
 //    k-major capacity-slot priority, per-expert offsets and tiles (then the shared
 //    expert's), per-token combine lists in ascending expert order;
 //  * work groups 1.. quantize x to Q8_0, 256 elements each.
-// (Folding the logits into this launch needs a device-scope handoff between work
-// groups -- an agent-scope release writes back the XCD's L2 -- which cost more than
-// the kernel boundary.)
+// (Folding the logits into this launch needs a hand-off between work groups: with an
+// agent-scope release, which writes back the XCD's L2, and with write-through stores
+// and agent-scope loads alike, it measured slower than the kernel boundary.)
 // ----------------------------------------------------------------------------
 struct DecodeRouteArgs {
     const float* x;
