@@ -12,7 +12,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# HY_ORACLE_LIB names another build of the same sources (the sanitizer test uses it).
+LIB_PATH = os.environ.get("HY_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libhy_ref.so")
 
 F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
