@@ -799,31 +799,110 @@ void hyo_router_logits_blocked(const float* x, const float* wr, uint32_t T, uint
             logits[(size_t)t * E + e] = hyo_blocked_dot(x + (size_t)t * H, wr + (size_t)e * H, H);
 }
 
-static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, float scale,
-                          float* w, int32_t* idx) {
-    float v[64];
-    hyo_topk_f32(l, E, K, v, idx); /* selection on logits, ties -> lower index */
-    const float m = v[0]; /* the largest logit */
-    float ex[64];
-    for (uint32_t e = 0; e < E; e++) ex[e] = hyo_expf(l[e] - m);
-    const float s = hyo_tree_sum64(ex, E);
-    float p[64], ps = 0.0f;
-    for (uint32_t k = 0; k < K; k++) {
-        p[k] = hyo_expf(l[idx[k]] - m) / s;
-        ps += p[k];
-    }
-    if (ps < 1e-8f) ps = 1e-8f;
+/* One token's routing.  Default: top-K on the logits.  Group-limited greedy
+ * (n_group > 0 and topk_group > 0): src/hunyuan_moe_full.cpp:135-178 step by step on
+ * the q probabilities.  probs (may be NULL) receives the (masked) probabilities. */
+static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, float scale, uint32_t n_group,
+                          uint32_t topk_group, float* w, int32_t* idx, float* probs) {
     /* norm 1 renormalises only when K > 1 (src/hunyuan_moe_full.cpp:230, the rule of
      * topkgating_full and so of moe_forward_full); norm 2 at every K
      * (src/attention.cpp:268-275, moe_forward_cpu; topkgating_easy :104-108) */
     const int rn = norm == 2 || (norm != 0 && K > 1);
-    for (uint32_t k = 0; k < K; k++) w[k] = rn ? p[k] / ps : p[k] * scale;
+    float m = l[0]; /* the largest logit */
+    for (uint32_t e = 1; e < E; e++)
+        if (l[e] > m) m = l[e];
+    float ex[64];
+    for (uint32_t e = 0; e < E; e++) ex[e] = hyo_expf(l[e] - m);
+    const float s = hyo_tree_sum64(ex, E);
+    float v[64], ps = 0.0f;
+    if (n_group == 0 || topk_group == 0) {
+        hyo_topk_f32(l, E, K, v, idx); /* selection on logits, ties -> lower index */
+        float p[64];
+        for (uint32_t k = 0; k < K; k++) {
+            p[k] = hyo_expf(l[idx[k]] - m) / s;
+            ps += p[k];
+        }
+        if (ps < 1e-8f) ps = 1e-8f;
+        for (uint32_t k = 0; k < K; k++) w[k] = rn ? p[k] / ps : p[k] * scale;
+        if (probs)
+            for (uint32_t e = 0; e < E; e++) probs[e] = hyo_expf(l[e] - m) / s;
+        return;
+    }
+    float p[64];
+    for (uint32_t e = 0; e < E; e++) p[e] = hyo_expf(l[e] - m) / s;
+    /* group scores: max over the group's experts, from 0 (:139-148) */
+    const uint32_t gs = E / n_group;
+    float gsc[64], gv[64];
+    int32_t gi[64];
+    for (uint32_t g = 0; g < n_group; g++) {
+        float mx = 0.0f;
+        for (uint32_t j = 0; j < gs; j++)
+            if (p[g * gs + j] > mx) mx = p[g * gs + j];
+        gsc[g] = mx;
+    }
+    /* the best topk_group groups; experts of the others are set to 0 (:150-165) */
+    hyo_topk_f32(gsc, n_group, topk_group, gv, gi);
+    uint8_t sel[64] = {0};
+    for (uint32_t kg = 0; kg < topk_group; kg++) sel[gi[kg]] = 1;
+    for (uint32_t g = 0; g < n_group; g++)
+        if (!sel[g])
+            for (uint32_t j = 0; j < gs; j++) p[g * gs + j] = 0.0f;
+    /* top-K of the masked probabilities (:168-178), weights from them (:229-243) */
+    hyo_topk_f32(p, E, K, v, idx);
+    for (uint32_t k = 0; k < K; k++) ps += v[k];
+    if (ps < 1e-8f) ps = 1e-8f;
+    for (uint32_t k = 0; k < K; k++) w[k] = rn ? v[k] / ps : v[k] * scale;
+    if (probs) memcpy(probs, p, E * sizeof(float));
 }
 
 void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm,
                     float scale, float* w, int32_t* idx) {
     for (uint32_t t = 0; t < T; t++)
-        hyo_route_one(logits + (size_t)t * E, E, K, norm, scale, w + (size_t)t * K, idx + (size_t)t * K);
+        hyo_route_one(logits + (size_t)t * E, E, K, norm, scale, 0, 0, w + (size_t)t * K, idx + (size_t)t * K,
+                      NULL);
+}
+
+void hyo_route_topk_groups(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm, float scale,
+                           uint32_t n_group, uint32_t topk_group, float* w, int32_t* idx, float* probs) {
+    for (uint32_t t = 0; t < T; t++)
+        hyo_route_one(logits + (size_t)t * E, E, K, norm, scale, n_group, topk_group, w + (size_t)t * K,
+                      idx + (size_t)t * K, probs ? probs + (size_t)t * E : NULL);
+}
+
+/* src/hunyuan_moe_full.cpp:182-206: the per-token expert mask summed as floats is the
+ * exact count; each sum runs over tokens in order, the products are rounded before
+ * they are added (no contraction in this build). */
+float hyo_aux_loss_q(const float* probs, const int32_t* idx, uint32_t T, uint32_t E, uint32_t K) {
+    float l = 0.0f;
+    for (uint32_t e = 0; e < E; e++) {
+        uint32_t n = 0;
+        float r = 0.0f;
+        for (uint32_t t = 0; t < T; t++) {
+            int hit = 0;
+            for (uint32_t k = 0; k < K; k++) hit |= idx[(size_t)t * K + k] == (int32_t)e;
+            n += (uint32_t)hit;
+            r += probs[(size_t)t * E + e];
+        }
+        const float tpe = (float)n / (float)T, rpe = r / (float)T;
+        l += tpe * rpe;
+    }
+    return l * (float)(E * E);
+}
+
+uint32_t hyo_drop_capacity(uint32_t T, uint32_t E, uint32_t K, float capacity_factor, uint32_t min_capacity) {
+    uint32_t c = (uint32_t)(capacity_factor * K * T / E);
+    if (c < K) c = K;
+    if (c < min_capacity) c = min_capacity;
+    return c;
+}
+
+void hyo_capacity_keep(const int32_t* idx, uint32_t T, uint32_t E, uint32_t K, uint32_t capacity, uint8_t* keep) {
+    uint32_t cnt[64] = {0};
+    for (uint32_t k = 0; k < K; k++)
+        for (uint32_t t = 0; t < T; t++) {
+            const int32_t e = idx[(size_t)t * K + k];
+            keep[(size_t)t * K + k] = (uint8_t)(e >= 0 && (uint32_t)e < E && cnt[e]++ < capacity);
+        }
 }
 
 /* y[r] = row r of W (type wt, n columns) . x ; xq is x quantized to Q8_0 (unused for
@@ -884,22 +963,26 @@ static int hyo_check_layer(const hyo_qlayer* L) {
     if (L->K > 64 || L->K > L->E || L->E > 64) return -1;
     if (L->H % HYO_QK || L->I % HYO_QK) return -1;
     if (L->wtype != HYO_F32 && L->wtype != HYO_Q8_0 && L->wtype != HYO_Q4_0) return -1;
+    if (L->n_group > 0 && L->topk_group > 0 && (L->n_group > 64 || L->topk_group > 64)) return -1;
     return 0;
 }
 
-static void hyo_token_q(const hyo_qlayer* L, const float* xt, float* ot, float* lg, float* w,
-                        int32_t* idx) {
+/* Routing of one token: logits (blocked order), then hyo_route_one. */
+static void hyo_token_route_q(const hyo_qlayer* L, const float* xt, float* lg, float* w, int32_t* idx,
+                              float* probs) {
+    const uint32_t H = L->H, E = L->E;
+    for (uint32_t e = 0; e < E; e++) lg[e] = hyo_blocked_dot(xt, L->router + (size_t)e * H, H);
+    hyo_route_one(lg, E, L->K, L->norm_topk_prob, L->routed_scaling_factor, L->n_group, L->topk_group, w, idx,
+                  probs);
+}
+
+/* The experts of one routed token: out = shared(x) + sum over its kept pairs with a
+ * nonzero weight, in ascending expert order (einsum_combine skips w == 0,
+ * src/hunyuan_moe_full.cpp:387-397).  keep may be NULL (all kept). */
+static void hyo_token_experts_q(const hyo_qlayer* L, const float* xt, float* ot, const float* wl,
+                                const int32_t* il, const uint8_t* keep) {
     const uint32_t H = L->H, I = L->I, E = L->E, K = L->K;
     const int wt = L->wtype;
-    float lgl[64];
-    float* lgp = lg ? lg : lgl;
-    for (uint32_t e = 0; e < E; e++) lgp[e] = hyo_blocked_dot(xt, L->router + (size_t)e * H, H);
-    float wl[64];
-    int32_t il[64];
-    hyo_route_one(lgp, E, K, L->norm_topk_prob, L->routed_scaling_factor, wl, il);
-    if (w) memcpy(w, wl, K * sizeof(float));
-    if (idx) memcpy(idx, il, K * sizeof(int32_t));
-
     void* xq = malloc(hyo_type_row_bytes(HYO_Q8_0, H));
     void* hq = malloc(hyo_type_row_bytes(HYO_Q8_0, I));
     float* gbuf = (float*)malloc(2 * (size_t)I * sizeof(float));
@@ -914,7 +997,7 @@ static void hyo_token_q(const hyo_qlayer* L, const float* xt, float* ot, float* 
         int k = -1;
         for (uint32_t j = 0; j < K; j++)
             if (il[j] == (int32_t)e) { k = (int)j; break; }
-        if (k < 0) continue;
+        if (k < 0 || (keep && !keep[k]) || wl[k] == 0.0f) continue;
         hyo_expert_q(wt, (const uint8_t*)L->gu + e * gu_bytes, (const uint8_t*)L->dn + e * dn_bytes,
                      H, I, xt, xq, y, gbuf, hbuf, hq);
         for (uint32_t r = 0; r < H; r++) comb[r] = fmaf(wl[k], y[r], comb[r]);
@@ -928,11 +1011,73 @@ static void hyo_token_q(const hyo_qlayer* L, const float* xt, float* ot, float* 
     free(xq); free(hq); free(gbuf); free(hbuf); free(y); free(comb);
 }
 
+static void hyo_token_q(const hyo_qlayer* L, const float* xt, float* ot, float* lg, float* w,
+                        int32_t* idx) {
+    float lgl[64], wl[64];
+    int32_t il[64];
+    hyo_token_route_q(L, xt, lg ? lg : lgl, wl, il, NULL);
+    if (w) memcpy(w, wl, L->K * sizeof(float));
+    if (idx) memcpy(idx, il, L->K * sizeof(int32_t));
+    hyo_token_experts_q(L, xt, ot, wl, il, NULL);
+}
+
+int hyo_moe_route_q(const hyo_qlayer* L, const float* x, uint32_t T, float* logits, float* w, int32_t* idx,
+                    float* probs, uint8_t* keep, int nthreads) {
+    if (hyo_check_layer(L) || !w || !idx) return -1;
+    const uint32_t E = L->E, K = L->K;
+#ifdef _OPENMP
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t t = 0; t < (int64_t)T; t++) {
+        float lgl[64];
+        hyo_token_route_q(L, x + (size_t)t * L->H, logits ? logits + (size_t)t * E : lgl, w + (size_t)t * K,
+                          idx + (size_t)t * K, probs ? probs + (size_t)t * E : NULL);
+    }
+    (void)nthreads;
+    if (keep) {
+        if (L->capacity > 0)
+            hyo_capacity_keep(idx, T, E, K, L->capacity, keep);
+        else
+            memset(keep, 1, (size_t)T * K);
+    }
+    return 0;
+}
+
+/* The layer with a capacity: the whole batch is routed first (a pair's slot depends
+ * on the earlier tokens), then the tokens' experts.  rows NULL: every token. */
+static int hyo_forward_q_capacity(const hyo_qlayer* L, const float* x, uint32_t T, const uint32_t* rows,
+                                  uint32_t n_rows, float* out, float* dbg_logits, float* dbg_w, int32_t* dbg_idx,
+                                  int nthreads) {
+    const uint32_t K = L->K;
+    float* w = (float*)malloc((size_t)T * K * sizeof(float));
+    int32_t* idx = (int32_t*)malloc((size_t)T * K * sizeof(int32_t));
+    uint8_t* keep = (uint8_t*)malloc((size_t)T * K);
+    int rc = hyo_moe_route_q(L, x, T, dbg_logits, w, idx, NULL, keep, nthreads);
+    if (rc == 0) {
+        const int64_t n = rows ? (int64_t)n_rows : (int64_t)T;
+#ifdef _OPENMP
+        if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+        for (int64_t i = 0; i < n; i++) {
+            const size_t t = rows ? rows[i] : (size_t)i;
+            hyo_token_experts_q(L, x + t * L->H, out + (size_t)i * L->H, w + t * K, idx + t * K, keep + t * K);
+        }
+        if (dbg_w) memcpy(dbg_w, w, (size_t)T * K * sizeof(float));
+        if (dbg_idx) memcpy(dbg_idx, idx, (size_t)T * K * sizeof(int32_t));
+    }
+    free(w); free(idx); free(keep);
+    (void)nthreads;
+    return rc;
+}
+
 int hyo_moe_forward_q_rows(const hyo_qlayer* L, const float* x, uint32_t T,
                            const uint32_t* rows, uint32_t n_rows, float* out, int nthreads) {
     if (hyo_check_layer(L)) return -1;
     for (uint32_t i = 0; i < n_rows; i++)
         if (rows[i] >= T) return -1;
+    if (L->capacity > 0) return hyo_forward_q_capacity(L, x, T, rows, n_rows, out, NULL, NULL, NULL, nthreads);
 #ifdef _OPENMP
     if (nthreads < 1) nthreads = 1;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
@@ -946,6 +1091,8 @@ int hyo_moe_forward_q_rows(const hyo_qlayer* L, const float* x, uint32_t T,
 int hyo_moe_forward_q(const hyo_qlayer* L, const float* x, uint32_t T, float* out,
                       float* dbg_logits, float* dbg_w, int32_t* dbg_idx, int nthreads) {
     if (hyo_check_layer(L)) return -1;
+    if (L->capacity > 0)
+        return hyo_forward_q_capacity(L, x, T, NULL, 0, out, dbg_logits, dbg_w, dbg_idx, nthreads);
 #ifdef _OPENMP
     if (nthreads < 1) nthreads = 1;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)

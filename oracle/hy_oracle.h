@@ -152,6 +152,25 @@ void hyo_router_logits_blocked(const float* x, const float* wr, uint32_t T, uint
  * src/attention.cpp:268-275), norm 0 never. */
 void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm,
                     float scale, float* w, int32_t* idx);
+/* The same with group-limited greedy (src/hunyuan_moe_full.cpp:135-166) when n_group > 0
+ * and topk_group > 0 (both <= 64): on the q probabilities p_e = hyo_expf(l_e - m) / s
+ * (s the 64-lane tree sum), group scores max(0, max p over the group's E/n_group
+ * experts), the topk_group best groups by hyo_topk_f32, experts of the other groups
+ * set to 0, then top-K by hyo_topk_f32 on the probabilities (equal values: lower
+ * index) and the weights from the (masked) probabilities.  probs (may be NULL)
+ * receives the masked probabilities [T][E], the gates the aux loss averages. */
+void hyo_route_topk_groups(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm, float scale,
+                           uint32_t n_group, uint32_t topk_group, float* w, int32_t* idx, float* probs);
+/* Load-balancing aux loss of src/hunyuan_moe_full.cpp:182-206 over the routing's
+ * probabilities [T][E] and indices [T][K]: tokens per expert / T times the expert's
+ * probability summed over tokens in order / T, summed over experts, times E*E. */
+float hyo_aux_loss_q(const float* probs, const int32_t* idx, uint32_t T, uint32_t E, uint32_t K);
+/* Expert capacity under token dropping (src/hunyuan_moe_full.cpp:210-214):
+ * max(K, (uint32)(capacity_factor * K * T / E)), then at least min_capacity. */
+uint32_t hyo_drop_capacity(uint32_t T, uint32_t E, uint32_t K, float capacity_factor, uint32_t min_capacity);
+/* keep[t][k] = 1 when pair (t, k) takes a capacity slot < capacity: slots are given in
+ * the order k = 0..K-1, t = 0..T-1 (src/hunyuan_moe_full.cpp:245-304). */
+void hyo_capacity_keep(const int32_t* idx, uint32_t T, uint32_t E, uint32_t K, uint32_t capacity, uint8_t* keep);
 
 /* One MoE layer over GGUF-layout weights of type wtype (F32, Q8_0 or Q4_0).
  * gu: [(E) experts][2I rows] rows of H elements; dn: [E][H rows] rows of I elements;
@@ -166,11 +185,20 @@ typedef struct {
     const void*  shared_dn;
     const void*  gu;
     const void*  dn;
+    /* routing options beyond the default, 0 = off */
+    uint32_t n_group, topk_group; /* group-limited greedy when both > 0 (hyo_route_topk_groups) */
+    uint32_t capacity;            /* token dropping: pairs past this capacity slot contribute nothing */
 } hyo_qlayer;
 
 int hyo_moe_forward_q(const hyo_qlayer* L, const float* x, uint32_t T, float* out,
                       float* dbg_logits, float* dbg_w, int32_t* dbg_idx, int nthreads);
-/* One token of the layer (row-independence lets callers sample tokens). */
+/* Routing of the whole batch: logits [T][E] (may be NULL), weights and indices [T][K],
+ * masked probabilities [T][E] (may be NULL) and keep [T][K] (may be NULL; all 1 without
+ * a capacity). */
+int hyo_moe_route_q(const hyo_qlayer* L, const float* x, uint32_t T, float* logits, float* w, int32_t* idx,
+                    float* probs, uint8_t* keep, int nthreads);
+/* Sampled tokens of the layer (rows are independent without a capacity; with one, the
+ * whole batch is routed first). */
 int hyo_moe_forward_q_rows(const hyo_qlayer* L, const float* x, uint32_t T,
                            const uint32_t* rows, uint32_t n_rows, float* out, int nthreads);
 /* RMSNorm(eps, unit weight) -> MoE -> residual, over n_layers layers. */

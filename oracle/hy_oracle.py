@@ -51,6 +51,7 @@ class QLayer(C.Structure):
         ("H", C.c_uint32), ("I", C.c_uint32), ("E", C.c_uint32), ("K", C.c_uint32),
         ("wtype", C.c_int), ("norm_topk_prob", C.c_int), ("routed_scaling_factor", C.c_float),
         ("router", _fp), ("shared_gu", _vp), ("shared_dn", _vp), ("gu", _vp), ("dn", _vp),
+        ("n_group", C.c_uint32), ("topk_group", C.c_uint32), ("capacity", C.c_uint32),
     ]
 
 
@@ -102,6 +103,12 @@ def lib():
                                               C.c_uint32, C.c_uint32, C.c_uint32, _fp, _fp, _fp, _ip]),
             "hyo_router_logits_blocked": (None, [_fp, _fp, C.c_uint32, C.c_uint32, C.c_uint32, _fp]),
             "hyo_route_topk": (None, [_fp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_float, _fp, _ip]),
+            "hyo_route_topk_groups": (None, [_fp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_float,
+                                             C.c_uint32, C.c_uint32, _fp, _ip, _fp]),
+            "hyo_aux_loss_q": (C.c_float, [_fp, _ip, C.c_uint32, C.c_uint32, C.c_uint32]),
+            "hyo_drop_capacity": (C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]),
+            "hyo_capacity_keep": (None, [_ip, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _vp]),
+            "hyo_moe_route_q": (C.c_int, [C.POINTER(QLayer), _fp, C.c_uint32, _fp, _fp, _ip, _fp, _vp, C.c_int]),
             "hyo_moe_forward_q": (C.c_int, [C.POINTER(QLayer), _fp, C.c_uint32, _fp, _fp, _fp, _ip, C.c_int]),
             "hyo_moe_forward_q_rows": (C.c_int, [C.POINTER(QLayer), _fp, C.c_uint32, _up, C.c_uint32, _fp, C.c_int]),
             "hyo_moe_stack_q": (C.c_int, [C.POINTER(QLayer), C.c_uint32, _fp, C.c_uint32, C.c_float, _fp, C.c_int]),
@@ -219,7 +226,7 @@ class Layer:
     """One MoE layer's weights in GGUF layout (ggml ne0 = in-features)."""
 
     def __init__(self, H, I, E, K, wtype, router, shared_gu, shared_dn, gu, dn,
-                 norm_topk_prob=True, routed_scaling_factor=1.0):
+                 norm_topk_prob=True, routed_scaling_factor=1.0, n_group=0, topk_group=0, capacity=0):
         self.H, self.I, self.E, self.K, self.wtype = H, I, E, K, wtype
         self.router = f32(router)
         self.shared_gu = None if shared_gu is None else np.ascontiguousarray(shared_gu)
@@ -228,6 +235,8 @@ class Layer:
         self.dn = np.ascontiguousarray(dn)
         self.norm_topk_prob = norm_topk_prob
         self.routed_scaling_factor = routed_scaling_factor
+        # group-limited greedy when both > 0; capacity > 0: token dropping at that capacity
+        self.n_group, self.topk_group, self.capacity = n_group, topk_group, capacity
 
     def c(self):
         s = QLayer()
@@ -239,6 +248,7 @@ class Layer:
         s.shared_dn = vp(self.shared_dn) if self.shared_dn is not None else None
         s.gu = vp(self.gu)
         s.dn = vp(self.dn)
+        s.n_group, s.topk_group, s.capacity = int(self.n_group), int(self.topk_group), int(self.capacity)
         return s
 
     def dequant(self):
@@ -356,6 +366,52 @@ def router_logits_blocked(x, wr):
     out = np.empty((T, E), dtype=np.float32)
     lib().hyo_router_logits_blocked(fp(x), fp(wr), T, H, E, fp(out))
     return out
+
+
+def route_topk_groups(logits, K, norm=True, scale=1.0, n_group=0, topk_group=0):
+    """q-semantics routing with group-limited greedy: weights, indices, masked probs."""
+    logits = f32(logits)
+    T, E = logits.shape
+    w = np.empty((T, K), dtype=np.float32)
+    idx = np.empty((T, K), dtype=np.int32)
+    probs = np.empty((T, E), dtype=np.float32)
+    lib().hyo_route_topk_groups(fp(logits), T, E, K, int(norm), scale, n_group, topk_group, fp(w), ip(idx),
+                                fp(probs))
+    return w, idx, probs
+
+
+def aux_loss_q(probs, idx):
+    probs, idx = f32(probs), np.ascontiguousarray(idx, dtype=np.int32)
+    T, E = probs.shape
+    return np.float32(lib().hyo_aux_loss_q(fp(probs), ip(idx), T, E, idx.shape[1]))
+
+
+def drop_capacity(T, E, K, capacity_factor, min_capacity):
+    return int(lib().hyo_drop_capacity(T, E, K, capacity_factor, min_capacity))
+
+
+def capacity_keep(idx, E, capacity):
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    T, K = idx.shape
+    keep = np.empty((T, K), dtype=np.uint8)
+    lib().hyo_capacity_keep(ip(idx), T, E, K, capacity, vp(keep))
+    return keep.astype(bool)
+
+
+def moe_route_q(layer: Layer, x, nthreads=1):
+    """Routing of the whole batch: logits, weights, indices, masked probs, keep [T][K]."""
+    x = f32(x)
+    T = x.shape[0]
+    lg = np.empty((T, layer.E), dtype=np.float32)
+    w = np.empty((T, layer.K), dtype=np.float32)
+    idx = np.empty((T, layer.K), dtype=np.int32)
+    probs = np.empty((T, layer.E), dtype=np.float32)
+    keep = np.empty((T, layer.K), dtype=np.uint8)
+    c = layer.c()
+    rc = lib().hyo_moe_route_q(C.byref(c), fp(x), T, fp(lg), fp(w), ip(idx), fp(probs), vp(keep), nthreads)
+    if rc != 0:
+        raise ValueError("hyo_moe_route_q rejected the layer")
+    return lg, w, idx, probs, keep.astype(bool)
 
 
 def route_topk(logits, K, norm=True, scale=1.0):
