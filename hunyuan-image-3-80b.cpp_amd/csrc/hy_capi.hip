@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -105,7 +106,13 @@ struct hy_moe_ctx {
     float* y = nullptr;
     float* xn = nullptr;
     float* cur = nullptr;
+    float* gates = nullptr;  // [max_tokens][E]: the gates the aux loss averages
+    float* aux = nullptr;    // the last forward's aux loss
     int max_tiles = 0;
+
+    // routing options beyond the default (resolved from the config)
+    int n_group = 0, topk_group = 0;  // group-limited greedy when n_group > 0
+    uint32_t last_T = 0;              // tokens of the last forward (gate statistics)
 
     // timing
     bool prof = false;
@@ -120,8 +127,8 @@ struct hy_moe_ctx {
 
 namespace {
 
-const char* kKernelNames[hy::KID_COUNT] = {"quant_q8_0", "router", "dispatch", "ffn_up",
-                                           "ffn_down",   "combine", "rms_norm"};
+const char* kKernelNames[hy::KID_COUNT] = {"quant_q8_0", "router",  "dispatch", "ffn_up",
+                                           "ffn_down",   "combine", "rms_norm", "aux_loss"};
 
 int get_event(hy_moe_ctx* c, hipEvent_t* ev) {
     if (!c->pool.empty()) {
@@ -202,10 +209,24 @@ int check_cfg(const hy_moe_config* c) {
         return fail(HY_ERR_INVALID, "max_tokens=%u must be in 1..16384", c->max_tokens);
     if (c->wtype != HY_TYPE_F32 && c->wtype != HY_TYPE_Q8_0 && c->wtype != HY_TYPE_Q4_0)
         return fail(HY_ERR_UNSUPPORTED, "weight type %d not supported (F32=0, Q4_0=2, Q8_0=8)", c->wtype);
-    if (c->group_limited_greedy || c->drop_tokens || c->compute_aux_loss)
-        return fail(HY_ERR_UNSUPPORTED,
-                    "group-limited greedy, token dropping and the aux loss are not run on the GPU path");
+    if (c->group_limited_greedy && c->n_group > 0 && c->topk_group > 0 && (c->n_group > 64 || c->topk_group > 64))
+        return fail(HY_ERR_INVALID, "n_group=%u / topk_group=%u must be <= 64", c->n_group, c->topk_group);
+    if (c->drop_tokens) {
+        // the capacity rule converts capacity_factor * K * T / E to uint32
+        const float most = c->capacity_factor * (float)c->topk * (float)c->max_tokens / (float)c->num_experts;
+        if (!(c->capacity_factor >= 0.0f) || !(most < 4294967040.0f))
+            return fail(HY_ERR_INVALID, "capacity_factor=%g gives no capacity in uint32 range", (double)c->capacity_factor);
+    }
     return HY_OK;
+}
+
+// Expert capacity under token dropping (src/hunyuan_moe_full.cpp:210-214): float
+// arithmetic left to right, truncated, at least K, at least min_capacity.
+uint32_t drop_capacity(const hy_moe_config& c, uint32_t T) {
+    uint32_t cap = (uint32_t)(c.capacity_factor * c.topk * T / c.num_experts);
+    if (cap < c.topk) cap = c.topk;
+    if (cap < c.min_capacity) cap = c.min_capacity;
+    return cap;
 }
 
 hy::MatView gu_view(const hy_moe_ctx* c, const LayerW& L) {
@@ -261,7 +282,10 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
                       (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
     const int shape = mfma ? hy::mfma_shape(iT, K, E, H, I) : -1;
     const int NT = mfma ? hy::mfma_shape_tokens(shape) : hy::gemv_tile_tokens();
-    if (!mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
+    // group-limited greedy, dropping and the aux loss take the general routing path
+    const bool ext = c->n_group > 0 || c->cfg.drop_tokens || c->cfg.compute_aux_loss;
+    c->last_T = T;
+    if (!ext && !mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
         // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
             return hy::launch_route_decode(x, L.router, iT, H, E, K, renorm,
@@ -277,16 +301,24 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
             HY_TRY(timed(c, hy::KID_QUANT, s, [&] {
                 return hy::launch_quant_q8_0(x, (size_t)T * H, c->xq, c->xd, c->xs, nullptr, s);
             }));
+        hy::RouteOpts opt;
+        opt.n_group = c->n_group;
+        opt.topk_group = c->topk_group;
+        opt.probs = c->cfg.compute_aux_loss ? c->gates : nullptr;
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
             return hy::launch_router_q(x, L.router, iT, H, E, K, renorm,
                                        c->cfg.routed_scaling_factor, c->logits, c->topw, c->topi,
-                                       fuse_quant ? c->xq : nullptr, c->xd, c->xs, s);
+                                       fuse_quant ? c->xq : nullptr, c->xd, c->xs, s, false, opt);
         }));
+        const int cap = c->cfg.drop_tokens ? (int)std::min<uint32_t>(drop_capacity(c->cfg, T), 0x7fffffffu)
+                                           : 0x7fffffff;
         HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] {
             return hy::launch_dispatch(c->topi, c->topw, iT, K, E, NT, has_shared, c->cnt, c->off, c->srt_tok,
                                        c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start, c->tile_n,
-                                       c->meta, c->dsp_scratch, s);
+                                       c->meta, c->dsp_scratch, s, cap);
         }));
+        if (c->cfg.compute_aux_loss)
+            HY_TRY(timed(c, hy::KID_AUX, s, [&] { return hy::launch_aux_loss(c->gates, c->cnt, iT, E, c->aux, s); }));
     }
     const hy::Routing R = routing(c);
     const hy::ActQ X{c->xq, c->xd, c->xs, H};
@@ -421,6 +453,10 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
     c->E = (int)cfg->num_experts;
     c->K = (int)cfg->topk;
     c->X = c->E + (cfg->has_shared ? 1 : 0);
+    if (cfg->group_limited_greedy && cfg->n_group > 0 && cfg->topk_group > 0) {
+        c->n_group = (int)cfg->n_group;
+        c->topk_group = (int)cfg->topk_group;
+    }
     const int wt = cfg->wtype;
     c->gu_qs_stride = align256(row_bytes(wt, c->H) * 2 * c->I);
     c->gu_sc_stride = wt == HY_TYPE_F32 ? 0 : (size_t)2 * c->I * (c->H / 32);
@@ -456,6 +492,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
         {(void**)&c->y, slots * H * 4},    {(void**)&c->xn, Tm * H * 4},
         {(void**)&c->cur, Tm * H * 4},
         {(void**)&c->dsp_scratch, hy::dispatch_scratch_bytes((int)Tm, (int)K, (int)E)},
+        {(void**)&c->gates, cfg->compute_aux_loss ? Tm * E * 4 : 16}, {(void**)&c->aux, 16},
     };
     size_t total = 0;
     for (auto& p : parts) total += align256(p.bytes);
@@ -750,6 +787,28 @@ int hy_route_logits(const float* lg, uint32_t T, uint32_t E, uint32_t K, int32_t
     return HY_OK;
 }
 
+int hy_route_logits_groups(const float* lg, uint32_t T, uint32_t E, uint32_t K, int32_t norm, float scale,
+                           uint32_t n_group, uint32_t topk_group, float* w, int32_t* idx, float* probs, void* stream) {
+    if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
+        return fail(HY_ERR_INVALID, "bad routing shape");
+    if (n_group > 64 || topk_group > 64) return fail(HY_ERR_INVALID, "n_group / topk_group must be <= 64");
+    hy::RouteOpts opt;
+    opt.n_group = (int)n_group;
+    opt.topk_group = (int)topk_group;
+    opt.probs = probs;
+    HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, renorm_rule(norm, K), scale, w, idx,
+                                        static_cast<hipStream_t>(stream), opt));
+    return HY_OK;
+}
+
+int hy_aux_loss(const float* probs, const int32_t* counts, uint32_t T, uint32_t E, float* out, void* stream) {
+    if (!probs || !counts || !out) return fail(HY_ERR_INVALID, "null pointer");
+    if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E) return fail(HY_ERR_INVALID, "bad aux-loss shape");
+    HIP_TRY(hy::launch_aux_loss(probs, counts, (int)T, (int)E, out, static_cast<hipStream_t>(stream)));
+    return HY_OK;
+}
+
 int hy_softmax_rows(float* x, uint32_t rows, uint32_t n, void* stream) {
     if (!x || rows == 0 || n == 0 || n > 1024) return fail(HY_ERR_INVALID, "bad softmax shape");
     HIP_TRY(hy::launch_softmax_rows(x, (int)rows, (int)n, static_cast<hipStream_t>(stream)));
@@ -1007,6 +1066,31 @@ int hy_moe_last_routing(hy_moe_ctx* c, uint32_t* distinct, int32_t* counts) {
     HIP_TRY(hipMemcpy(meta, c->meta, sizeof(meta), hipMemcpyDeviceToHost));
     if (distinct) *distinct = (uint32_t)meta[2];
     if (counts) HIP_TRY(hipMemcpy(counts, c->cnt, (size_t)c->E * 4, hipMemcpyDeviceToHost));
+    return HY_OK;
+}
+
+int hy_moe_last_gate(hy_moe_ctx* c, float* aux_loss, uint32_t* expert_capacity, float* exp_capacity_rate) {
+    if (!c) return fail(HY_ERR_INVALID, "null ctx");
+    if (c->last_T == 0) return fail(HY_ERR_STATE, "no forward has run");
+    HIP_TRY(hipStreamSynchronize(c->last_stream));
+    std::vector<int32_t> cnt(c->E);
+    HIP_TRY(hipMemcpy(cnt.data(), c->cnt, (size_t)c->E * 4, hipMemcpyDeviceToHost));
+    float aux = 0.0f;
+    if (c->cfg.compute_aux_loss) HIP_TRY(hipMemcpy(&aux, c->aux, 4, hipMemcpyDeviceToHost));
+    // src/hunyuan_moe_full.cpp:209-227: the capacity rule, or the largest count
+    uint32_t cap = 0;
+    if (c->cfg.drop_tokens) {
+        cap = drop_capacity(c->cfg, c->last_T);
+    } else {
+        for (int32_t n : cnt) cap = std::max(cap, (uint32_t)n);
+        cap = std::max(cap, c->cfg.min_capacity);
+    }
+    // :329-335: pairs given a slot, counted in floats, over T * K
+    float placed = 0.0f;
+    for (int32_t n : cnt) placed += (float)std::min<uint32_t>((uint32_t)n, cap);
+    if (aux_loss) *aux_loss = aux;
+    if (expert_capacity) *expert_capacity = cap;
+    if (exp_capacity_rate) *exp_capacity_rate = placed / (float)(c->last_T * (uint32_t)c->K);
     return HY_OK;
 }
 

@@ -485,7 +485,9 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 }
 
 // combine: out[t] = residual[t] + ( y_shared[t] + sum_{e ascending} w_e y_e[t] ), the
-// shared expert's output at slot T*K + t when has_shared.  One thread per 4 outputs
+// shared expert's output at slot T*K + t when has_shared.  A pair with w_e == 0 (a
+// dropped pair, or a zero gate) adds nothing, as einsum_combine skips it
+// (src/hunyuan_moe_full.cpp:387-397); its y row is read but not used.  One thread per 4 outputs
 // (16-byte loads of the y rows); each output keeps the scalar fmaf order.  The token's
 // KMAX list entries (indices clamped to K - 1) and then its y rows are all loaded
 // before the first fmaf, so a thread waits for two rounds of loads, not 2 K.
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __
     float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < KMAX; k++)
-        if (k < K)
+        if (k < K && w[k] != 0.0f)
             c = make_float4(fmaf(w[k], v[k].x, c.x), fmaf(w[k], v[k].y, c.y), fmaf(w[k], v[k].z, c.z),
                             fmaf(w[k], v[k].w, c.w));
     float4 o = c;

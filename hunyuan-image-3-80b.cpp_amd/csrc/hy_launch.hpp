@@ -11,13 +11,22 @@
 namespace hy {
 
 // routing side (hy_route.hip)
+// Routing options of topkgating_full beyond the default (zero: off): group-limited
+// greedy when n_group > 0 and topk_group > 0; probs [T][E] (may be null) receives the
+// gates (after the group mask) that the aux loss averages.
+struct RouteOpts {
+    int n_group = 0, topk_group = 0;
+    float* probs = nullptr;
+};
 hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                          float* logits, float* topw, int* topi, hipStream_t s);
 hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                            float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s,
-                           bool logits_only = false);
+                           bool logits_only = false, RouteOpts opt = {});
 hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, int norm, float scale, float* topw,
-                                   int* topi, hipStream_t s);
+                                   int* topi, hipStream_t s, RouteOpts opt = {});
+// aux loss from the gates [T][E] and the per-expert pair counts [E]: one float at out
+hipError_t launch_aux_loss(const float* probs, const int* cnt, int T, int E, float* out, hipStream_t s);
 hipError_t launch_softmax_rows(float* x, int rows, int n, hipStream_t s);
 hipError_t launch_quant_q8_0(const float* x, size_t n, int8_t* q, float* d, int* qsum, uint8_t* blocks,
                              hipStream_t s);
@@ -29,7 +38,8 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
 size_t dispatch_scratch_bytes(int T, int K, int E);
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared, int* cnt,
                            int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w, int* tile_e,
-                           int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s);
+                           int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s,
+                           int cap = 0x7fffffff);  // pairs at capacity slot >= cap: dropped
 hipError_t launch_rms_norm(const float* x, int T, int H, float eps, float* out, hipStream_t s);
 // RMSNorm (w may be null: unit weight) fused with the Q8_0 quantization of its output
 hipError_t launch_rms_norm_quant(const float* x, const float* w, int T, int H, float eps, float* xn, int8_t* q,
@@ -93,6 +103,7 @@ enum KernelId {
     KID_DOWN,
     KID_COMBINE,
     KID_RMSNORM,
+    KID_AUX,
     KID_COUNT
 };
 

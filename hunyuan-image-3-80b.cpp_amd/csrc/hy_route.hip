@@ -20,7 +20,7 @@ namespace hy {
 constexpr int ROUTER_WAVES = 4;
 
 __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, float scale, int lane,
-                                          float* w_out, int* i_out) {
+                                          float* w_out, int* i_out, float* p_out = nullptr) {
     float v = lane < E ? v_in : -INFINITY;
     const float orig = v;
     float m0 = 0.0f;
@@ -44,6 +44,65 @@ __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, fl
     if (ps < 1e-8f) ps = 1e-8f;
     if (lane < K) {
         w_out[lane] = norm ? p / ps : p * scale;
+        i_out[lane] = seli;
+    }
+    if (p_out && lane < E) p_out[lane] = hy_expf(orig - m0) / s;  // the gates the aux loss averages
+}
+
+// Group-limited greedy (src/hunyuan_moe_full.cpp:135-178) for one token, one expert
+// per lane, step by step on the probabilities p_e = exp(l_e - m) / s (the exp and the
+// 64-lane tree sum of topk_wave): group g of the E / n_group experts from g * (E /
+// n_group) scores max(0, its p_e); the topk_group best groups (wave max, lower index
+// on ties) stay, the other groups' experts get p = 0; the top K of the masked p (equal
+// values: lower index) are selected and weighted by their masked p.  Experts past
+// n_group * (E / n_group) belong to no group and keep their p.
+__device__ __forceinline__ void topk_groups_wave(float v_in, int E, int K, int norm, float scale, int n_group,
+                                                 int topk_group, int lane, float* w_out, int* i_out, float* p_out) {
+    const float orig = lane < E ? v_in : -INFINITY;
+    const float m0 = wave_max(orig);
+    const float s = wave_sum(lane < E ? hy_expf(orig - m0) : 0.0f);
+    float p = lane < E ? hy_expf(orig - m0) / s : 0.0f;
+    const int gs = E / n_group;
+    // lane g < n_group: the score of group g
+    float gsc = -INFINITY;
+    for (int g = 0; g < n_group; g++) {
+        const float m = wave_max(gs > 0 && lane >= g * gs && lane < (g + 1) * gs ? p : 0.0f);
+        if (lane == g) gsc = m;
+    }
+    // the best min(topk_group, n_group) groups (more rounds would re-pick group 0)
+    int keep_g = 0;
+    const int rounds = topk_group < n_group ? topk_group : n_group;
+    for (int r = 0; r < rounds; r++) {
+        const float m = wave_max(gsc);
+        const int sel = (int)__builtin_ctzll(__ballot(gsc == m));
+        if (lane == sel) {
+            keep_g = 1;
+            gsc = -INFINITY;
+        }
+    }
+    const int my_g = gs > 0 ? lane / gs : n_group;
+    const bool grouped = my_g < n_group;
+    const int kept = __shfl(keep_g, grouped ? my_g : 0, WAVE);
+    if (grouped && !kept) p = 0.0f;
+    if (p_out && lane < E) p_out[lane] = p;
+    // top K of the masked probabilities (p >= 0 > -inf, so K <= E rounds always find one)
+    float v = lane < E ? p : -INFINITY;
+    float selv = 0.0f;
+    int seli = 0;
+    for (int k = 0; k < K; k++) {
+        const float m = wave_max(v);
+        const int sel = (int)__builtin_ctzll(__ballot(v == m));
+        if (lane == k) {
+            selv = m;
+            seli = sel;
+        }
+        if (lane == sel) v = -INFINITY;
+    }
+    float ps = 0.0f;
+    for (int k = 0; k < K; k++) ps += __shfl(selv, k, WAVE);
+    if (ps < 1e-8f) ps = 1e-8f;
+    if (lane < K) {
+        w_out[lane] = norm ? selv / ps : selv * scale;
         i_out[lane] = seli;
     }
 }
@@ -178,7 +237,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(const float* __restri
                                                            int norm, float scale, float* __restrict__ topw,
                                                            int* __restrict__ topi, const float* __restrict__ x,
                                                            int H, int8_t* __restrict__ xq, float* __restrict__ xd,
-                                                           int* __restrict__ xs) {
+                                                           int* __restrict__ xs, RouteOpts opt) {
     const int sel_groups = (T + 3) / 4;
     if ((int)blockIdx.x >= sel_groups) {
         const size_t idx = (size_t)(blockIdx.x - sel_groups) * 256 + threadIdx.x;
@@ -188,7 +247,12 @@ __global__ __launch_bounds__(256) void route_select_kernel(const float* __restri
     const int tok = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (tok >= T) return;
     const float v = lane < E ? logits[(size_t)tok * E + lane] : 0.0f;
-    topk_wave(v, E, K, norm, scale, lane, topw + (size_t)tok * K, topi + (size_t)tok * K);
+    float* p_out = opt.probs ? opt.probs + (size_t)tok * E : nullptr;
+    if (opt.n_group > 0 && opt.topk_group > 0)
+        topk_groups_wave(v, E, K, norm, scale, opt.n_group, opt.topk_group, lane, topw + (size_t)tok * K,
+                         topi + (size_t)tok * K, p_out);
+    else
+        topk_wave(v, E, K, norm, scale, lane, topw + (size_t)tok * K, topi + (size_t)tok * K, p_out);
 }
 
 hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
@@ -198,7 +262,7 @@ hipError_t launch_router(const float* x, const float* wr, int T, int H, int E, i
 
 hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E, int K, int norm, float scale,
                            float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, hipStream_t s,
-                           bool logits_only) {
+                           bool logits_only, RouteOpts opt) {
     const dim3 blk(ROUTER_WAVES * WAVE);
     auto grid_for = [&](int tpw, int epw) {
         const int items = ((T + tpw - 1) / tpw) * ((E + epw - 1) / epw);
@@ -220,16 +284,53 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
     if (e != hipSuccess || logits_only) return e;
     const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + 255) / 256) : 0u;
     hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4 + quant_groups), dim3(256), 0, s, logits, T, E, K, norm,
-                       scale, topw, topi, x, H, xq, xd, xs);
+                       scale, topw, topi, x, H, xq, xd, xs, opt);
     return hipGetLastError();
 }
 
-// top-k gating from given logits (topkgating_easy, src/hunyuan_moe_full.cpp:88-113):
-// one wave per token.
+// top-k gating from given logits (topkgating_easy, src/hunyuan_moe_full.cpp:88-113;
+// with options, the selection of topkgating_full :129-243): one wave per token.
 hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, int norm, float scale, float* topw,
-                                   int* topi, hipStream_t s) {
+                                   int* topi, hipStream_t s, RouteOpts opt) {
     hipLaunchKernelGGL(route_select_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, norm, scale, topw,
-                       topi, nullptr, 0, nullptr, nullptr, nullptr);
+                       topi, nullptr, 0, nullptr, nullptr, nullptr, opt);
+    return hipGetLastError();
+}
+
+// Load-balancing aux loss (src/hunyuan_moe_full.cpp:182-206), one work group of one
+// thread per expert: tokens_per_expert = count / T (the per-token mask summed as floats
+// is the exact count; counts from the dispatch), router_prob_per_expert = the expert's
+// gate summed over tokens in order / T; then thread 0 adds the E products in expert
+// order and multiplies by E * E.  Eight tokens' gates are loaded per step, so the
+// loads overlap while the adds keep their order.
+__global__ __launch_bounds__(64) void aux_loss_kernel(const float* __restrict__ probs, const int* __restrict__ cnt,
+                                                      int T, int E, float* __restrict__ out) {
+    __shared__ float prod[MAX_E];
+    const int e = threadIdx.x;
+    if (e < E) {
+        float r = 0.0f;
+        int t = 0;
+        for (; t + 8 <= T; t += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = probs[(size_t)(t + j) * E + e];
+#pragma unroll
+            for (int j = 0; j < 8; j++) r += v[j];
+        }
+        for (; t < T; t++) r += probs[(size_t)t * E + e];
+        const float tpe = (float)cnt[e] / (float)T, rpe = r / (float)T;
+        prod[e] = tpe * rpe;
+    }
+    __syncthreads();
+    if (e == 0) {
+        float l = 0.0f;
+        for (int i = 0; i < E; i++) l += prod[i];
+        out[0] = l * (float)(E * E);
+    }
+}
+
+hipError_t launch_aux_loss(const float* probs, const int* cnt, int T, int E, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(64), 0, s, probs, cnt, T, E, out);
     return hipGetLastError();
 }
 
@@ -400,7 +501,7 @@ __global__ __launch_bounds__(DSP_BLOCK) void dispatch_rank_kernel(const int* __r
 
 // blk_cnt [K][nblk][E] (k-major: the priority order) -> exclusive bases in place
 __global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E, int NT, int has_shared, int nblk,
-                                                            int* __restrict__ blk_cnt, DispatchOut o) {
+                                                            int cap, int* __restrict__ blk_cnt, DispatchOut o) {
     __shared__ int cnt_s[MAX_E];
     const int tid = threadIdx.x, lane = tid % WAVE;
     const int nkb = K * nblk;
@@ -422,8 +523,11 @@ __global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E,
     }
     __syncthreads();
     if (tid < WAVE) {
+        // c pairs of the expert, the first min(c, cap) of them computed (capacity slots,
+        // src/hunyuan_moe_full.cpp:296-304: a pair at slot >= capacity is dropped)
         const int c = lane < E ? cnt_s[lane] : 0;
-        const int nt = (c + NT - 1) / NT;
+        const int kc = c < cap ? c : cap;
+        const int nt = (kc + NT - 1) / NT;
         const int off = wave_excl_scan(c, lane), toff = wave_excl_scan(nt, lane);
         const int total = __shfl(off + c, WAVE - 1, WAVE), routed = __shfl(toff + nt, WAVE - 1, WAVE);
         const int distinct = __popcll(__ballot(c > 0));
@@ -435,7 +539,7 @@ __global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E,
             for (int j = 0; j < nt; j++) {
                 o.tile_e[toff + j] = lane;
                 o.tile_start[toff + j] = j * NT;
-                o.tile_n[toff + j] = min(NT, c - j * NT);
+                o.tile_n[toff + j] = min(NT, kc - j * NT);
             }
         }
         if (lane == 0) {
@@ -456,14 +560,15 @@ __global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E,
 
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int* __restrict__ topi,
                                                                const float* __restrict__ topw, int T, int K, int E,
-                                                               int nblk, const int* __restrict__ blk_base,
+                                                               int nblk, int cap, const int* __restrict__ blk_base,
                                                                DispatchOut o) {
     const int p = blockIdx.x * 256 + threadIdx.x;
     if (p >= T * K) return;
     const int t = p / K, k = p - t * K;
     const int e = topi[p];
     if (e < 0 || e >= E) return;
-    const int pos = o.off[e] + blk_base[((size_t)k * nblk + t / DSP_BLOCK) * E + e] + o.pair_pos[p];
+    const int slot = blk_base[((size_t)k * nblk + t / DSP_BLOCK) * E + e] + o.pair_pos[p];
+    const int pos = o.off[e] + slot;
     o.pair_pos[p] = pos;
     o.srt_tok[pos] = t;
     // combine list slot: the token's experts are distinct, so the pair's place in
@@ -471,7 +576,7 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int* __rest
     int r = 0;
     for (int j = 0; j < K; j++) r += topi[(size_t)t * K + j] < e;
     o.comb_pos[(size_t)t * K + r] = pos;
-    o.comb_w[(size_t)t * K + r] = topw[p];
+    o.comb_w[(size_t)t * K + r] = slot < cap ? topw[p] : 0.0f;  // a dropped pair adds nothing
 }
 
 // ----------------------------------------------------------------------------
@@ -650,17 +755,17 @@ size_t dispatch_scratch_bytes(int T, int K, int E) {
 
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared,
                            int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos, float* comb_w,
-                           int* tile_e, int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s) {
+                           int* tile_e, int* tile_start, int* tile_n, int* meta, int* scratch, hipStream_t s, int cap) {
     DispatchOut o{cnt, off, srt_tok, pair_pos, comb_pos, comb_w, tile_e, tile_start, tile_n, meta};
     const int nblk = (T + DSP_BLOCK - 1) / DSP_BLOCK;
     hipLaunchKernelGGL(dispatch_rank_kernel, dim3(nblk, K), dim3(DSP_BLOCK), 0, s, topi, T, K, E, scratch, pair_pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(256), 0, s, T, K, E, NT, has_shared, nblk, scratch, o);
+    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(256), 0, s, T, K, E, NT, has_shared, nblk, cap, scratch, o);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3((T * K + 255) / 256), dim3(256), 0, s, topi, topw, T, K, E, nblk,
-                       scratch, o);
+                       cap, scratch, o);
     return hipGetLastError();
 }
 

@@ -37,10 +37,18 @@ private:
     size_t n_;
 };
 
-void require_default_routing(const MoERoutingConfig& c) {
-    if (c.group_limited_greedy || c.drop_tokens || c.compute_aux_loss)
-        throw hy::Error(HY_ERR_UNSUPPORTED,
-                        "group-limited greedy, token dropping and the aux loss are not run on the GPU path");
+bool use_groups(const MoERoutingConfig& c) { return c.group_limited_greedy && c.n_group > 0 && c.topk_group > 0; }
+
+// Expert capacity under token dropping (src/hunyuan_moe_full.cpp:210-214): float
+// arithmetic left to right, truncated to uint32, at least K, at least min_capacity.
+uint32_t drop_capacity(const MoERoutingConfig& c, uint32_t T) {
+    const float v = c.capacity_factor * c.moe_topk * T / c.num_experts;
+    if (!(v >= 0.0f) || !(v < 4294967040.0f))
+        throw hy::Error(HY_ERR_INVALID, "capacity_factor gives no capacity in uint32 range");
+    uint32_t cap = (uint32_t)v;
+    if (cap < c.moe_topk) cap = c.moe_topk;
+    if (cap < c.min_capacity) cap = c.min_capacity;
+    return cap;
 }
 
 hy_moe_config layer_config(uint32_t H, uint32_t I, uint32_t E, uint32_t K, uint32_t T, int wtype, bool shared,
@@ -60,6 +68,16 @@ hy_moe_config layer_config(uint32_t H, uint32_t I, uint32_t E, uint32_t K, uint3
     c.norm_topk_prob = rc ? (rc->norm_topk_prob ? HY_NORM_TOPK : HY_NORM_OFF) : HY_NORM_ALWAYS;
     c.routed_scaling_factor = rc ? rc->routed_scaling_factor : 1.0f;
     c.device = 0;
+    if (rc) {
+        // moe_forward_full routes with every option of its config; the aux loss it
+        // computes is not returned (src/hunyuan_moe_full.cpp:425-434), so it is not run
+        c.group_limited_greedy = rc->group_limited_greedy ? 1 : 0;
+        c.n_group = rc->n_group;
+        c.topk_group = rc->topk_group;
+        c.drop_tokens = rc->drop_tokens ? 1 : 0;
+        c.capacity_factor = rc->capacity_factor;
+        c.min_capacity = rc->min_capacity;
+    }
     return c;
 }
 
@@ -68,6 +86,9 @@ void run_layer(const float* x, uint32_t T, uint32_t H, const float* router, cons
                const void* gu, const void* dn, int wtype, uint32_t E, uint32_t I, uint32_t K,
                const MoERoutingConfig* rc, float* out, float* dbg_logits, float* dbg_w, int32_t* dbg_idx) {
     if (T == 0) return;
+    // token dropping gives capacity slots over the whole batch: one call, no chunks
+    if (rc && rc->drop_tokens && T > 16384)
+        throw hy::Error(HY_ERR_UNSUPPORTED, "token dropping over more than 16384 tokens in one call");
     const bool shared = sgu && sdn;
     hy::MoeStack m(layer_config(H, I, E, K, T, wtype, shared, rc));
     m.upload_layer(0, router, sgu, sdn, gu, dn);
@@ -142,24 +163,33 @@ void topkgating_easy(const float* logits, uint32_t T, uint32_t E, uint32_t K, fl
     id.down(idx, (size_t)T * K * 4);
 }
 
-// Default routing on the GPU; the dense [T,E,C] outputs are assembled from the
-// expert-sorted positions (the slot c of a pair is its position inside its expert,
-// in the reference's k-major priority order).  The buffers of `out` are (re)allocated
-// with the capacity this function picks, which keeps the strides consistent.
+// Routing on the GPU (group-limited greedy, the aux loss and token dropping included);
+// the dense [T,E,C] outputs are assembled from the expert-sorted positions (the slot c
+// of a pair is its position inside its expert, in the reference's k-major priority
+// order; a pair at c >= C is dropped).  The buffers of `out` are (re)allocated with the
+// capacity this function picks, which keeps the strides consistent.
+// random_routing_dropped_token is read by nothing in the reference and by nothing here.
 void topkgating_full(const float* logits, uint32_t T, const MoERoutingConfig& cfg, MoEGateOutput& out) {
-    require_default_routing(cfg);
     const uint32_t E = cfg.num_experts, K = cfg.moe_topk;
     if (T == 0) return;
     const size_t pairs = (size_t)T * K;
-    Dev l((size_t)T * E * 4), p((size_t)T * E * 4), wd(pairs * 4), id(pairs * 4), cnt((size_t)E * 4),
-        off((size_t)(E + 1) * 4), pos(pairs * 4);
+    const bool groups = use_groups(cfg);
+    Dev l((size_t)T * E * 4), p((size_t)T * E * 4), gates((size_t)T * E * 4), wd(pairs * 4), id(pairs * 4),
+        cnt((size_t)E * 4), off((size_t)(E + 1) * 4), pos(pairs * 4), aux(4);
     l.up(logits, (size_t)T * E * 4);
     p.up(logits, (size_t)T * E * 4);
-    check(hy_route_logits(l.as<float>(), T, E, K, cfg.norm_topk_prob ? HY_NORM_TOPK : HY_NORM_OFF, cfg.routed_scaling_factor,
-                          wd.as<float>(), id.as<int32_t>(), nullptr));
+    check(hy_route_logits_groups(l.as<float>(), T, E, K, cfg.norm_topk_prob ? HY_NORM_TOPK : HY_NORM_OFF,
+                                 cfg.routed_scaling_factor, groups ? cfg.n_group : 0, groups ? cfg.topk_group : 0,
+                                 wd.as<float>(), id.as<int32_t>(), gates.as<float>(), nullptr));
     check(hy_dispatch_pairs(id.as<int32_t>(), wd.as<float>(), T, K, E, cnt.as<int32_t>(), off.as<int32_t>(),
                             pos.as<int32_t>(), nullptr));
+    // the reference keeps router_probs from before the group mask (:124-125)
     check(hy_softmax_rows(p.as<float>(), T, E, nullptr));
+    float aux_loss = 0.0f;
+    if (cfg.compute_aux_loss) {
+        check(hy_aux_loss(gates.as<float>(), cnt.as<int32_t>(), T, E, aux.as<float>(), nullptr));
+        aux.down(&aux_loss, 4);
+    }
     std::vector<float> w(pairs), probs((size_t)T * E);
     std::vector<int32_t> idx(pairs), counts(E), offs(E + 1), ps(pairs);
     wd.down(w.data(), pairs * 4);
@@ -170,8 +200,12 @@ void topkgating_full(const float* logits, uint32_t T, const MoERoutingConfig& cf
     p.down(probs.data(), (size_t)T * E * 4);
 
     uint32_t C = 0;
-    for (uint32_t e = 0; e < E; e++) C = std::max(C, (uint32_t)counts[e]);
-    C = std::max(C, cfg.min_capacity);
+    if (cfg.drop_tokens) {
+        C = drop_capacity(cfg, T);
+    } else {
+        for (uint32_t e = 0; e < E; e++) C = std::max(C, (uint32_t)counts[e]);
+        C = std::max(C, cfg.min_capacity);
+    }
     free(out.combine_weights);
     free(out.dispatch_mask);
     free(out.exp_counts);
@@ -186,13 +220,14 @@ void topkgating_full(const float* logits, uint32_t T, const MoERoutingConfig& cf
             const size_t pr = (size_t)t * K + k;
             const int e = idx[pr];
             const uint32_t c = (uint32_t)(ps[pr] - offs[e]);
+            if (c >= C) continue;  // no capacity slot left: dropped (:296-304)
             out.dispatch_mask[((size_t)t * E + e) * C + c] = true;
             out.combine_weights[((size_t)t * E + e) * C + c] = w[pr];
         }
     memcpy(out.exp_counts, counts.data(), (size_t)E * 4);
     memcpy(out.router_probs, probs.data(), (size_t)T * E * 4);
     out.expert_capacity = C;
-    out.aux_loss = 0.0f;
+    out.aux_loss = aux_loss;
     float placed = 0;
     for (size_t i = 0; i < (size_t)T * E * C; i++)
         if (out.dispatch_mask[i]) placed += 1;
@@ -229,7 +264,6 @@ void moe_forward_full(const float* x, uint32_t T, uint32_t H, const float* route
 void moe_forward_full(const float* x, uint32_t T, uint32_t H, const float* router, const void* sgu, const void* sdn,
                       const void* gu, const void* dn, int wtype, uint32_t E, uint32_t I, const MoERoutingConfig& rc,
                       float* out) {
-    require_default_routing(rc);
     run_layer(x, T, H, router, sgu, sdn, gu, dn, wtype, E, I, rc.moe_topk, &rc, out, nullptr, nullptr, nullptr);
 }
 

@@ -34,6 +34,8 @@ class Config(C.Structure):
         ("wtype", C.c_int32), ("has_shared", C.c_int32), ("norm_topk_prob", C.c_int32),
         ("routed_scaling_factor", C.c_float), ("group_limited_greedy", C.c_int32),
         ("drop_tokens", C.c_int32), ("compute_aux_loss", C.c_int32), ("device", C.c_int32),
+        ("n_group", C.c_uint32), ("topk_group", C.c_uint32), ("capacity_factor", C.c_float),
+        ("min_capacity", C.c_uint32),
     ]
 
 
@@ -90,6 +92,9 @@ _SIGS = {
     "hy_moe_set_path": (C.c_int, [_vp, _i32]),
     "hy_router_topk": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _i32, _f, _vp, _vp, _vp, _vp]),
     "hy_topkgating_easy": (C.c_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "hy_route_logits_groups": (C.c_int, [_vp, _u32, _u32, _u32, _i32, _f, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "hy_aux_loss": (C.c_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "hy_moe_last_gate": (C.c_int, [_vp, C.POINTER(_f), C.POINTER(_u32), C.POINTER(_f)]),
     "hy_softmax_rows": (C.c_int, [_vp, _u32, _u32, _vp]),
     "hy_quantize_q8_0": (C.c_int, [_vp, _u32, _u32, _vp, _vp]),
     "hy_dequantize": (C.c_int, [_i32, _vp, C.c_size_t, _vp, _vp]),
@@ -267,18 +272,16 @@ class Moe:
     """A resident MoE stack (hy_moe_ctx)."""
 
     def __init__(self, H, I, E, K, wtype, num_layers=1, max_tokens=64, has_shared=True, norm_topk_prob=True,
-                 routed_scaling_factor=1.0, device=0, **unsupported):
-        extra = set(unsupported) - {"group_limited_greedy", "drop_tokens", "compute_aux_loss"}
-        if extra:
-            raise TypeError(f"Moe: unknown arguments {sorted(extra)}")
+                 routed_scaling_factor=1.0, device=0, group_limited_greedy=0, n_group=0, topk_group=0,
+                 drop_tokens=0, capacity_factor=1.0, min_capacity=0, compute_aux_loss=0):
         c = Config()
         c.hidden, c.intermediate, c.num_experts, c.topk = H, I, E, K
         c.num_layers, c.max_tokens, c.wtype = num_layers, max_tokens, wtype
         c.has_shared, c.norm_topk_prob = int(has_shared), int(norm_topk_prob)
         c.routed_scaling_factor = routed_scaling_factor
-        c.group_limited_greedy = int(unsupported.get("group_limited_greedy", 0))
-        c.drop_tokens = int(unsupported.get("drop_tokens", 0))
-        c.compute_aux_loss = int(unsupported.get("compute_aux_loss", 0))
+        c.group_limited_greedy, c.n_group, c.topk_group = int(group_limited_greedy), n_group, topk_group
+        c.drop_tokens, c.capacity_factor, c.min_capacity = int(drop_tokens), capacity_factor, min_capacity
+        c.compute_aux_loss = int(compute_aux_loss)
         c.device = device
         self.cfg = c
         self.H, self.I, self.E, self.K, self.wtype = H, I, E, K, wtype
@@ -363,6 +366,12 @@ class Moe:
         check(lib().hy_moe_last_routing(self.h, C.byref(d), counts.ctypes.data))
         return d.value, counts
 
+    def last_gate(self):
+        """(aux_loss, expert_capacity, exp_capacity_rate) of the last forward."""
+        aux, cap, rate = C.c_float(), C.c_uint32(), C.c_float()
+        check(lib().hy_moe_last_gate(self.h, C.byref(aux), C.byref(cap), C.byref(rate)))
+        return np.float32(aux.value), cap.value, np.float32(rate.value)
+
     # convenience: host in, host out
     def run(self, layer_idx, x, debug=False):
         x = np.ascontiguousarray(x, dtype=np.float32)
@@ -399,6 +408,26 @@ def topkgating_easy(logits, K):
     w, idx = Buf.empty((T, K)), Buf.empty((T, K), np.int32)
     check(lib().hy_topkgating_easy(lb.ptr, T, E, K, w.ptr, idx.ptr, None))
     return w.numpy(), idx.numpy()
+
+
+def route_logits_groups(logits, K, norm=1, scale=1.0, n_group=0, topk_group=0):
+    """Weights, indices and the masked gates of topkgating_full's selection."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    lb = Buf.from_array(logits)
+    w, idx, p = Buf.empty((T, K)), Buf.empty((T, K), np.int32), Buf.empty((T, E))
+    check(lib().hy_route_logits_groups(lb.ptr, T, E, K, int(norm), scale, n_group, topk_group, w.ptr, idx.ptr,
+                                       p.ptr, None))
+    return w.numpy(), idx.numpy(), p.numpy()
+
+
+def aux_loss(probs, counts):
+    probs = np.ascontiguousarray(probs, np.float32)
+    counts = np.ascontiguousarray(counts, np.int32)
+    T, E = probs.shape
+    pb, cb, ob = Buf.from_array(probs), Buf.from_array(counts), Buf.empty((1,))
+    check(lib().hy_aux_loss(pb.ptr, cb.ptr, T, E, ob.ptr, None))
+    return np.float32(ob.numpy()[0])
 
 
 def softmax_rows(x):

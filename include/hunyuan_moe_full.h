@@ -14,9 +14,11 @@
 //    no output is written on error;
 //  * expert selection compares logits (softmax is monotone), so experts whose
 //    probabilities round to the same float but whose logits differ are ordered by
-//    logit rather than by index;
-//  * topkgating_full / moe_forward_full run the default routing subset on the GPU
-//    (group-limited greedy, token dropping and the aux loss throw hy::Error);
+//    logit rather than by index (with group-limited greedy the selection compares the
+//    masked probabilities, as the reference does);
+//  * token dropping over more than 16384 tokens in one moe_forward_full call throws
+//    hy::Error (the capacity slots span the whole batch, which the GPU context holds
+//    up to 16384 tokens at a time);
 //  * MoEGateOutput cannot be copied (the reference's implicit copy double-frees).
 // Beyond the reference: quantized-weight (GGUF Q8_0 / Q4_0) overloads and
 // hy::MoeStack, a resident multi-layer context.

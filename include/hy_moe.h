@@ -45,9 +45,12 @@ enum { HY_TYPE_F32 = 0, HY_TYPE_Q4_0 = 2, HY_TYPE_Q8_0 = 8 };
 enum { HY_NORM_OFF = 0, HY_NORM_TOPK = 1, HY_NORM_ALWAYS = 2 };
 
 /* Shapes and routing of one resident MoE stack.  The routing fields mirror
- * MoERoutingConfig (src/hunyuan_moe_full.h:25-47); the GPU runs the default
- * subset (softmax -> top-k -> renormalise or scale), and hy_moe_create rejects
- * group-limited greedy, token dropping and the aux loss with HY_ERR_UNSUPPORTED. */
+ * MoERoutingConfig (src/hunyuan_moe_full.h:25-47) and topkgating_full's use of them
+ * (src/hunyuan_moe_full.cpp:117-335): softmax -> [group-limited greedy] -> top-k ->
+ * renormalise or scale -> [capacity slots, token dropping]; [aux loss].
+ * random_routing_dropped_token has no field: the reference declares it and never
+ * reads it.  Batches that use group-limited greedy, dropping or the aux loss are routed
+ * by the general path at every T (the one-launch decode routing covers the default). */
 typedef struct {
     uint32_t hidden;        /* H, multiple of 32 */
     uint32_t intermediate;  /* I, multiple of 32 */
@@ -59,10 +62,15 @@ typedef struct {
     int32_t  has_shared;    /* 1: one shared expert (num_shared_expert = 1) */
     int32_t  norm_topk_prob;       /* HY_NORM_*: moe_forward_full routes with HY_NORM_TOPK */
     float    routed_scaling_factor;
-    int32_t  group_limited_greedy; /* must be 0 */
-    int32_t  drop_tokens;          /* must be 0 */
-    int32_t  compute_aux_loss;     /* must be 0 */
+    int32_t  group_limited_greedy; /* 1: group-limited greedy with n_group / topk_group below */
+    int32_t  drop_tokens;          /* 1: capacity from capacity_factor / min_capacity, excess pairs dropped */
+    int32_t  compute_aux_loss;     /* 1: the load-balancing aux loss (hy_moe_last_gate) */
     int32_t  device;               /* HIP device ordinal */
+    /* appended after the fields above, which keep their offsets */
+    uint32_t n_group;              /* groups of num_experts / n_group experts (<= 64); 0: off */
+    uint32_t topk_group;           /* groups kept per token (<= 64); 0: off */
+    float    capacity_factor;      /* drop_tokens: capacity max(K, (uint32)(capacity_factor*K*T/E)) */
+    uint32_t min_capacity;         /* lower bound of the capacity, with or without dropping */
 } hy_moe_config;
 
 typedef struct hy_moe_ctx hy_moe_ctx;
@@ -212,6 +220,23 @@ int hy_topkgating_easy(const float* logits_dev, uint32_t T, uint32_t E, uint32_t
 int hy_route_logits(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K, int32_t norm_topk_prob,
                     float routed_scaling_factor, float* weights_dev, int32_t* indices_dev, void* stream);
 
+/* hy_route_logits with group-limited greedy (src/hunyuan_moe_full.cpp:135-166) when
+ * n_group > 0 and topk_group > 0 (both <= 64): per token, groups of E / n_group experts
+ * score the largest probability in them, the topk_group best groups stay and the other
+ * groups' experts get probability 0, then the top K of those probabilities (equal
+ * values: lower index) with their probabilities as weights.  probs_dev [T][E] (may be
+ * NULL) receives the probabilities after that mask, the gates the aux loss averages. */
+int hy_route_logits_groups(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K, int32_t norm_topk_prob,
+                           float routed_scaling_factor, uint32_t n_group, uint32_t topk_group, float* weights_dev,
+                           int32_t* indices_dev, float* probs_dev, void* stream);
+
+/* Load-balancing aux loss of topkgating_full (src/hunyuan_moe_full.cpp:182-206) from the
+ * gates probs_dev [T][E] and the pairs per expert counts_dev [E] (hy_dispatch_pairs):
+ * sum over experts of (count / T) * (gate summed over tokens in order / T), times E^2.
+ * One float at out_dev. */
+int hy_aux_loss(const float* probs_dev, const int32_t* counts_dev, uint32_t T, uint32_t E, float* out_dev,
+                void* stream);
+
 /* softmax_f32 (src/hunyuan_moe_full.h:148) over each of `rows` rows of n (n <= 1024). */
 int hy_softmax_rows(float* x_dev, uint32_t rows, uint32_t n, void* stream);
 
@@ -339,6 +364,14 @@ int32_t hy_moe_prof_count(void);
 /* Counters of the last forward (host copy after completion): distinct routed
  * experts D, and tokens routed to each expert (counts [E]). */
 int hy_moe_last_routing(hy_moe_ctx* ctx, uint32_t* distinct, int32_t* counts_host);
+
+/* Gate statistics of the last forward (of hy_moe_stack_forward: its last layer), as
+ * topkgating_full reports them in MoEGateOutput (src/hunyuan_moe_full.cpp:180-335):
+ * the aux loss (0 unless compute_aux_loss), the expert capacity (with drop_tokens the
+ * capacity rule, else the largest expert count; at least min_capacity) and the share
+ * of the T*K pairs that took a capacity slot.  Waits for the forward to finish; any
+ * output may be NULL. */
+int hy_moe_last_gate(hy_moe_ctx* ctx, float* aux_loss, uint32_t* expert_capacity, float* exp_capacity_rate);
 
 #ifdef __cplusplus
 }

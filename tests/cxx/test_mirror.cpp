@@ -97,15 +97,53 @@ int main() {
         report(ok && ecw < 2e-6 && epr < 2e-6, "topkgating_full (mask, slots, counts, capacity exact)",
                "cw " + errs(g.combine_weights, ref.combine_weights, n));
         hyo_gate_full_free(&ref);
-        bool threw = false;
-        try {
-            MoERoutingConfig bad;
-            bad.drop_tokens = true;
-            topkgating_full(lg.data(), T, bad, g);
-        } catch (const hy::Error& e) {
-            threw = e.code == HY_ERR_UNSUPPORTED;
+    }
+    // routing options: group-limited greedy, token dropping, the aux loss, alone and together
+    for (int opt = 0; opt < 4; opt++) {
+        const uint32_t To = 61, Eo = 16, Ko = 4;
+        std::vector<float> lo = synth(40 + opt, 0, 0, (size_t)To * Eo, 1.5f);
+        MoERoutingConfig cfg;
+        cfg.num_experts = Eo;
+        cfg.moe_topk = Ko;
+        hyo_routing_cfg rc;
+        hyo_routing_cfg_default(&rc);
+        rc.num_experts = Eo;
+        rc.moe_topk = Ko;
+        if (opt == 0 || opt == 3) {
+            cfg.group_limited_greedy = rc.group_limited_greedy = 1;
+            cfg.n_group = rc.n_group = 4;
+            cfg.topk_group = rc.topk_group = 2;
         }
-        report(threw, "topkgating_full rejects token dropping on the GPU path");
+        if (opt == 1 || opt == 3) {
+            cfg.drop_tokens = rc.drop_tokens = 1;
+            cfg.capacity_factor = rc.capacity_factor = 0.75f;
+            cfg.min_capacity = rc.min_capacity = 3;
+        }
+        if (opt == 2 || opt == 3) cfg.compute_aux_loss = rc.compute_aux_loss = 1;
+        MoEGateOutput g;
+        topkgating_full(lo.data(), To, cfg, g);
+        hyo_gate_full ref;
+        hyo_topkgating_full(lo.data(), To, &rc, &ref);
+        const size_t n = (size_t)To * Eo * ref.capacity;
+        bool ok = g.expert_capacity == ref.capacity && g.exp_capacity_rate == ref.exp_capacity_rate &&
+                  memcmp(g.exp_counts, ref.exp_counts, Eo * 4) == 0;
+        size_t placed = 0;
+        for (size_t i = 0; ok && i < n; i++) {
+            ok = (g.dispatch_mask[i] ? 1 : 0) == ref.dispatch_mask[i];
+            placed += ref.dispatch_mask[i] ? 1 : 0;
+        }
+        const double ecw = rel_err(g.combine_weights, ref.combine_weights, n);
+        const double epr = rel_err(g.router_probs, ref.router_probs, (size_t)To * Eo);
+        const double eaux = std::fabs((double)g.aux_loss - ref.aux_loss) / std::fmax(1e-30, std::fabs((double)ref.aux_loss));
+        const bool aux_ok = rc.compute_aux_loss ? eaux < 2e-5 : g.aux_loss == 0.0f;
+        const bool dropped = !rc.drop_tokens || placed < (size_t)To * Ko;  // the case does drop pairs
+        static const char* names[] = {"topkgating_full group-limited greedy", "topkgating_full token dropping",
+                                      "topkgating_full aux loss", "topkgating_full groups + dropping + aux loss"};
+        char det[160];
+        snprintf(det, sizeof(det), "cap %u/%u rate %g/%g cw %.2e probs %.2e aux %g/%g placed %zu", g.expert_capacity,
+                 ref.capacity, g.exp_capacity_rate, ref.exp_capacity_rate, ecw, epr, g.aux_loss, ref.aux_loss, placed);
+        report(ok && ecw < 2e-6 && epr < 2e-6 && aux_ok && dropped, names[opt], det);
+        hyo_gate_full_free(&ref);
     }
     // ---------------------------------------------------------------- einsum dispatch / combine
     {
@@ -168,6 +206,51 @@ int main() {
         report(bits_equal(out.data(), ref.data(), out.size()),
                wt == HYO_Q8_0 ? "moe_forward_full Q8_0 overload bit-exact" : "moe_forward_full Q4_0 overload bit-exact",
                errs(out.data(), ref.data(), out.size()));
+    }
+    // moe_forward_full with group-limited greedy and token dropping (F32 and Q8_0)
+    {
+        MoERoutingConfig oc = rcfg;
+        oc.group_limited_greedy = true;
+        oc.n_group = 4;
+        oc.topk_group = 3;
+        oc.drop_tokens = true;
+        oc.capacity_factor = 0.5f;  // capacity max(4, (uint32)(0.5 * 4 * 21 / 16)) = 4 < 5.25 pairs per expert
+        oc.min_capacity = 0;
+        hyo_routing_cfg rc;
+        hyo_routing_cfg_default(&rc);
+        rc.num_experts = Ex;
+        rc.moe_topk = Kx;
+        rc.group_limited_greedy = 1;
+        rc.n_group = 4;
+        rc.topk_group = 3;
+        rc.drop_tokens = 1;
+        rc.capacity_factor = 0.5f;
+        rc.min_capacity = 0;
+        const uint32_t cap = hyo_drop_capacity(Tl, Ex, Kx, 0.5f, 0);
+        std::vector<float> out((size_t)Tl * H), ref(out.size()), q(out.size());
+        moe_forward_full(x.data(), Tl, H, wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data(), Ex, I, oc, out.data());
+        hyo_moe_forward_full(x.data(), Tl, H, wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data(), Ex, I, &rc,
+                             ref.data());
+        hyo_qlayer L{H, I, Ex, Kx, HYO_F32, 1, 1.0f, wr.data(), sgu.data(), sdn.data(), gu.data(), dn.data(), 4, 3, cap};
+        hyo_moe_forward_q(&L, x.data(), Tl, q.data(), nullptr, nullptr, nullptr, 1);
+        report(bits_equal(out.data(), q.data(), out.size()), "moe_forward_full F32 groups + dropping == q semantics",
+               errs(out.data(), q.data(), out.size()));
+        report(rel_err(out.data(), ref.data(), out.size()) < 1e-4,
+               "moe_forward_full F32 groups + dropping vs reference semantics", errs(out.data(), ref.data(), out.size()));
+        const size_t rb_h = hyo_type_row_bytes(HYO_Q8_0, H), rb_i = hyo_type_row_bytes(HYO_Q8_0, I);
+        std::vector<uint8_t> qgu((size_t)Ex * 2 * I * rb_h), qdn((size_t)Ex * H * rb_i), qsgu(2 * I * rb_h),
+            qsdn(H * rb_i);
+        hyo_quantize_row_q8_0(gu.data(), qgu.data(), gu.size());
+        hyo_quantize_row_q8_0(dn.data(), qdn.data(), dn.size());
+        hyo_quantize_row_q8_0(sgu.data(), qsgu.data(), sgu.size());
+        hyo_quantize_row_q8_0(sdn.data(), qsdn.data(), sdn.size());
+        moe_forward_full(x.data(), Tl, H, wr.data(), qsgu.data(), qsdn.data(), qgu.data(), qdn.data(), HYO_Q8_0, Ex, I,
+                         oc, out.data());
+        hyo_qlayer LQ{H, I, Ex, Kx, HYO_Q8_0, 1, 1.0f, wr.data(), qsgu.data(), qsdn.data(), qgu.data(), qdn.data(),
+                      4, 3, cap};
+        hyo_moe_forward_q(&LQ, x.data(), Tl, q.data(), nullptr, nullptr, nullptr, 1);
+        report(bits_equal(out.data(), q.data(), out.size()), "moe_forward_full Q8_0 groups + dropping == q semantics",
+               errs(out.data(), q.data(), out.size()));
     }
     {
         std::vector<float> out((size_t)Tl * H), ref(out.size());

@@ -3,6 +3,7 @@ include/hy_moe.h declares, and rejects invalid configurations before touching a
 device."""
 import ctypes as C
 import os
+import subprocess
 
 import pytest
 
@@ -76,7 +77,10 @@ def _cfg(hy, **kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(hidden=100), -1), (dict(intermediate=48), -1), (dict(num_experts=65), -1), (dict(topk=17), -1),
     (dict(topk=0), -1), (dict(max_tokens=0), -1), (dict(max_tokens=20000), -1), (dict(wtype=1), -2),
-    (dict(group_limited_greedy=1), -2), (dict(drop_tokens=1), -2), (dict(compute_aux_loss=1), -2),
+    (dict(group_limited_greedy=1, n_group=65, topk_group=2), -1),
+    (dict(group_limited_greedy=1, n_group=8, topk_group=65), -1),
+    (dict(drop_tokens=1, capacity_factor=-1.0), -1), (dict(drop_tokens=1, capacity_factor=float("nan")), -1),
+    (dict(drop_tokens=1, capacity_factor=1e30), -1),
 ])
 def test_invalid_configs_rejected_before_device(hy, kw, code):
     h = C.c_void_p()
@@ -84,3 +88,26 @@ def test_invalid_configs_rejected_before_device(hy, kw, code):
     assert rc == code
     assert h.value is None
     assert hy.lib().hy_last_error().decode()
+
+
+def test_config_struct_layouts_match_header(hy, tmp_path):
+    """The ctypes mirrors of hy_moe_config, hy_attn_config and hy_model_config have the
+    C header's field offsets and sizes (fields appended later keep the earlier ones)."""
+    structs = {"hy_moe_config": hy.Config, "hy_attn_config": hy.AttnConfig, "hy_model_config": hy.ModelConfig}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "hy_moe.h"', '#include "hy_attn.h"',
+             'int main(void) {']
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{os.path.join(ROOT, 'include')}", str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, got):
+        cname, f, v = line.split()
+        py = structs[cname]
+        want = C.sizeof(py) if f == "size" else getattr(py, f).offset
+        assert int(v) == want, (cname, f, int(v), want)

@@ -1,0 +1,152 @@
+"""GPU parity of the routing options of topkgating_full beyond the default
+(src/hunyuan_moe_full.cpp:135-214, 245-304): group-limited greedy, capacity-limited
+token dropping and the load-balancing aux loss, through the C ABI, against the
+q-semantics oracle, bit for bit.  Decode batches (T <= 16) take the general routing
+path when an option is on, so every T regime is covered."""
+import numpy as np
+import pytest
+
+import hy_oracle as O
+from test_gpu_parity import assert_exact
+
+pytestmark = pytest.mark.gpu
+
+H, I = 256, 128
+
+
+def skewed_input(seed, T, E):
+    """x with x[:, 0] = 1 so the router bias column (router_bias) skews the logits."""
+    x = O.synth(seed, 0, O.T_X, 0, (T, H), 1.0)
+    x[:, 0] = 1.0
+    return x
+
+
+def bias(E, span=2.0):
+    return np.linspace(span, -span, E).astype(np.float32)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+def test_group_limited_greedy_layer(gpu, wtype):
+    E, K, ng, tg = 64, 8, 8, 3
+    layer = O.synth_layer(H, I, E, K, wtype, seed=120, std=0.05)
+    layer.n_group, layer.topk_group = ng, tg
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=300, group_limited_greedy=1, n_group=ng, topk_group=tg)
+    m.upload(0, layer)
+    paths = [gpu.PATH_AUTO] if wtype == O.F32 else [gpu.PATH_AUTO, gpu.PATH_VALU, gpu.PATH_MFMA]
+    for T in (1, 7, 40, 300):
+        x = O.synth(121 + T, 0, O.T_X, 0, (T, H), 1.0)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        for path in paths if T == 40 else [gpu.PATH_AUTO]:
+            m.set_path(path)
+            out, lg, w, idx = m.run(0, x, debug=True)
+            np.testing.assert_array_equal(lg.view(np.uint32), rlg.view(np.uint32))
+            np.testing.assert_array_equal(idx, ridx)
+            np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+            assert_exact(out, ref, f"groups wtype={wtype} T={T} path={path}")
+        # every selected expert lies in one of the topk_group kept groups
+        assert all(len(set((idx[t] // (E // ng)).tolist())) <= tg for t in range(T))
+    m.set_path(gpu.PATH_AUTO)
+    m.close()
+
+
+def test_group_limited_greedy_fillers(gpu):
+    """K larger than the kept groups' experts: masked experts fill with weight 0, which
+    the combine skips."""
+    E, K, ng, tg = 16, 6, 4, 1
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=130, std=0.05)
+    layer.n_group, layer.topk_group = ng, tg
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=64, group_limited_greedy=1, n_group=ng, topk_group=tg)
+    m.upload(0, layer)
+    for T in (3, 33):
+        x = O.synth(131 + T, 0, O.T_X, 0, (T, H), 1.0)
+        out, lg, w, idx = m.run(0, x, debug=True)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+        assert np.all(w[:, 4:] == 0.0)
+        assert_exact(out, ref, f"fillers T={T}")
+    m.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+@pytest.mark.parametrize("cf,mc", [(0.5, 0), (1.0, 3)])
+def test_token_dropping_layer(gpu, wtype, cf, mc):
+    E, K = 16, 4
+    layer = O.synth_layer(H, I, E, K, wtype, seed=140, std=0.05, router_bias=bias(E))
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=700, drop_tokens=1, capacity_factor=cf, min_capacity=mc)
+    m.upload(0, layer)
+    n_dropped = 0
+    for T in (5, 16, 40, 700):
+        x = skewed_input(141 + T, T, E)
+        cap = O.drop_capacity(T, E, K, cf, mc)
+        layer.capacity = cap
+        out, lg, w, idx = m.run(0, x, debug=True)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+        assert_exact(out, ref, f"drop wtype={wtype} cf={cf} T={T} cap={cap}")
+        keep = O.capacity_keep(ridx, E, cap)
+        n_dropped += int((~keep).sum())
+        aux, gcap, rate = m.last_gate()
+        assert gcap == cap and aux == 0.0
+        assert rate == np.float32(keep.sum()) / np.float32(T * K)
+        D, counts = m.last_routing()
+        np.testing.assert_array_equal(counts, np.bincount(ridx.ravel(), minlength=E))
+    assert n_dropped > 0
+    m.close()
+
+
+@pytest.mark.parametrize("groups", [False, True])
+def test_aux_loss(gpu, groups):
+    E, K = 64, 8
+    kw = dict(group_limited_greedy=1, n_group=8, topk_group=4) if groups else {}
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=150, std=0.05)
+    if groups:
+        layer.n_group, layer.topk_group = 8, 4
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=2000, compute_aux_loss=1, **kw)
+    m.upload(0, layer)
+    for T in (1, 16, 40, 2000):
+        x = O.synth(151 + T, 0, O.T_X, 0, (T, H), 1.0)
+        out = m.run(0, x)
+        lg, w, idx, probs, keep = O.moe_route_q(layer, x, nthreads=8)
+        aux, cap, rate = m.last_gate()
+        assert aux == O.aux_loss_q(probs, idx), (T, aux, O.aux_loss_q(probs, idx))
+        counts = np.bincount(idx.ravel(), minlength=E)
+        assert cap == max(int(counts.max()), 0) and rate == np.float32(1.0)
+        if T <= 40:
+            assert_exact(out, O.moe_forward_q(layer, x), f"aux T={T}")
+    m.close()
+
+
+def test_all_options_stack(gpu):
+    """Two stacked layers with groups, dropping and the aux loss on, decode and batch."""
+    E, K, L = 16, 4, 2
+    layers = [O.synth_layer(H, I, E, K, O.Q8_0, seed=160, layer=l, std=0.05) for l in range(L)]
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=100, num_layers=L, group_limited_greedy=1, n_group=4, topk_group=2,
+                drop_tokens=1, capacity_factor=0.75, min_capacity=0, compute_aux_loss=1)
+    for l in range(L):
+        m.synth(l, seed=160, std=0.05)
+    for T in (6, 100):
+        cap = O.drop_capacity(T, E, K, 0.75, 0)
+        for lyr in layers:
+            lyr.n_group, lyr.topk_group, lyr.capacity = 4, 2, cap
+        x = O.synth(161 + T, 0, O.T_X, 0, (T, H), 1.0)
+        xb, ob = gpu.Buf.from_array(x), gpu.Buf.empty((T, H))
+        m.stack_forward(0, L, xb, T, 1e-5, ob)
+        assert_exact(ob.numpy(), O.moe_stack_q(layers, x, eps=1e-5), f"options stack T={T}")
+    m.close()
+
+
+def test_route_logits_groups_and_aux_entry_points(gpu):
+    """hy_route_logits_groups and hy_aux_loss, the calls the C++ topkgating_full uses."""
+    rng = np.random.default_rng(170)
+    for T, E, K, ng, tg in ((37, 64, 8, 8, 3), (5, 16, 6, 4, 1), (300, 16, 4, 0, 0), (9, 64, 8, 3, 2)):
+        lg = (rng.standard_normal((T, E)) * 1.5).astype(np.float32)
+        for norm, scale in ((1, 1.0), (0, 2.5)):
+            w, idx, probs = gpu.route_logits_groups(lg, K, norm=norm, scale=scale, n_group=ng, topk_group=tg)
+            rw, ridx, rprobs = O.route_topk_groups(lg, K, norm=norm, scale=scale, n_group=ng, topk_group=tg)
+            np.testing.assert_array_equal(idx, ridx)
+            np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+            np.testing.assert_array_equal(probs.view(np.uint32), rprobs.view(np.uint32))
+            counts = np.bincount(idx.ravel(), minlength=E).astype(np.int32)
+            assert gpu.aux_loss(probs, counts) == O.aux_loss_q(rprobs, ridx)
