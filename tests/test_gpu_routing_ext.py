@@ -140,7 +140,8 @@ def test_all_options_stack(gpu):
 def test_route_logits_groups_and_aux_entry_points(gpu):
     """hy_route_logits_groups and hy_aux_loss, the calls the C++ topkgating_full uses."""
     rng = np.random.default_rng(170)
-    for T, E, K, ng, tg in ((37, 64, 8, 8, 3), (5, 16, 6, 4, 1), (300, 16, 4, 0, 0), (9, 64, 8, 3, 2)):
+    for T, E, K, ng, tg in ((37, 64, 8, 8, 3), (5, 16, 6, 4, 1), (300, 16, 4, 0, 0), (9, 64, 8, 3, 2),
+                            (20, 16, 4, 20, 3), (20, 16, 4, 4, 9), (25, 8, 1, 2, 1), (11, 64, 16, 64, 64)):
         lg = (rng.standard_normal((T, E)) * 1.5).astype(np.float32)
         for norm, scale in ((1, 1.0), (0, 2.5)):
             w, idx, probs = gpu.route_logits_groups(lg, K, norm=norm, scale=scale, n_group=ng, topk_group=tg)
@@ -150,3 +151,29 @@ def test_route_logits_groups_and_aux_entry_points(gpu):
             np.testing.assert_array_equal(probs.view(np.uint32), rprobs.view(np.uint32))
             counts = np.bincount(idx.ravel(), minlength=E).astype(np.int32)
             assert gpu.aux_loss(probs, counts) == O.aux_loss_q(rprobs, ridx)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+def test_options_without_shared_expert_and_single_topk(gpu, wtype):
+    """No shared expert (a token whose pairs are all dropped gets exactly 0) and K = 1
+    (weight p * scale under topkgating_full's rule), with groups and dropping."""
+    E, K = 8, 1
+    layer = O.synth_layer(H, I, E, K, wtype, seed=180, std=0.05, router_bias=bias(E, 3.0), shared=False)
+    layer.n_group, layer.topk_group = 2, 1
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=64, has_shared=False, routed_scaling_factor=1.5,
+                group_limited_greedy=1, n_group=2, topk_group=1, drop_tokens=1, capacity_factor=1.0, min_capacity=0)
+    layer.routed_scaling_factor = 1.5
+    m.upload(0, layer)
+    for T in (3, 16, 64):
+        x = skewed_input(181 + T, T, E)
+        cap = O.drop_capacity(T, E, K, 1.0, 0)
+        layer.capacity = cap
+        out, lg, w, idx = m.run(0, x, debug=True)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+        assert_exact(out, ref, f"no shared, K=1, T={T}")
+        keep = O.capacity_keep(ridx, E, cap)
+        if (~keep).any():
+            assert np.all(out[~keep[:, 0]] == 0.0)
+    m.close()
