@@ -112,7 +112,6 @@ struct hy_moe_ctx {
 
     // routing options beyond the default (resolved from the config)
     int n_group = 0, topk_group = 0;  // group-limited greedy when n_group > 0
-    uint32_t last_T = 0;              // tokens of the last forward (gate statistics)
 
     // timing
     bool prof = false;
@@ -284,7 +283,6 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int NT = mfma ? hy::mfma_shape_tokens(shape) : hy::gemv_tile_tokens();
     // group-limited greedy, dropping and the aux loss take the general routing path
     const bool ext = c->n_group > 0 || c->cfg.drop_tokens || c->cfg.compute_aux_loss;
-    c->last_T = T;
     if (!ext && !mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
         // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
@@ -1071,8 +1069,13 @@ int hy_moe_last_routing(hy_moe_ctx* c, uint32_t* distinct, int32_t* counts) {
 
 int hy_moe_last_gate(hy_moe_ctx* c, float* aux_loss, uint32_t* expert_capacity, float* exp_capacity_rate) {
     if (!c) return fail(HY_ERR_INVALID, "null ctx");
-    if (c->last_T == 0) return fail(HY_ERR_STATE, "no forward has run");
     HIP_TRY(hipStreamSynchronize(c->last_stream));
+    // the routing pass stores its token count beside the tile counts, so a graph replay
+    // reports its own batch
+    int meta[4];
+    HIP_TRY(hipMemcpy(meta, c->meta, sizeof(meta), hipMemcpyDeviceToHost));
+    const uint32_t T = (uint32_t)meta[3];
+    if (T == 0) return fail(HY_ERR_STATE, "no forward has run");
     std::vector<int32_t> cnt(c->E);
     HIP_TRY(hipMemcpy(cnt.data(), c->cnt, (size_t)c->E * 4, hipMemcpyDeviceToHost));
     float aux = 0.0f;
@@ -1080,7 +1083,7 @@ int hy_moe_last_gate(hy_moe_ctx* c, float* aux_loss, uint32_t* expert_capacity, 
     // src/hunyuan_moe_full.cpp:209-227: the capacity rule, or the largest count
     uint32_t cap = 0;
     if (c->cfg.drop_tokens) {
-        cap = drop_capacity(c->cfg, c->last_T);
+        cap = drop_capacity(c->cfg, T);
     } else {
         for (int32_t n : cnt) cap = std::max(cap, (uint32_t)n);
         cap = std::max(cap, c->cfg.min_capacity);
@@ -1090,7 +1093,7 @@ int hy_moe_last_gate(hy_moe_ctx* c, float* aux_loss, uint32_t* expert_capacity, 
     for (int32_t n : cnt) placed += (float)std::min<uint32_t>((uint32_t)n, cap);
     if (aux_loss) *aux_loss = aux;
     if (expert_capacity) *expert_capacity = cap;
-    if (exp_capacity_rate) *exp_capacity_rate = placed / (float)(c->last_T * (uint32_t)c->K);
+    if (exp_capacity_rate) *exp_capacity_rate = placed / (float)(T * (uint32_t)c->K);
     return HY_OK;
 }
 

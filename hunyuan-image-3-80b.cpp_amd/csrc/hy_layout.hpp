@@ -63,7 +63,7 @@ struct Routing {
     const int* tile_e;     // [max_tiles] expert (E = shared)
     const int* tile_start; // [max_tiles] first pair (routed) / token (shared)
     const int* tile_n;     // [max_tiles] tokens in tile
-    const int* meta;       // [0] n_routed_tiles, [1] n_tiles, [2] distinct experts,
+    const int* meta;       // [0] n_routed_tiles, [1] n_tiles, [2] distinct experts, [3] T,
                            // [META_TILE_OFF + e] first tile of expert e (e <= E + 1)
 };
 

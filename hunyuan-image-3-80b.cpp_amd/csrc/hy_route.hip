@@ -547,6 +547,7 @@ __global__ __launch_bounds__(256) void dispatch_scan_kernel(int T, int K, int E,
             o.meta[0] = routed;
             o.meta[1] = routed + ns;
             o.meta[2] = distinct;
+            o.meta[3] = T;
             o.meta[META_TILE_OFF + E] = routed;
             o.meta[META_TILE_OFF + E + 1] = routed + ns;
         }
@@ -701,6 +702,7 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(Decod
             a.o.meta[0] = routed;
             a.o.meta[1] = all;
             a.o.meta[2] = distinct;
+            a.o.meta[3] = T;
             a.o.meta[META_TILE_OFF + E] = routed;
             a.o.meta[META_TILE_OFF + E + 1] = all;
         }

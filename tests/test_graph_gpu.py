@@ -97,3 +97,33 @@ def test_stack_forward_replay(gpu):
 def test_capture_rejects_null_stream(gpu):
     with pytest.raises(gpu.HyError):
         gpu.check(gpu.lib().hy_graph_begin(None))
+
+
+@pytest.mark.parametrize("T", [4, 100])
+def test_routing_options_replay(gpu, T):
+    """Group-limited greedy, dropping and the aux loss under capture: every replay equals
+    the eager call, output and gate statistics (aux loss, capacity, capacity rate)."""
+    m = gpu.Moe(H, I, E, K, O.Q8_0, num_layers=1, max_tokens=128, group_limited_greedy=1, n_group=4,
+                topk_group=2, drop_tokens=1, capacity_factor=0.75, min_capacity=0, compute_aux_loss=1)
+    m.synth(0, seed=41, std=0.05)
+    st = gpu.Stream()
+    xb, outg = gpu.Buf.from_array(_x(9, T)), gpu.Buf.empty((T, H))
+    other = gpu.Buf.from_array(_x(10, 128))
+    other_out = gpu.Buf.empty((128, H))
+    g = gpu.Graph(st, lambda: m.forward(0, xb, T, outg, st.h))
+    try:
+        for rep in range(3):
+            m.forward(0, other, 128 - 60 * rep, other_out, st.h)
+            st.synchronize()
+            g.launch()
+            st.synchronize()
+            got, gate_g = outg.numpy(), m.last_gate()  # the replay's own T, not the eager call's
+            ref = gpu.Buf.empty((T, H))
+            m.forward(0, xb, T, ref, st.h)
+            st.synchronize()
+            np.testing.assert_array_equal(got.view(np.uint32), ref.numpy().view(np.uint32), err_msg=f"replay {rep}")
+            assert gate_g == m.last_gate()
+    finally:
+        g.close()
+        st.close()
+        m.close()
