@@ -9,7 +9,7 @@ namespace hy {
 constexpr int QK = 32;       // GGUF block length (Q8_0 and Q4_0)
 constexpr int WAVE = 64;     // CDNA wavefront
 constexpr int MAX_E = 64;    // experts per layer handled by the routing kernels
-constexpr int MAX_K = 16;    // top-k bound
+constexpr int MAX_K = 64;    // top-k bound: topk_f32's best[64] (src/hunyuan_moe_full.cpp:61)
 // dispatch meta block: [0] routed tiles, [1] all tiles, [2] distinct experts, [3] unused,
 // [4 + e] first tile of expert e (e = 0..E, E = shared), [4 + E + 1] end of the tiles
 constexpr int META_TILE_OFF = 4;

@@ -489,8 +489,9 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 // dropped pair, or a zero gate) adds nothing, as einsum_combine skips it
 // (src/hunyuan_moe_full.cpp:387-397); its y row is read but not used.  One thread per 4 outputs
 // (16-byte loads of the y rows); each output keeps the scalar fmaf order.  The token's
-// KMAX list entries (indices clamped to K - 1) and then its y rows are all loaded
-// before the first fmaf, so a thread waits for two rounds of loads, not 2 K.
+// list entries are taken KMAX at a time (one pass for K <= KMAX; indices clamped to
+// K - 1): a chunk's entries and then its y rows are all loaded before its first fmaf,
+// so a thread waits for two rounds of loads per chunk, not 2 K.
 template <int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __restrict__ y, int T, int H, int K,
                                                       int has_shared, const float* __restrict__ resid,
@@ -499,23 +500,25 @@ __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __
     const int H4 = H / 4;
     if (idx >= (size_t)T * H4) return;
     const int t = (int)(idx / H4), r4 = (int)(idx % H4);
-    int pos[KMAX];
-    float w[KMAX];
-#pragma unroll
-    for (int k = 0; k < KMAX; k++) {
-        const int kk = min(k, K - 1);
-        pos[k] = R.comb_pos[t * K + kk];
-        w[k] = R.comb_w[t * K + kk];
-    }
-    float4 v[KMAX];
-#pragma unroll
-    for (int k = 0; k < KMAX; k++) v[k] = reinterpret_cast<const float4*>(y + (size_t)pos[k] * H)[r4];
     float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k0 = 0; k0 < K; k0 += KMAX) {
+        int pos[KMAX];
+        float w[KMAX];
 #pragma unroll
-    for (int k = 0; k < KMAX; k++)
-        if (k < K && w[k] != 0.0f)
-            c = make_float4(fmaf(w[k], v[k].x, c.x), fmaf(w[k], v[k].y, c.y), fmaf(w[k], v[k].z, c.z),
-                            fmaf(w[k], v[k].w, c.w));
+        for (int k = 0; k < KMAX; k++) {
+            const int kk = min(k0 + k, K - 1);
+            pos[k] = R.comb_pos[t * K + kk];
+            w[k] = R.comb_w[t * K + kk];
+        }
+        float4 v[KMAX];
+#pragma unroll
+        for (int k = 0; k < KMAX; k++) v[k] = reinterpret_cast<const float4*>(y + (size_t)pos[k] * H)[r4];
+#pragma unroll
+        for (int k = 0; k < KMAX; k++)
+            if (k0 + k < K && w[k] != 0.0f)
+                c = make_float4(fmaf(w[k], v[k].x, c.x), fmaf(w[k], v[k].y, c.y), fmaf(w[k], v[k].z, c.z),
+                                fmaf(w[k], v[k].w, c.w));
+    }
     float4 o = c;
     if (has_shared) {
         const float4 u = reinterpret_cast<const float4*>(y + ((size_t)T * K + t) * H)[r4];
@@ -610,8 +613,8 @@ hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K,
         hipLaunchKernelGGL(combine_kernel<4>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
     else if (K <= 8)
         hipLaunchKernelGGL(combine_kernel<8>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
-    else
-        hipLaunchKernelGGL(combine_kernel<MAX_K>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
+    else  // 16 pairs per chunk (larger K loops over chunks)
+        hipLaunchKernelGGL(combine_kernel<16>, grid, dim3(256), 0, s, R, y, T, H, K, has_shared, resid, out);
     return hipGetLastError();
 }
 

@@ -55,7 +55,7 @@ typedef struct {
     uint32_t hidden;        /* H, multiple of 32 */
     uint32_t intermediate;  /* I, multiple of 32 */
     uint32_t num_experts;   /* E, 1..64 */
-    uint32_t topk;          /* K, 1..min(E, 16) */
+    uint32_t topk;          /* K, 1..min(E, 64) (topk_f32's bound) */
     uint32_t num_layers;    /* resident layers */
     uint32_t max_tokens;    /* largest T per call, 1..16384; sizes the work arena */
     int32_t  wtype;         /* HY_TYPE_F32 / HY_TYPE_Q8_0 / HY_TYPE_Q4_0 */
@@ -281,7 +281,7 @@ int hy_dispatch_pairs(const int32_t* indices_dev, const float* weights_dev, uint
  * callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  Same arguments and results; the
  * workspace is a fixed 4 MiB array in device memory that each GPU holds until the
- * process ends, enough for every shape hy_dispatch_pairs accepts (larger needs are
+ * process ends, enough for every call with T*K <= 262,144 pairs (larger needs are
  * rejected with HY_ERR_INVALID).  Stream-ordered: it returns without waiting, the
  * outputs are ready when the stream gets there.  All calls on one GPU share that
  * array, so calls that overlap on one GPU (different streams, or different threads

@@ -1,5 +1,6 @@
 """GPU parity at the limits the C ABI accepts: the largest batch (max_tokens = 16384),
-the largest top-k (16), top-k equal to the number of experts, and a single expert.
+large top-k (16, 32 and the bound 64, topk_f32's best[64]), top-k equal to the number of
+experts, and a single expert.
 
 Each token's output depends only on its own row (default routing: no capacity, no
 drops), so the oracle runs on sampled rows and row-permutation invariance covers the
@@ -75,3 +76,55 @@ def test_single_expert(gpu, wtype, shared):
         np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
         assert_exact(out, ref, f"E=1 wtype={wtype} shared={shared} T={T}")
     m.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.F32])
+def test_topk_64_every_expert(gpu, wtype):
+    """K = E = 64, the top-k bound: the one-launch decode routing while T*K <= 256 (T = 1,
+    4), the general routing above (T = 5), the grouped GEMM for batches (T = 100); the
+    combine sums 64 pairs per token in four chunks."""
+    H, I, E, K = 256, 128, 64, 64
+    layer = O.synth_layer(H, I, E, K, wtype, seed=190, std=0.05)
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=100)
+    m.upload(0, layer)
+    for T in ((1, 4, 5) if wtype == O.F32 else (1, 4, 5, 100)):
+        x = O.synth(191 + T, 0, O.T_X, 0, (T, H), 1.0)
+        out, lg, w, idx = m.run(0, x, debug=True)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+        assert np.all(np.sort(idx, axis=1) == np.arange(E))
+        assert_exact(out, ref, f"K=E=64 wtype={wtype} T={T}")
+    m.close()
+
+
+def test_topk_32_large_batch(gpu):
+    """K = 32 of 64 experts at T = 8192 (262,144 routed pairs): sampled rows against the
+    oracle, every row through permutation invariance; the combine takes two chunks."""
+    H, I, E, K, T = 256, 128, 64, 32, 8192
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=200, std=0.05)
+    x = O.synth(201, 0, O.T_X, 0, (T, H), 1.0)
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=T)
+    m.upload(0, layer)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    rows = sample_rows(T, n=24)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x[rows], debug=True)
+    np.testing.assert_array_equal(idx[rows], ridx)
+    np.testing.assert_array_equal(w[rows].view(np.uint32), rw.view(np.uint32))
+    assert_exact(out[rows], ref, f"K={K} T={T}")
+    D, counts = m.last_routing()
+    assert counts.sum() == T * K
+    assert_permutes(lambda v: m.run(0, v), x, f"K={K} T={T}")
+    m.close()
+
+
+def test_router_topk_64(gpu):
+    """The stateless router and gating entry points at K = 64."""
+    rng = np.random.default_rng(210)
+    x = rng.standard_normal((9, 256)).astype(np.float32)
+    wr = (rng.standard_normal((64, 256)) * 0.1).astype(np.float32)
+    lg, w, idx = gpu.router_topk(x, wr, 64)
+    np.testing.assert_array_equal(lg.view(np.uint32), O.router_logits_blocked(x, wr).view(np.uint32))
+    rw, ridx = O.route_topk(lg, 64)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))

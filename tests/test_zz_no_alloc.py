@@ -70,7 +70,9 @@ def test_noalloc_dispatch_back_to_back_on_one_stream(gpu):
 
 
 def test_noalloc_dispatch_rejects_bad_shapes(gpu):
-    for T, K, E in ((16385, 8, 64), (4, 17, 64), (4, 8, 65), (0, 8, 64)):
+    # too many tokens, top-k past its bound, too many experts, no tokens, and a shape
+    # whose workspace exceeds the fixed array (T*K = 524,288 pairs)
+    for T, K, E in ((16385, 8, 64), (4, 65, 64), (4, 8, 65), (0, 8, 64), (16384, 32, 64)):
         idx = gpu.Buf.empty((max(T, 1), K), np.int32)
         w = gpu.Buf.empty((max(T, 1), K))
         out = gpu.Buf.empty((max(T, 1) * K + E + 1,), np.int32)
