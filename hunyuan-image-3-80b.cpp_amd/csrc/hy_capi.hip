@@ -276,8 +276,13 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int iT = (int)T;
     const int has_shared = c->cfg.has_shared ? 1 : 0;
     const int renorm = renorm_rule(c->cfg.norm_topk_prob, c->cfg.topk);
-    // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode
-    const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) &&
+    // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode.  The
+    // grouped GEMM addresses activation rows with 32-bit offsets: x by token (T x H
+    // bytes) and h by slot (T*(K+1) x I bytes) must stay below 2^32 (at I = 3072 any
+    // T <= 16384 with K <= 64); beyond that the GEMV, which computes the same bits, runs.
+    const bool mfma_fits = (uint64_t)T * (uint64_t)H < (1ull << 32) &&
+                           (uint64_t)T * (uint64_t)(K + 1) * (uint64_t)I < (1ull << 32);
+    const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) && mfma_fits &&
                       (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
     const int shape = mfma ? hy::mfma_shape(iT, K, E, H, I) : -1;
     const int NT = mfma ? hy::mfma_shape_tokens(shape) : hy::gemv_tile_tokens();

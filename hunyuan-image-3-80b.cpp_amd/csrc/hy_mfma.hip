@@ -206,7 +206,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     // pieces; lane position p (copy v, lane l: p = 64 v + l) lands at +16 p, i.e. token
     // row p / 2, position p % 2, which holds half (p % 2) ^ (bit 3 of the row)
     constexpr int TPW = SH::TPW;
-    uint32_t b_off[SH::B_LOADS];
+    uint32_t b_off[SH::B_LOADS];  // 32-bit: the host keeps rows x Kd below 2^32
 #pragma unroll
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
