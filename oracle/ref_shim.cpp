@@ -88,15 +88,16 @@ void ref_einsum_combine(const float* cw, const float* eo, uint32_t T, uint32_t H
     einsum_combine(cw, eo, T, H, E, C, out);
 }
 
-// moe_forward_full without a shared expert.  min_capacity is raised to T so the
-// caller-side capacity (K*T/E+1, min min_capacity) and the gating's own capacity
-// (max count, min min_capacity) coincide and the reference's buffers are consistent.
+// moe_forward_full without a shared expert.  Without token dropping, min_capacity is
+// raised to T so the caller-side capacity (K*T/E+1, min min_capacity) and the gating's
+// own capacity (max count, min min_capacity) coincide and the reference's buffers are
+// consistent; with dropping both sides use the same capacity rule and it is kept.
 void ref_moe_forward_full_noshared(const float* x, uint32_t T, uint32_t H, const float* wr,
                                    const float* gu, const float* dn, uint32_t E, uint32_t I,
                                    const hyo_routing_cfg* c, float* out) {
     MoERoutingConfig cfg = to_cfg(c);
     cfg.num_experts = E;
-    if (cfg.min_capacity < T) cfg.min_capacity = T;
+    if (!cfg.drop_tokens && cfg.min_capacity < T) cfg.min_capacity = T;
     moe_forward_full(x, T, H, wr, nullptr, nullptr, gu, dn, E, I, cfg, out);
 }
 

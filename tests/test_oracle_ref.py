@@ -205,3 +205,33 @@ def test_live_moe_forward_full_vs_reference(refimpl, dims):
                                           C.byref(cfg), O.fp(out_r))
     out = oracle_moe_full(x, wr, gu, dn, E, I, K)
     np.testing.assert_array_equal(out.view(np.uint32), out_r.view(np.uint32))
+
+
+@pytest.mark.parametrize("kw", [
+    dict(drop_tokens=1, capacity_factor=1.0, min_capacity=2),
+    dict(drop_tokens=1, capacity_factor=0.5, min_capacity=0, group_limited_greedy=1, n_group=4, topk_group=2),
+    dict(drop_tokens=1, capacity_factor=0.75, min_capacity=0, compute_aux_loss=1, norm_topk_prob=0,
+         routed_scaling_factor=2.0),
+])
+def test_live_moe_forward_full_options_vs_reference(refimpl, kw):
+    """moe_forward_full with token dropping (alone, with group-limited greedy, with the aux
+    loss and scaling): with drop_tokens the reference sizes its buffers with the same
+    capacity topkgating_full writes, so these configurations run it as written."""
+    T, H, I, E, K = 40, 64, 32, 16, 4
+    seed = 77
+    x = O.synth(seed, 0, O.T_X, 0, (T, H), 1.0)
+    wr = O.synth(seed, 0, O.T_ROUTER, 0, (E, H), 0.3)
+    gu = O.synth(seed, 0, O.T_GU, 0, (E, 2 * I, H), 0.05)
+    dn = O.synth(seed, 0, O.T_DN, 0, (E, H, I), 0.05)
+    cfg = O.default_cfg(E, K, **kw)
+    out_r = np.zeros((T, H), dtype=np.float32)
+    refimpl.ref_moe_forward_full_noshared(O.fp(x), T, H, O.fp(wr), O.fp(gu), O.fp(dn), E, I,
+                                          C.byref(cfg), O.fp(out_r))
+    out = np.zeros((T, H), dtype=np.float32)
+    assert O.lib().hyo_moe_forward_full(O.fp(x), T, H, O.fp(wr), None, None, O.fp(gu), O.fp(dn), E, I,
+                                        C.byref(cfg), O.fp(out)) == 0
+    np.testing.assert_array_equal(out.view(np.uint32), out_r.view(np.uint32))
+    # the configuration does drop pairs
+    lg = np.zeros((T, E), dtype=np.float32)
+    O.lib().hyo_router_logits_seq(O.fp(x), O.fp(wr), T, H, E, O.fp(lg))
+    assert oracle_gating_full(lg, cfg)["rate"] < 1.0
