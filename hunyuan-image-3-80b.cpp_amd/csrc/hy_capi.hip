@@ -208,8 +208,8 @@ int check_cfg(const hy_moe_config* c) {
         return fail(HY_ERR_INVALID, "max_tokens=%u must be in 1..16384", c->max_tokens);
     if (c->wtype != HY_TYPE_F32 && c->wtype != HY_TYPE_Q8_0 && c->wtype != HY_TYPE_Q4_0)
         return fail(HY_ERR_UNSUPPORTED, "weight type %d not supported (F32=0, Q4_0=2, Q8_0=8)", c->wtype);
-    if (c->group_limited_greedy && c->n_group > 0 && c->topk_group > 0 && (c->n_group > 64 || c->topk_group > 64))
-        return fail(HY_ERR_INVALID, "n_group=%u / topk_group=%u must be <= 64", c->n_group, c->topk_group);
+    if (c->group_limited_greedy && c->n_group > 0 && c->topk_group > 64)
+        return fail(HY_ERR_INVALID, "topk_group=%u must be <= 64 (topk_f32's bound)", c->topk_group);
     if (c->drop_tokens) {
         // the capacity rule converts capacity_factor * K * T / E to uint32
         const float most = c->capacity_factor * (float)c->topk * (float)c->max_tokens / (float)c->num_experts;
@@ -458,7 +458,8 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
     c->K = (int)cfg->topk;
     c->X = c->E + (cfg->has_shared ? 1 : 0);
     if (cfg->group_limited_greedy && cfg->n_group > 0 && cfg->topk_group > 0) {
-        c->n_group = (int)cfg->n_group;
+        // n_group > E leaves every group empty (E / n_group == 0): E + 1 means the same
+        c->n_group = (int)std::min<uint32_t>(cfg->n_group, cfg->num_experts + 1);
         c->topk_group = (int)cfg->topk_group;
     }
     const int wt = cfg->wtype;
@@ -796,9 +797,10 @@ int hy_route_logits_groups(const float* lg, uint32_t T, uint32_t E, uint32_t K, 
     if (!lg || !w || !idx) return fail(HY_ERR_INVALID, "null pointer");
     if (T == 0 || E == 0 || E > (uint32_t)hy::MAX_E || K == 0 || K > E || K > (uint32_t)hy::MAX_K)
         return fail(HY_ERR_INVALID, "bad routing shape");
-    if (n_group > 64 || topk_group > 64) return fail(HY_ERR_INVALID, "n_group / topk_group must be <= 64");
+    if (n_group > 0 && topk_group > 64) return fail(HY_ERR_INVALID, "topk_group must be <= 64 (topk_f32's bound)");
     hy::RouteOpts opt;
-    opt.n_group = (int)n_group;
+    // n_group > E leaves every group empty (E / n_group == 0): E + 1 means the same
+    opt.n_group = (int)std::min<uint32_t>(n_group, E + 1);
     opt.topk_group = (int)topk_group;
     opt.probs = probs;
     HIP_TRY(hy::launch_topk_from_logits(lg, (int)T, (int)E, (int)K, renorm_rule(norm, K), scale, w, idx,

@@ -67,7 +67,7 @@ typedef struct {
     int32_t  compute_aux_loss;     /* 1: the load-balancing aux loss (hy_moe_last_gate) */
     int32_t  device;               /* HIP device ordinal */
     /* appended after the fields above, which keep their offsets */
-    uint32_t n_group;              /* groups of num_experts / n_group experts (<= 64); 0: off */
+    uint32_t n_group;              /* groups of num_experts / n_group experts; 0: off */
     uint32_t topk_group;           /* groups kept per token (<= 64); 0: off */
     float    capacity_factor;      /* drop_tokens: capacity max(K, (uint32)(capacity_factor*K*T/E)) */
     uint32_t min_capacity;         /* lower bound of the capacity, with or without dropping */
@@ -221,7 +221,7 @@ int hy_route_logits(const float* logits_dev, uint32_t T, uint32_t E, uint32_t K,
                     float routed_scaling_factor, float* weights_dev, int32_t* indices_dev, void* stream);
 
 /* hy_route_logits with group-limited greedy (src/hunyuan_moe_full.cpp:135-166) when
- * n_group > 0 and topk_group > 0 (both <= 64): per token, groups of E / n_group experts
+ * n_group > 0 and topk_group > 0 (topk_group <= 64): per token, groups of E / n_group experts
  * score the largest probability in them, the topk_group best groups stay and the other
  * groups' experts get probability 0, then the top K of those probabilities (equal
  * values: lower index) with their probabilities as weights.  probs_dev [T][E] (may be

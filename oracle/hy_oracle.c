@@ -830,23 +830,26 @@ static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, floa
     }
     float p[64];
     for (uint32_t e = 0; e < E; e++) p[e] = hyo_expf(l[e] - m) / s;
-    /* group scores: max over the group's experts, from 0 (:139-148) */
+    /* group scores: max over the group's experts, from 0 (:139-148).  With
+     * E / n_group == 0 (n_group > E) no expert is in a group and nothing is masked. */
     const uint32_t gs = E / n_group;
     float gsc[64], gv[64];
     int32_t gi[64];
-    for (uint32_t g = 0; g < n_group; g++) {
+    for (uint32_t g = 0; gs > 0 && g < n_group; g++) {
         float mx = 0.0f;
         for (uint32_t j = 0; j < gs; j++)
             if (p[g * gs + j] > mx) mx = p[g * gs + j];
         gsc[g] = mx;
     }
     /* the best topk_group groups; experts of the others are set to 0 (:150-165) */
-    hyo_topk_f32(gsc, n_group, topk_group, gv, gi);
-    uint8_t sel[64] = {0};
-    for (uint32_t kg = 0; kg < topk_group; kg++) sel[gi[kg]] = 1;
-    for (uint32_t g = 0; g < n_group; g++)
-        if (!sel[g])
-            for (uint32_t j = 0; j < gs; j++) p[g * gs + j] = 0.0f;
+    if (gs > 0) {
+        hyo_topk_f32(gsc, n_group, topk_group, gv, gi);
+        uint8_t sel[64] = {0};
+        for (uint32_t kg = 0; kg < topk_group; kg++) sel[gi[kg]] = 1;
+        for (uint32_t g = 0; g < n_group; g++)
+            if (!sel[g])
+                for (uint32_t j = 0; j < gs; j++) p[g * gs + j] = 0.0f;
+    }
     /* top-K of the masked probabilities (:168-178), weights from them (:229-243) */
     hyo_topk_f32(p, E, K, v, idx);
     for (uint32_t k = 0; k < K; k++) ps += v[k];
@@ -963,7 +966,7 @@ static int hyo_check_layer(const hyo_qlayer* L) {
     if (L->K > 64 || L->K > L->E || L->E > 64) return -1;
     if (L->H % HYO_QK || L->I % HYO_QK) return -1;
     if (L->wtype != HYO_F32 && L->wtype != HYO_Q8_0 && L->wtype != HYO_Q4_0) return -1;
-    if (L->n_group > 0 && L->topk_group > 0 && (L->n_group > 64 || L->topk_group > 64)) return -1;
+    if (L->n_group > 0 && L->topk_group > 64) return -1; /* topk_f32's best[64] */
     return 0;
 }
 

@@ -153,7 +153,7 @@ void hyo_router_logits_blocked(const float* x, const float* wr, uint32_t T, uint
 void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm,
                     float scale, float* w, int32_t* idx);
 /* The same with group-limited greedy (src/hunyuan_moe_full.cpp:135-166) when n_group > 0
- * and topk_group > 0 (both <= 64): on the q probabilities p_e = hyo_expf(l_e - m) / s
+ * and topk_group > 0 (topk_group <= 64; n_group > E puts no expert in a group): on the q probabilities p_e = hyo_expf(l_e - m) / s
  * (s the 64-lane tree sum), group scores max(0, max p over the group's E/n_group
  * experts), the topk_group best groups by hyo_topk_f32, experts of the other groups
  * set to 0, then top-K by hyo_topk_f32 on the probabilities (equal values: lower

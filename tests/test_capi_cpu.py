@@ -77,7 +77,6 @@ def _cfg(hy, **kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(hidden=100), -1), (dict(intermediate=48), -1), (dict(num_experts=65), -1), (dict(topk=17), -1),
     (dict(topk=0), -1), (dict(max_tokens=0), -1), (dict(max_tokens=20000), -1), (dict(wtype=1), -2),
-    (dict(group_limited_greedy=1, n_group=65, topk_group=2), -1),
     (dict(group_limited_greedy=1, n_group=8, topk_group=65), -1),
     (dict(drop_tokens=1, capacity_factor=-1.0), -1), (dict(drop_tokens=1, capacity_factor=float("nan")), -1),
     (dict(drop_tokens=1, capacity_factor=1e30), -1),

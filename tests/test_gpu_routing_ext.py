@@ -177,3 +177,39 @@ def test_options_without_shared_expert_and_single_topk(gpu, wtype):
         if (~keep).any():
             assert np.all(out[~keep[:, 0]] == 0.0)
     m.close()
+
+
+def test_random_configs_layer(gpu):
+    """24 seeded random configurations (E from 1 to 64, K up to E, groups including
+    n_group > E and topk_group >= n_group, dropping with small and large capacity
+    factors, the aux loss, both weight rules, with and without the shared expert, all
+    three weight types) through the layer: bit for bit against the q-semantics oracle,
+    with the gate statistics."""
+    from test_oracle_routing_ext import random_routing_configs
+    H2, I2 = 128, 128
+    for i, (T, E, K, kw) in enumerate(random_routing_configs(24, 21)):
+        wtype = (O.Q8_0, O.Q4_0, O.F32)[i % 3]
+        shared = i % 2 == 0
+        layer = O.synth_layer(H2, I2, E, K, wtype, seed=300 + i, std=0.05, shared=shared)
+        layer.norm_topk_prob = kw["norm_topk_prob"]
+        layer.routed_scaling_factor = kw["routed_scaling_factor"]
+        if kw.get("group_limited_greedy"):
+            layer.n_group, layer.topk_group = kw["n_group"], kw["topk_group"]
+        cap = O.drop_capacity(T, E, K, kw["capacity_factor"], kw["min_capacity"]) if kw.get("drop_tokens") else 0
+        layer.capacity = cap
+        m = gpu.Moe(H2, I2, E, K, wtype, max_tokens=T, has_shared=shared, **kw)
+        m.upload(0, layer)
+        x = O.synth(400 + i, 0, O.T_X, 0, (T, H2), 1.0)
+        what = f"case {i}: T={T} E={E} K={K} wtype={wtype} shared={shared} {kw}"
+        out, lg, w, idx = m.run(0, x, debug=True)
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        np.testing.assert_array_equal(idx, ridx, err_msg=what)
+        np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32), err_msg=what)
+        assert_exact(out, ref, what)
+        aux, gcap, rate = m.last_gate()
+        _, _, ridx2, probs, keep = O.moe_route_q(layer, x)
+        counts = np.bincount(ridx.ravel(), minlength=E)
+        assert gcap == (cap if cap else max(int(counts.max()), kw.get("min_capacity", 0))), what
+        assert rate == np.float32(keep.sum()) / np.float32(T * K), what
+        assert aux == (O.aux_loss_q(probs, ridx) if kw.get("compute_aux_loss") else 0.0), what
+        m.close()

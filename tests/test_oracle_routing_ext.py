@@ -192,3 +192,57 @@ def test_route_q_batch_matches_per_token(oracle):
     _, lg3, w3, i3 = O.moe_forward_q(layer, x, debug=True)
     np.testing.assert_array_equal(i3, idx)
     np.testing.assert_array_equal(lg3.view(np.uint32), lg.view(np.uint32))
+
+
+def random_routing_configs(n, seed):
+    """Seeded random routing configurations: shapes, groups (including E / n_group = 0
+    and topk_group >= n_group), dropping with small and large capacity factors, the aux
+    loss, both weight rules."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(rng.choice([1, 2, 3, 7, 8, 16, 33, 64]))
+        K = int(rng.integers(1, E + 1))
+        T = int(rng.integers(1, 120))
+        kw = dict(norm_topk_prob=int(rng.integers(0, 2)), routed_scaling_factor=float(rng.choice([1.0, 2.5])))
+        if rng.random() < 0.5:
+            kw.update(group_limited_greedy=1, n_group=int(rng.integers(1, 2 * E + 2)),
+                      topk_group=int(rng.integers(1, 9)))
+        if rng.random() < 0.5:
+            kw.update(drop_tokens=1, capacity_factor=float(rng.choice([0.25, 0.5, 1.0, 2.0])),
+                      min_capacity=int(rng.integers(0, 6)))
+        if rng.random() < 0.5:
+            kw.update(compute_aux_loss=1)
+        out.append((T, E, K, kw))
+    return out
+
+
+def test_random_configs_vs_reference_semantics(oracle):
+    """200 random configurations: the q-semantics pieces (selection, weights, kept pairs,
+    capacity, capacity rate, aux loss) against the reference-semantics gating."""
+    rng = np.random.default_rng(12)
+    for T, E, K, kw in random_routing_configs(200, 11):
+        lg = (rng.standard_normal((T, E)) * 1.5).astype(np.float32)
+        g = oracle_gating_full(lg, O.default_cfg(E, K, **kw))
+        groups = kw.get("group_limited_greedy", 0)
+        ng, tg = (kw["n_group"], kw["topk_group"]) if groups else (0, 0)
+        w, idx, probs = O.route_topk_groups(lg, K, norm=kw["norm_topk_prob"], scale=kw["routed_scaling_factor"],
+                                            n_group=ng, topk_group=tg)
+        what = f"T={T} E={E} K={K} {kw}"
+        counts = np.bincount(idx.ravel(), minlength=E)
+        np.testing.assert_array_equal(counts, g["counts"], err_msg=what)
+        if kw.get("drop_tokens"):
+            cap = O.drop_capacity(T, E, K, kw["capacity_factor"], kw["min_capacity"])
+        else:
+            cap = max(int(counts.max()), kw.get("min_capacity", 8))
+        assert cap == int(g["capacity"]), what
+        keep = O.capacity_keep(idx, E, cap)
+        assert np.float32(keep.sum()) / np.float32(T * K) == g["rate"], what
+        kept_ref = g["mask"].any(axis=2)
+        wref = g["cw"].sum(axis=2)
+        for t in range(T):
+            assert set(idx[t][keep[t]].tolist()) == set(np.nonzero(kept_ref[t])[0].tolist()), (what, t)
+            np.testing.assert_allclose(w[t][keep[t]], wref[t, idx[t][keep[t]]], rtol=3e-6, atol=1e-12,
+                                       err_msg=what)
+        if kw.get("compute_aux_loss"):
+            np.testing.assert_allclose(O.aux_loss_q(probs, idx), g["aux"], rtol=2e-5, err_msg=what)
