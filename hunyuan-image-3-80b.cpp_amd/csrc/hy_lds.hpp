@@ -1,5 +1,6 @@
-// hy_lds.hpp -- global->LDS DMA and explicitly waited LDS reads, shared by the kernels
-// that stream operands through LDS rings (grouped MFMA GEMM, decode GEMV).
+// hy_lds.hpp -- global->LDS DMA (flat addresses, or buffer descriptors with scalar
+// offsets) and explicitly waited LDS reads, shared by the kernels that stream operands
+// through LDS rings (grouped MFMA GEMM, decode GEMV).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -13,6 +14,26 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 // lds_wave_base + 16*i.  The wave's loads are tracked by vmcnt, not by barriers.
 __device__ __forceinline__ void g2l16(const void* g, void* lds_wave_base) {
     __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+// Buffer descriptor of a wave-uniform base with no range limit (raw buffer, stride 0,
+// the gfx9 format word 0x00020000).  Copies through it (b2l) take a 32-bit per-lane
+// byte offset in a VGPR and a wave-uniform byte offset in an SGPR, so a loop that
+// advances the uniform part does its address arithmetic in scalar registers.  The two
+// offsets must sum below 2^32.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* uniform_base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_base), (short)0, (int)0xffffffff, 0x00020000);
+}
+// global -> LDS copy of BYTES (4 or 16) per lane: lane l's bytes at base + lane_off +
+// s_off land at lds_wave_base + BYTES * l
+template <int BYTES = 16>
+__device__ __forceinline__ void b2l(__amdgpu_buffer_rsrc_t r, void* lds_wave_base, uint32_t lane_off,
+                                    uint32_t s_off) {
+    static_assert(BYTES == 4 || BYTES == 16, "4- or 16-byte copies");
+    auto* l = (__attribute__((address_space(3))) void*)(lds_wave_base);
+    if constexpr (BYTES == 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 4, lane_off, s_off, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, lane_off, s_off, 0, 0);
 }
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
 #define MM_WAIT_VM_LGKM(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (((N) >> 4) << 14))

@@ -227,33 +227,36 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 
     // issue the asynchronous copies of stage s into ring slot s % MM_RING; lanes
     // outside a copy's range are masked (the wave still issues it once)
+    // the copy sources as buffer descriptors: per copy a 32-bit lane offset (VGPR) and
+    // the stage's offset (SGPR).  Offsets stay below 2^32: A and its scales within one
+    // expert's chunk column, B rows x Kd (the host keeps that below 2^32), B scales
+    // rows x nb x 4.
+    const __amdgpu_buffer_rsrc_t r_a = buf_rsrc(a_src), r_as = buf_rsrc(as_src), r_b = buf_rsrc(a.aq),
+                                 r_bs = buf_rsrc(a.ad);
     auto issue = [&](int s) {
         uint8_t* st = ring[s % MM_RING];
-        const int kb0 = s * MM_KB;
-        const uint8_t* ab = a_src + (size_t)kb0 * CHB;
+        const uint32_t kb0 = (uint32_t)(s * MM_KB);
         uint8_t* ad = st + OFF_A + ch * CHB + half * (CHB / WPC);
         if (Q4 && WPC == 2) {
-            if (lane < 32) g2l16(ab + lane * 16, ad);  // 512 B
+            if (lane < 32) b2l(r_a, ad, 16u * lane, kb0 * CHB);  // 512 B
         } else {
 #pragma unroll
-            for (int c = 0; c < A_LOADS; c++) g2l16(ab + c * 1024 + (Q4 ? 16u * lane : a_sw), ad + c * 1024);
+            for (int c = 0; c < A_LOADS; c++) b2l(r_a, ad + c * 1024, (Q4 ? 16u * lane : a_sw) + c * 1024u, kb0 * CHB);
         }
         // B rows of this wave's tokens
-        const int8_t* bb = a.aq + (size_t)kb0 * QK;
         uint8_t* bdst = st + OFF_B + (wv % MM_KB) * (MM_TOK * 32) + (wv / MM_KB) * (TPW * 32);
 #pragma unroll
         for (int v = 0; v < SH::B_LOADS; v++)
-            if (v * WAVE + lane < SH::B_LANES) g2l16(bb + b_off[v], bdst + v * 1024);
+            if (v * WAVE + lane < SH::B_LANES) b2l(r_b, bdst + v * 1024, b_off[v], kb0 * QK);
         // A scales of the chunk: 64 fp16 = 128 B (lanes 0..7), or its half (lanes 0..3)
-        if (lane < 8 / WPC) g2l16(as_src + (size_t)kb0 * 64 + lane * 8, st + OFF_AS + ch * 128 + half * (128 / WPC));
+        if (lane < 8 / WPC) b2l(r_as, st + OFF_AS + ch * 128 + half * (128 / WPC), 16u * lane, kb0 * 128u);
         // B scales of this wave's tokens
-        const uint8_t* sb = reinterpret_cast<const uint8_t*>(a.ad + kb0);
         uint8_t* sdst = st + OFF_BS + wv * (MM_TOK / MM_WAVES) * MM_KB * 4;
         if (lane < BS_LANES) {
             if (MM_KB == 4)
-                g2l16(sb + bs_off, sdst);
+                b2l(r_bs, sdst, bs_off, kb0 * 4u);
             else
-                __builtin_amdgcn_global_load_lds(sb + bs_off, sdst, 4, 0, 0);
+                b2l<4>(r_bs, sdst, bs_off, kb0 * 4u);
         }
     };
 
@@ -282,14 +285,15 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     // rank-1 operands {d, 0, 0, ...}: only element 0 changes, the zeros stay in place
     v4i_t xa0 = {0, 0, 0, 0}, xa1 = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
 
-    // one 32-wide block kb of the stage whose slot starts at st
-    auto block = [&]<int KBI>(uint32_t st, uint32_t abase) {
+    // one 32-wide block kb of a stage: this lane's B row, scale and A row addresses in
+    // the stage's slot
+    auto block = [&]<int KBI>(uint32_t bq, uint32_t swq, uint32_t sxq, uint32_t abase) {
         v4i_t A0 = lds_b128_at<KBI * 2048>(abase);
         v4i_t A1 = lds_b128_at<KBI * 2048 + 1024>(abase);
-        v4i_t B = lds_b128_at<KBI * MM_TOK * 32>(st + b_lane);
-        uint32_t dw0 = lds_u16_at<KBI * 128>(st + sw_lane);
-        uint32_t dw1 = lds_u16_at<KBI * 128 + 64>(st + sw_lane);
-        uint32_t dxb = lds_b32_at<KBI * 4>(st + sx_lane);
+        v4i_t B = lds_b128_at<KBI * MM_TOK * 32>(bq);
+        uint32_t dw0 = lds_u16_at<KBI * 128>(swq);
+        uint32_t dw1 = lds_u16_at<KBI * 128 + 64>(swq);
+        uint32_t dxb = lds_b32_at<KBI * 4>(sxq);
         lds_wait(A0, A1, B, dw0, dw1, dxb);
         const v16i_t zero = {};
         const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
@@ -315,6 +319,10 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 #pragma unroll
     for (int i = 0; i < MM_RING - 1; i++)
         if (i < nstage) issue(i);
+    // per-lane LDS read bases at ring slot 0, plus the slot's offset (s % RING) * STAGE
+    // kept in a scalar that wraps at the ring's end: one vector add per address and stage
+    const uint32_t a_q0 = ring0 + a_lane, b_q0 = ring0 + b_lane, sw_q0 = ring0 + sw_lane, sx_q0 = ring0 + sx_lane;
+    uint32_t soff = 0;
     for (int s = 0; s < nstage; s++) {
         // stage s landed (this wave's loads), and every wave's (barrier)
         wait_copies<LOADS, MM_RING - 2>(nstage - 1 - s);
@@ -323,14 +331,14 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         // by every wave before this barrier -- issue it now so that RING - 1 stages are
         // in flight during this stage's math
         if (s + MM_RING - 1 < nstage) issue(s + MM_RING - 1);
-        const uint32_t st = ring0 + (uint32_t)((s % MM_RING) * STAGE);
+        soff = __builtin_amdgcn_readfirstlane(soff);
         uint32_t abase;
         if (Q4) {
             // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of
             // chunk t/64 (CHUNKS x 64 rows <= MM_THREADS)
             if (tid < SH::CHUNKS * 64) {
                 const int c = tid >> 6, r = tid & 63;
-                v4i_t wv4 = lds_b128(ring[s % MM_RING] + OFF_A + c * 1024 + r * 16);
+                v4i_t wv4 = lds_b128(ring[0] + soff + OFF_A + c * 1024 + r * 16);
                 lds_wait(wv4);
                 int4 lo, hi;
                 unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
@@ -342,13 +350,15 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
             __builtin_amdgcn_s_barrier();
             abase = aun0 + a_lane;
         } else {
-            abase = st + a_lane;
+            abase = a_q0 + soff;
         }
         if (active) {
+            const uint32_t bq = b_q0 + soff, swq = sw_q0 + soff, sxq = sx_q0 + soff;
             [&]<int... KBI>(std::integer_sequence<int, KBI...>) {
-                (block.template operator()<KBI>(st, abase), ...);
+                (block.template operator()<KBI>(bq, swq, sxq, abase), ...);
             }(std::make_integer_sequence<int, MM_KB>{});
         }
+        soff = soff + STAGE == (uint32_t)(MM_RING * STAGE) ? 0u : soff + STAGE;
     }
 
     // ---- epilogues
