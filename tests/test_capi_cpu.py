@@ -110,3 +110,25 @@ def test_config_struct_layouts_match_header(hy, tmp_path):
         py = structs[cname]
         want = C.sizeof(py) if f == "size" else getattr(py, f).offset
         assert int(v) == want, (cname, f, int(v), want)
+
+
+def test_integration_ctypes_stub_matches_headers(hy):
+    """The ctypes stub INTEGRATION.md gives callers: its structs have the package's
+    layouts (pinned to the C headers above) and every argtypes list has the header's
+    parameter count."""
+    import re
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    code = text.split("## 3. FFI stubs", 1)[1].split("```python", 1)[1].split("```", 1)[0]
+    code = code.replace("/path/to/repo/hunyuan-image-3-80b.cpp_amd/libhy_moe.so", hy.LIB_PATH)
+    ns = {}
+    exec(code, ns)
+    for stub, ours in ((ns["HyMoeConfig"], hy.Config), (ns["HyAttnConfig"], hy.AttnConfig)):
+        assert C.sizeof(stub) == C.sizeof(ours)
+        assert [f for f, _ in stub._fields_] == [f for f, _ in ours._fields_]
+    headers = "".join(open(os.path.join(ROOT, "include", h)).read() for h in ("hy_moe.h", "hy_attn.h"))
+    lib = ns["lib"]
+    for name in re.findall(r"lib\.(hy_\w+)\.argtypes", code):
+        decl = re.search(r"\bint\s+" + name + r"\s*\(([^)]*)\)", headers)
+        assert decl, name
+        n_params = len([p for p in decl.group(1).split(",") if p.strip() and p.strip() != "void"])
+        assert len(getattr(lib, name).argtypes) == n_params, name
