@@ -137,7 +137,9 @@ def measured_traffic(workload, kname, path=TRAFFIC_TABLE):
 def probe_block_mix(hy, variant=0, reps=3):
     """Rate (block-dot int8 ops/s) of the grouped GEMM's per-block instruction mix with
     no memory traffic: the best of `reps` launches of hy_probe_block_mix (variant 0: the
-    whole mix; 1: its four MFMAs only; 2: its 64 vector ops only)."""
+    whole mix; 1: its four MFMAs only; 2: its 64 vector ops only; 3: the f16 block-dot
+    alternative, without the operand unpack it would also need; 4: the same with the
+    int8 A operand unpacked to f16)."""
     out = hy.Buf.empty((PROBE_WGS * 512,))
     st = hy.Stream()
     ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
@@ -775,7 +777,9 @@ def main():
         stream_probe(hy, waves=a.stream_probe)
         return
     if a.mfma_probe:
-        rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"))}
+        rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"),
+                                                           (3, "f16_block_dots"),
+                                                           (4, "f16_block_dots_a_unpacked"))}
         print(json.dumps({"probe": "block_mix", "work_groups": PROBE_WGS, "iters_per_wave": PROBE_ITERS,
                           "block_dot_ops_per_s": rates, "frac_of_dense_int8": rates["mix"] / PEAK_INT8}),
               flush=True)

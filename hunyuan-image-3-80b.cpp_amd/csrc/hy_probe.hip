@@ -9,7 +9,9 @@
 // No memory traffic, no LDS, no barriers; launched at the GEMM's occupancy (8-wave
 // work groups, two per CU, at most 128 VGPRs: four waves per SIMD).  Its rate is the
 // ceiling the GEMM's instruction mix allows on this part; variants time the matrix
-// and vector halves alone.
+// and vector halves alone, and the alternative that takes the block dots from f16
+// MFMAs (int8 values are exact in f16 and a 32-term dot of them stays below 2^24, so
+// the fp32 result is the exact dot and needs no conversion).
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_lds.hpp"
@@ -22,11 +24,18 @@ typedef int v16i_p __attribute__((ext_vector_type(16)));
 typedef float v16f_p __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h_p __attribute__((ext_vector_type(8)));
 typedef int v4i_p __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h_p __attribute__((ext_vector_type(2)));
 
 constexpr int PROBE_THREADS = 512;
 
 // VARIANT 0: the full per-block mix; 1: the four MFMAs only; 2: the 64 vector ops only, plus
-// 32 integer adds that vary their operands
+// 32 integer adds that vary their operands; 3: the block dots as two chained
+// v_mfma_f32_32x32x16_f16 per tile (K = 32), the same two rank-1 scale MFMAs and 32 fmas,
+// no conversions (operands already f16: the int8 -> f16 unpack it would also need is
+// not counted); 4: variant 3 with the shared A operand unpacked from the 16 int8 a lane
+// holds (byte ^ 0x80 placed under an 0x64 high byte is the f16 1152 + q, so a v_perm_b32
+// and a packed f16 add of -1152 give two exact values), as a kernel reading int8
+// weights from LDS would need; the B operand is taken as already f16
 template <int VARIANT>
 __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, int seed, float* __restrict__ out) {
     const int lane = threadIdx.x % WAVE;
@@ -42,6 +51,7 @@ __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, 
     const v16f_p zf = {};
     v16i_p S0 = zi, S1 = zi;
     v16f_p C0 = zf, C1 = zf;
+    const v2h_p f16_bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     if (VARIANT == 2)
         for (int v = 0; v < 16; v++) {
             S0[v] = v * seed + lane;
@@ -61,6 +71,38 @@ __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, 
             for (int v = 0; v < 16; v++) {
                 acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
                 acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
+            }
+        } else if (VARIANT == 3 || VARIANT == 4) {
+            // four distinct products, each varying per iteration, so none is hoisted or merged
+            v8h_p xc = xb;
+            xc[1] = (_Float16)(float)(it & 3);
+            v8h_p a_lo = xa, a_hi = xc;
+            if (VARIANT == 4) {
+                A0.y += 5;
+                A0.z ^= it;
+                A0.w += 3;
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint32_t x = (uint32_t)A0[d] ^ 0x80808080u;
+                    const v2h_p lo = __builtin_bit_cast(v2h_p, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) + f16_bias;
+                    const v2h_p hi = __builtin_bit_cast(v2h_p, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) + f16_bias;
+                    v8h_p& a = d < 2 ? a_lo : a_hi;
+                    a[4 * (d & 1)] = lo[0];
+                    a[4 * (d & 1) + 1] = lo[1];
+                    a[4 * (d & 1) + 2] = hi[0];
+                    a[4 * (d & 1) + 3] = hi[1];
+                }
+            }
+            const v16f_p D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                a_hi, xa, __builtin_amdgcn_mfma_f32_32x32x16_f16(a_lo, xc, zf, 0, 0, 0), 0, 0, 0);
+            const v16f_p D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                a_hi, xc, __builtin_amdgcn_mfma_f32_32x32x16_f16(a_lo, xa, zf, 0, 0, 0), 0, 0, 0);
+            C0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa, xb, zf, 0, 0, 0);
+            C1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xb, xa, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                acc0[v] = fmaf(D0[v], C0[v], acc0[v]);
+                acc1[v] = fmaf(D1[v], C1[v], acc1[v]);
             }
         } else if (VARIANT == 1) {
             // chained through the accumulators so that nothing is hoisted
@@ -151,6 +193,10 @@ hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int s
         hipLaunchKernelGGL(block_mix_kernel<1>, grid, blk, 0, s, iters, seed, out);
     else if (variant == 2)
         hipLaunchKernelGGL(block_mix_kernel<2>, grid, blk, 0, s, iters, seed, out);
+    else if (variant == 3)
+        hipLaunchKernelGGL(block_mix_kernel<3>, grid, blk, 0, s, iters, seed, out);
+    else if (variant == 4)
+        hipLaunchKernelGGL(block_mix_kernel<4>, grid, blk, 0, s, iters, seed, out);
     else
         hipLaunchKernelGGL(block_mix_kernel<0>, grid, blk, 0, s, iters, seed, out);
     return hipGetLastError();

@@ -317,7 +317,10 @@ int hy_copy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
  * dots of two 32x32 tiles, two rank-1 f16 MFMAs for the scale products, 32 int->float
  * conversions and 32 fmas per lane) `iters` times per wave, at the GEMM's occupancy;
  * variant 1 runs only the four MFMAs, variant 2 only the 64 vector ops (plus 32 integer
- * adds that vary their operands).  Each wave does
+ * adds that vary their operands), variant 3 the f16 alternative (each block dot from two
+ * f16 32x32x16 MFMAs, exact in fp32, then the scale MFMAs and 32 fmas, no conversions;
+ * the operand unpack to f16 is not counted), variant 4 variant 3 plus the unpack of the
+ * shared int8 A operand to f16 (16 values per lane).  Each wave does
  * iters * 2 * 32*32*32 block-dot MACs; out_dev holds work_groups * 512 floats. */
 int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream);
 /* Measurement only, no counterpart in the reference: reads `bytes` of buf_dev as the
