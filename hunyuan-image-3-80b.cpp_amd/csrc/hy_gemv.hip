@@ -145,7 +145,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
         auto load = [&](int set, int b) {
             const float* p = wbase + (size_t)min(b, nb - 1) * 64 * QK;  // in bounds
 #pragma unroll
-            for (int c = 0; c < 8; c++) w[set][c] = *reinterpret_cast<const v4f_t*>(p + c * 256);
+            for (int c = 0; c < 8; c++) w[set][c] = __builtin_nontemporal_load(reinterpret_cast<const v4f_t*>(p + c * 256));
         };
         auto consume = [&](int set, int b) {
 #pragma unroll
@@ -335,10 +335,10 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
         const uint8_t* src = wq + (size_t)st_i * GQ_U * WBYTES;
 #pragma unroll
         for (int u = 0; u < GQ_U; u++) {
-            g2l16(src + u * WBYTES, st + SL::W + u * WBYTES);
-            if (!Q4) g2l16(src + u * WBYTES + 1024, st + SL::W + u * WBYTES + 1024);
+            g2l16_nt(src + u * WBYTES, st + SL::W + u * WBYTES);
+            if (!Q4) g2l16_nt(src + u * WBYTES + 1024, st + SL::W + u * WBYTES + 1024);
         }
-        g2l16(wsc + (size_t)st_i * GQ_U * 64, st + SL::S);
+        g2l16_nt(wsc + (size_t)st_i * GQ_U * 64, st + SL::S);
     };
 #pragma unroll
     for (int s = 0; s < NSTEP; s++) issue_w(s);
