@@ -510,19 +510,19 @@ __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __
             pos[k] = R.comb_pos[t * K + kk];
             w[k] = R.comb_w[t * K + kk];
         }
-        float4 v[KMAX];
+        v4f_t v[KMAX];
 #pragma unroll
-        for (int k = 0; k < KMAX; k++) v[k] = reinterpret_cast<const float4*>(y + (size_t)pos[k] * H)[r4];
+        for (int k = 0; k < KMAX; k++) v[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f_t*>(y + (size_t)pos[k] * H) + r4);
 #pragma unroll
         for (int k = 0; k < KMAX; k++)
             if (k0 + k < K && w[k] != 0.0f)
-                c = make_float4(fmaf(w[k], v[k].x, c.x), fmaf(w[k], v[k].y, c.y), fmaf(w[k], v[k].z, c.z),
-                                fmaf(w[k], v[k].w, c.w));
+                c = make_float4(fmaf(w[k], v[k][0], c.x), fmaf(w[k], v[k][1], c.y), fmaf(w[k], v[k][2], c.z),
+                                fmaf(w[k], v[k][3], c.w));
     }
     float4 o = c;
     if (has_shared) {
-        const float4 u = reinterpret_cast<const float4*>(y + ((size_t)T * K + t) * H)[r4];
-        o = make_float4(u.x + c.x, u.y + c.y, u.z + c.z, u.w + c.w);
+        const v4f_t u = __builtin_nontemporal_load(reinterpret_cast<const v4f_t*>(y + ((size_t)T * K + t) * H) + r4);
+        o = make_float4(u[0] + c.x, u[1] + c.y, u[2] + c.z, u[3] + c.w);
     }
     if (resid) {
         const float4 q = reinterpret_cast<const float4*>(resid + (size_t)t * H)[r4];
