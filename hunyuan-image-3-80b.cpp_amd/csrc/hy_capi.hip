@@ -288,7 +288,15 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int NT = mfma ? hy::mfma_shape_tokens(shape) : hy::gemv_tile_tokens();
     // group-limited greedy, dropping and the aux loss take the general routing path
     const bool ext = c->n_group > 0 || c->cfg.drop_tokens || c->cfg.compute_aux_loss;
-    if (!ext && !mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
+    // one token: the router logits and the Q8_0 of x in one launch; the gate/up GEMV's
+    // own waves then select the top-k and write the dispatch lists (the selection pass
+    // and its kernel boundary go away)
+    const bool route1 = !ext && !mfma && iT == 1 && hy::gemv_route1_ok(wt, H);
+    if (route1) {
+        HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
+            return hy::launch_decode_logits(x, L.router, H, E, c->logits, prequant ? nullptr : c->xq, c->xd, c->xs, s);
+        }));
+    } else if (!ext && !mfma && wt != HY_TYPE_F32 && T <= kGemvMaxTokens && iT * K <= hy::MAX_DECODE_PAIRS) {
         // decode: router logits, then top-k, dispatch lists and Q8_0 of x in one launch
         HY_TRY(timed(c, hy::KID_ROUTER, s, [&] {
             return hy::launch_route_decode(x, L.router, iT, H, E, K, renorm,
@@ -343,10 +351,19 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
         }));
         return HY_OK;
     }
-    HY_TRY(timed(c, hy::KID_UP, s, [&] {
-        return hy::launch_gemv_up(wt, routed_bound + shared_tiles, gu_view(c, L), R, X, x, iT, H, I, E, K, c->hq,
-                                  c->hd, c->hs, c->hf, s);
-    }));
+    if (route1) {
+        const hy::Route1Out r1{c->logits, renorm, c->cfg.routed_scaling_factor, has_shared, c->topw, c->topi, c->cnt,
+                               c->off, c->srt_tok, c->pair_pos, c->comb_pos, c->comb_w, c->tile_e, c->tile_start,
+                               c->tile_n, c->meta};
+        HY_TRY(timed(c, hy::KID_UP, s, [&] {
+            return hy::launch_gemv_up_route1(wt, gu_view(c, L), r1, X, H, I, E, K, c->hq, c->hd, c->hs, s);
+        }));
+    } else {
+        HY_TRY(timed(c, hy::KID_UP, s, [&] {
+            return hy::launch_gemv_up(wt, routed_bound + shared_tiles, gu_view(c, L), R, X, x, iT, H, I, E, K, c->hq,
+                                      c->hd, c->hs, c->hf, s);
+        }));
+    }
     // decode: routed and shared down products in one launch (the shared expert's rows
     // no longer wait behind the routed ones), then the combine.  (Folding the combine
     // into the down launch through per-row-group completion counters made it slower:

@@ -136,4 +136,40 @@ __device__ __forceinline__ float swiglu(float g, float u) {
     return g * (1.0f / (1.0f + hy_expf(-g))) * u;
 }
 
+// Top-k of one token's logits, one expert per lane (lanes >= E hold none): K rounds
+// of a wave max, the lowest lane among equal maxima (lower expert index wins ties,
+// src/hunyuan_moe_full.cpp:67), then p_k = exp(l_k - m) / sum_e exp(l_e - m) with the
+// denominator summed in the 64-lane tree, renormalised by max(sum_k p_k, 1e-8) or
+// scaled (src/hunyuan_moe_full.cpp:230-243; norm = 0 when K = 1).  Lanes k < K write
+// w_out[k], i_out[k]; p_out (optional) gets every expert's probability.
+__device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, float scale, int lane,
+                                          float* w_out, int* i_out, float* p_out = nullptr) {
+    float v = lane < E ? v_in : -INFINITY;
+    const float orig = v;
+    float m0 = 0.0f;
+    float selv = 0.0f;
+    int seli = 0;
+    for (int k = 0; k < K; k++) {
+        const float m = wave_max(v);
+        const unsigned long long bal = __ballot(v == m);
+        const int sel = (int)__builtin_ctzll(bal);
+        if (k == 0) m0 = m;
+        if (lane == k) { selv = m; seli = sel; }
+        if (lane == sel) v = -INFINITY;
+    }
+    // denominator: 64-lane tree of exp(l_e - m) (lanes >= E add 0)
+    const float s = wave_sum(lane < E ? hy_expf(orig - m0) : 0.0f);
+    // p_k for the lane's own rank k = lane (lanes >= K carry 0)
+    const float p = lane < K ? hy_expf(selv - m0) / s : 0.0f;
+    // sum_k p_k in rank order (every lane computes the same value)
+    float ps = 0.0f;
+    for (int k = 0; k < K; k++) ps += __shfl(p, k, WAVE);
+    if (ps < 1e-8f) ps = 1e-8f;
+    if (lane < K) {
+        w_out[lane] = norm ? p / ps : p * scale;
+        i_out[lane] = seli;
+    }
+    if (p_out && lane < E) p_out[lane] = hy_expf(orig - m0) / s;  // the gates the aux loss averages
+}
+
 }  // namespace hy

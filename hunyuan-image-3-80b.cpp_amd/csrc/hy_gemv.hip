@@ -77,6 +77,7 @@ struct GvArgs {
     int* hs;
     float* hf;
     float* y;           // mode 1 output
+    Route1Out r1;       // one-token batches routed inside the gate/up GEMV (launch_gemv_up_route1)
 };
 
 template <int WT, int NT, int MODE>
@@ -298,6 +299,66 @@ struct GqSlot {
     static_assert(2 * NT * GQ_U == WAVE, "one 4-byte copy per lane moves the step's scales and sums");
 };
 
+// One-token routing inside the gate/up GEMV (launch_gemv_up_route1): the wave selects
+// the top-k of logits[E] exactly as the decode routing pass does (topk_wave), and its
+// tile is the tile-th selected expert in ascending order (each selected expert has
+// the token's one pair: one tile, slot = rank); tile K is the shared expert's, which
+// needs no routing.  The writer wave (tile 0, row group 0) also stores every routing
+// product that pass stores for T = 1, for the down GEMV, the combine and the caller:
+// top-k weights and ids, per-expert counts and offsets, the sorted token list, pair
+// positions, the combine list in ascending expert order, the tiles and meta.
+__device__ __forceinline__ int route1_tile(const GvArgs& a, int tile, int lane, bool writer) {
+    const Route1Out& r = a.r1;
+    const int E = a.E, K = a.K;
+    if (tile >= K && !writer) return E;
+    __shared__ float selw_s[MAX_K];
+    __shared__ int seli_s[MAX_K];
+    const float lv = lane < E ? r.logits[lane] : 0.0f;
+    topk_wave(lv, E, K, r.norm, r.scale, lane, selw_s, seli_s);
+    __syncthreads();
+    int kq = -1;  // this lane's expert's rank in the top-k, -1 if not selected
+    for (int k = 0; k < K; k++) kq = seli_s[k] == lane ? k : kq;
+    const bool sel = kq >= 0;
+    const int rank = __popcll(__ballot(sel) & ((1ull << lane) - 1ull));  // selected experts below this one
+    if (writer) {
+        if (lane < K) {
+            r.topw[lane] = selw_s[lane];
+            r.topi[lane] = seli_s[lane];
+            r.srt_tok[lane] = 0;
+        }
+        if (lane < E) {
+            r.cnt[lane] = sel ? 1 : 0;
+            r.off[lane] = rank;
+            r.meta[META_TILE_OFF + lane] = rank;
+        }
+        if (sel) {
+            r.pair_pos[kq] = rank;
+            r.comb_pos[rank] = rank;
+            r.comb_w[rank] = selw_s[kq];
+            r.tile_e[rank] = lane;
+            r.tile_start[rank] = 0;
+            r.tile_n[rank] = 1;
+        }
+        if (lane == 0) {
+            const int all = K + r.has_shared;
+            r.off[E] = K;
+            r.meta[0] = K;
+            r.meta[1] = all;
+            r.meta[2] = K;
+            r.meta[3] = 1;
+            r.meta[META_TILE_OFF + E] = K;
+            r.meta[META_TILE_OFF + E + 1] = all;
+            if (r.has_shared) {
+                r.tile_e[K] = E;
+                r.tile_start[K] = 0;
+                r.tile_n[K] = 1;
+            }
+        }
+    }
+    if (tile >= K) return E;
+    return (int)__builtin_ctzll(__ballot(sel && rank == tile));
+}
+
 // consume the last NSTEP steps: before step base + J, wait until at most the
 // NSTEP - 1 - J younger steps' copies are outstanding
 template <int J, int NSTEP, int LOADS, class F>
@@ -309,8 +370,9 @@ __device__ __forceinline__ void gemv_tail(F& step, int base) {
     }
 }
 
-template <int WT, int NT, int MODE, int NSTEP>
+template <int WT, int NT, int MODE, int NSTEP, bool R1 = false>
 __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
+    static_assert(!R1 || MODE == 0, "routing inside the launch: gate/up only");
     static_assert(MODE == 0 || MODE == 1, "routed/shared products only (the combine runs separately)");
     using SL = GqSlot<WT, NT>;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
@@ -325,9 +387,16 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 
     // start the weight stream first: tile_e[tile] is in the arena for every launched
     // tile; a stale entry (tile past this call's count) is clamped into the table and
-    // its copies are drained before the work group exits
-    int e = a.R.tile_e[tile];
-    e = e < 0 ? 0 : (e >= a.W.n_mats ? a.W.n_mats - 1 : e);
+    // its copies are drained before the work group exits.  R1: the wave routes the
+    // token itself (the shared tile starts at once).
+    int e;
+    if constexpr (R1) {
+        e = route1_tile(a, tile, lane, tile == 0 && G == 0);
+        e = e < 0 ? 0 : (e >= a.W.n_mats ? a.W.n_mats - 1 : e);  // in the table whatever the logits hold
+    } else {
+        e = a.R.tile_e[tile];
+        e = e < 0 ? 0 : (e >= a.W.n_mats ? a.W.n_mats - 1 : e);
+    }
     const uint8_t* wq = a.W.qs + (size_t)e * a.W.qs_stride + (size_t)G * nb * WBYTES + lane * 16;
     const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64 + lane * 8;
     auto issue_w = [&](int st_i) {
@@ -343,11 +412,13 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 #pragma unroll
     for (int s = 0; s < NSTEP; s++) issue_w(s);
 
-    if (tile >= a.R.meta[1]) {
+    if (!R1 && tile >= a.R.meta[1]) {
         MM_WAIT_VM_LGKM(0);
         return;
     }
-    const int start = a.R.tile_start[tile], n = a.R.tile_n[tile];
+    // R1: one pair per tile (the routed tile's slot is its rank, tile; the shared
+    // tile's is T * K)
+    const int start = R1 ? 0 : a.R.tile_start[tile], n = R1 ? 1 : a.R.tile_n[tile];
     const bool shared = e == a.E;
     if (lane < NT) {
         int tok = 0, slot = 0;
@@ -355,6 +426,8 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
             if (shared) {
                 tok = start + lane;
                 slot = a.T * a.K + tok;
+            } else if (R1) {
+                slot = tile;
             } else {
                 slot = a.R.off[e] + start + lane;
                 tok = a.R.srt_tok[slot];
@@ -596,6 +669,29 @@ hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Rout
                           hipStream_t s) {
     GvArgs a{W, R, X.q, X.d, X.s, xf, T, H, I, E, K, H, 2 * I / 64, 0, hq, hd, hs, hf, nullptr};
     return gemv_launch<0>(wtype, max_tiles, s, a);
+}
+
+bool gemv_route1_ok(int wtype, int H) {
+    return (wtype == HY_TYPE_Q8_0 && gemv_q_fits<HY_TYPE_Q8_0>(H)) || (wtype == HY_TYPE_Q4_0 && gemv_q_fits<HY_TYPE_Q4_0>(H));
+}
+
+hipError_t launch_gemv_up_route1(int wtype, const MatView& W, const Route1Out& r, const ActQ& X, int H, int I, int E,
+                                 int K, int8_t* hq, float* hd, int* hs, hipStream_t s) {
+    if (!gemv_route1_ok(wtype, H) || K < 1 || K > E || E > MAX_E) return hipErrorInvalidValue;
+    GvArgs a{W, Routing{}, X.q, X.d, X.s, nullptr, 1, H, I, E, K, H, 2 * I / 64, 1, hq, hd, hs, nullptr, nullptr, r};
+    const dim3 grid((unsigned)(K + r.has_shared), (unsigned)a.n_groups);
+    // one token: K + 1 tiles x row groups; the deeper ring when every wave is resident
+    const bool deep = (long)grid.x * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3));
+    if (wtype == HY_TYPE_Q8_0)
+        hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, 0, 2, true>), grid, dim3(GQ_THREADS),
+                           gemv_q_smem<HY_TYPE_Q8_0>(2), s, a);
+    else if (deep)
+        hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, 0, 3, true>), grid, dim3(GQ_THREADS),
+                           gemv_q_smem<HY_TYPE_Q4_0>(3), s, a);
+    else
+        hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, 0, 2, true>), grid, dim3(GQ_THREADS),
+                           gemv_q_smem<HY_TYPE_Q4_0>(2), s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_down(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const int8_t* hq,

@@ -34,6 +34,10 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
                                float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, int NT,
                                int has_shared, int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos,
                                float* comb_w, int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s);
+// one-token batches whose routing runs inside the gate/up GEMV: the router logits
+// [E] and, when xq is not null, the Q8_0 form of x, in one launch
+hipError_t launch_decode_logits(const float* x, const float* wr, int H, int E, float* logits, int8_t* xq, float* xd,
+                                int* xs, hipStream_t s);
 // scratch: dispatch_scratch_bytes(T, K, E) of device memory (per-block counts)
 size_t dispatch_scratch_bytes(int T, int K, int E);
 hipError_t launch_dispatch(const int* topi, const float* topw, int T, int K, int E, int NT, int has_shared, int* cnt,
@@ -51,6 +55,32 @@ int gemv_tile_tokens();
 hipError_t launch_gemv_up(int wtype, int max_tiles, const MatView& W, const Routing& R, const ActQ& X, const float* xf,
                           int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs, float* hf,
                           hipStream_t s);
+// Routing products a one-token gate/up GEMV writes (launch_gemv_up_route1): the
+// top-k of logits[E] and every dispatch list launch_route_decode writes for T = 1.
+struct Route1Out {
+    const float* logits;
+    int norm;
+    float scale;
+    int has_shared;
+    float* topw;
+    int* topi;
+    int* cnt;
+    int* off;
+    int* srt_tok;
+    int* pair_pos;
+    int* comb_pos;
+    float* comb_w;
+    int* tile_e;
+    int* tile_start;
+    int* tile_n;
+    int* meta;
+};
+// the gate/up GEMV of a one-token batch (T = 1, Q8_0 / Q4_0 ring kernel) with the
+// routing done by its own waves from r.logits: K routed tiles (ascending expert) and
+// the shared tile; false from gemv_route1_ok when the ring kernel does not take H
+bool gemv_route1_ok(int wtype, int H);
+hipError_t launch_gemv_up_route1(int wtype, const MatView& W, const Route1Out& r, const ActQ& X, int H, int I, int E,
+                                 int K, int8_t* hq, float* hd, int* hs, hipStream_t s);
 hipError_t launch_gemv_down(int wtype, int n_tiles_bound, const MatView& W, const Routing& R, const int8_t* hq,
                             const float* hd, const int* hs, const float* hf, int T, int H, int I, int E, int K,
                             float* y, hipStream_t s);

@@ -19,36 +19,6 @@ namespace hy {
 // ----------------------------------------------------------------------------
 constexpr int ROUTER_WAVES = 4;
 
-__device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, float scale, int lane,
-                                          float* w_out, int* i_out, float* p_out = nullptr) {
-    float v = lane < E ? v_in : -INFINITY;
-    const float orig = v;
-    float m0 = 0.0f;
-    float selv = 0.0f;
-    int seli = 0;
-    for (int k = 0; k < K; k++) {
-        const float m = wave_max(v);
-        const unsigned long long bal = __ballot(v == m);
-        const int sel = (int)__builtin_ctzll(bal);
-        if (k == 0) m0 = m;
-        if (lane == k) { selv = m; seli = sel; }
-        if (lane == sel) v = -INFINITY;
-    }
-    // denominator: 64-lane tree of exp(l_e - m) (lanes >= E add 0)
-    const float s = wave_sum(lane < E ? hy_expf(orig - m0) : 0.0f);
-    // p_k for the lane's own rank k = lane (lanes >= K carry 0)
-    const float p = lane < K ? hy_expf(selv - m0) / s : 0.0f;
-    // sum_k p_k in rank order (every lane computes the same value)
-    float ps = 0.0f;
-    for (int k = 0; k < K; k++) ps += __shfl(p, k, WAVE);
-    if (ps < 1e-8f) ps = 1e-8f;
-    if (lane < K) {
-        w_out[lane] = norm ? p / ps : p * scale;
-        i_out[lane] = seli;
-    }
-    if (p_out && lane < E) p_out[lane] = hy_expf(orig - m0) / s;  // the gates the aux loss averages
-}
-
 // Group-limited greedy (src/hunyuan_moe_full.cpp:135-178) for one token, one expert
 // per lane, step by step on the probabilities p_e = exp(l_e - m) / s (the exp and the
 // 64-lane tree sum of topk_wave): group g of the E / n_group experts from g * (E /
@@ -119,11 +89,11 @@ __device__ __forceinline__ void topk_groups_wave(float v_in, int E, int K, int n
 // SIMD, so the wave itself must cover the memory latency).  The per-lane
 // accumulation order is unchanged.
 template <int TPW, int EPW>
-__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
-    const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, float* __restrict__ logits) {
+__device__ __forceinline__ void router_logits_block(const float* __restrict__ x, const float* __restrict__ wr, int T,
+                                                    int H, int E, float* __restrict__ logits, int block) {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int n_eg = (E + EPW - 1) / EPW;
-    const int item = blockIdx.x * ROUTER_WAVES + wave;
+    const int item = block * ROUTER_WAVES + wave;
     const int t0 = (item / n_eg) * TPW, e0 = (item % n_eg) * EPW;
     if (t0 >= T) return;
     float acc[TPW][EPW];
@@ -196,6 +166,12 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
             for (int e = 0; e < EPW; e++)
                 if (t0 + t < T && e0 + e < E) logits[(size_t)(t0 + t) * E + e0 + e] = acc[t][e];
     }
+}
+
+template <int TPW, int EPW>
+__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
+    const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, float* __restrict__ logits) {
+    router_logits_block<TPW, EPW>(x, wr, T, H, E, logits, (int)blockIdx.x);
 }
 
 // Top-k + weights per token (one wave each), optionally quantizing the token's
@@ -748,6 +724,32 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
     // no quantization work groups when the caller quantized x already (xq == null)
     const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + 255) / 256) : 0u;
     hipLaunchKernelGGL(route_decode_kernel, dim3(1 + quant_groups), dim3(ROUTER_WAVES * WAVE), 0, s, a);
+    return hipGetLastError();
+}
+
+// One-token batches whose routing runs inside the gate/up GEMV (hy_gemv.hip): the
+// router logits (one dot per wave, the <1,1> item) and, in the work groups after
+// those, the Q8_0 quantization of x (256 elements each) in one launch.
+__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void decode_logits_kernel(const float* __restrict__ x,
+                                                                          const float* __restrict__ wr, int H, int E,
+                                                                          int logit_blocks, float* __restrict__ logits,
+                                                                          int8_t* xq, float* xd, int* xs) {
+    if ((int)blockIdx.x < logit_blocks) {
+        router_logits_block<1, 1>(x, wr, 1, H, E, logits, (int)blockIdx.x);
+        return;
+    }
+    const size_t idx = (size_t)((int)blockIdx.x - logit_blocks) * 256 + threadIdx.x;
+    quant_q8_0_elem(x, (size_t)H, idx, xq, xd, xs, nullptr);
+}
+
+hipError_t launch_decode_logits(const float* x, const float* wr, int H, int E, float* logits, int8_t* xq, float* xd,
+                                int* xs, hipStream_t s) {
+    if (H % 32 != 0 || E < 1 || E > MAX_E) return hipErrorInvalidValue;
+    const int logit_blocks = (E + ROUTER_WAVES - 1) / ROUTER_WAVES;
+    // no quantization work groups when the caller quantized x already (xq == null)
+    const int quant_groups = xq ? (H + 255) / 256 : 0;
+    hipLaunchKernelGGL(decode_logits_kernel, dim3((unsigned)(logit_blocks + quant_groups)), dim3(ROUTER_WAVES * WAVE),
+                       0, s, x, wr, H, E, logit_blocks, logits, xq, xd, xs);
     return hipGetLastError();
 }
 
