@@ -466,8 +466,9 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
         const uint32_t st = lds_off(ring + (st_i % NSTEP) * SL::BYTES);
         const uint32_t wrow = st + SL::W + lane * BPB;
         const uint32_t srow_l = st + SL::S + lane * 2;
-        v4i_t w0[GQ_U], w1[GQ_U];
+        v4i_t w0[GQ_U], w1[GQ_U], wlo[GQ_U], whi[GQ_U];
         uint32_t dwb[GQ_U];
+        float dwf[GQ_U];
         [&]<int... U>(std::integer_sequence<int, U...>) {
             ((w0[U] = lds_b128_at<U * WBYTES>(wrow)), ...);
             if constexpr (!Q4) ((w1[U] = lds_b128_at<U * WBYTES + 16>(wrow)), ...);
@@ -488,11 +489,22 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
                 }(std::make_integer_sequence<int, GQ_U>{});
                 lds_wait();
                 if (i == 0) {
+                    // weight-side work shared by the tile's tokens: Q4_0 nibbles unpacked
+                    // and fp16 scales converted once per block
 #pragma unroll
                     for (int u = 0; u < GQ_U; u++) {
                         lds_pin(w0[u]);
                         if (!Q4) lds_pin(w1[u]);
                         lds_pin(dwb[u]);
+                        dwf[u] = h2f((uint16_t)dwb[u]);
+                        if (Q4) {
+                            const int m = 0x0F0F0F0F;
+#pragma unroll
+                            for (int j = 0; j < 4; j++) {
+                                wlo[u][j] = w0[u][j] & m;
+                                whi[u][j] = (w0[u][j] >> 4) & m;
+                            }
+                        }
                     }
                 }
 #pragma unroll
@@ -501,18 +513,22 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
                     lds_pin(x1[u]);
                     lds_pin(xdb[u]);
                     if (Q4) lds_pin(xsb[u]);
-                    const int4 W0 = make_int4(w0[u][0], w0[u][1], w0[u][2], w0[u][3]);
-                    const int4 X0 = make_int4(x0[u][0], x0[u][1], x0[u][2], x0[u][3]);
-                    const int4 X1 = make_int4(x1[u][0], x1[u][1], x1[u][2], x1[u][3]);
                     int sdot;
                     if (Q4) {
-                        sdot = dot_q4_block(W0, X0, X1, (int)xsb[u]);
+                        // sum (n - 8) x = sum n x - 8 sum x, from the activation block's sum
+                        sdot = -8 * (int)xsb[u];
+#pragma unroll
+                        for (int j = 0; j < 4; j++) sdot = dot4(wlo[u][j], x0[u][j], sdot);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) sdot = dot4(whi[u][j], x1[u][j], sdot);
                     } else {
+                        const int4 W0 = make_int4(w0[u][0], w0[u][1], w0[u][2], w0[u][3]);
                         const int4 W1 = make_int4(w1[u][0], w1[u][1], w1[u][2], w1[u][3]);
+                        const int4 X0 = make_int4(x0[u][0], x0[u][1], x0[u][2], x0[u][3]);
+                        const int4 X1 = make_int4(x1[u][0], x1[u][1], x1[u][2], x1[u][3]);
                         sdot = dot_q8_block(W0, W1, X0, X1);
                     }
-                    const float dw = h2f((uint16_t)dwb[u]);
-                    acc[i] = fmaf((float)sdot, dw * __builtin_bit_cast(float, xdb[u]), acc[i]);
+                    acc[i] = fmaf((float)sdot, dwf[u] * __builtin_bit_cast(float, xdb[u]), acc[i]);
                 }
                 pin_f32(acc[i]);  // token i done before token i+1's reads
             }
