@@ -166,8 +166,9 @@ def stream_probe(hy, waves=864, kb_per_wave=144, sets=8, launches=40):
     """HBM read rate of the decode GEMV's access pattern: `waves` single-wave streams of
     kb_per_wave KB each (864 x 144 KB is the Q4_0 T=1 gate/up launch: 9 experts x 96
     row groups of 64 rows x 4096 columns), rotating over `sets` separate buffers so the
-    256 MB Infinity Cache cannot serve a repeat; variant 1 reads the same bytes with a
-    grid-stride vector loop."""
+    256 MB Infinity Cache cannot serve a repeat; variant 2 streams with non-temporal
+    copies (as the decode GEMV does), variant 1 reads the same bytes with a grid-stride
+    vector loop."""
     per = waves * kb_per_wave * 1024
     buf = hy.Buf(per * sets, np.uint8)
     hy.check(hy.lib().hy_memset(buf.ptr, 1, per * sets))
@@ -177,7 +178,7 @@ def stream_probe(hy, waves=864, kb_per_wave=144, sets=8, launches=40):
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
     res = {}
-    for variant, name in ((0, "dma_streams"), (1, "vector_grid_stride")):
+    for variant, name in ((0, "dma_streams"), (2, "dma_streams_nontemporal"), (1, "vector_grid_stride")):
         for i in range(sets):
             hy.check(hy.lib().hy_probe_stream(variant, buf.ptr + i * per, per, waves, out.ptr, st.h))
         hy.check(hy.lib().hy_event_record(ev0, st.h))

@@ -971,7 +971,7 @@ int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, fl
 int hy_probe_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev,
                     void* stream) {
     const uint64_t per = (uint64_t)waves * hy::probe_stream_step_bytes();
-    if (!buf_dev || !out_dev || waves == 0 || (variant != 0 && variant != 1) || bytes == 0 || bytes % per ||
+    if (!buf_dev || !out_dev || waves == 0 || (variant < 0 || variant > 2) || bytes == 0 || bytes % per ||
         (variant == 1 && waves % 4))
         return fail(HY_ERR_INVALID,
                     "bad stream probe arguments (variant %d, %llu bytes, %u waves: bytes must be a multiple of "

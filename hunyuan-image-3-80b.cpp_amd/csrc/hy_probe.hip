@@ -131,9 +131,11 @@ __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, 
 // global->LDS copies into a private 3-step ring of 8 KB steps (8 copies of 1 KB per
 // step, two steps in flight), as the decode GEMV streams one 64-row group of an
 // expert; it reads back one word per step so every step is consumed.  Variant 1: a
-// grid-stride 16-byte vector read of the same bytes into registers.
+// grid-stride 16-byte vector read of the same bytes into registers.  Variant 2:
+// variant 0 with the copies' non-temporal cache policy (as the decode GEMV streams).
 constexpr int STREAM_STEP = 8192, STREAM_RING = 3;
 
+template <bool NT>
 __global__ __launch_bounds__(WAVE) void stream_dma_kernel(const uint8_t* __restrict__ base, uint32_t steps,
                                                           float* __restrict__ out) {
     __shared__ __align__(16) uint8_t ring[STREAM_RING][STREAM_STEP];
@@ -142,7 +144,12 @@ __global__ __launch_bounds__(WAVE) void stream_dma_kernel(const uint8_t* __restr
     auto issue = [&](uint32_t st) {
         uint8_t* dst = ring[st % STREAM_RING];
 #pragma unroll
-        for (int c = 0; c < STREAM_STEP / 1024; c++) g2l16(src + (size_t)st * STREAM_STEP + c * 1024, dst + c * 1024);
+        for (int c = 0; c < STREAM_STEP / 1024; c++) {
+            if (NT)
+                g2l16_nt(src + (size_t)st * STREAM_STEP + c * 1024, dst + c * 1024);
+            else
+                g2l16(src + (size_t)st * STREAM_STEP + c * 1024, dst + c * 1024);
+        }
     };
     constexpr int LOADS = STREAM_STEP / 1024;
     for (uint32_t i = 0; i < STREAM_RING - 1 && i < steps; i++) issue(i);
@@ -176,10 +183,14 @@ __global__ __launch_bounds__(256) void stream_vec_kernel(const int4* __restrict_
 size_t probe_stream_step_bytes() { return STREAM_STEP; }
 
 hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s) {
-    if (variant == 0) {
+    if (variant == 0 || variant == 2) {
         const uint32_t steps = (uint32_t)(bytes / ((size_t)waves * STREAM_STEP));
-        hipLaunchKernelGGL(stream_dma_kernel, dim3((unsigned)waves), dim3(WAVE), 0, s,
-                           static_cast<const uint8_t*>(buf), steps, out);
+        if (variant == 2)
+            hipLaunchKernelGGL(stream_dma_kernel<true>, dim3((unsigned)waves), dim3(WAVE), 0, s,
+                               static_cast<const uint8_t*>(buf), steps, out);
+        else
+            hipLaunchKernelGGL(stream_dma_kernel<false>, dim3((unsigned)waves), dim3(WAVE), 0, s,
+                               static_cast<const uint8_t*>(buf), steps, out);
     } else {
         hipLaunchKernelGGL(stream_vec_kernel, dim3((unsigned)(waves * WAVE / 256)), dim3(256), 0, s,
                            static_cast<const int4*>(buf), bytes / 16, out);

@@ -327,8 +327,8 @@ int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, fl
  * decode GEMV streams its weights.  Variant 0: `waves` single-wave work groups, each
  * streaming its own contiguous bytes / waves with 16-byte global->LDS copies through
  * a private 3-step ring of 8 KB steps (bytes a multiple of waves x 8192); variant 1: a
- * grid-stride 16-byte vector read by waves x 64 threads (waves a multiple of 4).
- * out_dev holds waves x 64 floats. */
+ * grid-stride 16-byte vector read by waves x 64 threads (waves a multiple of 4);
+ * variant 2: variant 0 with non-temporal copies.  out_dev holds waves x 64 floats. */
 int hy_probe_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev,
                     void* stream);
 int hy_device_synchronize(void);

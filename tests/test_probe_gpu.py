@@ -16,8 +16,9 @@ def test_stream_probe_reads_every_step(gpu):
     buf = gpu.Buf(nbytes, np.uint8)
     gpu.check(gpu.lib().hy_memset(buf.ptr, 1, nbytes))
     out = gpu.Buf.empty((waves * 64,))
-    gpu.check(gpu.lib().hy_probe_stream(0, buf.ptr, nbytes, waves, out.ptr, None))
-    np.testing.assert_array_equal(out.numpy(), np.full(waves * 64, np.float32(steps * 0x01010101)))
+    for variant in (0, 2):  # plain and non-temporal copies
+        gpu.check(gpu.lib().hy_probe_stream(variant, buf.ptr, nbytes, waves, out.ptr, None))
+        np.testing.assert_array_equal(out.numpy(), np.full(waves * 64, np.float32(steps * 0x01010101)))
     gpu.check(gpu.lib().hy_probe_stream(1, buf.ptr, nbytes, waves, out.ptr, None))
     assert np.all(np.isfinite(out.numpy()))
 
@@ -25,7 +26,7 @@ def test_stream_probe_reads_every_step(gpu):
 def test_stream_probe_rejects_bad_sizes(gpu):
     buf = gpu.Buf(8192 * 8, np.uint8)
     out = gpu.Buf.empty((8 * 64,))
-    for variant, nbytes, waves in ((0, 8192 * 8 - 16, 8), (0, 8192 * 8, 0), (2, 8192 * 8, 8), (1, 8192 * 6, 6)):
+    for variant, nbytes, waves in ((0, 8192 * 8 - 16, 8), (0, 8192 * 8, 0), (3, 8192 * 8, 8), (1, 8192 * 6, 6)):
         with pytest.raises(gpu.HyError):
             gpu.check(gpu.lib().hy_probe_stream(variant, buf.ptr, nbytes, waves, out.ptr, None))
 
