@@ -781,8 +781,14 @@ def main():
         rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"),
                                                            (3, "f16_block_dots"),
                                                            (4, "f16_block_dots_a_unpacked"))}
+        # launch times of the overlap variants: equal to the longer of mfma and valu if
+        # the units overlapped, to their sum if not
+        ovl = {name: PROBE_WGS * 8.0 * PROBE_ITERS * 2 * 32 * 32 * 32 * 2 / probe_block_mix(hy, v) * 1e6
+               for v, name in ((5, "mfma"), (6, "valu"), (7, "both_one_wave"), (8, "both_one_wave_mfma_prio"),
+                               (9, "split_waves"), (10, "split_waves_mfma_prio"))}
         print(json.dumps({"probe": "block_mix", "work_groups": PROBE_WGS, "iters_per_wave": PROBE_ITERS,
-                          "block_dot_ops_per_s": rates, "frac_of_dense_int8": rates["mix"] / PEAK_INT8}),
+                          "block_dot_ops_per_s": rates, "frac_of_dense_int8": rates["mix"] / PEAK_INT8,
+                          "overlap_us_per_launch": ovl}),
               flush=True)
         return
     wl = WORKLOADS[a.config]

@@ -960,7 +960,7 @@ int hy_copy_d2d(void* d, const void* src, size_t b, void* stream) {
     return HY_OK;
 }
 int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream) {
-    if (!out_dev || work_groups == 0 || iters == 0 || variant < 0 || variant > 4)
+    if (!out_dev || work_groups == 0 || iters == 0 || variant < 0 || variant > 10)
         return fail(HY_ERR_INVALID, "bad probe arguments (variant %d, %u work groups, %u iterations)", variant,
                     work_groups, iters);
     HIP_TRY(hy::launch_probe_block_mix(variant, (int)work_groups, (int)iters, 3, out_dev,

@@ -321,7 +321,12 @@ int hy_copy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
  * f16 32x32x16 MFMAs, exact in fp32, then the scale MFMAs and 32 fmas, no conversions;
  * the operand unpack to f16 is not counted), variant 4 variant 3 plus the unpack of the
  * shared int8 A operand to f16 (16 values per lane).  Each wave does
- * iters * 2 * 32*32*32 block-dot MACs; out_dev holds work_groups * 512 floats. */
+ * iters * 2 * 32*32*32 block-dot MACs; out_dev holds work_groups * 512 floats.
+ * Variants 5-10 time whether the matrix and vector units overlap: per iteration four
+ * i8 MFMAs on independent accumulators (5), 64 fmas in 16 chains (6), both in one wave
+ * (7), both with the MFMAs at raised wave priority (8), the two split over alternate
+ * waves at twice the iterations (9), the split with the MFMA waves at raised priority
+ * (10). */
 int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream);
 /* Measurement only, no counterpart in the reference: reads `bytes` of buf_dev as the
  * decode GEMV streams its weights.  Variant 0: `waves` single-wave work groups, each
