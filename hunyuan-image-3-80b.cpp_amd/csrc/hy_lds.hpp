@@ -113,6 +113,11 @@ __device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, uint32_t& c, uint32
 __device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, uint32_t& d, uint32_t& e, uint32_t& f) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
 }
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c, v4i_t& c2, uint32_t& d, uint32_t& e,
+                                         uint32_t& f, uint32_t& f2) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a), "+v"(b), "+v"(c), "+v"(c2), "+v"(d), "+v"(e), "+v"(f), "+v"(f2)::"memory");
+}
 
 // ds_read_b128 / b32 at base + a compile-time byte offset (no address arithmetic)
 template <int OFF>

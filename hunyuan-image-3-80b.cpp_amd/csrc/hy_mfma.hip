@@ -5,15 +5,17 @@
 // expert (or TOK consecutive tokens for the shared expert), a row block is ROWS weight
 // rows (ROWS/64 row groups of the row-group-interleaved weights).  Each K step copies
 // KB GGUF blocks of the ROWS weight rows and of the tile's TOK activation rows
-// straight from global memory into an LDS ring of 3 stages (two in flight while one is
-// consumed).  Two shapes, picked per call from the mean pairs per expert:
-//   wide  (ROWS 128, TOK 128, KB 2): 2 row slabs x 4 token quarters -- more reuse of
-//         each weight byte for large batches (two waves share each A chunk's copies);
-//   tall  (ROWS 256, TOK  64, KB 2): 4 row slabs x 2 token halves -- keeps all eight
-//         waves busy when experts see ~64 pairs.
-// Both fit two work groups per CU.
-// Eight waves; every wave owns 2 x (32 rows x 32 tokens) output tiles and, per
-// 32-wide block, issues
+// straight from global memory into an LDS ring of stages.  Two shapes, picked per call
+// from the mean pairs per expert:
+//   wide  (ROWS 128, TOK 128, KB 2): four waves, 2 row slabs x 2 token halves, each
+//         wave 2 x 2 output tiles (64 rows x 64 tokens: one LDS read of each A and B
+//         operand serves two tiles), a 2-stage ring (one stage in flight while one is
+//         consumed), three work groups per CU (at most 168 VGPRs);
+//   tall  (ROWS 256, TOK  64, KB 2): eight waves, 4 row slabs x 2 token halves, each
+//         wave 2 x 1 tiles, a 3-stage ring, two work groups per CU -- keeps the waves
+//         busy when experts see ~64 pairs.
+// Every wave owns 2 (or 2 x 2) output tiles of 32 rows x 32 tokens and, per 32-wide
+// block and 32 tokens, issues
 // v_mfma_i32_32x32x32_i8: K = 32 is exactly one GGUF block, so each MFMA result is the
 // exact int32 block dot sum_j w_j x_j of ggml's vec_dot, which is then rescaled in
 // fp32 with the blocks taken in order: acc = fmaf(float(S), d_w * d_x, acc) -- the
@@ -55,16 +57,17 @@ constexpr int MM_XCD = 8;                  // XCDs of the device (work-group rou
 // the swap rows r and r+8 share banks and every read takes two passes.  The copies
 // keep their contiguous LDS destinations and fetch the swapped halves instead.
 //
-// WAVES waves per work group (one 64-row slab x 32-token group each); RING LDS stage
+// WAVES waves per work group (one 64-row slab x 32 * TT tokens each); RING LDS stage
 // slots (one computed, RING - 1 in flight).  8-wave shapes run two work groups per
-// CU, the 16-wave shape one, with a deeper ring in the LDS that frees.
-template <int ROWS_, int TOK_, int KB_, int WAVES_ = 8, int RING_ = 3>
+// CU, the 4-wave 2 x 2 shape three, a 16-wave shape one.
+template <int ROWS_, int TOK_, int KB_, int WAVES_ = 8, int RING_ = 3, int TT_ = 1>
 struct MmShape {
     static constexpr int ROWS = ROWS_, TOK = TOK_, KB = KB_, WAVES = WAVES_, RING = RING_;
+    static constexpr int TT = TT_;                   // 32-token tiles per wave (1 or 2)
     static constexpr int THREADS = WAVES * WAVE;
-    static constexpr int WG_PER_CU = WAVES == 16 ? 1 : 2;
+    static constexpr int WG_PER_CU = WAVES == 16 ? 1 : (TT == 2 ? 3 : 2);
     static constexpr int SLABS = ROWS / 64;          // 64-row slabs (one per row group)
-    static constexpr int TQ = WAVES / SLABS;         // 32-token column groups
+    static constexpr int TQ = WAVES / SLABS;         // column groups of 32 * TT tokens
     static constexpr int CHUNKS = SLABS * KB;
     static constexpr int ST_A = CHUNKS * 64 * 32;
     static constexpr int ST_AR = CHUNKS * 64 * 16;
@@ -77,14 +80,14 @@ struct MmShape {
     static constexpr int B_LOADS = (B_LANES + WAVE - 1) / WAVE;
     static constexpr int WPC = WAVES / CHUNKS;        // waves sharing one A chunk's copies
     static_assert(CHUNKS * WPC == WAVES && (WPC == 1 || WPC == 2), "A chunks split evenly over the waves");
-    static_assert(WAVES == 8 || WAVES == 16, "two 8-wave or one 16-wave work group per CU");
-    static_assert(RING >= 3, "at least one stage in flight while one is refilled");
-    static_assert(TQ * 32 == TOK, "token groups must cover the tile");
+    static_assert(WAVES == 8 || WAVES == 16 || (WAVES == 4 && TT == 2), "work group shapes");
+    static_assert(RING >= 2, "at least one stage in flight while one is consumed");
+    static_assert(TQ * 32 * TT == TOK, "token groups must cover the tile");
     static_assert(B_LANES % WAVE == 0 || B_LOADS == 1, "partial B loads only as a single load");
     static_assert(KB == 4 || KB == 2 || KB == 1, "B-scale copy handles 16, 8 or 4 B per token");
     static_assert(WAVES % KB == 0 && TPW % 2 == 0, "B copies: whole token rows per wave");
 };
-using ShapeWide = MmShape<128, 128, 2>;
+using ShapeWide = MmShape<128, 128, 2, 4, 2, 2>;
 using ShapeTall = MmShape<256, 64, 2>;
 
 struct MmArgs {
@@ -262,13 +265,20 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 
     const int sl = wave % MM_SLABS;    // 64-row slab within the row block
     const int nq = wave / MM_SLABS;    // 32-token column group of the tile
-    const bool active = nq * 32 < n;   // waves past the tile's last pair skip the math
+    constexpr int TT = SH::TT;
+    const bool active = nq * 32 * TT < n;   // waves past the tile's last pair skip the math
     const int lr = lane % 32, lg = lane / 32;
-    float acc0[16], acc1[16];
+    // acc0 / acc1: rows 0-31 / 32-63 of the slab x the first 32 tokens; acc2 / acc3 the
+    // same rows x the second 32 tokens (TT = 2)
+    float acc0[16], acc1[16], acc2[TT == 2 ? 16 : 1], acc3[TT == 2 ? 16 : 1];
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         acc0[v] = 0.0f;
         acc1[v] = 0.0f;
+        if constexpr (TT == 2) {
+            acc2[v] = 0.0f;
+            acc3[v] = 0.0f;
+        }
     }
     // per-lane LDS offsets inside a stage slot (the block kb adds a constant):
     //   A rows lr and 32+lr of this wave's slab, 16-byte half lg (swizzled)
@@ -277,9 +287,9 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     //   d_x of token nq*32+lr; lanes of the upper half read zeros
     const int hsw = lg ^ ((lr >> 3) & 1);
     const uint32_t a_lane = (uint32_t)((Q4 ? 0 : OFF_A) + sl * MM_KB * 2048 + lr * 32 + 16 * hsw);
-    const uint32_t b_lane = (uint32_t)(OFF_B + (nq * 32 + lr) * 32 + 16 * hsw);
+    const uint32_t b_lane = (uint32_t)(OFF_B + (nq * 32 * TT + lr) * 32 + 16 * hsw);
     const uint32_t sw_lane = (uint32_t)(lg == 0 ? OFF_AS + sl * MM_KB * 128 + lr * 2 : OFF_Z);
-    const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 + lr) * MM_KB * 4 : OFF_Z);
+    const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 * TT + lr) * MM_KB * 4 : OFF_Z);
     const uint32_t ring0 = lds_off(ring[0]);
     const uint32_t aun0 = lds_off(aun);
     // rank-1 operands {d, 0, 0, ...}: only element 0 changes, the zeros stay in place
@@ -294,7 +304,15 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         uint32_t dw0 = lds_u16_at<KBI * 128>(swq);
         uint32_t dw1 = lds_u16_at<KBI * 128 + 64>(swq);
         uint32_t dxb = lds_b32_at<KBI * 4>(sxq);
-        lds_wait(A0, A1, B, dw0, dw1, dxb);
+        v4i_t B1;
+        uint32_t dxb1;
+        if constexpr (TT == 2) {
+            B1 = lds_b128_at<KBI * MM_TOK * 32 + 1024>(bq);
+            dxb1 = lds_b32_at<KBI * 4 + 32 * MM_KB * 4>(sxq);
+            lds_wait(A0, A1, B, B1, dw0, dw1, dxb, dxb1);
+        } else {
+            lds_wait(A0, A1, B, dw0, dw1, dxb);
+        }
         const v16i_t zero = {};
         // gate/up: the block's four MFMAs issue at raised wave priority, so a wave whose
         // operands are ready reaches the matrix unit ahead of the other waves' rescale
@@ -317,6 +335,23 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         for (int v = 0; v < 16; v++) {
             acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
             acc1[v] = fmaf((float)S1[v], C1[v], acc1[v]);
+        }
+        if constexpr (TT == 2) {
+            // the second 32 tokens: same A operands and weight scales
+            if constexpr (MODE == 0) __builtin_amdgcn_s_setprio(1);
+            const v16i_t S2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, zero, 0, 0, 0);
+            const v16i_t S3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, zero, 0, 0, 0);
+            xb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, dxb1), 0.0f));
+            const v16f_t C2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa0),
+                                                                     __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
+            const v16f_t C3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa1),
+                                                                     __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
+            if constexpr (MODE == 0) __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                acc2[v] = fmaf((float)S2[v], C2[v], acc2[v]);
+                acc3[v] = fmaf((float)S3[v], C3[v], acc3[v]);
+            }
         }
     };
 
@@ -366,57 +401,62 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         soff = soff + STAGE == (uint32_t)(MM_RING * STAGE) ? 0u : soff + STAGE;
     }
 
-    // ---- epilogues
-    const int j = nq * 32 + lr;  // pair index within the tile
-    if (!active || j >= n) return;
-    if (MODE == 0) {
-        // acc0 = gate rows, acc1 = matching up rows of slab (MM_SLABS * rb + sl)
-        const int slab = MM_SLABS * rb + sl;
-        float h[16];
-        float amax = 0.0f;
+    // ---- epilogues: one per 32-token column group of the wave (ag = the rows of the
+    // slab's first half, au = the second half)
+    auto epilogue = [&](const float (&ag)[16], const float (&au)[16], int j) {
+        if (j >= n) return;
+        if (MODE == 0) {
+            // ag = gate rows, au = matching up rows of slab (MM_SLABS * rb + sl)
+            const int slab = MM_SLABS * rb + sl;
+            float h[16];
+            float amax = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            h[v] = swiglu(acc0[v], acc1[v]);
-            amax = fmaxf(amax, fabsf(h[v]));
-        }
-        amax = fmaxf(amax, __shfl_xor(amax, 32, WAVE));
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        int qsum = 0;
-        int packed[4];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            uint32_t p = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int q = (int)__builtin_roundf(h[4 * g + i] * id);
-                qsum += q;
-                p |= ((uint32_t)(q & 0xff)) << (8 * i);
+            for (int v = 0; v < 16; v++) {
+                h[v] = swiglu(ag[v], au[v]);
+                amax = fmaxf(amax, fabsf(h[v]));
             }
-            packed[g] = (int)p;
-        }
-        qsum += __shfl_xor(qsum, 32, WAVE);
-        const size_t slot = (size_t)slot_s[j];
-        int8_t* dst = a.hq + slot * a.I + (size_t)slab * QK;
+            amax = fmaxf(amax, __shfl_xor(amax, 32, WAVE));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            int qsum = 0;
+            int packed[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) *reinterpret_cast<int*>(dst + 8 * g + 4 * lg) = packed[g];
-        if (lg == 0) {
-            const size_t nbi = a.I / QK;
-            a.hd[slot * nbi + slab] = h2f(f2h(d));
-            a.hs[slot * nbi + slab] = qsum;
-        }
-    } else {
-        const int rbase = row0 + sl * 64;
-        float* yr = a.y + (size_t)slot_s[j] * a.H;
+            for (int g = 0; g < 4; g++) {
+                uint32_t p = 0;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int r = 8 * g + 4 * lg;
-            *reinterpret_cast<float4*>(yr + rbase + r) =
-                make_float4(acc0[4 * g], acc0[4 * g + 1], acc0[4 * g + 2], acc0[4 * g + 3]);
-            *reinterpret_cast<float4*>(yr + rbase + 32 + r) =
-                make_float4(acc1[4 * g], acc1[4 * g + 1], acc1[4 * g + 2], acc1[4 * g + 3]);
+                for (int i = 0; i < 4; i++) {
+                    const int q = (int)__builtin_roundf(h[4 * g + i] * id);
+                    qsum += q;
+                    p |= ((uint32_t)(q & 0xff)) << (8 * i);
+                }
+                packed[g] = (int)p;
+            }
+            qsum += __shfl_xor(qsum, 32, WAVE);
+            const size_t slot = (size_t)slot_s[j];
+            int8_t* dst = a.hq + slot * a.I + (size_t)slab * QK;
+#pragma unroll
+            for (int g = 0; g < 4; g++) *reinterpret_cast<int*>(dst + 8 * g + 4 * lg) = packed[g];
+            if (lg == 0) {
+                const size_t nbi = a.I / QK;
+                a.hd[slot * nbi + slab] = h2f(f2h(d));
+                a.hs[slot * nbi + slab] = qsum;
+            }
+        } else {
+            const int rbase = row0 + sl * 64;
+            float* yr = a.y + (size_t)slot_s[j] * a.H;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int r = 8 * g + 4 * lg;
+                *reinterpret_cast<float4*>(yr + rbase + r) = make_float4(ag[4 * g], ag[4 * g + 1], ag[4 * g + 2], ag[4 * g + 3]);
+                *reinterpret_cast<float4*>(yr + rbase + 32 + r) =
+                    make_float4(au[4 * g], au[4 * g + 1], au[4 * g + 2], au[4 * g + 3]);
+            }
         }
-    }
+    };
+    if (!active) return;
+    const int j0 = nq * 32 * TT + lr;  // pair index within the tile
+    epilogue(acc0, acc1, j0);
+    if constexpr (TT == 2) epilogue(acc2, acc3, j0 + 32);
 }
 
 template <int MODE, class SH>
