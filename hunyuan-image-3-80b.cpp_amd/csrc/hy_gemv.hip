@@ -381,8 +381,11 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ int tok_s[NT], slot_s[NT];
     const int lane = threadIdx.x;
-    const int G = blockIdx.y;  // 64-row group (grid.y == n_groups)
-    const int tile = blockIdx.x;
+    // grid (row groups, tiles), dispatched tile by tile from the last tile: the shared
+    // expert's tiles (the list's last, and with the most tokens) start first, so
+    // their heavier waves do not form the launch's tail
+    const int G = blockIdx.x;  // 64-row group (grid.x == n_groups)
+    const int tile = (int)gridDim.y - 1 - (int)blockIdx.y;
     const int Kd = a.Kd, nb = Kd / QK, nsteps = nb / GQ_U;
 
     // start the weight stream first: tile_e[tile] is in the arena for every launched
@@ -647,7 +650,7 @@ template <int MODE>
 static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     a.nx = a.T < GEMV_NT ? a.T : GEMV_NT;
     const dim3 grid_v(tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
-    const dim3 grid_q(tiles, a.n_groups);
+    const dim3 grid_q(a.n_groups, tiles);
     switch (wtype) {
     case HY_TYPE_Q8_0:
         if (gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
@@ -695,7 +698,7 @@ hipError_t launch_gemv_up_route1(int wtype, const MatView& W, const Route1Out& r
                                  int K, int8_t* hq, float* hd, int* hs, hipStream_t s) {
     if (!gemv_route1_ok(wtype, H) || K < 1 || K > E || E > MAX_E) return hipErrorInvalidValue;
     GvArgs a{W, Routing{}, X.q, X.d, X.s, nullptr, 1, H, I, E, K, H, 2 * I / 64, 1, hq, hd, hs, nullptr, nullptr, r};
-    const dim3 grid((unsigned)(K + r.has_shared), (unsigned)a.n_groups);
+    const dim3 grid((unsigned)a.n_groups, (unsigned)(K + r.has_shared));
     // one token: K + 1 tiles x row groups; the deeper ring when every wave is resident
     const bool deep = (long)grid.x * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3));
     if (wtype == HY_TYPE_Q8_0)
