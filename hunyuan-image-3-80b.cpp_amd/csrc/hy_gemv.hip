@@ -85,7 +85,9 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int tok_s[NT], slot_s[NT];
     // mode 1 covers every tile, routed and shared
-    const int tile = (int)blockIdx.x;
+    // grid (row-group quads, tiles), dispatched tile by tile from the last tile (the
+    // shared expert's, with the most tokens) as the ring kernel's
+    const int tile = (int)gridDim.y - 1 - (int)blockIdx.y;
     if (tile >= a.R.meta[1]) return;
     const int e = a.R.tile_e[tile], start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
     __syncthreads();
 
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int G = blockIdx.y * GV_WAVES + wave;
+    const int G = blockIdx.x * GV_WAVES + wave;
     if (G >= a.n_groups) return;
     float acc[NT];
 #pragma unroll
@@ -649,7 +651,7 @@ static int gemv_q_slots(size_t smem) { return 256 * (int)((160u * 1024u) / smem)
 template <int MODE>
 static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     a.nx = a.T < GEMV_NT ? a.T : GEMV_NT;
-    const dim3 grid_v(tiles, (a.n_groups + GV_WAVES - 1) / GV_WAVES);
+    const dim3 grid_v((a.n_groups + GV_WAVES - 1) / GV_WAVES, tiles);
     const dim3 grid_q(a.n_groups, tiles);
     switch (wtype) {
     case HY_TYPE_Q8_0:
