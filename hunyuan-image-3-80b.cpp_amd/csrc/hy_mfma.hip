@@ -314,10 +314,10 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
             lds_wait(A0, A1, B, dw0, dw1, dxb);
         }
         const v16i_t zero = {};
-        // gate/up: the block's four MFMAs issue at raised wave priority, so a wave whose
-        // operands are ready reaches the matrix unit ahead of the other waves' rescale
-        // (c5 ffn_up -2 %, c4 -3 %, c2 -4 %; the down products gain nothing from it)
-        if constexpr (MODE == 0) __builtin_amdgcn_s_setprio(1);
+        // the block's MFMAs issue at raised wave priority, so a wave whose operands are
+        // ready reaches the matrix unit ahead of the other waves' rescale (c5 ffn_up
+        // -2 %, c4 -3 %, c2 -4 %; ffn_down -2 % with the 2 x 2 tiles, nothing with 2 x 1)
+        __builtin_amdgcn_s_setprio(1);
         const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
         const v16i_t S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
         // the upper lanes read zeros; d_x is an fp16 value stored as f32, so the
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
                                                                  __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
         const v16f_t C1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa1),
                                                                  __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
-        if constexpr (MODE == 0) __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             acc0[v] = fmaf((float)S0[v], C0[v], acc0[v]);
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         }
         if constexpr (TT == 2) {
             // the second 32 tokens: same A operands and weight scales
-            if constexpr (MODE == 0) __builtin_amdgcn_s_setprio(1);
+            __builtin_amdgcn_s_setprio(1);
             const v16i_t S2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, zero, 0, 0, 0);
             const v16i_t S3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, zero, 0, 0, 0);
             xb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, dxb1), 0.0f));
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
                                                                      __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
             const v16f_t C3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa1),
                                                                      __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
-            if constexpr (MODE == 0) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 acc2[v] = fmaf((float)S2[v], C2[v], acc2[v]);
