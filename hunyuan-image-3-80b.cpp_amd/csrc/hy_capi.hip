@@ -190,8 +190,21 @@ int tile_bound_routed(int T, int K, int E, int NT) {
 // moe_forward_cpu (src/attention.cpp:268-275), which renormalise at every K.
 int renorm_rule(int32_t norm, uint32_t K) { return (norm == HY_NORM_ALWAYS || (norm != HY_NORM_OFF && K > 1)) ? 1 : 0; }
 
-// largest batch the decode GEMV takes in AUTO mode; above it the MFMA grouped GEMM
+// largest batch the one-launch decode routing takes; the decode GEMV takes at least
+// these in AUTO mode
 constexpr uint32_t kGemvMaxTokens = 16;
+
+// AUTO mode: the decode GEMV or the MFMA grouped GEMM.  Measured crossover on one MI355X
+// (H 4096, I 3072, E 64, K 8, layer steps over rotating weight sets): Q4_0 GEMV 374 vs
+// MFMA 423 us at T=32, 515 vs 478 at T=48 (up to ~5 pairs per expert); Q8_0 452 vs 464
+// us at T=20, 512 vs 474 at T=24 (up to ~2.5 pairs per expert).
+bool gemv_batch(int wt, uint32_t T, int K, int E) {
+    if (T <= kGemvMaxTokens) return true;
+    const uint64_t pairs = (uint64_t)T * (uint64_t)K;
+    if (wt == HY_TYPE_Q4_0) return pairs <= 5ull * (uint64_t)E;
+    if (wt == HY_TYPE_Q8_0) return 2 * pairs <= 5ull * (uint64_t)E;
+    return false;
+}
 
 int check_cfg(const hy_moe_config* c) {
     if (!c) return fail(HY_ERR_INVALID, "null config");
@@ -283,7 +296,7 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const bool mfma_fits = (uint64_t)T * (uint64_t)H < (1ull << 32) &&
                            (uint64_t)T * (uint64_t)(K + 1) * (uint64_t)I < (1ull << 32);
     const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) && mfma_fits &&
-                      (c->path == HY_PATH_MFMA || T > kGemvMaxTokens);
+                      (c->path == HY_PATH_MFMA || !gemv_batch(wt, T, K, E));
     const int shape = mfma ? hy::mfma_shape(iT, K, E, H, I) : -1;
     const int NT = mfma ? hy::mfma_shape_tokens(shape) : hy::gemv_tile_tokens();
     // group-limited greedy, dropping and the aux loss take the general routing path
