@@ -73,10 +73,28 @@ __device__ __forceinline__ float tree_sum64(float v) {
     return v;
 }
 
+// max(v, the value of the lane the DPP control CTRL names); every source lane of the
+// controls used here is in range, and the callers run whole waves
+template <int CTRL>
+__device__ __forceinline__ float dpp_fmax(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+    return fmaxf(v, __builtin_bit_cast(float, o));
+}
+__device__ __forceinline__ float lane_f32(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// 64-lane maximum, in every lane (call with the whole wave active).  Inside each 16-lane
+// row: quad permutes [1,0,3,2] and [2,3,0,1] (xor 1, xor 2), then the half-row mirror
+// and the row mirror, which pair lanes whose quads / half-rows already agree; then the
+// four rows' maxima are read as scalars.  No LDS-crossbar shuffles (ds_bpermute), which
+// made the top-k's serial argmax rounds latency-bound.  max is exact and order-free:
+// any pairing gives the same value.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, shfl_xor(v, s));
-    return v;
+    v = dpp_fmax<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_fmax<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_fmax<0x141>(v);  // row_half_mirror
+    v = dpp_fmax<0x140>(v);  // row_mirror
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
