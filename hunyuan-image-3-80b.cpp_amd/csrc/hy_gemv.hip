@@ -701,14 +701,12 @@ hipError_t launch_gemv_up_route1(int wtype, const MatView& W, const Route1Out& r
     if (!gemv_route1_ok(wtype, H) || K < 1 || K > E || E > MAX_E) return hipErrorInvalidValue;
     GvArgs a{W, Routing{}, X.q, X.d, X.s, nullptr, 1, H, I, E, K, H, 2 * I / 64, 1, hq, hd, hs, nullptr, nullptr, r};
     const dim3 grid((unsigned)a.n_groups, (unsigned)(K + r.has_shared));
-    // one token: K + 1 tiles x row groups; the deeper ring when every wave is resident
-    const bool deep = (long)grid.x * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3));
+    // one token: K + 1 tiles x row groups, a 2-step ring for both types (at T = 1 with
+    // E = 64, K = 8, H = 4096, Q4_0, the 3-step ring, every wave still resident, was
+    // 1 % slower: gate/up 27.6-27.7 against 27.4 us)
     if (wtype == HY_TYPE_Q8_0)
         hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, 0, 2, true>), grid, dim3(GQ_THREADS),
                            gemv_q_smem<HY_TYPE_Q8_0>(2), s, a);
-    else if (deep)
-        hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, 0, 3, true>), grid, dim3(GQ_THREADS),
-                           gemv_q_smem<HY_TYPE_Q4_0>(3), s, a);
     else
         hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, 0, 2, true>), grid, dim3(GQ_THREADS),
                            gemv_q_smem<HY_TYPE_Q4_0>(2), s, a);
