@@ -665,8 +665,9 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     case HY_TYPE_Q4_0:
         if (gemv_q_fits<HY_TYPE_Q4_0>(a.Kd)) {
             // tiles is the host's bound on the routed + shared tiles: the deeper ring
-            // when every launched wave is resident at once
-            if ((long)tiles * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3)))
+            // for gate/up when every launched wave is resident at once; the down
+            // products take 2 steps (T=2: 23.9 -> 22.8 us, T=1 and T=4 unchanged)
+            if (MODE == 0 && (long)tiles * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3)))
                 hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE, 3>), grid_q, dim3(GQ_THREADS),
                                    gemv_q_smem<HY_TYPE_Q4_0>(3), s, a);
             else
