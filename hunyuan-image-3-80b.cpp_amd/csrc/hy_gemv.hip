@@ -594,6 +594,12 @@ __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __
     const int H4 = H / 4;
     if (idx >= (size_t)T * H4) return;
     const int t = (int)(idx / H4), r4 = (int)(idx % H4);
+    // the shared expert's row and the residual do not depend on the lists: their loads
+    // are issued first, so they overlap the list and y-row round trips instead of
+    // following them
+    v4f_t u = {0.f, 0.f, 0.f, 0.f}, q = {0.f, 0.f, 0.f, 0.f};
+    if (has_shared) u = __builtin_nontemporal_load(reinterpret_cast<const v4f_t*>(y + ((size_t)T * K + t) * H) + r4);
+    if (resid) q = reinterpret_cast<const v4f_t*>(resid + (size_t)t * H)[r4];
     float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k0 = 0; k0 < K; k0 += KMAX) {
         int pos[KMAX];
@@ -614,14 +620,8 @@ __global__ __launch_bounds__(256) void combine_kernel(Routing R, const float* __
                                 fmaf(w[k], v[k][3], c.w));
     }
     float4 o = c;
-    if (has_shared) {
-        const v4f_t u = __builtin_nontemporal_load(reinterpret_cast<const v4f_t*>(y + ((size_t)T * K + t) * H) + r4);
-        o = make_float4(u[0] + c.x, u[1] + c.y, u[2] + c.z, u[3] + c.w);
-    }
-    if (resid) {
-        const float4 q = reinterpret_cast<const float4*>(resid + (size_t)t * H)[r4];
-        o = make_float4(q.x + o.x, q.y + o.y, q.z + o.z, q.w + o.w);
-    }
+    if (has_shared) o = make_float4(u[0] + c.x, u[1] + c.y, u[2] + c.z, u[3] + c.w);
+    if (resid) o = make_float4(q[0] + o.x, q[1] + o.y, q[2] + o.z, q[3] + o.w);
     reinterpret_cast<float4*>(out + (size_t)t * H)[r4] = o;
 }
 
