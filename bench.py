@@ -7,8 +7,9 @@ with GGUF Q8_0 weights, all resident in HBM (about 84 GB): per layer RMSNorm (ep
 add, T=4096 tokens per step, inputs resident in HBM.  A step is the whole stack;
 tokens/s = T / step time.  Weights are random-init N(0, 0.02) seeded by layer index
 (synthetic, generated on the device), activations N(0, 1).  The same line carries the
-decode (Q4_0, T=1 and T=8) and the Zipf-skewed image-token (Q4_0, T=4096) layers as
-`extras`, each timed in its own region.
+decode (Q4_0, T=1, 2, 4 and 8) and the Zipf-skewed image-token (Q4_0, T=4096) layers as
+`extras`, each timed in its own region, with the T=512 Q8_0 layer and the F32 T=16
+layer, so that every configuration has a number in the one line.
 
 Other workloads (--config): c1 F32 T=16, c2 Q8_0 T=512, c3 Q4_0 decode (--tokens
 1/2/4/8), c4 Q4_0 T=4096 Zipf-skewed routing, c5 the stack (default).
@@ -45,7 +46,7 @@ PEAK_FP32_MFMA = 157.3e12  # FLOP/s, dense fp32 MFMA
 # The grouped int8 GEMM keeps ggml's per-block fp32 rescale: every 32-MAC block partial
 # costs an int->float conversion and an fma on the vector ALUs, and a rank-1 MFMA forms
 # the scale products.  Its ceiling is measured in the same run by a compute-only probe
-# of exactly that per-block instruction mix (hy_probe_block_mix, probe_block_mix below)
+# of exactly that per-block instruction mix (hyp_block_mix in libhy_probe.so, probe_block_mix below)
 PROBE_WGS, PROBE_ITERS = 512, 4000
 ATTN = dict(H=4096, nh=32, nkv=8, hd=128)   # HunyuanImage-3 attention shape
 PARAMS_PER_EXPERT = 3 * H * I
@@ -134,9 +135,36 @@ def measured_traffic(workload, kname, path=TRAFFIC_TABLE):
     return None
 
 
+PROBE_LIB = os.path.join(ROOT, "hunyuan-image-3-80b.cpp_amd", "libhy_probe.so")
+_probe = None
+
+
+def probe_lib():
+    """libhy_probe.so: the measurement probes (hunyuan-image-3-80b.cpp_amd/probe/), a
+    library of their own beside the product library."""
+    global _probe
+    if _probe is None:
+        import ctypes as C
+        if not os.path.exists(PROBE_LIB):
+            raise RuntimeError(f"{PROBE_LIB} is not built: run python hunyuan-image-3-80b.cpp_amd/build.py")
+        L = C.CDLL(PROBE_LIB)
+        L.hyp_last_error.restype = C.c_char_p
+        L.hyp_block_mix.restype = C.c_int
+        L.hyp_block_mix.argtypes = [C.c_int32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
+        L.hyp_stream.restype = C.c_int
+        L.hyp_stream.argtypes = [C.c_int32, C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_void_p]
+        _probe = L
+    return _probe
+
+
+def probe_check(rc):
+    if rc != 0:
+        raise RuntimeError(f"probe error: {probe_lib().hyp_last_error().decode()}")
+
+
 def probe_block_mix(hy, variant=0, reps=3):
     """Rate (block-dot int8 ops/s) of the grouped GEMM's per-block instruction mix with
-    no memory traffic: the best of `reps` launches of hy_probe_block_mix (variant 0: the
+    no memory traffic: the best of `reps` launches of hyp_block_mix (variant 0: the
     whole mix; 1: its four MFMAs only; 2: its 64 vector ops only; 3: the f16 block-dot
     alternative, without the operand unpack it would also need; 4: the same with the
     int8 A operand unpacked to f16)."""
@@ -145,11 +173,11 @@ def probe_block_mix(hy, variant=0, reps=3):
     ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
     hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
-    hy.check(hy.lib().hy_probe_block_mix(variant, PROBE_WGS, 100, out.ptr, st.h))
+    probe_check(probe_lib().hyp_block_mix(variant, PROBE_WGS, 100, out.ptr, st.h))
     best = None
     for _ in range(reps):
         hy.check(hy.lib().hy_event_record(ev0, st.h))
-        hy.check(hy.lib().hy_probe_block_mix(variant, PROBE_WGS, PROBE_ITERS, out.ptr, st.h))
+        probe_check(probe_lib().hyp_block_mix(variant, PROBE_WGS, PROBE_ITERS, out.ptr, st.h))
         hy.check(hy.lib().hy_event_record(ev1, st.h))
         st.synchronize()
         ms = hy.C.c_float()
@@ -180,10 +208,10 @@ def stream_probe(hy, waves=864, kb_per_wave=144, sets=8, launches=40):
     res = {}
     for variant, name in ((0, "dma_streams"), (2, "dma_streams_nontemporal"), (1, "vector_grid_stride")):
         for i in range(sets):
-            hy.check(hy.lib().hy_probe_stream(variant, buf.ptr + i * per, per, waves, out.ptr, st.h))
+            probe_check(probe_lib().hyp_stream(variant, buf.ptr + i * per, per, waves, out.ptr, st.h))
         hy.check(hy.lib().hy_event_record(ev0, st.h))
         for i in range(launches):
-            hy.check(hy.lib().hy_probe_stream(variant, buf.ptr + (i % sets) * per, per, waves, out.ptr, st.h))
+            probe_check(probe_lib().hyp_stream(variant, buf.ptr + (i % sets) * per, per, waves, out.ptr, st.h))
         hy.check(hy.lib().hy_event_record(ev1, st.h))
         st.synchronize()
         ms = hy.C.c_float()
@@ -699,7 +727,7 @@ def run_moe(hy, wl, steps, warmup, seed, graph=False, tokens=None, mix_ceiling=N
         if mix_ceiling:
             roof["rescale_ceiling"] = {"peak": mix_ceiling / 1e12, "unit": "TOP/s",
                                        "frac": ops / avg_s / mix_ceiling,
-                                       "source": "hy_probe_block_mix, the per-block mix alone, same run"}
+                                       "source": "hyp_block_mix, the per-block mix alone, same run"}
     top8 = float(np.sort(counts)[::-1][:8].sum() / max(1, counts.sum()))
     res = {
         "value": tokens_per_s, "ms_per_step": ms_per_step,
@@ -725,9 +753,12 @@ def run_moe(hy, wl, steps, warmup, seed, graph=False, tokens=None, mix_ceiling=N
     return res
 
 
-# extra workloads timed after the headline in the same run: the decode and skewed
-# image-token targets (name, workload, tokens, steps multiplier)
-EXTRAS = (("decode_t1", "c3", 1, 10), ("decode_t8", "c3", 8, 10), ("zipf_t4096", "c4", None, 1))
+# extra workloads timed after the headline in the same run, so that every configuration
+# has a number in the one JSON line: the decode batches, the skewed image-token layer,
+# the T=512 prefill layer and the F32 layer (name, workload, tokens, steps multiplier)
+EXTRAS = (("decode_t1", "c3", 1, 10), ("decode_t2", "c3", 2, 10), ("decode_t4", "c3", 4, 10),
+          ("decode_t8", "c3", 8, 10), ("zipf_t4096", "c4", None, 1), ("prefill_t512", "c2", None, 5),
+          ("f32_t16", "c1", None, 5))
 
 
 def main():
@@ -781,14 +812,8 @@ def main():
         rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"),
                                                            (3, "f16_block_dots"),
                                                            (4, "f16_block_dots_a_unpacked"))}
-        # launch times of the overlap variants: equal to the longer of mfma and valu if
-        # the units overlapped, to their sum if not
-        ovl = {name: PROBE_WGS * 8.0 * PROBE_ITERS * 2 * 32 * 32 * 32 * 2 / probe_block_mix(hy, v) * 1e6
-               for v, name in ((5, "mfma"), (6, "valu"), (7, "both_one_wave"), (8, "both_one_wave_mfma_prio"),
-                               (9, "split_waves"), (10, "split_waves_mfma_prio"))}
         print(json.dumps({"probe": "block_mix", "work_groups": PROBE_WGS, "iters_per_wave": PROBE_ITERS,
-                          "block_dot_ops_per_s": rates, "frac_of_dense_int8": rates["mix"] / PEAK_INT8,
-                          "overlap_us_per_launch": ovl}),
+                          "block_dot_ops_per_s": rates, "frac_of_dense_int8": rates["mix"] / PEAK_INT8}),
               flush=True)
         return
     wl = WORKLOADS[a.config]

@@ -22,6 +22,8 @@ CSRC = os.path.join(HERE, "csrc")
 HOST = os.path.join(HERE, "host")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhy_moe.so")
+PROBE = os.path.join(HERE, "probe")
+PROBE_LIB = os.path.join(HERE, "libhy_probe.so")   # bench.py's measurement probes only
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}"]
@@ -79,8 +81,26 @@ def build_cxx_tests():
 def build_all(asm=False, jobs=8, verbose=False):
     build_oracle()
     lib = build(asm=asm, jobs=jobs, verbose=verbose)
+    build_probe()
     build_cxx_tests()
     return lib
+
+
+def build_probe():
+    """libhy_probe.so: the measurement probes bench.py reports ceilings from.  A separate
+    library, so that nothing of it is linked into or exported by libhy_moe.so."""
+    os.makedirs(BUILD, exist_ok=True)
+    cc = hipcc()
+    objs = []
+    for f in sorted(os.listdir(PROBE)):
+        if f.endswith(".hip"):
+            obj = os.path.join(BUILD, "probe_" + f + ".o")
+            _run([cc] + COMMON + DEVICE + [f"-I{PROBE}", "-c", os.path.join(PROBE, f), "-o", obj])
+            objs.append(obj)
+    tmp = PROBE_LIB + ".tmp"
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs)
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def build(asm=False, jobs=8, verbose=False):

@@ -972,29 +972,6 @@ int hy_copy_d2d(void* d, const void* src, size_t b, void* stream) {
     HIP_TRY(hy::launch_copy(d, src, b, (hipStream_t)stream));
     return HY_OK;
 }
-int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream) {
-    if (!out_dev || work_groups == 0 || iters == 0 || variant < 0 || variant > 10)
-        return fail(HY_ERR_INVALID, "bad probe arguments (variant %d, %u work groups, %u iterations)", variant,
-                    work_groups, iters);
-    HIP_TRY(hy::launch_probe_block_mix(variant, (int)work_groups, (int)iters, 3, out_dev,
-                                       static_cast<hipStream_t>(stream)));
-    return HY_OK;
-}
-
-int hy_probe_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev,
-                    void* stream) {
-    const uint64_t per = (uint64_t)waves * hy::probe_stream_step_bytes();
-    if (!buf_dev || !out_dev || waves == 0 || (variant < 0 || variant > 2) || bytes == 0 || bytes % per ||
-        (variant == 1 && waves % 4))
-        return fail(HY_ERR_INVALID,
-                    "bad stream probe arguments (variant %d, %llu bytes, %u waves: bytes must be a multiple of "
-                    "waves x %zu, waves a multiple of 4 for variant 1)",
-                    variant, (unsigned long long)bytes, waves, hy::probe_stream_step_bytes());
-    HIP_TRY(hy::launch_probe_stream(variant, buf_dev, (size_t)bytes, (int)waves, out_dev,
-                                    static_cast<hipStream_t>(stream)));
-    return HY_OK;
-}
-
 int hy_device_synchronize(void) {
     HIP_TRY(hipDeviceSynchronize());
     return HY_OK;

@@ -105,10 +105,6 @@ hipError_t launch_ffn_down_mfma(int wtype, int shape, int n_tiles_bound, const M
 
 // residency (hy_data.hip)
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
-// compute-only probe of the grouped GEMM's per-block mix (hy_probe.hip)
-hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int seed, float* out, hipStream_t s);
-size_t probe_stream_step_bytes();
-hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s);
 hipError_t launch_synth_matrix(int wtype, uint64_t key, float scale, int rows, int cols, int gu_I, uint8_t* qs,
                                uint16_t* sc, hipStream_t s);
 hipError_t launch_synth_fill(float* out, size_t n, uint64_t key, float scale, hipStream_t s);

@@ -119,8 +119,6 @@ _SIGS = {
     "hy_moe_upload_layer_gguf": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint32]),
     "hy_dispatch_pairs": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]),
     "hy_dispatch_pairs_noalloc": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]),
-    "hy_probe_block_mix": (C.c_int, [C.c_int32, _u32, _u32, _vp, _vp]),
-    "hy_probe_stream": (C.c_int, [C.c_int32, _vp, C.c_uint64, _u32, _vp, _vp]),
     "hy_device_synchronize": (C.c_int, []),
     "hy_stream_create": (C.c_int, [C.POINTER(_vp)]),
     "hy_stream_destroy": (C.c_int, [_vp]),

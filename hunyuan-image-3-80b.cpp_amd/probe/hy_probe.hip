@@ -1,4 +1,5 @@
-// hy_probe.hip -- measurement probes: the grouped GEMM's per-block instruction mix
+// hy_probe.hip -- measurement probes (bench.py only; built into libhy_probe.so, not into
+// the product library libhy_moe.so): the grouped GEMM's per-block instruction mix
 // (compute only) and the HBM read rate of the decode GEMV's access pattern.
 //
 // Each wave repeats, `iters` times, exactly the math the grouped int8 GEMM issues for
@@ -15,6 +16,9 @@
 #include "hy_device.hpp"
 #include "hy_launch.hpp"
 #include "hy_lds.hpp"
+#include "hy_probe.h"
+
+#include <cstdio>
 
 namespace hy {
 
@@ -126,54 +130,6 @@ __global__ __launch_bounds__(PROBE_THREADS, 2) void block_mix_kernel(int iters, 
     out[(size_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = r;
 }
 
-// Overlap of the matrix and vector units: per iteration and wave, the MFMA work is four
-// v_mfma_i32_32x32x32_i8 on independent accumulators (chained over the iterations), the
-// vector work 64 v_fmac_f32 in 16 dependent chains.  VARIANT 5: MFMA work only; 6: vector
-// work only; 7: both in one wave; 8: both, s_setprio 1 around the MFMAs; 9: split over
-// the waves (even waves twice the MFMA work, odd waves twice the vector work); 10: the
-// split with the MFMA waves at priority 1.  If the units overlapped, 7-10 would take the
-// longer of 5 and 6; if not, their sum.
-template <int VARIANT>
-__global__ __launch_bounds__(PROBE_THREADS, 2) void overlap_kernel(int iters, int seed, float* __restrict__ out) {
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-    v4i_p A0 = {lane, seed, 3, 4}, A1 = {5, 6, seed, 7}, B = {1, 2, seed, 5};
-    v16i_p S0 = {}, S1 = {}, S2 = {}, S3 = {};
-    float acc[16], x[16];
-    for (int v = 0; v < 16; v++) {
-        acc[v] = 0.0f;
-        x[v] = 0.001f * (float)(v + lane);
-    }
-    const float y = 1.0001f + 1e-7f * (float)seed;
-    const bool split = VARIANT == 9 || VARIANT == 10;
-    const bool do_m = VARIANT == 5 || VARIANT == 7 || VARIANT == 8 || (split && (wave & 1) == 0);
-    const bool do_v = VARIANT == 6 || VARIANT == 7 || VARIANT == 8 || (split && (wave & 1) == 1);
-    const int n = split ? 2 * iters : iters;
-    if (VARIANT == 10 && do_m) __builtin_amdgcn_s_setprio(1);
-    for (int it = 0; it < n; it++) {
-        A0.x += 1;
-        if (do_m) {
-            if (VARIANT == 8) __builtin_amdgcn_s_setprio(1);
-            S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, S0, 0, 0, 0);
-            S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, S1, 0, 0, 0);
-            S2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(B, A0, S2, 0, 0, 0);
-            S3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(B, A1, S3, 0, 0, 0);
-            if (VARIANT == 8) __builtin_amdgcn_s_setprio(0);
-        }
-        if (do_v) {
-#pragma unroll
-            for (int r = 0; r < 2; r++) {
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[v] = fmaf(x[v], y, acc[v]);
-#pragma unroll
-                for (int v = 0; v < 16; v++) x[v] = fmaf(acc[v], y, x[v]);
-            }
-        }
-    }
-    float r = 0.0f;
-    for (int v = 0; v < 16; v++) r += acc[v] + x[v] + (float)(S0[v] + S1[v] + S2[v] + S3[v]);
-    out[(size_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = r;
-}
-
 // ---- read-rate probes (the decode GEMV's streams) ------------------------------
 // Variant 0: one wave per work group streams its own contiguous range with 16-byte
 // global->LDS copies into a private 3-step ring of 8 KB steps (8 copies of 1 KB per
@@ -228,9 +184,7 @@ __global__ __launch_bounds__(256) void stream_vec_kernel(const int4* __restrict_
 
 }  // namespace
 
-size_t probe_stream_step_bytes() { return STREAM_STEP; }
-
-hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s) {
+static hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s) {
     if (variant == 0 || variant == 2) {
         const uint32_t steps = (uint32_t)(bytes / ((size_t)waves * STREAM_STEP));
         if (variant == 2)
@@ -246,7 +200,7 @@ hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int w
     return hipGetLastError();
 }
 
-hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int seed, float* out, hipStream_t s) {
+static hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int seed, float* out, hipStream_t s) {
     const dim3 grid((unsigned)work_groups), blk(PROBE_THREADS);
     if (variant == 1)
         hipLaunchKernelGGL(block_mix_kernel<1>, grid, blk, 0, s, iters, seed, out);
@@ -256,21 +210,47 @@ hipError_t launch_probe_block_mix(int variant, int work_groups, int iters, int s
         hipLaunchKernelGGL(block_mix_kernel<3>, grid, blk, 0, s, iters, seed, out);
     else if (variant == 4)
         hipLaunchKernelGGL(block_mix_kernel<4>, grid, blk, 0, s, iters, seed, out);
-    else if (variant == 5)
-        hipLaunchKernelGGL(overlap_kernel<5>, grid, blk, 0, s, iters, seed, out);
-    else if (variant == 6)
-        hipLaunchKernelGGL(overlap_kernel<6>, grid, blk, 0, s, iters, seed, out);
-    else if (variant == 7)
-        hipLaunchKernelGGL(overlap_kernel<7>, grid, blk, 0, s, iters, seed, out);
-    else if (variant == 8)
-        hipLaunchKernelGGL(overlap_kernel<8>, grid, blk, 0, s, iters, seed, out);
-    else if (variant == 9)
-        hipLaunchKernelGGL(overlap_kernel<9>, grid, blk, 0, s, iters, seed, out);
-    else if (variant == 10)
-        hipLaunchKernelGGL(overlap_kernel<10>, grid, blk, 0, s, iters, seed, out);
     else
         hipLaunchKernelGGL(block_mix_kernel<0>, grid, blk, 0, s, iters, seed, out);
     return hipGetLastError();
 }
 
 }  // namespace hy
+
+// ---- C entry points (bench.py loads libhy_probe.so; nothing in libhy_moe.so calls these)
+
+static thread_local char g_probe_err[256];
+
+static int probe_fail(const char* msg) {
+    snprintf(g_probe_err, sizeof g_probe_err, "%s", msg);
+    return -1;
+}
+
+static int probe_hip(hipError_t e) {
+    if (e == hipSuccess) return 0;
+    snprintf(g_probe_err, sizeof g_probe_err, "HIP error: %s", hipGetErrorString(e));
+    return -1;
+}
+
+extern "C" {
+
+const char* hyp_last_error(void) { return g_probe_err; }
+
+int hyp_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream) {
+    if (!out_dev || work_groups == 0 || iters == 0 || variant < 0 || variant > 4)
+        return probe_fail("bad block-mix probe arguments (variant 0-4, work groups and iterations > 0)");
+    return probe_hip(hy::launch_probe_block_mix(variant, (int)work_groups, (int)iters, 3, out_dev,
+                                                static_cast<hipStream_t>(stream)));
+}
+
+int hyp_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev, void* stream) {
+    const uint64_t per = (uint64_t)waves * hy::STREAM_STEP;
+    if (!buf_dev || !out_dev || waves == 0 || variant < 0 || variant > 2 || bytes == 0 || bytes % per ||
+        (variant == 1 && waves % 4))
+        return probe_fail("bad stream probe arguments: bytes a multiple of waves x 8192, waves a multiple of 4 "
+                          "for variant 1, variant 0-2");
+    return probe_hip(hy::launch_probe_stream(variant, buf_dev, (size_t)bytes, (int)waves, out_dev,
+                                             static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

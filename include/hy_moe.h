@@ -312,30 +312,6 @@ int hy_memset(void* dst_dev, int value, size_t bytes);
  * copy engine).  Besides moving data it is the yardstick for the hardware byte
  * counters: a copy of n bytes reads n and writes n. */
 int hy_copy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
-/* Measurement only, no counterpart in the reference: a compute-only kernel that repeats
- * the grouped int8 GEMM's per-block instruction mix (two i8 MFMAs for the exact block
- * dots of two 32x32 tiles, two rank-1 f16 MFMAs for the scale products, 32 int->float
- * conversions and 32 fmas per lane) `iters` times per wave, at the GEMM's occupancy;
- * variant 1 runs only the four MFMAs, variant 2 only the 64 vector ops (plus 32 integer
- * adds that vary their operands), variant 3 the f16 alternative (each block dot from two
- * f16 32x32x16 MFMAs, exact in fp32, then the scale MFMAs and 32 fmas, no conversions;
- * the operand unpack to f16 is not counted), variant 4 variant 3 plus the unpack of the
- * shared int8 A operand to f16 (16 values per lane).  Each wave does
- * iters * 2 * 32*32*32 block-dot MACs; out_dev holds work_groups * 512 floats.
- * Variants 5-10 time whether the matrix and vector units overlap: per iteration four
- * i8 MFMAs on independent accumulators (5), 64 fmas in 16 chains (6), both in one wave
- * (7), both with the MFMAs at raised wave priority (8), the two split over alternate
- * waves at twice the iterations (9), the split with the MFMA waves at raised priority
- * (10). */
-int hy_probe_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* out_dev, void* stream);
-/* Measurement only, no counterpart in the reference: reads `bytes` of buf_dev as the
- * decode GEMV streams its weights.  Variant 0: `waves` single-wave work groups, each
- * streaming its own contiguous bytes / waves with 16-byte global->LDS copies through
- * a private 3-step ring of 8 KB steps (bytes a multiple of waves x 8192); variant 1: a
- * grid-stride 16-byte vector read by waves x 64 threads (waves a multiple of 4);
- * variant 2: variant 0 with non-temporal copies.  out_dev holds waves x 64 floats. */
-int hy_probe_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev,
-                    void* stream);
 int hy_device_synchronize(void);
 int hy_stream_create(void** stream);
 int hy_stream_destroy(void* stream);
