@@ -870,9 +870,13 @@ int hy_block_dots(int32_t wtype, const void* w, const void* x, uint32_t rows, ui
                   void* stream) {
     if (!w || !x || !out || n % 32 || rows == 0 || rows > 4096) return fail(HY_ERR_INVALID, "bad block-dot args");
     if (wtype != HY_TYPE_Q8_0 && wtype != HY_TYPE_Q4_0) return fail(HY_ERR_UNSUPPORTED, "wtype %d", wtype);
-    if (path != 0) return fail(HY_ERR_UNSUPPORTED, "path %d not built", path);
-    HIP_TRY(hy::launch_block_dots_valu(wtype, static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(x),
-                                       (int)rows, (int)(n / 32), out, static_cast<hipStream_t>(stream)));
+    if (path != 0 && path != 1) return fail(HY_ERR_INVALID, "block-dot path %d (0 = VALU, 1 = MFMA)", path);
+    auto* wb = static_cast<const uint8_t*>(w);
+    auto* xb = static_cast<const uint8_t*>(x);
+    if (path == 0)
+        HIP_TRY(hy::launch_block_dots_valu(wtype, wb, xb, (int)rows, (int)(n / 32), out, static_cast<hipStream_t>(stream)));
+    else
+        HIP_TRY(hy::launch_block_dots_mfma(wtype, wb, xb, (int)rows, (int)(n / 32), out, static_cast<hipStream_t>(stream)));
     return HY_OK;
 }
 

@@ -154,26 +154,46 @@ __device__ __forceinline__ float swiglu(float g, float u) {
     return g * (1.0f / (1.0f + hy_expf(-g))) * u;
 }
 
+// One round of a wave top-k: the lowest untaken lane (open) holding the largest value
+// m of the untaken lanes (v of taken lanes and lanes past the candidates is -inf), so
+// equal values go to the lower index (src/hunyuan_moe_full.cpp:67).  A NaN ranks below
+// every number: wave_max skips NaN operands, and once only NaNs are left (no open lane
+// equals m) the lowest open lane is taken -- an all-NaN row selects 0, 1, 2, ... as the
+// reference's insertion top-k does.  `open` must hold at least one lane.
+__device__ __forceinline__ int wave_argmax_round(float v, bool open, float& m) {
+    m = wave_max(v);
+    unsigned long long bal = __ballot(open && v == m);
+    if (bal == 0) {
+        bal = __ballot(open);
+        m = __builtin_nanf("");
+    }
+    return (int)__builtin_ctzll(bal);
+}
+
 // Top-k of one token's logits, one expert per lane (lanes >= E hold none): K rounds
-// of a wave max, the lowest lane among equal maxima (lower expert index wins ties,
-// src/hunyuan_moe_full.cpp:67), then p_k = exp(l_k - m) / sum_e exp(l_e - m) with the
-// denominator summed in the 64-lane tree, renormalised by max(sum_k p_k, 1e-8) or
-// scaled (src/hunyuan_moe_full.cpp:230-243; norm = 0 when K = 1).  Lanes k < K write
-// w_out[k], i_out[k]; p_out (optional) gets every expert's probability.
+// of wave_argmax_round (K <= E), then p_k = exp(l_k - m) / sum_e exp(l_e - m), m the
+// largest logit (NaN skipped; NaN when every logit is), with the denominator summed in
+// the 64-lane tree,
+// renormalised by max(sum_k p_k, 1e-8) or scaled (src/hunyuan_moe_full.cpp:230-243;
+// norm = 0 when K = 1).  Lanes k < K write w_out[k], i_out[k]; p_out (optional) gets
+// every expert's probability.
 __device__ __forceinline__ void topk_wave(float v_in, int E, int K, int norm, float scale, int lane,
                                           float* w_out, int* i_out, float* p_out = nullptr) {
     float v = lane < E ? v_in : -INFINITY;
     const float orig = v;
+    bool open = lane < E;
     float m0 = 0.0f;
     float selv = 0.0f;
     int seli = 0;
     for (int k = 0; k < K; k++) {
-        const float m = wave_max(v);
-        const unsigned long long bal = __ballot(v == m);
-        const int sel = (int)__builtin_ctzll(bal);
+        float m;
+        const int sel = wave_argmax_round(v, open, m);
         if (k == 0) m0 = m;
         if (lane == k) { selv = m; seli = sel; }
-        if (lane == sel) v = -INFINITY;
+        if (lane == sel) {
+            v = -INFINITY;
+            open = false;
+        }
     }
     // denominator: 64-lane tree of exp(l_e - m) (lanes >= E add 0)
     const float s = wave_sum(lane < E ? hy_expf(orig - m0) : 0.0f);

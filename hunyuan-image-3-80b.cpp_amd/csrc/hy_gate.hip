@@ -11,7 +11,10 @@ namespace hy {
 // Top-k of each row of n values, descending, equal values keep the lower index (the
 // insertion order of topk_f32).  One wave per row; lane l owns elements l, l+64, ...
 // (n <= 4096, so at most 64 per lane, tracked in a 64-bit taken mask).  k > n pads
-// with value 0 / index 0 as the reference's zero-initialised best[] does.
+// with value 0 / index 0 as the reference's zero-initialised best[] does.  A NaN ranks
+// below every number and NaNs are taken in index order (an all-NaN row gives indices
+// 0, 1, 2, ... as the reference's insertion does; where NaNs and numbers mix, the
+// reference's result depends on their positions and is not reproduced).
 __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict__ x, int rows, int n, int k,
                                                         float* __restrict__ vals, int* __restrict__ idx) {
     const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -29,10 +32,23 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
                 bi = i;
             }
         }
-        const float m = wave_max(bv);
+        float m = wave_max(bv);
         int cand = bv == m ? bi : 0x7fffffff;
 #pragma unroll
         for (int s = 32; s >= 1; s >>= 1) cand = min(cand, __shfl_xor(cand, s, WAVE));
+        if (cand == 0x7fffffff && r < n) {
+            // only NaNs are left (they rank below every number): the lowest untaken index
+            int low = 0x7fffffff;
+            for (int j = 0, i = lane; i < n; j++, i += WAVE)
+                if (!((taken >> j) & 1ull)) {
+                    low = i;
+                    break;
+                }
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) low = min(low, __shfl_xor(low, s, WAVE));
+            cand = low;
+            m = xr[cand];
+        }
         if (cand == 0x7fffffff) {  // fewer than k values
             if (lane == 0) {
                 vals[(size_t)row * k + r] = 0.0f;

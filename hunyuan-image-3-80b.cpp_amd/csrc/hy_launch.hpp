@@ -88,6 +88,9 @@ hipError_t launch_combine(const Routing& R, const float* y, int T, int H, int K,
                           float* out, hipStream_t s);
 hipError_t launch_block_dots_valu(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
                                   hipStream_t s);
+// the same dots through the grouped GEMM's LDS operand layout and block-dot MFMAs
+hipError_t launch_block_dots_mfma(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
+                                  hipStream_t s);
 
 // expert products, MFMA path (hy_mfma.hip)
 bool mfma_path_ok(int wtype, int H, int I);

@@ -104,6 +104,9 @@ __device__ __forceinline__ void pin_f32(float& v) { asm volatile("" : "+v"(v)); 
 // wait for the ds_reads whose results are passed in: the values are threaded through
 // the asm so no consumer can be scheduled ahead of the wait
 __device__ __forceinline__ void lds_wait(v4i_t& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
+}
 __device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, uint32_t& c) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
 }

@@ -113,6 +113,32 @@ __device__ __forceinline__ void unpack_q4(const int4 w, int4& lo, int4& hi) {
     hi = make_int4(cv((w.x >> 4) & m), cv((w.y >> 4) & m), cv((w.z >> 4) & m), cv((w.w >> 4) & m));
 }
 
+// Byte offset, inside a 32-byte operand row, of the row's 16-byte half h: the halves
+// are swapped when bit 3 of the row is set (conflict-free MFMA operand reads).
+__device__ __forceinline__ int swz_half(int row, int h) { return 16 * (h ^ ((row >> 3) & 1)); }
+
+// Offset, inside a 32-row operand tile of 32-byte rows, of the 16 bytes MFMA lane
+// (lr = l % 32, lg = l / 32) reads: row lr, half lg.
+__device__ __forceinline__ int operand_lane_off(int lr, int lg) { return lr * 32 + swz_half(lr, lg); }
+
+// Q4_0 stage unpack of one chunk row: the 16 nibble bytes of row r (LDS, at nib) to
+// the 32 int8 values n - 8 of operand row r of the chunk at dst, swizzled.
+__device__ __forceinline__ void unpack_q4_row(const void* nib, int8_t* dst, int r) {
+    v4i_t wv4 = lds_b128(nib);
+    lds_wait(wv4);
+    int4 lo, hi;
+    unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
+    lds_st128(dst + r * 32 + swz_half(r, 0), v4i_t{lo.x, lo.y, lo.z, lo.w});
+    lds_st128(dst + r * 32 + swz_half(r, 1), v4i_t{hi.x, hi.y, hi.z, hi.w});
+}
+
+// The exact int32 dots of one 32-wide GGUF block over a 32x32 tile (K = 32 is one
+// block): v_mfma_i32_32x32x32_i8 with a zero accumulator.
+__device__ __forceinline__ v16i_t block_dot_tile(v4i_t A, v4i_t B) {
+    const v16i_t zero = {};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, zero, 0, 0, 0);
+}
+
 // Per-block scale products c[row][tok] = d_w[row] * d_x[tok] for a 32x32 tile from one
 // f16 MFMA: A holds d_w in k-slot 0 of lane group 0, B holds d_x in the same slot,
 // every other slot is zero.  The product of two fp16 values is exact in fp32, so c
@@ -214,13 +240,13 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
         const int bt = (wave / MM_KB) * TPW + (p % SH::B_LANES) / 2;  // in range for masked lanes too
-        const int hb = (p & 1) ^ ((bt >> 3) & 1);
-        b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (wave % MM_KB) * 32 + hb * 16;
+        b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (wave % MM_KB) * 32 +
+                   swz_half(bt, p & 1);
     }
     // A rows (int8): copy lane l lands at +16 l (row l / 2 of a 32-row piece, position
     // l % 2) and fetches half (l % 2) ^ (bit 3 of the row); Q4_0 nibbles are copied as
     // they are and swizzled when unpacked
-    const uint32_t a_sw = 16u * (uint32_t)(lane ^ ((lane >> 4) & 1));
+    const uint32_t a_sw = (uint32_t)((lane / 2) * 32 + swz_half(lane / 2, lane & 1));
     // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each: KB = 4 as one
     // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces
     constexpr int BS_LANES = MM_KB == 4 ? MM_TOK / MM_WAVES : MM_TOK / MM_WAVES * MM_KB;
@@ -285,9 +311,8 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     //   B row (token) nq*32+lr of the block, half lg (swizzled)
     //   rank-1 scale operands: lanes of the lower half read d_w of rows lr / 32+lr and
     //   d_x of token nq*32+lr; lanes of the upper half read zeros
-    const int hsw = lg ^ ((lr >> 3) & 1);
-    const uint32_t a_lane = (uint32_t)((Q4 ? 0 : OFF_A) + sl * MM_KB * 2048 + lr * 32 + 16 * hsw);
-    const uint32_t b_lane = (uint32_t)(OFF_B + (nq * 32 * TT + lr) * 32 + 16 * hsw);
+    const uint32_t a_lane = (uint32_t)((Q4 ? 0 : OFF_A) + sl * MM_KB * 2048 + operand_lane_off(lr, lg));
+    const uint32_t b_lane = (uint32_t)(OFF_B + nq * 32 * TT * 32 + operand_lane_off(lr, lg));
     const uint32_t sw_lane = (uint32_t)(lg == 0 ? OFF_AS + sl * MM_KB * 128 + lr * 2 : OFF_Z);
     const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 * TT + lr) * MM_KB * 4 : OFF_Z);
     const uint32_t ring0 = lds_off(ring[0]);
@@ -313,13 +338,12 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         } else {
             lds_wait(A0, A1, B, dw0, dw1, dxb);
         }
-        const v16i_t zero = {};
         // the block's MFMAs issue at raised wave priority, so a wave whose operands are
         // ready reaches the matrix unit ahead of the other waves' rescale (c5 ffn_up
         // -2 %, c4 -3 %, c2 -4 %; ffn_down -2 % with the 2 x 2 tiles, nothing with 2 x 1)
         __builtin_amdgcn_s_setprio(1);
-        const v16i_t S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
-        const v16i_t S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
+        const v16i_t S0 = block_dot_tile(A0, B);
+        const v16i_t S1 = block_dot_tile(A1, B);
         // the upper lanes read zeros; d_x is an fp16 value stored as f32, so the
         // truncating pack is exact
         xa0[0] = (int)dw0;
@@ -339,8 +363,8 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         if constexpr (TT == 2) {
             // the second 32 tokens: same A operands and weight scales
             __builtin_amdgcn_s_setprio(1);
-            const v16i_t S2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, zero, 0, 0, 0);
-            const v16i_t S3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, zero, 0, 0, 0);
+            const v16i_t S2 = block_dot_tile(A0, B1);
+            const v16i_t S3 = block_dot_tile(A1, B1);
             xb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, dxb1), 0.0f));
             const v16f_t C2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, xa0),
                                                                      __builtin_bit_cast(v8h_t, xb), zf, 0, 0, 0);
@@ -378,13 +402,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
             // chunk t/64 (CHUNKS x 64 rows <= MM_THREADS)
             if (tid < SH::CHUNKS * 64) {
                 const int c = tid >> 6, r = tid & 63;
-                v4i_t wv4 = lds_b128(ring[0] + soff + OFF_A + c * 1024 + r * 16);
-                lds_wait(wv4);
-                int4 lo, hi;
-                unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
-                const int sw = 16 * ((r >> 3) & 1);
-                lds_st128(aun + c * 2048 + r * 32 + sw, v4i_t{lo.x, lo.y, lo.z, lo.w});
-                lds_st128(aun + c * 2048 + r * 32 + (16 ^ sw), v4i_t{hi.x, hi.y, hi.z, hi.w});
+                unpack_q4_row(ring[0] + soff + OFF_A + c * 1024 + r * 16, aun + c * 2048, r);
                 lds_wait();
             }
             __builtin_amdgcn_s_barrier();
@@ -457,6 +475,77 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     const int j0 = nq * 32 * TT + lr;  // pair index within the tile
     epilogue(acc0, acc1, j0);
     if constexpr (TT == 2) epilogue(acc2, acc3, j0 + 32);
+}
+
+// Per-block int32 dots through the grouped GEMM's own operand path (hy_block_dots
+// path 1), one wave per (64-row group, block).  The wave stages the block's 64 weight
+// rows in the GEMM's LDS operand layout -- Q8_0 as swizzled 32-byte rows; Q4_0 as the
+// raw 16-byte nibble rows, then the GEMM's stage unpack (unpack_q4_row) -- and the
+// activation block into all 32 token rows of a B tile with the same swizzle, reads its
+// A0 / A1 / B operands at the GEMM's lane offsets (operand_lane_off) and issues the
+// GEMM's two block-dot MFMAs (block_dot_tile).  Every entry of the two 32x32 results
+// is the dot of its weight row with the replicated activation block; the one written
+// for (row r, block b) sits in column (r + b) % 32, so that over the rows and blocks
+// every lane and every result register of both tiles is read out.  Rows past `rows`
+// stage zeros and write nothing.
+template <int WT>
+__global__ __launch_bounds__(WAVE) void block_dots_mfma_kernel(const uint8_t* __restrict__ w,
+                                                               const uint8_t* __restrict__ x, int rows, int nb,
+                                                               int* __restrict__ out) {
+    constexpr bool Q4 = WT == HY_TYPE_Q4_0;
+    constexpr int BB = Q4 ? 18 : 34;  // GGUF block bytes (fp16 scale + quants)
+    __shared__ __align__(16) int8_t a_s[64 * 32];
+    __shared__ __align__(16) uint8_t nib_s[Q4 ? 64 * 16 : 16];
+    __shared__ __align__(16) int8_t b_s[32 * 32];
+    const int g = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const int r = g * 64 + lane;  // weight row this lane stages
+    // GGUF blocks are only 2-byte aligned: assemble the dwords bytewise
+    auto dw4 = [](const uint8_t* p) {
+        int v[4];
+        for (int i = 0; i < 4; i++)
+            v[i] = (int)((uint32_t)p[4 * i] | ((uint32_t)p[4 * i + 1] << 8) | ((uint32_t)p[4 * i + 2] << 16) |
+                         ((uint32_t)p[4 * i + 3] << 24));
+        return v4i_t{v[0], v[1], v[2], v[3]};
+    };
+    const v4i_t zero4 = {0, 0, 0, 0};
+    const uint8_t* wq = w + ((size_t)(r < rows ? r : 0) * nb + b) * BB + 2;
+    if constexpr (Q4) {
+        lds_st128(nib_s + lane * 16, r < rows ? dw4(wq) : zero4);
+        lds_wait();
+        __syncthreads();
+        unpack_q4_row(nib_s + lane * 16, a_s, lane);
+    } else {
+        lds_st128(a_s + lane * 32 + swz_half(lane, 0), r < rows ? dw4(wq) : zero4);
+        lds_st128(a_s + lane * 32 + swz_half(lane, 1), r < rows ? dw4(wq + 16) : zero4);
+    }
+    // B: every token row holds activation block b; lane l writes half l / 32 of row l % 32
+    const int lr = lane % 32, lg = lane / 32;
+    lds_st128(b_s + lr * 32 + swz_half(lr, lg), dw4(x + (size_t)b * 34 + 2 + 16 * lg));
+    lds_wait();
+    __syncthreads();
+    const int off = operand_lane_off(lr, lg);
+    v4i_t A0 = lds_b128(a_s + off), A1 = lds_b128(a_s + 1024 + off), B = lds_b128(b_s + off);
+    lds_wait(A0, A1, B);
+    const v16i_t S0 = block_dot_tile(A0, B), S1 = block_dot_tile(A1, B);
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int i = 8 * (v / 4) + 4 * lg + v % 4;  // tile row of result register v
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rr = g * 64 + 32 * t + i;
+            if (rr < rows && lr == (rr + b) % 32) out[(size_t)rr * nb + b] = t ? S1[v] : S0[v];
+        }
+    }
+}
+
+hipError_t launch_block_dots_mfma(int wtype, const uint8_t* w, const uint8_t* x, int rows, int nb, int* out,
+                                  hipStream_t s) {
+    const dim3 grid((unsigned)((rows + 63) / 64), (unsigned)nb);
+    if (wtype == HY_TYPE_Q4_0)
+        hipLaunchKernelGGL(block_dots_mfma_kernel<HY_TYPE_Q4_0>, grid, dim3(WAVE), 0, s, w, x, rows, nb, out);
+    else
+        hipLaunchKernelGGL(block_dots_mfma_kernel<HY_TYPE_Q8_0>, grid, dim3(WAVE), 0, s, w, x, rows, nb, out);
+    return hipGetLastError();
 }
 
 template <int MODE, class SH>

@@ -55,18 +55,22 @@ __device__ __forceinline__ void topk_groups_wave(float v_in, int E, int K, int n
     const int kept = __shfl(keep_g, grouped ? my_g : 0, WAVE);
     if (grouped && !kept) p = 0.0f;
     if (p_out && lane < E) p_out[lane] = p;
-    // top K of the masked probabilities (p >= 0 > -inf, so K <= E rounds always find one)
+    // top K of the masked probabilities (K <= E open lanes; NaN ranks lowest)
     float v = lane < E ? p : -INFINITY;
+    bool open = lane < E;
     float selv = 0.0f;
     int seli = 0;
     for (int k = 0; k < K; k++) {
-        const float m = wave_max(v);
-        const int sel = (int)__builtin_ctzll(__ballot(v == m));
+        float m;
+        const int sel = wave_argmax_round(v, open, m);
         if (lane == k) {
             selv = m;
             seli = sel;
         }
-        if (lane == sel) v = -INFINITY;
+        if (lane == sel) {
+            v = -INFINITY;
+            open = false;
+        }
     }
     float ps = 0.0f;
     for (int k = 0; k < K; k++) ps += __shfl(selv, k, WAVE);

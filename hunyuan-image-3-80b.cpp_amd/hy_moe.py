@@ -92,6 +92,7 @@ _SIGS = {
     "hy_moe_set_path": (C.c_int, [_vp, _i32]),
     "hy_router_topk": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _i32, _f, _vp, _vp, _vp, _vp]),
     "hy_topkgating_easy": (C.c_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "hy_topk_rows": (C.c_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "hy_route_logits_groups": (C.c_int, [_vp, _u32, _u32, _u32, _i32, _f, _u32, _u32, _vp, _vp, _vp, _vp]),
     "hy_aux_loss": (C.c_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "hy_moe_last_gate": (C.c_int, [_vp, C.POINTER(_f), C.POINTER(_u32), C.POINTER(_f)]),
@@ -406,6 +407,16 @@ def topkgating_easy(logits, K):
     w, idx = Buf.empty((T, K)), Buf.empty((T, K), np.int32)
     check(lib().hy_topkgating_easy(lb.ptr, T, E, K, w.ptr, idx.ptr, None))
     return w.numpy(), idx.numpy()
+
+
+def topk_rows(x, k):
+    """topk_f32 over each row: values and indices [rows][k]."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    xb = Buf.from_array(x)
+    v, i = Buf.empty((rows, k)), Buf.empty((rows, k), np.int32)
+    check(lib().hy_topk_rows(xb.ptr, rows, n, k, v.ptr, i.ptr, None))
+    return v.numpy(), i.numpy()
 
 
 def route_logits_groups(logits, K, norm=1, scale=1.0, n_group=0, topk_group=0):

@@ -250,8 +250,12 @@ int hy_dequantize(int32_t type, const void* blocks_dev, size_t n, float* out_dev
 
 /* Exact per-32-block int32 dots of weight blocks (Q8_0 or Q4_0 rows) with Q8_0
  * activation blocks, computed by the device dot routines the expert kernels use:
- * out[r][b] = sum_j w[r][b][j] * x[b][j].  `path` 0 = VALU dot4 routine, 1 = MFMA tile
- * routine.  rows <= 4096. */
+ * out[r][b] = sum_j w[r][b][j] * x[b][j].  `path` 0 = the decode GEMV's VALU dot4
+ * routine; 1 = the grouped GEMM's operand path: the weight rows staged in its LDS layout
+ * (Q4_0 through its stage unpack), the activation block in a swizzled B tile, and its
+ * v_mfma_i32_32x32x32_i8 block-dot tiles.  rows <= 4096.  No counterpart in the
+ * reference (ggml's vec_dot block sums, the per-block part of src/hunyuan_gguf_loader.cpp:
+ * 10-72's formats). */
 int hy_block_dots(int32_t wtype, const void* w_blocks_dev, const void* x_blocks_dev, uint32_t rows,
                   uint32_t n, int32_t path, int32_t* out_dev, void* stream);
 

@@ -802,21 +802,42 @@ void hyo_router_logits_blocked(const float* x, const float* wr, uint32_t T, uint
 /* One token's routing.  Default: top-K on the logits.  Group-limited greedy
  * (n_group > 0 and topk_group > 0): src/hunyuan_moe_full.cpp:135-178 step by step on
  * the q probabilities.  probs (may be NULL) receives the (masked) probabilities. */
+/* q-semantics selection (the GPU's wave_argmax_round): k rounds of the largest
+ * untaken value, equal values to the lower index; a NaN ranks below every number and
+ * NaNs are taken in index order, so an all-NaN row selects 0..k-1 as the reference's
+ * insertion top-k does.  For rows without NaN this is topk_f32
+ * (src/hunyuan_moe_full.cpp:56-82) exactly.  n <= 64. */
+void hyo_select_q(const float* x, uint32_t n, uint32_t k, float* vals, int32_t* idx) {
+    uint8_t taken[64] = {0};
+    for (uint32_t r = 0; r < k; r++) {
+        int best = -1;
+        for (uint32_t i = 0; i < n; i++) {
+            if (taken[i] || x[i] != x[i]) continue;
+            if (best < 0 || x[i] > x[best]) best = (int)i;
+        }
+        if (best < 0)
+            for (uint32_t i = 0; i < n; i++)
+                if (!taken[i]) { best = (int)i; break; }
+        taken[best] = 1;
+        vals[r] = x[best];
+        idx[r] = best;
+    }
+}
+
 static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, float scale, uint32_t n_group,
                           uint32_t topk_group, float* w, int32_t* idx, float* probs) {
     /* norm 1 renormalises only when K > 1 (src/hunyuan_moe_full.cpp:230, the rule of
      * topkgating_full and so of moe_forward_full); norm 2 at every K
      * (src/attention.cpp:268-275, moe_forward_cpu; topkgating_easy :104-108) */
     const int rn = norm == 2 || (norm != 0 && K > 1);
-    float m = l[0]; /* the largest logit */
-    for (uint32_t e = 1; e < E; e++)
-        if (l[e] > m) m = l[e];
+    float m = l[0]; /* the largest logit (NaN skipped; NaN when every logit is) */
+    for (uint32_t e = 1; e < E; e++) m = fmaxf(m, l[e]);
     float ex[64];
     for (uint32_t e = 0; e < E; e++) ex[e] = hyo_expf(l[e] - m);
     const float s = hyo_tree_sum64(ex, E);
     float v[64], ps = 0.0f;
     if (n_group == 0 || topk_group == 0) {
-        hyo_topk_f32(l, E, K, v, idx); /* selection on logits, ties -> lower index */
+        hyo_select_q(l, E, K, v, idx); /* selection on logits, ties -> lower index */
         float p[64];
         for (uint32_t k = 0; k < K; k++) {
             p[k] = hyo_expf(l[idx[k]] - m) / s;
@@ -851,7 +872,7 @@ static void hyo_route_one(const float* l, uint32_t E, uint32_t K, int norm, floa
                 for (uint32_t j = 0; j < gs; j++) p[g * gs + j] = 0.0f;
     }
     /* top-K of the masked probabilities (:168-178), weights from them (:229-243) */
-    hyo_topk_f32(p, E, K, v, idx);
+    hyo_select_q(p, E, K, v, idx);
     for (uint32_t k = 0; k < K; k++) ps += v[k];
     if (ps < 1e-8f) ps = 1e-8f;
     for (uint32_t k = 0; k < K; k++) w[k] = rn ? v[k] / ps : v[k] * scale;

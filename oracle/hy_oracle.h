@@ -150,6 +150,9 @@ void hyo_router_logits_blocked(const float* x, const float* wr, uint32_t T, uint
  * multiplied by scale.  norm 1 renormalises only when K > 1 (topkgating_full,
  * src/hunyuan_moe_full.cpp:230), norm 2 at every K (moe_forward_cpu,
  * src/attention.cpp:268-275), norm 0 never. */
+/* q-semantics top-k selection (NaN ranks below every number, NaNs in index order;
+ * topk_f32 for rows without NaN), n <= 64 */
+void hyo_select_q(const float* x, uint32_t n, uint32_t k, float* vals, int32_t* idx);
 void hyo_route_topk(const float* logits, uint32_t T, uint32_t E, uint32_t K, int norm,
                     float scale, float* w, int32_t* idx);
 /* The same with group-limited greedy (src/hunyuan_moe_full.cpp:135-166) when n_group > 0

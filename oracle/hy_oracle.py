@@ -114,6 +114,7 @@ def lib():
             "hyo_moe_stack_q": (C.c_int, [C.POINTER(QLayer), C.c_uint32, _fp, C.c_uint32, C.c_float, _fp, C.c_int]),
             "hyo_moe_stack_qw": (C.c_int, [C.POINTER(QLayer), C.POINTER(_fp), C.c_uint32, _fp, C.c_uint32,
                                            C.c_float, _fp, C.c_int]),
+            "hyo_select_q": (None, [_fp, C.c_uint32, C.c_uint32, _fp, _ip]),
             "hyo_rms_norm_blocked_rows": (None, [_fp, _fp, _fp, C.c_uint32, C.c_uint32, C.c_float]),
             "hyo_free": (None, [_vp]),
         }

@@ -70,24 +70,66 @@ def test_dequantize_bit_exact(gpu, wtype):
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
-def test_block_dots_exact(gpu, wtype):
-    rng = np.random.default_rng(2)
-    rows, n = 33, 4096
+def brute_block_dots(wtype, w, x, rows, n):
+    """int64 brute force from the raw GGUF bytes: Q8_0 int8 quants; Q4_0 element j in
+    the low nibble of byte j, element j + 16 in the high nibble, value nibble - 8."""
+    nb = n // 32
+    xq = x.reshape(nb, 34)[:, 2:].view(np.int8).astype(np.int64)                  # [nb, 32]
+    if wtype == O.Q8_0:
+        wq = w.reshape(rows, nb, 34)[:, :, 2:].view(np.int8).astype(np.int64)     # [rows, nb, 32]
+    else:
+        nib = w.reshape(rows, nb, 18)[:, :, 2:].astype(np.int64)                  # [rows, nb, 16]
+        wq = np.concatenate([nib & 0xF, nib >> 4], axis=2) - 8
+    return np.einsum("rbj,bj->rb", wq, xq)
+
+
+@pytest.mark.parametrize("path", [0, 1])
+@pytest.mark.parametrize("wtype,rows", [(O.Q8_0, 33), (O.Q4_0, 33), (O.Q8_0, 200), (O.Q4_0, 130)])
+def test_block_dots_exact(gpu, wtype, rows, path):
+    """Per-block int32 dots of the decode GEMV's VALU routine (path 0) and of the grouped
+    GEMM's MFMA operand path (path 1) against int64 brute force.  Extremes: Q8_0
+    weights over the full int8 range including -128 and whole blocks of -128 and 127,
+    an activation block of -128 and one of 127; Q4_0 blocks of nibble 0x0 (-8) and 0xF
+    (7).  Row counts that are not multiples of 64 cover the MFMA path's partial row
+    group."""
+    rng = np.random.default_rng(2 + rows)
+    n = 4096
+    nb = n // 32
     w = O.quantize(rng.standard_normal((rows, n)).astype(np.float32), wtype)
     if wtype == O.Q8_0:   # full int8 range incl. -128
-        wq = w.reshape(rows, n // 32, 34)
+        wq = w.reshape(rows, nb, 34)
         wq[:, :, 2:] = rng.integers(0, 256, size=wq[:, :, 2:].shape, dtype=np.uint8)
-        w = wq.reshape(rows, -1)
+        wq[0, 1, 2:] = np.uint8(0x80)
+        wq[rows - 1, 2, 2:] = np.uint8(0x7F)
+    else:
+        wq = w.reshape(rows, nb, 18)
+        wq[0, 0, 2:] = np.uint8(0x00)
+        wq[rows - 1, 1, 2:] = np.uint8(0xFF)
+        wq[rows // 2, 0:nb:2, 2:] = np.uint8(0x0F)     # low nibbles 0xF, high 0x0
+    w = wq.reshape(rows, -1)
     x = O.quantize(rng.standard_normal((1, n)).astype(np.float32), O.Q8_0)
-    xb = x.reshape(n // 32, 34)
+    xb = x.reshape(nb, 34)
     xb[0, 2:] = np.uint8(0x80)            # a block of -128
-    got = gpu.block_dots(wtype, w, x, rows, n, path=0)
+    xb[1, 2:] = np.uint8(0x7F)            # a block of 127
+    got = gpu.block_dots(wtype, w, x, rows, n, path=path)
+    ref = brute_block_dots(wtype, w, x, rows, n)
+    assert np.abs(ref).max() <= 32 * 128 * 128
+    np.testing.assert_array_equal(got.astype(np.int64), ref)
+    if wtype == O.Q8_0:   # a block of -128 against a block of 127
+        assert got[0, 1] == 32 * -128 * 127
+    else:                 # nibbles 0xF (7) against a block of 127
+        assert got[rows - 1, 1] == 32 * 7 * 127
+    # the oracle's block dots agree too
     f = O.lib().hyo_block_dots_q8_0_q8_0 if wtype == O.Q8_0 else O.lib().hyo_block_dots_q4_0_q8_0
-    for r in range(rows):
-        ref = np.zeros(n // 32, np.int32)
-        f(O.vp(np.ascontiguousarray(w[r])), O.vp(x), n, O.ip(ref))
-        np.testing.assert_array_equal(got[r], ref)
+    for r in (0, rows // 2, rows - 1):
+        o = np.zeros(nb, np.int32)
+        f(O.vp(np.ascontiguousarray(w[r])), O.vp(x), n, O.ip(o))
+        np.testing.assert_array_equal(got[r], o)
+
+
+def test_block_dots_rejects_bad_path(gpu):
+    with pytest.raises(gpu.HyError):
+        gpu.block_dots(O.Q8_0, np.zeros((1, 34), np.uint8), np.zeros((1, 34), np.uint8), 1, 32, path=2)
 
 
 # ------------------------------------------------------------------ routing

@@ -213,3 +213,67 @@ def test_random_configs_layer(gpu):
         assert rate == np.float32(keep.sum()) / np.float32(T * K), what
         assert aux == (O.aux_loss_q(probs, ridx) if kw.get("compute_aux_loss") else 0.0), what
         m.close()
+
+
+# ------------------------------------------------------------------ NaN logits
+
+def assert_weights(w, rw):
+    """Weights equal bit for bit where the oracle's are numbers, NaN where its are."""
+    np.testing.assert_array_equal(np.isnan(w), np.isnan(rw))
+    ok = ~np.isnan(rw)
+    np.testing.assert_array_equal(w[ok].view(np.uint32), rw[ok].view(np.uint32))
+
+
+@pytest.mark.parametrize("E,K", [(64, 8), (16, 4), (64, 64)])
+def test_nan_and_infinite_logits(gpu, E, K):
+    """Selection with NaN and infinite logits: an all-NaN row selects experts 0..K-1
+    (the reference's insertion order for NaN), numbers rank above NaN, -inf ties go to
+    the lower index; every index stays in [0, E) and distinct.  Default and grouped
+    selection against the oracle."""
+    rng = np.random.default_rng(E + K)
+    T = 6
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[1] = np.nan
+    lg[3, ::3] = np.nan
+    lg[4] = -np.inf
+    lg[4, 5] = 0.0
+    lg[5, 2] = np.inf
+    w, idx, _ = gpu.route_logits_groups(lg, K)
+    rw, ridx = O.route_topk(lg, K)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_array_equal(idx[1], np.arange(K))
+    assert all(len(set(r)) == K for r in idx.tolist()) and idx.min() >= 0 and idx.max() < E
+    assert_weights(w, rw)
+    if E % 4 == 0:
+        w, idx, p = gpu.route_logits_groups(lg, K, n_group=4, topk_group=2)
+        rw, ridx, rp = O.route_topk_groups(lg, K, n_group=4, topk_group=2)
+        np.testing.assert_array_equal(idx, ridx)
+        assert_weights(w, rw)
+        assert_weights(p, rp)
+    vals, ti = gpu.topk_rows(lg, K)
+    np.testing.assert_array_equal(ti[1], np.arange(K))
+    assert np.isnan(vals[1]).all()
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_nan_token_in_layer(gpu, T):
+    """A token whose activations are NaN routes to experts 0..K-1 and gets a NaN
+    output row; the other tokens are bit-exact against the oracle (one-token routing
+    inside the gate/up launch, the decode routing pass, the grouped GEMM)."""
+    E, K = 64, 8
+    layer = O.synth_layer(H, I, E, K, O.Q8_0, seed=130, std=0.05)
+    m = gpu.Moe(H, I, E, K, O.Q8_0, max_tokens=64)
+    m.upload(0, layer)
+    x = O.synth(131, 0, O.T_X, 0, (T, H), 1.0)
+    bad = T // 2
+    xn = x.copy()
+    xn[bad] = np.nan
+    out, lg, w, idx = m.run(0, xn, debug=True)
+    np.testing.assert_array_equal(idx[bad], np.arange(K))
+    assert np.isnan(out[bad]).all()
+    rest = [t for t in range(T) if t != bad]
+    if rest:
+        ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+        np.testing.assert_array_equal(idx[rest], ridx[rest])
+        assert_exact(out[rest], ref[rest], f"T={T} rows beside the NaN token")
+    m.close()

@@ -246,3 +246,65 @@ def test_random_configs_vs_reference_semantics(oracle):
                                        err_msg=what)
         if kw.get("compute_aux_loss"):
             np.testing.assert_allclose(O.aux_loss_q(probs, idx), g["aux"], rtol=2e-5, err_msg=what)
+
+
+# ------------------------------------------------------------------ NaN logits
+
+def select_q(x, k):
+    x = O.f32(x)
+    v = np.empty(k, np.float32)
+    i = np.empty(k, np.int32)
+    O.lib().hyo_select_q(O.fp(x), x.size, k, O.fp(v), O.ip(i))
+    return v, i
+
+
+def test_select_q_is_topk_f32_without_nan(oracle):
+    """Rows without NaN (with ties and infinities): the q selection equals the
+    reference's insertion top-k (src/hunyuan_moe_full.cpp:56-82) exactly."""
+    rng = np.random.default_rng(11)
+    for trial in range(400):
+        n = int(rng.integers(1, 65))
+        k = int(rng.integers(1, n + 1))
+        x = rng.integers(-4, 5, n).astype(np.float32)          # many ties
+        if trial % 3 == 0:
+            x[rng.integers(0, n, 2)] = -np.inf
+        if trial % 5 == 0:
+            x[rng.integers(0, n)] = np.inf
+        v, i = select_q(x, k)
+        rv = np.empty(k, np.float32)
+        ri = np.empty(k, np.int32)
+        O.lib().hyo_topk_f32(O.fp(x), n, k, O.fp(rv), O.ip(ri))
+        np.testing.assert_array_equal(i, ri)
+        np.testing.assert_array_equal(v, rv)
+
+
+def test_select_q_nan_rows(oracle):
+    """An all-NaN row selects 0..k-1 (the reference's insertion order for NaN); in a
+    mixed row every number ranks above every NaN and NaNs follow in index order."""
+    v, i = select_q(np.full(64, np.nan, np.float32), 8)
+    np.testing.assert_array_equal(i, np.arange(8))
+    assert np.isnan(v).all()
+    rv = np.empty(8, np.float32)
+    ri = np.empty(8, np.int32)
+    O.lib().hyo_topk_f32(O.fp(np.full(64, np.nan, np.float32)), 64, 8, O.fp(rv), O.ip(ri))
+    np.testing.assert_array_equal(ri, np.arange(8))
+    x = np.array([np.nan, 5, np.nan, 3, -np.inf, np.nan, 5], np.float32)
+    v, i = select_q(x, 6)
+    np.testing.assert_array_equal(i, [1, 6, 3, 4, 0, 2])
+    np.testing.assert_array_equal(v[:4], [5, 5, 3, -np.inf])
+    assert np.isnan(v[4:]).all()
+
+
+def test_route_q_nan_row(oracle):
+    """The q routing of a token whose logits are all NaN: experts 0..K-1, NaN weights;
+    the other tokens of the batch are unaffected."""
+    rng = np.random.default_rng(3)
+    lg = rng.standard_normal((4, 16)).astype(np.float32)
+    ref_w, ref_i = O.route_topk(lg, 4)
+    lg[2] = np.nan
+    w, i = O.route_topk(lg, 4)
+    np.testing.assert_array_equal(i[2], np.arange(4))
+    assert np.isnan(w[2]).all()
+    keep = [0, 1, 3]
+    np.testing.assert_array_equal(i[keep], ref_i[keep])
+    np.testing.assert_array_equal(w[keep], ref_w[keep])
