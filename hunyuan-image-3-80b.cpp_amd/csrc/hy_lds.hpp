@@ -86,6 +86,9 @@ __device__ __forceinline__ uint32_t lds_b32(const void* p) {
 __device__ __forceinline__ void lds_st128(void* p, v4i_t v) {
     asm volatile("ds_write_b128 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
 }
+__device__ __forceinline__ void lds_st128_at(uint32_t off, v4i_t v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(off), "v"(v) : "memory");
+}
 __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // wait until at most N of this wave's LDS reads are outstanding (they complete in
 // order); pin each consumed result afterwards (lds_pin)

@@ -121,15 +121,20 @@ __device__ __forceinline__ int swz_half(int row, int h) { return 16 * (h ^ ((row
 // (lr = l % 32, lg = l / 32) reads: row lr, half lg.
 __device__ __forceinline__ int operand_lane_off(int lr, int lg) { return lr * 32 + swz_half(lr, lg); }
 
-// Q4_0 stage unpack of one chunk row: the 16 nibble bytes of row r (LDS, at nib) to
-// the 32 int8 values n - 8 of operand row r of the chunk at dst, swizzled.
-__device__ __forceinline__ void unpack_q4_row(const void* nib, int8_t* dst, int r) {
-    v4i_t wv4 = lds_b128(nib);
+// Q4_0 stage unpack of one chunk row r: the 16 nibble bytes at LDS offset nib to the
+// 32 int8 values n - 8 of operand row r, whose two swizzled halves sit at LDS offsets
+// dst_row + swz_half(r, 0) (elements 0-15) and dst_row + swz_half(r, 1) (16-31).
+__device__ __forceinline__ void unpack_q4_row_at(uint32_t nib, uint32_t dst_lo, uint32_t dst_hi) {
+    v4i_t wv4 = lds_b128_at<0>(nib);
     lds_wait(wv4);
     int4 lo, hi;
     unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
-    lds_st128(dst + r * 32 + swz_half(r, 0), v4i_t{lo.x, lo.y, lo.z, lo.w});
-    lds_st128(dst + r * 32 + swz_half(r, 1), v4i_t{hi.x, hi.y, hi.z, hi.w});
+    lds_st128_at(dst_lo, v4i_t{lo.x, lo.y, lo.z, lo.w});
+    lds_st128_at(dst_hi, v4i_t{hi.x, hi.y, hi.z, hi.w});
+}
+__device__ __forceinline__ void unpack_q4_row(const void* nib, int8_t* dst, int r) {
+    const uint32_t row = lds_off(dst) + (uint32_t)(r * 32);
+    unpack_q4_row_at(lds_off(nib), row + swz_half(r, 0), row + swz_half(r, 1));
 }
 
 // The exact int32 dots of one 32-wide GGUF block over a 32x32 tile (K = 32 is one
@@ -164,7 +169,12 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     constexpr int ZBYTES = 512;
     constexpr int STAGE = SH::ST_A * (Q4 ? 0 : 1) + (Q4 ? SH::ST_AR : 0) + SH::ST_B + SH::ST_AS + SH::ST_BS + ZBYTES;
     __shared__ __align__(16) uint8_t ring[MM_RING][STAGE];
-    __shared__ __align__(16) int8_t aun[Q4 ? SH::ST_A : 16];  // Q4_0: unpacked A of the current stage
+    // Q4_0: the unpacked int8 A of a stage, double-buffered (stage s in aun[s & 1])
+    __shared__ __align__(16) int8_t aun[Q4 ? 2 : 1][Q4 ? SH::ST_A : 16];
+    static_assert(!Q4 || (SH::WPC == 1 && SH::CHUNKS * 64 == SH::THREADS),
+                  "Q4_0: each wave copies whole nibble chunks and unpacks exactly the chunk it copied");
+    static_assert((MM_RING * STAGE + (Q4 ? 2 * SH::ST_A : 16) + 8 * MM_TOK) * SH::WG_PER_CU <= 160 * 1024,
+                  "the work groups of a CU fit its 160 KB of LDS");
     __shared__ int tok_s[MM_TOK], slot_s[MM_TOK];
     constexpr int OFF_A = 0;                                  // Q8_0: int8 A; Q4_0: raw nibbles
     constexpr int OFF_B = Q4 ? SH::ST_AR : SH::ST_A;
@@ -317,6 +327,12 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     const uint32_t sx_lane = (uint32_t)(lg == 0 ? OFF_BS + (nq * 32 * TT + lr) * MM_KB * 4 : OFF_Z);
     const uint32_t ring0 = lds_off(ring[0]);
     const uint32_t aun0 = lds_off(aun);
+    // Q4_0 unpack: this thread's nibble row in a stage slot (chunk tid / 64, row tid % 64)
+    // and the two swizzled halves of its int8 row in aun[0]
+    const int un_c = tid >> 6, un_r = tid & 63;
+    const uint32_t un_src = ring0 + (uint32_t)(OFF_A + un_c * 1024 + un_r * 16);
+    const uint32_t un_lo = aun0 + (uint32_t)(un_c * 2048 + un_r * 32 + swz_half(un_r, 0));
+    const uint32_t un_hi = aun0 + (uint32_t)(un_c * 2048 + un_r * 32 + swz_half(un_r, 1));
     // rank-1 operands {d, 0, 0, ...}: only element 0 changes, the zeros stay in place
     v4i_t xa0 = {0, 0, 0, 0}, xa1 = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
 
@@ -388,28 +404,28 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     const uint32_t a_q0 = ring0 + a_lane, b_q0 = ring0 + b_lane, sw_q0 = ring0 + sw_lane, sx_q0 = ring0 + sx_lane;
     uint32_t soff = 0;
     for (int s = 0; s < nstage; s++) {
-        // stage s landed (this wave's loads), and every wave's (barrier)
-        wait_copies<LOADS, MM_RING - 2>(nstage - 1 - s);
-        __builtin_amdgcn_s_barrier();
-        // refill: slot (s + RING - 1) % RING was last read in iteration s-1, finished
-        // by every wave before this barrier -- issue it now so that RING - 1 stages are
-        // in flight during this stage's math
-        if (s + MM_RING - 1 < nstage) issue(s + MM_RING - 1);
         soff = __builtin_amdgcn_readfirstlane(soff);
+        // stage s landed (this wave's loads)
+        wait_copies<LOADS, MM_RING - 2>(nstage - 1 - s);
         uint32_t abase;
-        if (Q4) {
-            // nibbles -> int8 (n - 8) once per stage: thread t converts row t%64 of
-            // chunk t/64 (CHUNKS x 64 rows <= MM_THREADS)
-            if (tid < SH::CHUNKS * 64) {
-                const int c = tid >> 6, r = tid & 63;
-                unpack_q4_row(ring[0] + soff + OFF_A + c * 1024 + r * 16, aun + c * 2048, r);
-                lds_wait();
-            }
-            __builtin_amdgcn_s_barrier();
-            abase = aun0 + a_lane;
+        if constexpr (Q4) {
+            // nibbles -> int8 (n - 8): wave w converts chunk w, the chunk it copied itself
+            // (row = lane), so its own copies having landed is enough; the result goes to
+            // aun[s & 1], last read by stage s - 2's math, which every wave finished before
+            // the previous barrier
+            const uint32_t ab = (uint32_t)((s & 1) * SH::ST_A);
+            unpack_q4_row_at(un_src + soff, un_lo + ab, un_hi + ab);
+            lds_wait();
+            abase = aun0 + ab + a_lane;
         } else {
             abase = a_q0 + soff;
         }
+        // every wave's copies of stage s landed (and, for Q4_0, its unpack is written)
+        __builtin_amdgcn_s_barrier();
+        // refill: slot (s + RING - 1) % RING was last read in iteration s-1 (its B by the
+        // math, its Q4_0 nibbles by the unpack), finished by every wave before this
+        // barrier -- issue it now so that RING - 1 stages are in flight during the math
+        if (s + MM_RING - 1 < nstage) issue(s + MM_RING - 1);
         if (active) {
             const uint32_t bq = b_q0 + soff, swq = sw_q0 + soff, sxq = sx_q0 + soff;
             [&]<int... KBI>(std::integer_sequence<int, KBI...>) {
