@@ -464,7 +464,16 @@ int hy_lm_head_f32(const float* x, const float* w, const float* resid, uint32_t 
     // mid-size grids take the stream-K split, which needs a scratch of partial tiles:
     // one per device, allocated on the first such call and kept for the process.  A
     // call waits (on the device) for the previous call's use of it to finish, so calls
-    // on different streams stay ordered.
+    // on different streams stay ordered.  That ordering is an event recorded by eager
+    // calls, which a captured graph's replays would not follow: such a shape is refused
+    // under stream capture (graph users run the lm_head through hy_model_forward, whose
+    // context owns its scratch).
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(HY_ERR_UNSUPPORTED,
+                    "hy_lm_head_f32 with T=%u vocab=%u uses a shared scratch and cannot be captured into a graph",
+                    T, vocab);
     static std::mutex mu;
     static std::vector<LmScratch> per_dev;
     std::lock_guard<std::mutex> lock(mu);
@@ -473,11 +482,16 @@ int hy_lm_head_f32(const float* x, const float* w, const float* resid, uint32_t 
     if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1);
     LmScratch& sc = per_dev[dev];
     if (!sc.ws) {
-        if (hipMalloc(reinterpret_cast<void**>(&sc.ws), hy::gemm_nt_f32_ws_bytes()) != hipSuccess) {
-            sc.ws = nullptr;
+        // both resources exist before the scratch is published; a failure leaves none
+        hipEvent_t ev = nullptr;
+        HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        float* ws = nullptr;
+        if (hipMalloc(reinterpret_cast<void**>(&ws), hy::gemm_nt_f32_ws_bytes()) != hipSuccess) {
+            (void)hipEventDestroy(ev);
             return fail(HY_ERR_NOMEM, "GEMM scratch allocation failed");
         }
-        HIP_TRY(hipEventCreateWithFlags(&sc.done, hipEventDisableTiming));
+        sc.done = ev;
+        sc.ws = ws;
     } else {
         HIP_TRY(hipStreamWaitEvent(s, sc.done, 0));
     }

@@ -431,8 +431,8 @@ hipError_t launch_dispatch_ws(const int32_t* topi, const float* topw, uint32_t T
 
 // Scratch of hy_dispatch_pairs_noalloc: a file-scope device array, one copy on every
 // GPU the library runs on, held until the process ends (4 MiB covers every call with
-// T*K <= 262,144 pairs: T = 16384, K = 16, E = 64 needs about 3.6 MB; larger needs are
-// rejected).  Host
+// T*K <= 262,144 pairs, e.g. T = 16384 at K = 16 with E = 64: about 3.6 MB; larger
+// needs are rejected).  Host
 // code never passes the array's name to a kernel: that name is a host-side stand-in,
 // not a device address.  The device address comes from hipGetSymbolAddress, taken
 // once per device with that device current.

@@ -277,32 +277,82 @@ hipError_t launch_topk_from_logits(const float* logits, int T, int E, int K, int
     return hipGetLastError();
 }
 
-// Load-balancing aux loss (src/hunyuan_moe_full.cpp:182-206), one work group of one
-// thread per expert: tokens_per_expert = count / T (the per-token mask summed as floats
-// is the exact count; counts from the dispatch), router_prob_per_expert = the expert's
-// gate summed over tokens in order / T; then thread 0 adds the E products in expert
-// order and multiplies by E * E.  Eight tokens' gates are loaded per step, so the
-// loads overlap while the adds keep their order.
-__global__ __launch_bounds__(64) void aux_loss_kernel(const float* __restrict__ probs, const int* __restrict__ cnt,
-                                                      int T, int E, float* __restrict__ out) {
+// Load-balancing aux loss (src/hunyuan_moe_full.cpp:182-206), one work group:
+// tokens_per_expert = count / T (the per-token mask summed as floats is the exact count;
+// counts from the dispatch), router_prob_per_expert = the expert's gate summed over
+// tokens in order / T (thread e sums column e); then thread 0 adds the E products in
+// expert order and multiplies by E * E.
+constexpr int AUX_THREADS = 1024, AUX_ROWS = 128, AUX_D = 4;  // rows per chunk, chunks in flight
+
+__global__ __launch_bounds__(AUX_THREADS) void aux_loss_kernel(const float* __restrict__ probs,
+                                                               const int* __restrict__ cnt, int T, int E,
+                                                               float* __restrict__ out) {
+    // gate rows arrive in chunks of AUX_ROWS x E floats, read by all threads with
+    // coalesced loads AUX_D chunks ahead (one work group streams the whole matrix, so
+    // its bytes in flight set the rate) into registers, then through a double-buffered
+    // LDS stage; thread e < E adds its expert's column in token order, one rounding per
+    // add, as the sequential sum does
+    __shared__ float stage[2][AUX_ROWS * MAX_E];
     __shared__ float prod[MAX_E];
-    const int e = threadIdx.x;
-    if (e < E) {
-        float r = 0.0f;
-        int t = 0;
-        for (; t + 8 <= T; t += 8) {
-            float v[8];
+    constexpr int PER = AUX_ROWS * MAX_E / AUX_THREADS;
+    const int tid = threadIdx.x;
+    const int chunk = AUX_ROWS * E;                 // floats per chunk
+    const size_t total = (size_t)T * E;
+    const int nchunks = (T + AUX_ROWS - 1) / AUX_ROWS;
+    float v[AUX_D][PER];
+    // unconditional loads from clamped addresses (a value past the chunk or the matrix
+    // is never stored): branch-free, so each store waits only for its own chunk's loads
+    auto load = [&](int c, float (&dst)[PER]) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = probs[(size_t)(t + j) * E + e];
-#pragma unroll
-            for (int j = 0; j < 8; j++) r += v[j];
+        for (int j = 0; j < PER; j++) {
+            const size_t g = (size_t)c * chunk + (size_t)(j * AUX_THREADS + tid);
+            dst[j] = probs[g < total ? g : total - 1];
         }
-        for (; t < T; t++) r += probs[(size_t)t * E + e];
-        const float tpe = (float)cnt[e] / (float)T, rpe = r / (float)T;
-        prod[e] = tpe * rpe;
+    };
+    auto store = [&](int buf, const float (&src)[PER]) {
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int i = j * AUX_THREADS + tid;
+            if (i < chunk) stage[buf][i] = src[j];
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < AUX_D; d++)
+        if (d < nchunks) load(d, v[d]);
+    store(0, v[0]);
+    __syncthreads();
+    float r = 0.0f;
+    for (int c0 = 0; c0 < nchunks; c0 += AUX_D) {
+#pragma unroll
+        for (int d = 0; d < AUX_D; d++) {
+            const int c = c0 + d;   // chunk c's rows are in stage[c & 1]; v[d] held them
+            if (c >= nchunks) break;
+            if (tid < E) {
+                const int rows = min(AUX_ROWS, T - c * AUX_ROWS);
+                const float* col = stage[c & 1] + tid;
+                int k = 0;
+                for (; k + 16 <= rows; k += 16) {   // 16 reads in flight, then their adds in order
+                    float q[16];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) q[j] = col[(k + j) * E];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) r += q[j];
+                }
+                for (; k < rows; k++) r += col[k * E];
+            }
+            // chunk c + 1 into the other buffer (summed, as chunk c - 1, before the last
+            // barrier), and chunk c + AUX_D into the registers chunk c came from
+            if (c + 1 < nchunks) store((c + 1) & 1, v[(d + 1) % AUX_D]);
+            if (c + AUX_D < nchunks) load(c + AUX_D, v[d]);
+            __syncthreads();
+        }
+    }
+    if (tid < E) {
+        const float tpe = (float)cnt[tid] / (float)T, rpe = r / (float)T;
+        prod[tid] = tpe * rpe;
     }
     __syncthreads();
-    if (e == 0) {
+    if (tid == 0) {
         float l = 0.0f;
         for (int i = 0; i < E; i++) l += prod[i];
         out[0] = l * (float)(E * E);
@@ -310,7 +360,7 @@ __global__ __launch_bounds__(64) void aux_loss_kernel(const float* __restrict__ 
 }
 
 hipError_t launch_aux_loss(const float* probs, const int* cnt, int T, int E, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(64), 0, s, probs, cnt, T, E, out);
+    hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(AUX_THREADS), 0, s, probs, cnt, T, E, out);
     return hipGetLastError();
 }
 

@@ -148,7 +148,10 @@ int hy_model_forward_hidden(hy_model_ctx* ctx, const float* inputs_embeds_dev, u
 /* lm_head_f32 (src/hunyuan_full_model.cpp:298-318) and the projections' GEMM:
  * out[t][v] = sum_h x[t][h] * w[v][h] (+ resid[t][v] when resid_dev is not NULL),
  * fp32 MFMA; x [T][hidden], w [vocab][hidden], all device memory; hidden a multiple
- * of 16. */
+ * of 16.  Mid-size shapes split the reduction over a per-device scratch that the
+ * library allocates on first use and orders between calls with an event: those shapes
+ * return HY_ERR_UNSUPPORTED under stream capture (hy_model_forward, whose context
+ * owns its scratch, can be captured). */
 int hy_lm_head_f32(const float* x_dev, const float* w_dev, const float* resid_dev, uint32_t T, uint32_t hidden,
                    uint32_t vocab, float* out_dev, void* stream);
 

@@ -18,9 +18,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
 def test_layer_at_max_tokens_and_topk(gpu, wtype):
-    """T = 16384 (the largest batch a context takes) and K = 16 (the largest top-k) over
-    64 experts: all 262,144 pairs dispatched, the routing of every row and sampled output
-    rows against the oracle, every row through permutation invariance."""
+    """T = 16384 (the largest batch a context takes) at K = 16 over 64 experts: T*K =
+    262,144 pairs, the most the dispatch scratch is sized for, all dispatched; the
+    routing of every row and sampled output rows against the oracle, every row through
+    permutation invariance.  (Larger K up to 64 is covered at smaller T below.)"""
     H, I, E, K, T = 256, 128, 64, 16, 16384
     layer = O.synth_layer(H, I, E, K, wtype, seed=71, std=0.05)
     x = O.synth(72, 0, O.T_X, 0, (T, H), 1.0)

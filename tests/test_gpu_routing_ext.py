@@ -277,3 +277,37 @@ def test_nan_token_in_layer(gpu, T):
         np.testing.assert_array_equal(idx[rest], ridx[rest])
         assert_exact(out[rest], ref[rest], f"T={T} rows beside the NaN token")
     m.close()
+
+
+@pytest.mark.parametrize("E", [1, 7, 16, 64])
+def test_aux_loss_kernel_shapes(gpu, E):
+    """hy_aux_loss on gate rows staged in 128-row chunks: partial last chunks, expert
+    counts that do not divide the stage, T = 1 .. 4096, bit-exact against the oracle's
+    sequential sums.  Prints the T=4096, E=64 kernel time."""
+    rng = np.random.default_rng(E)
+    for T in (1, 127, 128, 129, 300, 4096):
+        probs = rng.random((T, E)).astype(np.float32)
+        probs /= probs.sum(axis=1, keepdims=True)
+        K = min(E, 4)
+        idx = np.argsort(-probs, axis=1, kind="stable")[:, :K].astype(np.int32)
+        counts = np.bincount(idx.ravel(), minlength=E).astype(np.int32)
+        got = gpu.aux_loss(probs, counts)
+        assert got == O.aux_loss_q(probs, idx), (E, T)
+    if E == 64:
+        pb, cb, ob = gpu.Buf.from_array(probs), gpu.Buf.from_array(counts), gpu.Buf.empty((1,))
+        st = gpu.Stream()
+        ev0, ev1 = gpu.C.c_void_p(), gpu.C.c_void_p()
+        gpu.check(gpu.lib().hy_event_create(gpu.C.byref(ev0)))
+        gpu.check(gpu.lib().hy_event_create(gpu.C.byref(ev1)))
+        gpu.check(gpu.lib().hy_aux_loss(pb.ptr, cb.ptr, 4096, E, ob.ptr, st.h))
+        gpu.check(gpu.lib().hy_event_record(ev0, st.h))
+        for _ in range(20):
+            gpu.check(gpu.lib().hy_aux_loss(pb.ptr, cb.ptr, 4096, E, ob.ptr, st.h))
+        gpu.check(gpu.lib().hy_event_record(ev1, st.h))
+        st.synchronize()
+        ms = gpu.C.c_float()
+        gpu.check(gpu.lib().hy_event_elapsed_ms(ev0, ev1, gpu.C.byref(ms)))
+        print(f"\naux_loss T=4096 E=64: {ms.value / 20 * 1e3:.1f} us per call")
+        for e in (ev0, ev1):
+            gpu.lib().hy_event_destroy(e)
+        st.close()

@@ -127,3 +127,23 @@ def test_routing_options_replay(gpu, T):
         g.close()
         st.close()
         m.close()
+
+
+def test_lm_head_scratch_shape_refused_under_capture(gpu):
+    """hy_lm_head_f32 shapes that take the stream-K split share a per-device scratch
+    ordered by an event of the eager calls: under capture they are refused before
+    anything is launched, and eager calls before and after agree bit for bit."""
+    T, Hd, V = 256, 1024, 4096   # 64 output tiles of 128 x 128: the stream-K range
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((T, Hd)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((V, Hd))).astype(np.float32)
+    before = gpu.lm_head_f32(x, w)
+    xb, wb, ob = gpu.Buf.from_array(x), gpu.Buf.from_array(w), gpu.Buf.empty((T, V))
+    st = gpu.Stream()
+    with pytest.raises(gpu.HyError, match="cannot be captured"):
+        gpu.Graph(st, lambda: gpu.check(gpu.lib().hy_lm_head_f32(xb.ptr, wb.ptr, None, T, Hd, V, ob.ptr, st.h)))
+    st.close()
+    after = gpu.lm_head_f32(x, w)
+    np.testing.assert_array_equal(after.view(np.uint32), before.view(np.uint32))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.abs(after - ref).max() / np.abs(ref).max() < 1e-5
