@@ -89,6 +89,11 @@ __device__ __forceinline__ void lds_st128(void* p, v4i_t v) {
 __device__ __forceinline__ void lds_st128_at(uint32_t off, v4i_t v) {
     asm volatile("ds_write_b128 %0, %1" ::"v"(off), "v"(v) : "memory");
 }
+// ds_write_b128 at base + a compile-time byte offset
+template <int OFF>
+__device__ __forceinline__ void lds_st128_at(uint32_t base, v4i_t v) {
+    asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(base), "v"(v), "i"(OFF) : "memory");
+}
 __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // wait until at most N of this wave's LDS reads are outstanding (they complete in
 // order); pin each consumed result afterwards (lds_pin)
@@ -107,6 +112,9 @@ __device__ __forceinline__ void pin_f32(float& v) { asm volatile("" : "+v"(v)); 
 // wait for the ds_reads whose results are passed in: the values are threaded through
 // the asm so no consumer can be scheduled ahead of the wait
 __device__ __forceinline__ void lds_wait(v4i_t& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
+__device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b)::"memory");
+}
 __device__ __forceinline__ void lds_wait(v4i_t& a, v4i_t& b, v4i_t& c) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
 }

@@ -105,14 +105,6 @@ struct MmArgs {
     float* y;           // mode 1 output
 };
 
-// Q4_0 nibbles (16 bytes, GGUF order) -> 32 int8 values n-8 in element order.
-__device__ __forceinline__ void unpack_q4(const int4 w, int4& lo, int4& hi) {
-    const int m = 0x0F0F0F0F;
-    auto cv = [](int v) { return ((v | (int)0x80808080) - 0x08080808) ^ (int)0x80808080; };
-    lo = make_int4(cv(w.x & m), cv(w.y & m), cv(w.z & m), cv(w.w & m));
-    hi = make_int4(cv((w.x >> 4) & m), cv((w.y >> 4) & m), cv((w.z >> 4) & m), cv((w.w >> 4) & m));
-}
-
 // Byte offset, inside a 32-byte operand row, of the row's 16-byte half h: the halves
 // are swapped when bit 3 of the row is set (conflict-free MFMA operand reads).
 __device__ __forceinline__ int swz_half(int row, int h) { return 16 * (h ^ ((row >> 3) & 1)); }
@@ -121,21 +113,25 @@ __device__ __forceinline__ int swz_half(int row, int h) { return 16 * (h ^ ((row
 // (lr = l % 32, lg = l / 32) reads: row lr, half lg.
 __device__ __forceinline__ int operand_lane_off(int lr, int lg) { return lr * 32 + swz_half(lr, lg); }
 
-// Q4_0 stage unpack of one chunk row r: the 16 nibble bytes at LDS offset nib to the
-// 32 int8 values n - 8 of operand row r, whose two swizzled halves sit at LDS offsets
-// dst_row + swz_half(r, 0) (elements 0-15) and dst_row + swz_half(r, 1) (16-31).
-__device__ __forceinline__ void unpack_q4_row_at(uint32_t nib, uint32_t dst_lo, uint32_t dst_hi) {
-    v4i_t wv4 = lds_b128_at<0>(nib);
-    lds_wait(wv4);
-    int4 lo, hi;
-    unpack_q4(make_int4(wv4[0], wv4[1], wv4[2], wv4[3]), lo, hi);
-    lds_st128_at(dst_lo, v4i_t{lo.x, lo.y, lo.z, lo.w});
-    lds_st128_at(dst_hi, v4i_t{hi.x, hi.y, hi.z, hi.w});
+// Q4_0 unpack of one 64-row chunk by one wave, as contiguous 16-byte stores: lane l
+// writes pieces l and 64 + l of the chunk's int8 operand rows (32 bytes each, halves
+// swizzled by swz_half).  Piece d is half h = (d % 2) ^ (bit 3 of row d / 2) of row
+// d / 2: the values n - 8 of the low (h = 0, elements 0-15) or high (h = 1, elements
+// 16-31) nibbles of the row's 16 stored bytes; lanes 2j and 2j + 1 read the same
+// nibble row.  nib = the chunk's nibble rows + 16 * (l / 2), dst = its int8 rows + 16 l,
+// sh = 4 h (the same for rows l / 2 and 32 + l / 2).
+__device__ __forceinline__ void unpack_q4_chunk_at(uint32_t nib, uint32_t dst, uint32_t sh) {
+    v4i_t w0 = lds_b128_at<0>(nib);
+    v4i_t w1 = lds_b128_at<512>(nib);
+    lds_wait(w0, w1);
+    auto cv = [sh](int v) {
+        const uint32_t x = ((uint32_t)v >> sh) & 0x0F0F0F0Fu;
+        return (int)(((x | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+    };
+    lds_st128_at<0>(dst, v4i_t{cv(w0[0]), cv(w0[1]), cv(w0[2]), cv(w0[3])});
+    lds_st128_at<1024>(dst, v4i_t{cv(w1[0]), cv(w1[1]), cv(w1[2]), cv(w1[3])});
 }
-__device__ __forceinline__ void unpack_q4_row(const void* nib, int8_t* dst, int r) {
-    const uint32_t row = lds_off(dst) + (uint32_t)(r * 32);
-    unpack_q4_row_at(lds_off(nib), row + swz_half(r, 0), row + swz_half(r, 1));
-}
+__device__ __forceinline__ uint32_t unpack_q4_shift(int lane) { return 4u * (uint32_t)((lane & 1) ^ ((lane >> 4) & 1)); }
 
 // The exact int32 dots of one 32-wide GGUF block over a 32x32 tile (K = 32 is one
 // block): v_mfma_i32_32x32x32_i8 with a zero accumulator.
@@ -329,10 +325,10 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     const uint32_t aun0 = lds_off(aun);
     // Q4_0 unpack: this thread's nibble row in a stage slot (chunk tid / 64, row tid % 64)
     // and the two swizzled halves of its int8 row in aun[0]
-    const int un_c = tid >> 6, un_r = tid & 63;
-    const uint32_t un_src = ring0 + (uint32_t)(OFF_A + un_c * 1024 + un_r * 16);
-    const uint32_t un_lo = aun0 + (uint32_t)(un_c * 2048 + un_r * 32 + swz_half(un_r, 0));
-    const uint32_t un_hi = aun0 + (uint32_t)(un_c * 2048 + un_r * 32 + swz_half(un_r, 1));
+    const int un_c = tid >> 6;
+    const uint32_t un_src = ring0 + (uint32_t)(OFF_A + un_c * 1024 + (lane >> 1) * 16);
+    const uint32_t un_dst = aun0 + (uint32_t)(un_c * 2048 + lane * 16);
+    const uint32_t un_sh = unpack_q4_shift(lane);
     // rank-1 operands {d, 0, 0, ...}: only element 0 changes, the zeros stay in place
     v4i_t xa0 = {0, 0, 0, 0}, xa1 = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
 
@@ -414,7 +410,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
             // aun[s & 1], last read by stage s - 2's math, which every wave finished before
             // the previous barrier
             const uint32_t ab = (uint32_t)((s & 1) * SH::ST_A);
-            unpack_q4_row_at(un_src + soff, un_lo + ab, un_hi + ab);
+            unpack_q4_chunk_at(un_src + soff, un_dst + ab, un_sh);
             lds_wait();
             abase = aun0 + ab + a_lane;
         } else {
@@ -496,7 +492,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 // Per-block int32 dots through the grouped GEMM's own operand path (hy_block_dots
 // path 1), one wave per (64-row group, block).  The wave stages the block's 64 weight
 // rows in the GEMM's LDS operand layout -- Q8_0 as swizzled 32-byte rows; Q4_0 as the
-// raw 16-byte nibble rows, then the GEMM's stage unpack (unpack_q4_row) -- and the
+// raw 16-byte nibble rows, then the GEMM's stage unpack (unpack_q4_chunk_at) -- and the
 // activation block into all 32 token rows of a B tile with the same swizzle, reads its
 // A0 / A1 / B operands at the GEMM's lane offsets (operand_lane_off) and issues the
 // GEMM's two block-dot MFMAs (block_dot_tile).  Every entry of the two 32x32 results
@@ -529,7 +525,8 @@ __global__ __launch_bounds__(WAVE) void block_dots_mfma_kernel(const uint8_t* __
         lds_st128(nib_s + lane * 16, r < rows ? dw4(wq) : zero4);
         lds_wait();
         __syncthreads();
-        unpack_q4_row(nib_s + lane * 16, a_s, lane);
+        unpack_q4_chunk_at(lds_off(nib_s) + (uint32_t)((lane >> 1) * 16), lds_off(a_s) + (uint32_t)(lane * 16),
+                           unpack_q4_shift(lane));
     } else {
         lds_st128(a_s + lane * 32 + swz_half(lane, 0), r < rows ? dw4(wq) : zero4);
         lds_st128(a_s + lane * 32 + swz_half(lane, 1), r < rows ? dw4(wq + 16) : zero4);
