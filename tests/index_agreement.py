@@ -30,7 +30,8 @@ module measures that on given inputs and checks it against a bound:
   same bound holds for two experts the methods order differently.
 
 compare() asserts the elementwise bound for every (token, expert) and the pair bound
-for every disagreement, and returns the counts DESIGN.md reports.
+for every disagreement, and returns the counts (set and order differences, near ties,
+probability ties, the worst disagreement against its bound).
 """
 import concurrent.futures as cf
 import os

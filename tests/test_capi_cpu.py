@@ -113,9 +113,9 @@ def test_config_struct_layouts_match_header(hy, tmp_path):
 
 
 def test_integration_ctypes_stub_matches_headers(hy):
-    """The ctypes stub INTEGRATION.md gives callers: its structs have the package's
-    layouts (pinned to the C headers above) and every argtypes list has the header's
-    parameter count."""
+    """The ctypes stub the integration guide (section "FFI stubs") gives callers: its
+    structs have the package's layouts (pinned to the C headers above) and every
+    argtypes list has the header's parameter count."""
     import re
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     code = text.split("## 3. FFI stubs", 1)[1].split("```python", 1)[1].split("```", 1)[0]

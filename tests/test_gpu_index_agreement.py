@@ -7,7 +7,7 @@ its routing computed both ways on the host: the reference's sequential RMSNorm,
 sequential router dot, softmax and top-k on probabilities, against the blocked RMSNorm
 and router and the top-k on logits that the GPU uses (tests/index_agreement.py states
 the bound each disagreement must meet).  Layer 0 is also covered by the CPU test
-test_index_agreement.py; the counts are recorded in DESIGN.md.
+test_index_agreement.py; the counts are printed (pytest -s).
 """
 import numpy as np
 import pytest

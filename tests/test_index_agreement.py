@@ -7,7 +7,7 @@ reference's sequential logits + softmax + top-k on probabilities (bit-exact agai
 the reference build), and the GPU's blocked logits + top-k on logits.  Every logit
 must lie within the rounding bound of the other method's, and every token whose
 selected set or order differs must have its disagreeing experts within the bound of
-each other.  The counts are printed (pytest -s) and recorded in DESIGN.md.
+each other.  The counts are printed (pytest -s).
 
 The 32-layer stack's layers past the first take the GPU's own activations as input:
 tests/test_gpu_index_agreement.py.
