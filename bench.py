@@ -17,6 +17,7 @@ Other workloads (--config): c1 F32 T=16, c2 Q8_0 T=512, c3 Q4_0 decode (--tokens
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--no-cpu] [--no-extras]
     python bench.py --mfma-probe          # the grouped GEMM's per-block instruction mix alone
     python bench.py --stream-probe 864    # HBM read rate of the decode GEMV's streams
+    python bench.py --l2-probe            # global->LDS copy rate from L2 / Infinity Cache / HBM windows
     python bench.py --copy-probe 1024     # plain 1 GiB device copy (counter yardstick)
     python bench.py --gguf-load /tmp/l.gguf [--config c2]   # layer load from a GGUF file
     python bench.py --attn [--tokens 4096]   # attention half of a decoder layer (fp32)
@@ -153,6 +154,8 @@ def probe_lib():
         L.hyp_block_mix.argtypes = [C.c_int32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
         L.hyp_stream.restype = C.c_int
         L.hyp_stream.argtypes = [C.c_int32, C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_void_p]
+        L.hyp_l2_window.restype = C.c_int
+        L.hyp_l2_window.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
         _probe = L
     return _probe
 
@@ -223,6 +226,39 @@ def stream_probe(hy, waves=864, kb_per_wave=144, sets=8, launches=40):
     st.close()
     print(json.dumps({"probe": "stream_read", "waves": waves, "bytes_per_wave": kb_per_wave * 1024,
                       "bytes_per_launch": per, "rotating_sets": sets, "launches": launches, **res}), flush=True)
+
+
+def l2_probe(hy, windows_kb=(1024, 65536, 1048576), wgs_per_cu=4, launches=5):
+    """Copy rate of 1 KB global->LDS copies (the grouped GEMM's operand copies) from a
+    window of each size: 1 MiB stays in every XCD's 4 MB L2, 64 MiB in the 256 MB
+    Infinity Cache, 1 GiB comes from HBM."""
+    wgs = 256 * wgs_per_cu
+    out = hy.Buf.empty((wgs * 256,))
+    st = hy.Stream()
+    ev0, ev1 = hy.C.c_void_p(), hy.C.c_void_p()
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev0)))
+    hy.check(hy.lib().hy_event_create(hy.C.byref(ev1)))
+    res = {}
+    for kb in windows_kb:
+        buf = hy.Buf(kb * 1024, np.uint8)
+        hy.check(hy.lib().hy_memset(buf.ptr, 1, kb * 1024))
+        iters = max(4, int(2e9 / (wgs * 4 * 8 * 1024)))  # ~2 GB copied per launch
+        probe_check(probe_lib().hyp_l2_window(buf.ptr, kb * 1024, wgs, iters, out.ptr, st.h))
+        hy.check(hy.lib().hy_event_record(ev0, st.h))
+        for _ in range(launches):
+            probe_check(probe_lib().hyp_l2_window(buf.ptr, kb * 1024, wgs, iters, out.ptr, st.h))
+        hy.check(hy.lib().hy_event_record(ev1, st.h))
+        st.synchronize()
+        ms = hy.C.c_float()
+        hy.check(hy.lib().hy_event_elapsed_ms(ev0, ev1, hy.C.byref(ms)))
+        t = ms.value / launches / 1e3
+        nbytes = wgs * 4 * 8 * 1024 * iters
+        res[f"window_{kb // 1024}MiB"] = {"us_per_launch": t * 1e6, "TBps": nbytes / t / 1e12}
+        buf.free()
+    for e in (ev0, ev1):
+        hy.lib().hy_event_destroy(e)
+    st.close()
+    print(json.dumps({"probe": "l2_window_copies", "work_groups": wgs, "copies_per_batch": 8, **res}), flush=True)
 
 
 def copy_probe(hy, mib, steps):
@@ -776,6 +812,8 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     ap.add_argument("--stream-probe", type=int, default=0, metavar="WAVES",
                     help="HBM read rate of WAVES single-wave 144 KB streams (864: the decode T=1 gate/up shape)")
+    ap.add_argument("--l2-probe", action="store_true",
+                    help="global->LDS copy rate of 1 KB copies from 1 MiB / 64 MiB / 1 GiB windows")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="rate of the grouped GEMM's per-block instruction mix alone (and of its halves)")
     ap.add_argument("--attn", action="store_true", help="time the attention half instead of the MoE layer")
@@ -807,6 +845,9 @@ def main():
         return
     if a.stream_probe:
         stream_probe(hy, waves=a.stream_probe)
+        return
+    if a.l2_probe:
+        l2_probe(hy)
         return
     if a.mfma_probe:
         rates = {name: probe_block_mix(hy, v) for v, name in ((0, "mix"), (1, "mfma_only"), (2, "valu_only"),

@@ -1,8 +1,8 @@
 /* hy_probe.h -- measurement probes of libhy_probe.so (bench.py only).
  *
  * Not part of the product library libhy_moe.so and not declared in include/: these
- * kernels measure the ceilings the product's kernels are reported against.  Both
- * return 0, or -1 with the reason in hyp_last_error(). */
+ * kernels measure the ceilings the product's kernels are reported against.  Each
+ * returns 0, or -1 with the reason in hyp_last_error(). */
 #pragma once
 #include <stdint.h>
 
@@ -30,6 +30,14 @@ int hyp_block_mix(int32_t variant, uint32_t work_groups, uint32_t iters, float* 
  * (waves a multiple of 4); variant 2: variant 0 with non-temporal copies.  out_dev holds
  * waves x 64 floats: lane l of wave w sums word l of every step it streamed. */
 int hyp_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t waves, float* out_dev, void* stream);
+
+/* Copy rate from a window of `bytes` (a power-of-two number of KB; small enough to stay
+ * in L2): work_groups 4-wave work groups, each wave issuing `iters` batches of eight
+ * 1 KB global->LDS copies of the window's chunks into its own 8 KB of LDS, waiting for
+ * each batch.  Each launch copies work_groups x 4 x iters x 8 KB.  out_dev holds
+ * work_groups x 256 floats. */
+int hyp_l2_window(const void* buf_dev, uint64_t bytes, uint32_t work_groups, uint32_t iters, float* out_dev,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,7 @@
 // hy_probe.hip -- measurement probes (bench.py only; built into libhy_probe.so, not into
 // the product library libhy_moe.so): the grouped GEMM's per-block instruction mix
-// (compute only) and the HBM read rate of the decode GEMV's access pattern.
+// (compute only), the HBM read rate of the decode GEMV's access pattern, and the copy
+// rate from an L2-resident window.
 //
 // Each wave repeats, `iters` times, exactly the math the grouped int8 GEMM issues for
 // one 32-wide GGUF block of its two 32x32 output tiles (hy_mfma.hip):
@@ -163,8 +164,10 @@ __global__ __launch_bounds__(WAVE) void stream_dma_kernel(const uint8_t* __restr
             MM_WAIT_VM_LGKM(LOADS);   // step st landed, step st + 1 may stay in flight
         else
             MM_WAIT_VM_LGKM(0);
-        acc += lds_b32(ring[st % STREAM_RING] + 4 * lane);
+        uint32_t w = lds_b32(ring[st % STREAM_RING] + 4 * lane);
         lds_wait();
+        lds_pin(w);  // the read's register stays live until its wait
+        acc += w;
         // every lane has read its word of slot st before the refill of that slot
         if (st + STREAM_RING - 1 < steps) issue(st + STREAM_RING - 1);
     }
@@ -182,7 +185,38 @@ __global__ __launch_bounds__(256) void stream_vec_kernel(const int4* __restrict_
     out[tid] = (float)a;
 }
 
+// Variant 3: copy throughput from a window small enough to stay in L2 (the grouped
+// GEMM's operand copies hit L2 for most of their bytes): every wave of a 4-wave work
+// group issues batches of 8 one-KB global -> LDS copies of chunks (c + d) & mask of the
+// window (mask + 1 KB, a power of two) into its own 8 KB of LDS and waits for them.
+constexpr int L2W_BATCH = 8;
+
+__global__ __launch_bounds__(256) void l2_window_kernel(const uint8_t* __restrict__ base, uint32_t mask, uint32_t iters,
+                                                        float* __restrict__ out) {
+    __shared__ __align__(16) uint8_t lds[4][L2W_BATCH * 1024];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const uint32_t wid = blockIdx.x * 4 + wave;
+    uint32_t c = wid * 7919u;
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+        for (int d = 0; d < L2W_BATCH; d++)
+            g2l16(base + (size_t)((c + d) & mask) * 1024 + 16 * lane, lds[wave] + d * 1024);
+        MM_WAIT_VM_LGKM(0);
+        c += L2W_BATCH;
+    }
+    // a plain LDS load: the compiler waits for it before the value is used (the copies
+    // landed at the last batch's vmcnt wait)
+    out[(size_t)wid * WAVE + lane] = (float)reinterpret_cast<const uint32_t*>(lds[wave])[lane];
+}
+
 }  // namespace
+
+static hipError_t launch_probe_l2(const void* buf, size_t bytes, int work_groups, uint32_t iters, float* out,
+                                  hipStream_t s) {
+    hipLaunchKernelGGL(l2_window_kernel, dim3((unsigned)work_groups), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(buf), (uint32_t)(bytes / 1024 - 1), iters, out);
+    return hipGetLastError();
+}
 
 static hipError_t launch_probe_stream(int variant, const void* buf, size_t bytes, int waves, float* out, hipStream_t s) {
     if (variant == 0 || variant == 2) {
@@ -251,6 +285,17 @@ int hyp_stream(int32_t variant, const void* buf_dev, uint64_t bytes, uint32_t wa
                           "for variant 1, variant 0-2");
     return probe_hip(hy::launch_probe_stream(variant, buf_dev, (size_t)bytes, (int)waves, out_dev,
                                              static_cast<hipStream_t>(stream)));
+}
+
+int hyp_l2_window(const void* buf_dev, uint64_t bytes, uint32_t work_groups, uint32_t iters, float* out_dev,
+                  void* stream) {
+    const uint64_t kb = bytes / 1024;
+    if (!buf_dev || !out_dev || work_groups == 0 || iters == 0 || bytes % 1024 || kb == 0 || (kb & (kb - 1)) ||
+        kb > (1u << 31))
+        return probe_fail("bad L2 window probe arguments: bytes a power-of-two number of KB, work groups and "
+                          "iterations > 0 (out holds work_groups x 256 floats)");
+    return probe_hip(hy::launch_probe_l2(buf_dev, (size_t)bytes, (int)work_groups, iters, out_dev,
+                                         static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -49,3 +49,20 @@ def test_block_mix_probe_variants(gpu):
     for variant in (5, -1):
         with pytest.raises(RuntimeError, match="bad block-mix probe arguments"):
             bench.probe_check(P.hyp_block_mix(variant, wgs, 20, out.ptr, None))
+
+
+def test_l2_window_probe_copies(gpu):
+    """Every wave's lane l reads back word l of the last batch's first copied KB: with the
+    window set to bytes of 1 it is 0x01010101, so a batch read before its copies landed
+    would show; windows that are not a power-of-two number of KB are rejected."""
+    P = bench.probe_lib()
+    kb, wgs = 64, 16
+    buf = gpu.Buf(kb * 1024, np.uint8)
+    gpu.check(gpu.lib().hy_memset(buf.ptr, 1, kb * 1024))
+    out = gpu.Buf.empty((wgs * 256,))
+    bench.probe_check(P.hyp_l2_window(buf.ptr, kb * 1024, wgs, 7, out.ptr, None))
+    gpu.sync()
+    np.testing.assert_array_equal(out.numpy(), np.full(wgs * 256, np.float32(0x01010101)))
+    for nbytes in (kb * 1024 - 16, 48 * 1024, 0):
+        with pytest.raises(RuntimeError, match="bad L2 window probe arguments"):
+            bench.probe_check(P.hyp_l2_window(buf.ptr, nbytes, wgs, 7, out.ptr, None))
