@@ -636,10 +636,14 @@ struct DecodeRouteArgs {
 };
 
 
-__global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(DecodeRouteArgs a) {
+// route_decode_kernel's work group: RD_WAVES waves, one per token of a decode batch
+// (4, 8 or 16 for T <= 4, 8, 16; at T = 8 one token per wave instead of two: router
+// 12.6-13.0 -> 10.7-11.0 us)
+template <int RD_WAVES>
+__global__ __launch_bounds__(RD_WAVES * WAVE) void route_decode_kernel(DecodeRouteArgs a) {
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     if (blockIdx.x > 0) {
-        const size_t idx = (size_t)(blockIdx.x - 1) * 256 + tid;
+        const size_t idx = (size_t)(blockIdx.x - 1) * (RD_WAVES * WAVE) + tid;
         quant_q8_0_elem(a.x, (size_t)a.T * a.H, idx, a.xq, a.xd, a.xs, nullptr);
         return;
     }
@@ -652,16 +656,16 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(Decod
     __shared__ int cnt_s[MAX_E], off_s[MAX_E + 1], toff_s[MAX_E + 2];
     // a wave's tokens t = wave + 4i: all their logits rows are loaded before the first
     // selection, so the loads' latency is paid once
-    constexpr int TPWV = (16 + ROUTER_WAVES - 1) / ROUTER_WAVES;  // decode batches: T <= 16
+    constexpr int TPWV = (16 + RD_WAVES - 1) / RD_WAVES;  // decode batches: T <= 16
     float lv[TPWV];
 #pragma unroll
     for (int i = 0; i < TPWV; i++) {
-        const int t = wave + i * ROUTER_WAVES;
+        const int t = wave + i * RD_WAVES;
         lv[i] = (t < T && lane < E) ? a.logits[(size_t)t * E + lane] : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < TPWV; i++) {
-        const int t = wave + i * ROUTER_WAVES;
+        const int t = wave + i * RD_WAVES;
         if (t >= T) break;
         topk_wave(lv[i], E, K, a.norm, a.scale, lane, sel_w + t * K, sel_e + t * K);
         if (lane < K) {
@@ -675,8 +679,8 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(Decod
     // earlier ranks, then the same rank's earlier tokens).  Thread q takes the q-th pair
     // of that order (token q % T, rank q / T); the pairs before it with the same expert
     // are counted from each wave's ballots of the expert ids' six bits.
-    static_assert(MAX_E <= 64 && MAX_DECODE_PAIRS <= ROUTER_WAVES * WAVE, "six id bits, one pair per thread");
-    __shared__ unsigned long long bal_s[ROUTER_WAVES][7];
+    static_assert(MAX_E <= 64 && MAX_DECODE_PAIRS <= RD_WAVES * WAVE, "six id bits, one pair per thread");
+    __shared__ unsigned long long bal_s[RD_WAVES][7];
     const int P = T * K;
     const bool qv = tid < P;
     const int qt = tid % T, qk = tid / T;
@@ -740,7 +744,7 @@ __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void route_decode_kernel(Decod
     __syncthreads();
     if (a.has_shared) {
         const int ns = (T + NT - 1) / NT;
-        for (int j = tid; j < ns; j += ROUTER_WAVES * WAVE) {
+        for (int j = tid; j < ns; j += RD_WAVES * WAVE) {
             a.o.tile_e[toff_s[E] + j] = E;
             a.o.tile_start[toff_s[E] + j] = j * NT;
             a.o.tile_n[toff_s[E] + j] = min(NT, T - j * NT);
@@ -768,7 +772,7 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
                                float* logits, float* topw, int* topi, int8_t* xq, float* xd, int* xs, int NT,
                                int has_shared, int* cnt, int* off, int* srt_tok, int* pair_pos, int* comb_pos,
                                float* comb_w, int* tile_e, int* tile_start, int* tile_n, int* meta, hipStream_t s) {
-    // one work group selects and lists every pair: T <= 16 tokens (4 per wave), T*K <= 256 pairs
+    // one work group selects and lists every pair: T <= 16 tokens (one per wave), T*K <= 256 pairs
     if (T < 1 || T > 16 || T * K > MAX_DECODE_PAIRS || E > MAX_E) return hipErrorInvalidValue;
     hipError_t e = launch_router_q(x, wr, T, H, E, K, norm, scale, logits, topw, topi, nullptr, nullptr, nullptr, s,
                                    /*logits_only=*/true);
@@ -776,8 +780,14 @@ hipError_t launch_route_decode(const float* x, const float* wr, int T, int H, in
     DecodeRouteArgs a{x, logits, T, H, E, K, norm, scale, topw, topi, xq, xd, xs, NT, has_shared,
                       DispatchOut{cnt, off, srt_tok, pair_pos, comb_pos, comb_w, tile_e, tile_start, tile_n, meta}};
     // no quantization work groups when the caller quantized x already (xq == null)
-    const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + 255) / 256) : 0u;
-    hipLaunchKernelGGL(route_decode_kernel, dim3(1 + quant_groups), dim3(ROUTER_WAVES * WAVE), 0, s, a);
+    const int waves = T <= 4 ? 4 : (T <= 8 ? 8 : 16);
+    const unsigned quant_groups = xq ? (unsigned)(((size_t)T * H + waves * WAVE - 1) / (waves * WAVE)) : 0u;
+    if (waves == 4)
+        hipLaunchKernelGGL(route_decode_kernel<4>, dim3(1 + quant_groups), dim3(4 * WAVE), 0, s, a);
+    else if (waves == 8)
+        hipLaunchKernelGGL(route_decode_kernel<8>, dim3(1 + quant_groups), dim3(8 * WAVE), 0, s, a);
+    else
+        hipLaunchKernelGGL(route_decode_kernel<16>, dim3(1 + quant_groups), dim3(16 * WAVE), 0, s, a);
     return hipGetLastError();
 }
 
