@@ -261,6 +261,36 @@ def test_layer_small(gpu, small_layers, wtype, T):
 
 
 # with E=16, K=4 the grouped GEMM tiles 64 pairs up to T=383 and 128 pairs from T=384
+DECODE = dict(H=768, I=768, E=64, K=8)
+
+
+@pytest.fixture(scope="module")
+def decode_layers():
+    return {wt: O.synth_layer(DECODE["H"], DECODE["I"], DECODE["E"], DECODE["K"], wt, seed=31, std=0.05)
+            for wt in (O.Q8_0, O.Q4_0)}
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("T", [2, 4, 5, 8, 9, 16])
+def test_decode_batch_routing(gpu, decode_layers, wtype, T):
+    """Decode batches of 2-16 tokens route in one selection pass whose work group has
+    4, 8 or 16 waves (one per token), then run the ring GEMV (768-wide rows: three or
+    more 8-block steps): logits, indices, weights and outputs bit-exact against the
+    oracle at the real expert count (64 routed experts, top-8)."""
+    H, I, E, K = DECODE["H"], DECODE["I"], DECODE["E"], DECODE["K"]
+    layer = decode_layers[wtype]
+    m = gpu.Moe(H, I, E, K, wtype, max_tokens=16)
+    m.upload(0, layer)
+    x = O.synth(300 + T, 0, O.T_X, 0, (T, H), 1.0)
+    out, lg, w, idx = m.run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(layer, x, debug=True)
+    np.testing.assert_array_equal(lg.view(np.uint32), rlg.view(np.uint32))
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_array_equal(w.view(np.uint32), rw.view(np.uint32))
+    assert_exact(out, ref, f"decode T={T} wtype={wtype}")
+    m.close()
+
+
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("T", [1, 17, 64, 65, 130, 300, 383, 384, 700])
 def test_layer_small_mfma_path(gpu, small_layers, wtype, T):
