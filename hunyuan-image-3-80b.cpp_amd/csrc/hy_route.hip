@@ -92,7 +92,14 @@ __device__ __forceinline__ void topk_groups_wave(float v_in, int E, int K, int n
 // are in flight while a chunk is accumulated (a large batch has about one wave per
 // SIMD, so the wave itself must cover the memory latency).  The per-lane
 // accumulation order is unchanged.
-template <int TPW, int EPW>
+// chunks of 256 elements in flight per lane: about 144 VGPRs of staged operands
+constexpr int router_depth(int tpw, int epw) {
+    return 144 / (4 * (tpw + epw)) >= 8 ? 8 : (144 / (4 * (tpw + epw)) < 2 ? 2 : 144 / (4 * (tpw + epw)));
+}
+
+// FULL: every lane's every chunk is in range (H a multiple of 256, and of D chunks),
+// so the accumulation needs no per-chunk select
+template <int TPW, int EPW, bool FULL = false>
 __device__ __forceinline__ void router_logits_block(const float* __restrict__ x, const float* __restrict__ wr, int T,
                                                     int H, int E, float* __restrict__ logits, int block) {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -105,9 +112,7 @@ __device__ __forceinline__ void router_logits_block(const float* __restrict__ x,
     for (int t = 0; t < TPW; t++)
 #pragma unroll
         for (int e = 0; e < EPW; e++) acc[t][e] = 0.0f;
-    // chunks in flight: about 144 VGPRs of staged operands
-    constexpr int PER = 4 * (TPW + EPW);
-    constexpr int D = 144 / PER >= 8 ? 8 : (144 / PER < 2 ? 2 : 144 / PER);
+    constexpr int D = router_depth(TPW, EPW);
     const int nch = (H + 4 * WAVE - 1) / (4 * WAVE);
     float4 xb[D][TPW], wb[D][EPW];
     // chunk i of this lane: elements h0 = 4 lane + 256 i .. + 3 (H % 4 == 0: a lane's
@@ -140,7 +145,7 @@ __device__ __forceinline__ void router_logits_block(const float* __restrict__ x,
             __builtin_amdgcn_sched_barrier(0);  // keep the refill ahead of the math
             // chunk past the lane's end: the accumulators keep their values (a select,
             // not a branch, so no wait is forced on the loads in flight)
-            const bool ok = i < nch && 4 * lane + 4 * WAVE * i < H;
+            const bool ok = FULL || (i < nch && 4 * lane + 4 * WAVE * i < H);
 #pragma unroll
             for (int t = 0; t < TPW; t++)
 #pragma unroll
@@ -172,10 +177,10 @@ __device__ __forceinline__ void router_logits_block(const float* __restrict__ x,
     }
 }
 
-template <int TPW, int EPW>
+template <int TPW, int EPW, bool FULL = false>
 __global__ __launch_bounds__(ROUTER_WAVES * WAVE) void router_logits_kernel(
     const float* __restrict__ x, const float* __restrict__ wr, int T, int H, int E, float* __restrict__ logits) {
-    router_logits_block<TPW, EPW>(x, wr, T, H, E, logits, (int)blockIdx.x);
+    router_logits_block<TPW, EPW, FULL>(x, wr, T, H, E, logits, (int)blockIdx.x);
 }
 
 // Top-k + weights per token (one wave each), optionally quantizing the token's
@@ -255,10 +260,19 @@ hipError_t launch_router_q(const float* x, const float* wr, int T, int H, int E,
     } else if (T <= 32) {
         hipLaunchKernelGGL((router_logits_kernel<8, 1>), grid_for(8, 1), blk, 0, s, x, wr, T, H, E, logits);
     } else {
-        if (T >= 2048)
-            hipLaunchKernelGGL((router_logits_kernel<8, 8>), grid_for(8, 8), blk, 0, s, x, wr, T, H, E, logits);
-        else
-            hipLaunchKernelGGL((router_logits_kernel<4, 8>), grid_for(4, 8), blk, 0, s, x, wr, T, H, E, logits);
+        // full chunks: H a multiple of D x 256 elements
+        auto full = [&](int d) { return H % (4 * WAVE * d) == 0; };
+        if (T >= 2048) {
+            if (full(router_depth(8, 8)))
+                hipLaunchKernelGGL((router_logits_kernel<8, 8, true>), grid_for(8, 8), blk, 0, s, x, wr, T, H, E, logits);
+            else
+                hipLaunchKernelGGL((router_logits_kernel<8, 8>), grid_for(8, 8), blk, 0, s, x, wr, T, H, E, logits);
+        } else {
+            if (full(router_depth(4, 8)))
+                hipLaunchKernelGGL((router_logits_kernel<4, 8, true>), grid_for(4, 8), blk, 0, s, x, wr, T, H, E, logits);
+            else
+                hipLaunchKernelGGL((router_logits_kernel<4, 8>), grid_for(4, 8), blk, 0, s, x, wr, T, H, E, logits);
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || logits_only) return e;
