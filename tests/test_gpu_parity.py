@@ -136,7 +136,8 @@ def test_block_dots_rejects_bad_path(gpu):
 
 @pytest.mark.parametrize("T,H,E,K", [(37, 4096, 64, 8), (5, 256, 16, 4), (1, 4096, 64, 8), (64, 512, 8, 2),
                                    (2, 196, 64, 8), (4, 324, 16, 4), (100, 452, 64, 8), (33, 68, 12, 2),
-                                   (512, 4096, 64, 8)])
+                                   (512, 4096, 64, 8), (300, 768, 64, 8), (2048, 1024, 64, 8),
+                                   (2050, 452, 40, 8)])
 def test_router_logits_and_indices_bit_exact(gpu, T, H, E, K):
     x = O.synth(3, 0, O.T_X, 0, (T, H), 1.0)
     wr = O.synth(3, 0, O.T_ROUTER, 0, (E, H), 0.02)
