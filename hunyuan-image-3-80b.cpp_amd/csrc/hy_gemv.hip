@@ -262,11 +262,12 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 // Quantized weights (Q8_0 / Q4_0): the same per-row block-sequential accumulation as
 // gemv_kernel, with the operand streams decoupled from the arithmetic.  Each work
 // group is one wave owning one 64-row group of one tile (<= NT tokens).  A private LDS
-// ring holds NSTEP steps; a step is GQ_U = 8 consecutive blocks:
-//   weights  GQ_U x (64 rows x 16 B / 32 B)   one DMA per block (two for Q8_0)
-//   scales   GQ_U x 64 fp16                   one 1 KB DMA (contiguous in the plane)
-//   x        NT tokens x GQ_U x 32 B int8     one DMA (token = lane / 16)
-//   x scales / block sums  NT x GQ_U x 4 B    one DMA (lanes 0..31 / 32..63)
+// ring holds NSTEP steps; a step is U (8, or 4 when a launch's waves outnumber the LDS
+// slots) consecutive blocks:
+//   weights  U x (64 rows x 16 B / 32 B)      one DMA per block (two for Q8_0)
+//   scales   U x 64 fp16                      one DMA (contiguous in the plane)
+//   x        NT tokens x U x 32 B int8        one DMA (token = lane / (2 U))
+//   x scales / block sums  NT x U x 4 B       one DMA (lanes 0..NT U-1 / NT U..2 NT U-1)
 // Token slots past the tile's n read token 0's row (valid, never used), so every
 // step issues the same number of copies and the vmcnt waits are constants.  Copies
 // complete in order; no barrier is needed because a wave only reads what it copied.
@@ -275,30 +276,38 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 // first copies; the first activation copies follow, and one full wait joins both.
 // The last NSTEP steps are consumed by an unrolled tail whose waits count down to
 // zero: the wave leaves no copy in flight.
-constexpr int GQ_U = 8;       // blocks per step
+constexpr int GQ_U = 8;       // blocks per step (GQ_U_SMALL when waves outnumber the LDS slots)
+constexpr int GQ_U_SMALL = 4;
+constexpr int GQ_U_TINY = 2;
 constexpr int GQ_WAVES = 1;   // one wave per work group: work groups spread over every CU
 constexpr int GQ_THREADS = GQ_WAVES * WAVE;
 
-// Ring depth: Q4_0 3 steps (31 KB of LDS, 5 waves a CU), Q8_0 2 (37 KB, 4 a CU); copies
-// in flight <= 36 < 64 (vmcnt).  A launch with more waves than the deeper ring leaves
-// resident takes 2 steps for Q4_0 (21 KB, 7 a CU): one round of waves instead of a
-// second, short one (T=2: 15 tiles x 96 row groups = 1,440 waves for 1,280 slots).
+// Ring depth: Q4_0 3 steps of 8 blocks (31 KB of LDS, 5 waves a CU), Q8_0 2 (37 KB, 4 a
+// CU); copies in flight <= 36 < 64 (vmcnt).  A launch with more waves than the deeper
+// ring leaves resident takes 2 steps for Q4_0 (21 KB, 7 a CU): one round of waves
+// instead of a second, short one (T=2: 15 tiles x 96 row groups = 1,440 waves for 1,280
+// slots); larger launches take 2 steps of 4 blocks (Q4_0 10 KB, 15 a CU) or 2 blocks
+// (5 KB, 31 a CU) when that keeps every wave resident (gemv_launch).
 template <int WT>
 struct GqSteps {
     static constexpr int value = WT == HY_TYPE_Q4_0 ? 3 : 2;
 };
 
-template <int WT, int NT>
+template <int WT, int NT, int U>
 struct GqSlot {
     static constexpr int BPB = WT == HY_TYPE_Q4_0 ? 16 : 32;
     static constexpr int W = 0;                             // weights
-    static constexpr int S = W + GQ_U * 64 * BPB;           // weight scales
-    static constexpr int X = S + GQ_U * 64 * 2;             // activation quants
-    static constexpr int XD = X + NT * GQ_U * QK;           // activation scales, then block sums
-    static constexpr int BYTES = XD + 2 * NT * GQ_U * 4;
-    static constexpr int LOADS = GQ_U * (WT == HY_TYPE_Q4_0 ? 1 : 2) + 1 + 1 + 1;
-    static_assert(NT * GQ_U * QK == WAVE * 16, "one 16-byte copy per lane moves the step's activations");
-    static_assert(2 * NT * GQ_U == WAVE, "one 4-byte copy per lane moves the step's scales and sums");
+    static constexpr int S = W + U * 64 * BPB;              // weight scales
+    static constexpr int X = S + U * 64 * 2;                // activation quants
+    static constexpr int XD = X + NT * U * QK;              // activation scales, then block sums
+    static constexpr int BYTES = XD + 2 * NT * U * 4;
+    static constexpr int LOADS = U * (WT == HY_TYPE_Q4_0 ? 1 : 2) + 1 + 1 + 1;
+    // lanes that carry a copy: weight scales (16 B each), activations (16 B each), their
+    // scales and block sums (4 B each); the other lanes are masked
+    static constexpr int SC_LANES = U * 64 * 2 / 16, X_LANES = NT * U * QK / 16, XD_LANES = 2 * NT * U;
+    static_assert(U == 2 || U == 4 || U == 8, "steps of 2, 4 or 8 blocks");
+    static_assert(SC_LANES <= WAVE && X_LANES <= WAVE && XD_LANES <= WAVE, "one copy per lane moves each part");
+    static_assert(X_LANES % NT == 0, "whole token rows per copy");
 };
 
 // One-token routing inside the gate/up GEMV (launch_gemv_up_route1): the wave selects
@@ -372,11 +381,11 @@ __device__ __forceinline__ void gemv_tail(F& step, int base) {
     }
 }
 
-template <int WT, int NT, int MODE, int NSTEP, bool R1 = false>
+template <int WT, int NT, int MODE, int NSTEP, bool R1 = false, int U = GQ_U>
 __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     static_assert(!R1 || MODE == 0, "routing inside the launch: gate/up only");
     static_assert(MODE == 0 || MODE == 1, "routed/shared products only (the combine runs separately)");
-    using SL = GqSlot<WT, NT>;
+    using SL = GqSlot<WT, NT, U>;
     constexpr bool Q4 = WT == HY_TYPE_Q4_0;
     constexpr int BPB = SL::BPB;
     constexpr int WBYTES = 64 * BPB;  // one block of a 64-row group
@@ -388,7 +397,7 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     // their heavier waves do not form the launch's tail
     const int G = blockIdx.x;  // 64-row group (grid.x == n_groups)
     const int tile = (int)gridDim.y - 1 - (int)blockIdx.y;
-    const int Kd = a.Kd, nb = Kd / QK, nsteps = nb / GQ_U;
+    const int Kd = a.Kd, nb = Kd / QK, nsteps = nb / U;
 
     // start the weight stream first: tile_e[tile] is in the arena for every launched
     // tile; a stale entry (tile past this call's count) is clamped into the table and
@@ -406,13 +415,13 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     const uint16_t* wsc = a.W.sc + (size_t)e * a.W.sc_stride + (size_t)G * nb * 64 + lane * 8;
     auto issue_w = [&](int st_i) {
         uint8_t* st = ring + (st_i % NSTEP) * SL::BYTES;
-        const uint8_t* src = wq + (size_t)st_i * GQ_U * WBYTES;
+        const uint8_t* src = wq + (size_t)st_i * U * WBYTES;
 #pragma unroll
-        for (int u = 0; u < GQ_U; u++) {
+        for (int u = 0; u < U; u++) {
             g2l16_nt(src + u * WBYTES, st + SL::W + u * WBYTES);
             if (!Q4) g2l16_nt(src + u * WBYTES + 1024, st + SL::W + u * WBYTES + 1024);
         }
-        g2l16_nt(wsc + (size_t)st_i * GQ_U * 64, st + SL::S);
+        if (SL::SC_LANES == WAVE || lane < SL::SC_LANES) g2l16_nt(wsc + (size_t)st_i * U * 64, st + SL::S);
     };
 #pragma unroll
     for (int s = 0; s < NSTEP; s++) issue_w(s);
@@ -442,21 +451,26 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
         slot_s[lane] = slot;
     }
     __syncthreads();
-    // this lane's activation sources: x piece (token lane/16, 16 B piece lane%16 of the
-    // step's 256 B) and the scale (lanes < 32) or block sum (lanes >= 32) of token
-    // (lane%32)/8, block lane%8; token slots >= n read token 0's row
-    const int xt = lane / 16, st_tok = (lane % 32) / 8;
+    // this lane's activation sources: x piece (token lane / PPT, 16 B piece lane % PPT
+    // of the step's U * 32 B per token) and the scale (lanes < NT * U) or block sum
+    // (lanes NT * U .. 2 NT * U - 1) of token (lane % NT * U) / U, block lane % U; token
+    // slots >= n read token 0's row, lanes past a part's copy read in-range sources
+    constexpr int PPT = U * QK / 16, NTU = NT * U;
+    const int xt = lane / PPT;
+    const bool is_sum = lane >= NTU;
+    const int sidx = lane % NTU, st_tok = sidx / U;
     const int xrow = MODE == 0 ? tok_s[xt < n ? xt : 0] : slot_s[xt < n ? xt : 0];
     const int srow = MODE == 0 ? tok_s[st_tok < n ? st_tok : 0] : slot_s[st_tok < n ? st_tok : 0];
-    const int8_t* xsrc = a.aq + (size_t)xrow * Kd + (lane % 16) * 16;
-    const void* ssrc = lane < 32 ? (const void*)(a.ad + (size_t)srow * nb + lane % 8)
-                                 : (Q4 ? (const void*)(a.as + (size_t)srow * nb + lane % 8)
-                                       : (const void*)(a.ad + (size_t)srow * nb + lane % 8));
+    const int8_t* xsrc = a.aq + (size_t)xrow * Kd + (lane % PPT) * 16;
+    const void* ssrc = !is_sum ? (const void*)(a.ad + (size_t)srow * nb + sidx % U)
+                               : (Q4 ? (const void*)(a.as + (size_t)srow * nb + sidx % U)
+                                     : (const void*)(a.ad + (size_t)srow * nb + sidx % U));
     auto issue_x = [&](int st_i) {
         uint8_t* st = ring + (st_i % NSTEP) * SL::BYTES;
-        g2l16(xsrc + (size_t)st_i * GQ_U * QK, st + SL::X);
-        __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(ssrc) + (size_t)st_i * GQ_U * 4, st + SL::XD, 4, 0,
-                                         0);
+        if (SL::X_LANES == WAVE || lane < SL::X_LANES) g2l16(xsrc + (size_t)st_i * U * QK, st + SL::X);
+        if (SL::XD_LANES == WAVE || lane < SL::XD_LANES)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(ssrc) + (size_t)st_i * U * 4, st + SL::XD, 4,
+                                             0, 0);
     };
 #pragma unroll
     for (int s = 0; s < NSTEP; s++) issue_x(s);
@@ -471,33 +485,33 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
         const uint32_t st = lds_off(ring + (st_i % NSTEP) * SL::BYTES);
         const uint32_t wrow = st + SL::W + lane * BPB;
         const uint32_t srow_l = st + SL::S + lane * 2;
-        v4i_t w0[GQ_U], w1[GQ_U], wlo[GQ_U], whi[GQ_U];
-        uint32_t dwb[GQ_U];
-        float dwf[GQ_U];
-        [&]<int... U>(std::integer_sequence<int, U...>) {
-            ((w0[U] = lds_b128_at<U * WBYTES>(wrow)), ...);
-            if constexpr (!Q4) ((w1[U] = lds_b128_at<U * WBYTES + 16>(wrow)), ...);
-            ((dwb[U] = lds_u16_at<U * 128>(srow_l)), ...);
-        }(std::make_integer_sequence<int, GQ_U>{});
+        v4i_t w0[U], w1[U], wlo[U], whi[U];
+        uint32_t dwb[U];
+        float dwf[U];
+        [&]<int... UU>(std::integer_sequence<int, UU...>) {
+            ((w0[UU] = lds_b128_at<UU * WBYTES>(wrow)), ...);
+            if constexpr (!Q4) ((w1[UU] = lds_b128_at<UU * WBYTES + 16>(wrow)), ...);
+            ((dwb[UU] = lds_u16_at<UU * 128>(srow_l)), ...);
+        }(std::make_integer_sequence<int, U>{});
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (i < n) {
-                const uint32_t xb = st + SL::X + i * GQ_U * QK;
-                const uint32_t db = st + SL::XD + i * GQ_U * 4;
-                v4i_t x0[GQ_U], x1[GQ_U];
-                uint32_t xdb[GQ_U], xsb[GQ_U];
-                [&]<int... U>(std::integer_sequence<int, U...>) {
-                    ((x0[U] = lds_b128_at<U * QK>(xb)), ...);
-                    ((x1[U] = lds_b128_at<U * QK + 16>(xb)), ...);
-                    ((xdb[U] = lds_b32_at<U * 4>(db)), ...);
-                    if constexpr (Q4) ((xsb[U] = lds_b32_at<NT * GQ_U * 4 + U * 4>(db)), ...);
-                }(std::make_integer_sequence<int, GQ_U>{});
+                const uint32_t xb = st + SL::X + i * U * QK;
+                const uint32_t db = st + SL::XD + i * U * 4;
+                v4i_t x0[U], x1[U];
+                uint32_t xdb[U], xsb[U];
+                [&]<int... UU>(std::integer_sequence<int, UU...>) {
+                    ((x0[UU] = lds_b128_at<UU * QK>(xb)), ...);
+                    ((x1[UU] = lds_b128_at<UU * QK + 16>(xb)), ...);
+                    ((xdb[UU] = lds_b32_at<UU * 4>(db)), ...);
+                    if constexpr (Q4) ((xsb[UU] = lds_b32_at<NTU * 4 + UU * 4>(db)), ...);
+                }(std::make_integer_sequence<int, U>{});
                 lds_wait();
                 if (i == 0) {
                     // weight-side work shared by the tile's tokens: Q4_0 nibbles unpacked
                     // and fp16 scales converted once per block
 #pragma unroll
-                    for (int u = 0; u < GQ_U; u++) {
+                    for (int u = 0; u < U; u++) {
                         lds_pin(w0[u]);
                         if (!Q4) lds_pin(w1[u]);
                         lds_pin(dwb[u]);
@@ -513,7 +527,7 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < GQ_U; u++) {
+                for (int u = 0; u < U; u++) {
                     lds_pin(x0[u]);
                     lds_pin(x1[u]);
                     lds_pin(xdb[u]);
@@ -634,28 +648,53 @@ size_t gemv_smem(int wtype, int Kd) {
 }
 
 // LDS of gemv_q_kernel: a ring of NSTEP steps
-template <int WT>
+template <int WT, int U = GQ_U>
 static size_t gemv_q_smem(int nstep) {
-    return (size_t)nstep * GqSlot<WT, GEMV_NT>::BYTES;
+    return (size_t)nstep * GqSlot<WT, GEMV_NT, U>::BYTES;
 }
 
-template <int WT>
+template <int WT, int U = GQ_U>
 static bool gemv_q_fits(int Kd) {
     const int nb = Kd / QK;
-    return nb % GQ_U == 0 && nb / GQ_U >= GqSteps<WT>::value;
+    return nb % U == 0 && nb / U >= GqSteps<WT>::value;
 }
 
 // resident one-wave work groups per CU at this LDS footprint (160 KB of LDS a CU)
-static int gemv_q_slots(size_t smem) { return 256 * (int)((160u * 1024u) / smem); }
+static int gemv_q_slots(size_t smem) {
+    const int per_cu = (int)((160u * 1024u) / smem);
+    return 256 * (per_cu < 32 ? per_cu : 32);  // at most 32 one-wave work groups a CU (8 waves a SIMD)
+}
 
 template <int MODE>
 static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
     a.nx = a.T < GEMV_NT ? a.T : GEMV_NT;
     const dim3 grid_v((a.n_groups + GV_WAVES - 1) / GV_WAVES, tiles);
     const dim3 grid_q(a.n_groups, tiles);
+    // tiles is the host's bound on the routed + shared tiles.  Steps of 4 or 2 blocks (2x /
+    // 4x the resident waves) when the smaller steps, and not the larger ones, hold the
+    // whole launch at once (Q4_0 steps: T=4 125.4-127.7 -> 119.3-120.2 us, T=6 161.5-165.1
+    // -> 154.3-157.5, T=8 184.0-192.9 -> 174.6-181.9); a launch too large for every size
+    // stays on 8-block steps (T=8 on 4-block steps: 185.9-189.7 against 184.8-186.5 us)
+    const long waves = (long)tiles * a.n_groups;
+    auto small_steps = [&](auto wt) {
+        constexpr int WT = decltype(wt)::value;
+        return gemv_q_fits<WT, GQ_U_SMALL>(a.Kd) && waves > gemv_q_slots(gemv_q_smem<WT>(2)) &&
+               waves <= gemv_q_slots(gemv_q_smem<WT, GQ_U_SMALL>(2));
+    };
+    auto tiny_steps = [&](auto wt) {
+        constexpr int WT = decltype(wt)::value;
+        return gemv_q_fits<WT, GQ_U_TINY>(a.Kd) && waves > gemv_q_slots(gemv_q_smem<WT, GQ_U_SMALL>(2)) &&
+               waves <= gemv_q_slots(gemv_q_smem<WT, GQ_U_TINY>(2));
+    };
     switch (wtype) {
     case HY_TYPE_Q8_0:
-        if (gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
+        if (tiny_steps(std::integral_constant<int, HY_TYPE_Q8_0>{}))
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE, 2, false, GQ_U_TINY>), grid_q,
+                               dim3(GQ_THREADS), (gemv_q_smem<HY_TYPE_Q8_0, GQ_U_TINY>(2)), s, a);
+        else if (small_steps(std::integral_constant<int, HY_TYPE_Q8_0>{}))
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE, 2, false, GQ_U_SMALL>), grid_q,
+                               dim3(GQ_THREADS), (gemv_q_smem<HY_TYPE_Q8_0, GQ_U_SMALL>(2)), s, a);
+        else if (gemv_q_fits<HY_TYPE_Q8_0>(a.Kd))
             hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q8_0, GEMV_NT, MODE, 2>), grid_q, dim3(GQ_THREADS),
                                gemv_q_smem<HY_TYPE_Q8_0>(2), s, a);
         else
@@ -663,11 +702,16 @@ static hipError_t gemv_launch(int wtype, int tiles, hipStream_t s, GvArgs a) {
                                gemv_smem(wtype, a.Kd), s, a);
         break;
     case HY_TYPE_Q4_0:
-        if (gemv_q_fits<HY_TYPE_Q4_0>(a.Kd)) {
-            // tiles is the host's bound on the routed + shared tiles: the deeper ring
-            // for gate/up when every launched wave is resident at once; the down
-            // products take 2 steps (T=2: 23.9 -> 22.8 us, T=1 and T=4 unchanged)
-            if (MODE == 0 && (long)tiles * a.n_groups <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3)))
+        if (tiny_steps(std::integral_constant<int, HY_TYPE_Q4_0>{})) {
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE, 2, false, GQ_U_TINY>), grid_q,
+                               dim3(GQ_THREADS), (gemv_q_smem<HY_TYPE_Q4_0, GQ_U_TINY>(2)), s, a);
+        } else if (small_steps(std::integral_constant<int, HY_TYPE_Q4_0>{})) {
+            hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE, 2, false, GQ_U_SMALL>), grid_q,
+                               dim3(GQ_THREADS), (gemv_q_smem<HY_TYPE_Q4_0, GQ_U_SMALL>(2)), s, a);
+        } else if (gemv_q_fits<HY_TYPE_Q4_0>(a.Kd)) {
+            // the deeper ring for gate/up when every launched wave is resident at once; the
+            // down products take 2 steps (T=2: 23.9 -> 22.8 us, T=1 and T=4 unchanged)
+            if (MODE == 0 && waves <= gemv_q_slots(gemv_q_smem<HY_TYPE_Q4_0>(3)))
                 hipLaunchKernelGGL((gemv_q_kernel<HY_TYPE_Q4_0, GEMV_NT, MODE, 3>), grid_q, dim3(GQ_THREADS),
                                    gemv_q_smem<HY_TYPE_Q4_0>(3), s, a);
             else

@@ -30,16 +30,23 @@ def ctxs(gpu, full_layers):
         m.close()
 
 
-@pytest.mark.parametrize("T", [1, 2, 4, 8])
-def test_decode_q4_0_full_shape(gpu, full_layers, ctxs, T):
-    """Bit-exact decode; T=1 runs the up GEMV with the 3-step ring (864 waves), T >= 2
-    with the 2-step ring (more waves than the 3-step ring keeps resident)."""
+@pytest.mark.parametrize("wt,T", [(O.Q4_0, 1), (O.Q4_0, 2), (O.Q4_0, 3), (O.Q4_0, 4), (O.Q4_0, 6), (O.Q4_0, 8),
+                                   (O.Q8_0, 2), (O.Q8_0, 4), (O.Q8_0, 8)])
+def test_decode_full_shape(gpu, full_layers, ctxs, wt, T):
+    """Bit-exact decode at every ring-step size the launcher picks from the launch's
+    wave bound (row groups x tile bound; 64 + 1 experts, top-8, 4-token tiles):
+    Q4_0 T=1: 864 gate/up waves, 8-block steps (the one-token routed launch);
+    T=2: 1,632, 8-block steps; T=3: 2,400 gate/up on 4-block steps, 1,600 down on 8;
+    T=4: 3,168 / 2,112 on 4-block steps; T=6: 4,800 gate/up on 2-block steps, 3,200 down
+    on 4; T=8: 6,336 / 4,224 on 2-block steps.  Q8_0 T=2: 1,632 / 1,088 on 4-block
+    steps; T=4: 3,168 / 2,112 on 2-block steps; T=8: 6,336 gate/up on 8-block steps
+    (more waves than any step size keeps resident), 4,224 down on 2-block steps."""
     x = O.synth(100 + T, 0, O.T_X, 0, (T, H), 1.0)
-    out, lg, w, idx = ctxs[O.Q4_0].run(0, x, debug=True)
-    ref, rlg, rw, ridx = O.moe_forward_q(full_layers[O.Q4_0], x, debug=True, nthreads=16)
+    out, lg, w, idx = ctxs[wt].run(0, x, debug=True)
+    ref, rlg, rw, ridx = O.moe_forward_q(full_layers[wt], x, debug=True, nthreads=16)
     np.testing.assert_array_equal(lg.view(np.uint32), rlg.view(np.uint32))
     np.testing.assert_array_equal(idx, ridx)
-    assert_exact(out, ref, f"decode T={T}")
+    assert_exact(out, ref, f"decode wt={wt} T={T}")
 
 
 @pytest.mark.parametrize("wt,T", [(O.Q8_0, 512), (O.Q4_0, 4096), (O.Q8_0, 100)])
