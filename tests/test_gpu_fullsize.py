@@ -31,16 +31,17 @@ def ctxs(gpu, full_layers):
 
 
 @pytest.mark.parametrize("wt,T", [(O.Q4_0, 1), (O.Q4_0, 2), (O.Q4_0, 3), (O.Q4_0, 4), (O.Q4_0, 6), (O.Q4_0, 8),
-                                   (O.Q8_0, 2), (O.Q8_0, 4), (O.Q8_0, 8)])
+                                   (O.Q4_0, 16), (O.Q8_0, 2), (O.Q8_0, 4), (O.Q8_0, 8)])
 def test_decode_full_shape(gpu, full_layers, ctxs, wt, T):
     """Bit-exact decode at every ring-step size the launcher picks from the launch's
-    wave bound (row groups x tile bound; 64 + 1 experts, top-8, 4-token tiles):
-    Q4_0 T=1: 864 gate/up waves, 8-block steps (the one-token routed launch);
-    T=2: 1,632, 8-block steps; T=3: 2,400 gate/up on 4-block steps, 1,600 down on 8;
-    T=4: 3,168 / 2,112 on 4-block steps; T=6: 4,800 gate/up on 2-block steps, 3,200 down
-    on 4; T=8: 6,336 / 4,224 on 2-block steps.  Q8_0 T=2: 1,632 / 1,088 on 4-block
-    steps; T=4: 3,168 / 2,112 on 2-block steps; T=8: 6,336 gate/up on 8-block steps
-    (more waves than any step size keeps resident), 4,224 down on 2-block steps."""
+    wave bound (row groups x tile bound; 64 + 1 experts, top-8, 4-token tiles).
+    Q4_0: T=1 864 gate/up waves on 8-block steps (the one-token routed launch); T=2
+    1,632 on 8-block steps; T=3 2,400 gate/up on 4-block steps, 1,600 down on 8; T=4
+    3,168 / 2,112 on 4-block steps; T=6 4,800 gate/up on 2-block steps, 3,200 down on 4;
+    T=8 6,336 / 4,224 on 2-block steps; T=16 8,064 gate/up on 8-block steps (more waves
+    than any step size keeps resident), 5,376 down on 2-block steps.  Q8_0: T=2 1,632 /
+    1,088 on 4-block steps; T=4 3,168 / 2,112 on 2-block steps; T=8 6,336 gate/up on
+    8-block steps, 4,224 down on 2-block steps."""
     x = O.synth(100 + T, 0, O.T_X, 0, (T, H), 1.0)
     out, lg, w, idx = ctxs[wt].run(0, x, debug=True)
     ref, rlg, rw, ridx = O.moe_forward_q(full_layers[wt], x, debug=True, nthreads=16)
