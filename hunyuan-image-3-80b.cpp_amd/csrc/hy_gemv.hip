@@ -64,9 +64,9 @@ __device__ __forceinline__ int dot_q4_block(const int4 w, const int4 a0, const i
 struct GvArgs {
     MatView W;
     Routing R;
-    const int8_t* aq;   // activations: x (mode 0) or h (modes 1, 2), int8 [rows][Kd]
-    const float* ad;    // scales [rows][Kd/32]
-    const int* as;      // block sums [rows][Kd/32]
+    const int8_t* aq;   // activations int8: x [T][H] (mode 0); h block-major [I/32][slots][32] (mode 1)
+    const float* ad;    // their scales: x [T][H/32]; h [I/32][slots]
+    const int* as;      // their block sums, laid out as the scales
     const float* af;    // f32 activations (F32 weights): x or hf
     int T, H, I, E, K;
     int Kd;             // reduction length
@@ -79,6 +79,9 @@ struct GvArgs {
     float* y;           // mode 1 output
     Route1Out r1;       // one-token batches routed inside the gate/up GEMV (launch_gemv_up_route1)
 };
+
+// rows of the block-major h planes: every routed pair's slot and the shared expert's T
+__device__ __forceinline__ int h_slots(const GvArgs& a) { return a.T * a.K + a.T; }
 
 template <int WT, int NT, int MODE>
 __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
@@ -119,15 +122,17 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
             int4 val = make_int4(0, 0, 0, 0);
             if (i < n) {
                 const int row = MODE == 0 ? tok_s[i] : slot_s[i];
-                val = reinterpret_cast<const int4*>(a.aq + (size_t)row * Kd)[c];
+                val = MODE == 0 ? reinterpret_cast<const int4*>(a.aq + (size_t)row * Kd)[c]
+                                : reinterpret_cast<const int4*>(a.aq + ((size_t)(c / 2) * h_slots(a) + row) * QK)[c % 2];
             }
             reinterpret_cast<int4*>(xs_l + (size_t)i * Kd)[c] = val;
         }
         for (int v = threadIdx.x; v < NT * nb; v += GV_THREADS) {
             const int i = v / nb, b = v % nb;
             const int row = MODE == 0 ? tok_s[i] : slot_s[i];
-            xd_l[v] = i < n ? a.ad[(size_t)row * nb + b] : 0.0f;
-            if (WT == HY_TYPE_Q4_0) xsum_l[v] = i < n ? a.as[(size_t)row * nb + b] : 0;
+            const size_t si = MODE == 0 ? (size_t)row * nb + b : (size_t)b * h_slots(a) + row;
+            xd_l[v] = i < n ? a.ad[si] : 0.0f;
+            if (WT == HY_TYPE_Q4_0) xsum_l[v] = i < n ? a.as[si] : 0;
         }
     }
     __syncthreads();
@@ -241,10 +246,11 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 #pragma unroll
                 for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
                 if (lane < 32) {
-                    a.hq[slot * a.I + (size_t)G * QK + lane] = r.q;
+                    const size_t hi = (size_t)G * h_slots(a) + slot;  // block-major h
+                    a.hq[hi * QK + lane] = r.q;
                     if (lane == 0) {
-                        a.hd[slot * nb_i + G] = h2f(r.dh);
-                        a.hs[slot * nb_i + G] = s;
+                        a.hd[hi] = h2f(r.dh);
+                        a.hs[hi] = s;
                     }
                 }
             }
@@ -461,15 +467,20 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
     const int sidx = lane % NTU, st_tok = sidx / U;
     const int xrow = MODE == 0 ? tok_s[xt < n ? xt : 0] : slot_s[xt < n ? xt : 0];
     const int srow = MODE == 0 ? tok_s[st_tok < n ? st_tok : 0] : slot_s[st_tok < n ? st_tok : 0];
-    const int8_t* xsrc = a.aq + (size_t)xrow * Kd + (lane % PPT) * 16;
-    const void* ssrc = !is_sum ? (const void*)(a.ad + (size_t)srow * nb + sidx % U)
-                               : (Q4 ? (const void*)(a.as + (size_t)srow * nb + sidx % U)
-                                     : (const void*)(a.ad + (size_t)srow * nb + sidx % U));
+    // mode 1 reads h block-major: block b of slot r at (b * slots + r) * 32, its scale and
+    // sum at b * slots + r; a step advances U block planes
+    const size_t hs_n = MODE == 0 ? 1 : (size_t)h_slots(a);
+    const int8_t* xsrc = MODE == 0 ? a.aq + (size_t)xrow * Kd + (lane % PPT) * 16
+                                   : a.aq + ((size_t)((lane % PPT) / 2) * hs_n + xrow) * QK + (lane % 2) * 16;
+    const size_t sofs = MODE == 0 ? (size_t)srow * nb + sidx % U : (size_t)(sidx % U) * hs_n + srow;
+    const void* ssrc = !is_sum ? (const void*)(a.ad + sofs)
+                               : (Q4 ? (const void*)(a.as + sofs) : (const void*)(a.ad + sofs));
+    const size_t x_step = (size_t)U * QK * hs_n, s_step = (size_t)U * 4 * hs_n;  // bytes per step
     auto issue_x = [&](int st_i) {
         uint8_t* st = ring + (st_i % NSTEP) * SL::BYTES;
-        if (SL::X_LANES == WAVE || lane < SL::X_LANES) g2l16(xsrc + (size_t)st_i * U * QK, st + SL::X);
+        if (SL::X_LANES == WAVE || lane < SL::X_LANES) g2l16(xsrc + (size_t)st_i * x_step, st + SL::X);
         if (SL::XD_LANES == WAVE || lane < SL::XD_LANES)
-            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(ssrc) + (size_t)st_i * U * 4, st + SL::XD, 4,
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(ssrc) + (size_t)st_i * s_step, st + SL::XD, 4,
                                              0, 0);
     };
 #pragma unroll
@@ -575,10 +586,11 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 #pragma unroll
             for (int m = 16; m >= 1; m >>= 1) s += shfl_xor(s, m, 32);
             if (lane < 32) {
-                a.hq[slot * a.I + (size_t)G * QK + lane] = r.q;
+                const size_t hi = (size_t)G * h_slots(a) + slot;  // block-major h
+                a.hq[hi * QK + lane] = r.q;
                 if (lane == 0) {
-                    a.hd[slot * nb_i + G] = h2f(r.dh);
-                    a.hs[slot * nb_i + G] = s;
+                    a.hd[hi] = h2f(r.dh);
+                    a.hs[hi] = s;
                 }
             }
         }

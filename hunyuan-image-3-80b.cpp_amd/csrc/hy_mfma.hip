@@ -93,8 +93,8 @@ using ShapeTall = MmShape<256, 64, 2>;
 struct MmArgs {
     MatView W;
     Routing R;
-    const int8_t* aq;   // activations int8 [rows][Kdim] (x for mode 0, h for modes 1/2)
-    const float* ad;    // activation scales [rows][Kdim/32] (exact fp16 values)
+    const int8_t* aq;   // activations int8: x [T][H] (mode 0); h block-major [I/32][slots][32] (mode 1)
+    const float* ad;    // their scales (exact fp16 values): x [T][H/32]; h [I/32][slots]
     int T, H, I, E, K;
     int Kdim;           // reduction length (H for mode 0, I for modes 1/2)
     int nrb;            // row blocks of the weight matrix
@@ -239,26 +239,35 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
                              half * (64 / WPC);
     // B rows: wave w copies block w % KB of tokens (w / KB) * TPW .. + TPW, as 16-byte
     // pieces; lane position p (copy v, lane l: p = 64 v + l) lands at +16 p, i.e. token
-    // row p / 2, position p % 2, which holds half (p % 2) ^ (bit 3 of the row)
+    // row p / 2, position p % 2, which holds half (p % 2) ^ (bit 3 of the row).  Mode 0
+    // gathers x rows [T][H]; mode 1 reads h block-major ([I/32][slots][32 B]), where the
+    // tile's consecutive slots are consecutive 32-byte pieces of one block plane, so each
+    // copy reads one contiguous 1 KB (the per-stage step is kb0 planes)
     constexpr int TPW = SH::TPW;
+    const uint32_t n_slots = (uint32_t)(a.T * a.K + a.T);  // rows of the h planes
     uint32_t b_off[SH::B_LOADS];  // 32-bit: the host keeps rows x Kd below 2^32
 #pragma unroll
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
         const int bt = (wave / MM_KB) * TPW + (p % SH::B_LANES) / 2;  // in range for masked lanes too
-        b_off[v] = (uint32_t)(MODE == 0 ? tok_s[bt] : slot_s[bt]) * (uint32_t)Kd + (wave % MM_KB) * 32 +
-                   swz_half(bt, p & 1);
+        b_off[v] = MODE == 0 ? (uint32_t)tok_s[bt] * (uint32_t)Kd + (wave % MM_KB) * 32 + swz_half(bt, p & 1)
+                             : ((uint32_t)(wave % MM_KB) * n_slots + (uint32_t)slot_s[bt]) * 32u + swz_half(bt, p & 1);
     }
+    const uint32_t b_step = MODE == 0 ? (uint32_t)QK : n_slots * 32u;  // bytes per block of the B source
     // A rows (int8): copy lane l lands at +16 l (row l / 2 of a 32-row piece, position
     // l % 2) and fetches half (l % 2) ^ (bit 3 of the row); Q4_0 nibbles are copied as
     // they are and swizzled when unpacked
     const uint32_t a_sw = (uint32_t)((lane / 2) * 32 + swz_half(lane / 2, lane & 1));
     // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each: KB = 4 as one
-    // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces
+    // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces (mode 1: the
+    // token's KB scales sit in KB block planes)
+    static_assert(MODE == 0 || MM_KB != 4, "block-major h scales: one 4-byte piece per (token, block)");
     constexpr int BS_LANES = MM_KB == 4 ? MM_TOK / MM_WAVES : MM_TOK / MM_WAVES * MM_KB;
     const int bst = wave * (MM_TOK / MM_WAVES) + (MM_KB == 4 ? lane : lane / MM_KB) % (MM_TOK / MM_WAVES);
     const uint32_t bs_off =
-        ((uint32_t)(MODE == 0 ? tok_s[bst] : slot_s[bst]) * (uint32_t)nb + (MM_KB == 4 ? 0 : lane % MM_KB)) * 4;
+        MODE == 0 ? ((uint32_t)tok_s[bst] * (uint32_t)nb + (MM_KB == 4 ? 0 : lane % MM_KB)) * 4
+                  : ((uint32_t)(lane % MM_KB) * n_slots + (uint32_t)slot_s[bst]) * 4;
+    const uint32_t bs_step = MODE == 0 ? 4u : n_slots * 4u;  // bytes per block of the B-scale source
 
     // issue the asynchronous copies of stage s into ring slot s % MM_RING; lanes
     // outside a copy's range are masked (the wave still issues it once)
@@ -282,16 +291,16 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         uint8_t* bdst = st + OFF_B + (wv % MM_KB) * (MM_TOK * 32) + (wv / MM_KB) * (TPW * 32);
 #pragma unroll
         for (int v = 0; v < SH::B_LOADS; v++)
-            if (v * WAVE + lane < SH::B_LANES) b2l(r_b, bdst + v * 1024, b_off[v], kb0 * QK);
+            if (v * WAVE + lane < SH::B_LANES) b2l(r_b, bdst + v * 1024, b_off[v], kb0 * b_step);
         // A scales of the chunk: 64 fp16 = 128 B (lanes 0..7), or its half (lanes 0..3)
         if (lane < 8 / WPC) b2l(r_as, st + OFF_AS + ch * 128 + half * (128 / WPC), 16u * lane, kb0 * 128u);
         // B scales of this wave's tokens
         uint8_t* sdst = st + OFF_BS + wv * (MM_TOK / MM_WAVES) * MM_KB * 4;
         if (lane < BS_LANES) {
             if (MM_KB == 4)
-                b2l(r_bs, sdst, bs_off, kb0 * 4u);
+                b2l(r_bs, sdst, bs_off, kb0 * bs_step);
             else
-                b2l<4>(r_bs, sdst, bs_off, kb0 * 4u);
+                b2l<4>(r_bs, sdst, bs_off, kb0 * bs_step);
         }
     };
 
@@ -462,14 +471,14 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
                 packed[g] = (int)p;
             }
             qsum += __shfl_xor(qsum, 32, WAVE);
-            const size_t slot = (size_t)slot_s[j];
-            int8_t* dst = a.hq + slot * a.I + (size_t)slab * QK;
+            // h block-major: block (slab) plane, slot row of 32 bytes
+            const size_t hi = (size_t)slab * (size_t)(a.T * a.K + a.T) + (size_t)slot_s[j];
+            int8_t* dst = a.hq + hi * QK;
 #pragma unroll
             for (int g = 0; g < 4; g++) *reinterpret_cast<int*>(dst + 8 * g + 4 * lg) = packed[g];
             if (lg == 0) {
-                const size_t nbi = a.I / QK;
-                a.hd[slot * nbi + slab] = h2f(f2h(d));
-                a.hs[slot * nbi + slab] = qsum;
+                a.hd[hi] = h2f(f2h(d));
+                a.hs[hi] = qsum;
             }
         } else {
             const int rbase = row0 + sl * 64;
