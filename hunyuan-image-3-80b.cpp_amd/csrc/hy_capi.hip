@@ -99,9 +99,11 @@ struct hy_moe_ctx {
     float* comb_w = nullptr;
     int *tile_e = nullptr, *tile_start = nullptr, *tile_n = nullptr, *meta = nullptr;
     int* dsp_scratch = nullptr;  // per-block counts of the dispatch
-    int8_t* hq = nullptr;
+    int8_t* hq = nullptr;  // h, block-major in slot order [I/32][T*K+T][32]
     float* hd = nullptr;
     int* hs = nullptr;
+    int8_t* xg = nullptr;  // the grouped GEMM's gathered x, block-major in slot order [H/32][T*K+T][32]
+    float* xgd = nullptr;
     float* hf = nullptr;
     float* y = nullptr;
     float* xn = nullptr;
@@ -290,10 +292,10 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int has_shared = c->cfg.has_shared ? 1 : 0;
     const int renorm = renorm_rule(c->cfg.norm_topk_prob, c->cfg.topk);
     // expert products: int8 MFMA grouped GEMM for batches, dequant-GEMV for decode.  The
-    // grouped GEMM addresses activation rows with 32-bit offsets: x by token (T x H
-    // bytes) and h by slot (T*(K+1) x I bytes) must stay below 2^32 (at I = 3072 any
-    // T <= 16384 with K <= 64); beyond that the GEMV, which computes the same bits, runs.
-    const bool mfma_fits = (uint64_t)T * (uint64_t)H < (1ull << 32) &&
+    // grouped GEMM addresses its slot-ordered operands with 32-bit offsets: the gathered
+    // x (T*(K+1) x H bytes) and h (T*(K+1) x I bytes) must stay below 2^32 (at H = 4096
+    // any T <= 16384 with K <= 62); beyond that the GEMV, which computes the same bits, runs.
+    const bool mfma_fits = (uint64_t)T * (uint64_t)(K + 1) * (uint64_t)H < (1ull << 32) &&
                            (uint64_t)T * (uint64_t)(K + 1) * (uint64_t)I < (1ull << 32);
     const bool mfma = c->path != HY_PATH_VALU && hy::mfma_path_ok(wt, H, I) && mfma_fits &&
                       (c->path == HY_PATH_MFMA || !gemv_batch(wt, T, K, E));
@@ -349,9 +351,12 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int routed_bound = tile_bound_routed(iT, K, E, NT);
     const int shared_tiles = has_shared ? (iT + NT - 1) / NT : 0;
     if (mfma) {
+        // the dispatched activations: x's Q8_0 rows copied into slot order, block-major
+        HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] { return hy::launch_gather_act(X, R, iT, K, H, c->xg, c->xgd, s); }));
+        const hy::ActQ XG{c->xg, c->xgd, nullptr, H};
         HY_TRY(timed(c, hy::KID_UP, s, [&] {
-            return hy::launch_ffn_up_mfma(wt, shape, routed_bound + shared_tiles, gu_view(c, L), R, X, iT, H, I, E, K, c->hq,
-                                          c->hd, c->hs, s);
+            return hy::launch_ffn_up_mfma(wt, shape, routed_bound + shared_tiles, gu_view(c, L), R, XG, iT, H, I, E, K,
+                                          c->hq, c->hd, c->hs, s);
         }));
         // routed and shared down products in one launch (y rows for every slot), then
         // the combine
@@ -523,6 +528,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
         {(void**)&c->tile_n, (size_t)c->max_tiles * 4}, {(void**)&c->meta, (size_t)hy::META_INTS * 4},
         {(void**)&c->hq, slots * I},       {(void**)&c->hd, slots * (I / 32) * 4},
         {(void**)&c->hs, slots * (I / 32) * 4},
+        {(void**)&c->xg, wt == HY_TYPE_F32 ? 16 : slots * H}, {(void**)&c->xgd, wt == HY_TYPE_F32 ? 16 : slots * (H / 32) * 4},
         {(void**)&c->hf, wt == HY_TYPE_F32 ? slots * I * 4 : 16},
         {(void**)&c->y, slots * H * 4},    {(void**)&c->xn, Tm * H * 4},
         {(void**)&c->cur, Tm * H * 4},

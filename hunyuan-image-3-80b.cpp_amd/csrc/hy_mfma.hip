@@ -84,7 +84,7 @@ struct MmShape {
     static_assert(RING >= 2, "at least one stage in flight while one is consumed");
     static_assert(TQ * 32 * TT == TOK, "token groups must cover the tile");
     static_assert(B_LANES % WAVE == 0 || B_LOADS == 1, "partial B loads only as a single load");
-    static_assert(KB == 4 || KB == 2 || KB == 1, "B-scale copy handles 16, 8 or 4 B per token");
+    static_assert(KB == 2 || KB == 1, "B-scale copy: one 4-byte piece per (token, block)");
     static_assert(WAVES % KB == 0 && TPW % 2 == 0, "B copies: whole token rows per wave");
 };
 using ShapeWide = MmShape<128, 128, 2, 4, 2, 2>;
@@ -93,8 +93,9 @@ using ShapeTall = MmShape<256, 64, 2>;
 struct MmArgs {
     MatView W;
     Routing R;
-    const int8_t* aq;   // activations int8: x [T][H] (mode 0); h block-major [I/32][slots][32] (mode 1)
-    const float* ad;    // their scales (exact fp16 values): x [T][H/32]; h [I/32][slots]
+    const int8_t* aq;   // activations int8, block-major in slot order [Kdim/32][slots][32]: the
+                        // gathered x (mode 0, gather_act_kernel) or h (mode 1)
+    const float* ad;    // their scales (exact fp16 values) [Kdim/32][slots]
     int T, H, I, E, K;
     int Kdim;           // reduction length (H for mode 0, I for modes 1/2)
     int nrb;            // row blocks of the weight matrix
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
                   "Q4_0: each wave copies whole nibble chunks and unpacks exactly the chunk it copied");
     static_assert((MM_RING * STAGE + (Q4 ? 2 * SH::ST_A : 16) + 8 * MM_TOK) * SH::WG_PER_CU <= 160 * 1024,
                   "the work groups of a CU fit its 160 KB of LDS");
-    __shared__ int tok_s[MM_TOK], slot_s[MM_TOK];
+    __shared__ int slot_s[MM_TOK];
     constexpr int OFF_A = 0;                                  // Q8_0: int8 A; Q4_0: raw nibbles
     constexpr int OFF_B = Q4 ? SH::ST_AR : SH::ST_A;
     constexpr int OFF_AS = OFF_B + SH::ST_B;
@@ -205,17 +206,9 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     const int wave = tid / WAVE, lane = tid % WAVE;
 
     if (tid < MM_TOK) {
-        int tok = 0, slot = 0;
-        if (tid < n) {
-            if (shared) {
-                tok = start + tid;
-                slot = a.T * a.K + tok;
-            } else {
-                slot = a.R.off[e] + start + tid;
-                tok = a.R.srt_tok[slot];
-            }
-        }
-        tok_s[tid] = tok;
+        // the pair's slot: the row of the slot-ordered operands (gathered x, h) and of y
+        int slot = 0;
+        if (tid < n) slot = shared ? a.T * a.K + start + tid : a.R.off[e] + start + tid;
         slot_s[tid] = slot;
     }
     __syncthreads();
@@ -239,35 +232,31 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
                              half * (64 / WPC);
     // B rows: wave w copies block w % KB of tokens (w / KB) * TPW .. + TPW, as 16-byte
     // pieces; lane position p (copy v, lane l: p = 64 v + l) lands at +16 p, i.e. token
-    // row p / 2, position p % 2, which holds half (p % 2) ^ (bit 3 of the row).  Mode 0
-    // gathers x rows [T][H]; mode 1 reads h block-major ([I/32][slots][32 B]), where the
-    // tile's consecutive slots are consecutive 32-byte pieces of one block plane, so each
-    // copy reads one contiguous 1 KB (the per-stage step is kb0 planes)
+    // row p / 2, position p % 2, which holds half (p % 2) ^ (bit 3 of the row).  The
+    // operand is block-major in slot order ([Kdim/32][slots][32 B]): the tile's
+    // consecutive slots are consecutive 32-byte pieces of one block plane, so each copy
+    // reads one contiguous 1 KB; a stage advances KB planes
     constexpr int TPW = SH::TPW;
-    const uint32_t n_slots = (uint32_t)(a.T * a.K + a.T);  // rows of the h planes
-    uint32_t b_off[SH::B_LOADS];  // 32-bit: the host keeps rows x Kd below 2^32
+    const uint32_t n_slots = (uint32_t)(a.T * a.K + a.T);  // rows of the block planes
+    uint32_t b_off[SH::B_LOADS];  // 32-bit: the host keeps slots x Kd below 2^32
 #pragma unroll
     for (int v = 0; v < SH::B_LOADS; v++) {
         const int p = v * WAVE + lane;
         const int bt = (wave / MM_KB) * TPW + (p % SH::B_LANES) / 2;  // in range for masked lanes too
-        b_off[v] = MODE == 0 ? (uint32_t)tok_s[bt] * (uint32_t)Kd + (wave % MM_KB) * 32 + swz_half(bt, p & 1)
-                             : ((uint32_t)(wave % MM_KB) * n_slots + (uint32_t)slot_s[bt]) * 32u + swz_half(bt, p & 1);
+        b_off[v] = ((uint32_t)(wave % MM_KB) * n_slots + (uint32_t)slot_s[bt]) * 32u + swz_half(bt, p & 1);
     }
-    const uint32_t b_step = MODE == 0 ? (uint32_t)QK : n_slots * 32u;  // bytes per block of the B source
+    const uint32_t b_step = n_slots * 32u;  // bytes per block plane of the B source
     // A rows (int8): copy lane l lands at +16 l (row l / 2 of a 32-row piece, position
     // l % 2) and fetches half (l % 2) ^ (bit 3 of the row); Q4_0 nibbles are copied as
     // they are and swizzled when unpacked
     const uint32_t a_sw = (uint32_t)((lane / 2) * 32 + swz_half(lane / 2, lane & 1));
-    // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each: KB = 4 as one
-    // 16-byte piece per token (lanes < TOK/8), KB = 2 as two 4-byte pieces (mode 1: the
-    // token's KB scales sit in KB block planes)
-    static_assert(MODE == 0 || MM_KB != 4, "block-major h scales: one 4-byte piece per (token, block)");
-    constexpr int BS_LANES = MM_KB == 4 ? MM_TOK / MM_WAVES : MM_TOK / MM_WAVES * MM_KB;
-    const int bst = wave * (MM_TOK / MM_WAVES) + (MM_KB == 4 ? lane : lane / MM_KB) % (MM_TOK / MM_WAVES);
-    const uint32_t bs_off =
-        MODE == 0 ? ((uint32_t)tok_s[bst] * (uint32_t)nb + (MM_KB == 4 ? 0 : lane % MM_KB)) * 4
-                  : ((uint32_t)(lane % MM_KB) * n_slots + (uint32_t)slot_s[bst]) * 4;
-    const uint32_t bs_step = MODE == 0 ? 4u : n_slots * 4u;  // bytes per block of the B-scale source
+    // B scales: wave w copies tokens w*TOK/8 .. +TOK/8, KB f32 each, as KB 4-byte pieces
+    // (the token's KB scales sit in KB block planes)
+    static_assert(MM_KB <= 2, "B scales: one 4-byte piece per (token, block), KB of them per token");
+    constexpr int BS_LANES = MM_TOK / MM_WAVES * MM_KB;
+    const int bst = wave * (MM_TOK / MM_WAVES) + (lane / MM_KB) % (MM_TOK / MM_WAVES);
+    const uint32_t bs_off = ((uint32_t)(lane % MM_KB) * n_slots + (uint32_t)slot_s[bst]) * 4;
+    const uint32_t bs_step = n_slots * 4u;  // bytes per block plane of the B-scale source
 
     // issue the asynchronous copies of stage s into ring slot s % MM_RING; lanes
     // outside a copy's range are masked (the wave still issues it once)
@@ -296,12 +285,7 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
         if (lane < 8 / WPC) b2l(r_as, st + OFF_AS + ch * 128 + half * (128 / WPC), 16u * lane, kb0 * 128u);
         // B scales of this wave's tokens
         uint8_t* sdst = st + OFF_BS + wv * (MM_TOK / MM_WAVES) * MM_KB * 4;
-        if (lane < BS_LANES) {
-            if (MM_KB == 4)
-                b2l(r_bs, sdst, bs_off, kb0 * bs_step);
-            else
-                b2l<4>(r_bs, sdst, bs_off, kb0 * bs_step);
-        }
+        if (lane < BS_LANES) b2l<4>(r_bs, sdst, bs_off, kb0 * bs_step);
     };
 
     const int sl = wave % MM_SLABS;    // 64-row slab within the row block
@@ -498,6 +482,27 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     if constexpr (TT == 2) epilogue(acc2, acc3, j0 + 32);
 }
 
+// The dispatched activations of the gate/up products (einsum_dispatch,
+// src/hunyuan_moe_full.cpp:352-373, as a copy of the Q8_0 activations): slot r of the
+// expert-sorted pair order (the shared expert's token t at slot T*K + t) receives its
+// token's quantized row, block-major -- plane b holds every slot's block b (32 bytes)
+// and its scale -- so that the grouped GEMM's copies of a tile's consecutive slots read
+// contiguous memory.  One thread per 16-byte piece, consecutive threads writing
+// consecutive pieces of one plane; the token rows are read from L2.
+__global__ __launch_bounds__(256) void gather_act_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                         const int* __restrict__ srt_tok, int T, int TK, int n_slots,
+                                                         int nb, int8_t* __restrict__ gq, float* __restrict__ gd) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;  // piece: ((b * n_slots) + r) * 2 + half
+    if (idx >= (size_t)nb * n_slots * 2) return;
+    const size_t br = idx >> 1;
+    const int r = (int)(br % (size_t)n_slots), b = (int)(br / (size_t)n_slots);
+    int tok = r < TK ? srt_tok[r] : r - TK;
+    tok = tok < 0 ? 0 : (tok >= T ? T - 1 : tok);
+    const v4i_t v = *reinterpret_cast<const v4i_t*>(xq + ((size_t)tok * nb + b) * QK + (idx & 1) * 16);
+    *reinterpret_cast<v4i_t*>(gq + idx * 16) = v;
+    if ((idx & 1) == 0) gd[br] = xd[(size_t)tok * nb + b];
+}
+
 // Per-block int32 dots through the grouped GEMM's own operand path (hy_block_dots
 // path 1), one wave per (64-row group, block).  The wave stages the block's 64 weight
 // rows in the GEMM's LDS operand layout -- Q8_0 as swizzled 32-byte rows; Q4_0 as the
@@ -607,6 +612,15 @@ int mfma_shape(int T, int K, int E, int H, int I) {
 
 int mfma_shape_tokens(int shape) {
     return shape == MM_SHAPE_TALL ? ShapeTall::TOK : ShapeWide::TOK;
+}
+
+hipError_t launch_gather_act(const ActQ& X, const Routing& R, int T, int K, int H, int8_t* gq, float* gd,
+                             hipStream_t s) {
+    const int n_slots = T * K + T, nb = H / QK;
+    const size_t pieces = (size_t)nb * n_slots * 2;
+    hipLaunchKernelGGL(gather_act_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, X.q, X.d, R.srt_tok, T,
+                       T * K, n_slots, nb, gq, gd);
+    return hipGetLastError();
 }
 
 hipError_t launch_ffn_up_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
