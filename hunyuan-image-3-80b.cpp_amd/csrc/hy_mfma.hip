@@ -60,10 +60,11 @@ constexpr int MM_XCD = 8;                  // XCDs of the device (work-group rou
 // WAVES waves per work group (one 64-row slab x 32 * TT tokens each); RING LDS stage
 // slots (one computed, RING - 1 in flight).  8-wave shapes run two work groups per
 // CU, the 4-wave 2 x 2 shape three, a 16-wave shape one.
-template <int ROWS_, int TOK_, int KB_, int WAVES_ = 8, int RING_ = 3, int TT_ = 1>
+template <int ROWS_, int TOK_, int KB_, int WAVES_ = 8, int RING_ = 3, int TT_ = 1, int GROUP_ = 1>
 struct MmShape {
     static constexpr int ROWS = ROWS_, TOK = TOK_, KB = KB_, WAVES = WAVES_, RING = RING_;
     static constexpr int TT = TT_;                   // 32-token tiles per wave (1 or 2)
+    static constexpr int GROUP = GROUP_;             // consecutive tiles scheduled together on one XCD
     static constexpr int THREADS = WAVES * WAVE;
     static constexpr int WG_PER_CU = WAVES == 16 ? 1 : (TT == 2 ? 3 : 2);
     static constexpr int SLABS = ROWS / 64;          // 64-row slabs (one per row group)
@@ -87,7 +88,7 @@ struct MmShape {
     static_assert(KB == 2 || KB == 1, "B-scale copy: one 4-byte piece per (token, block)");
     static_assert(WAVES % KB == 0 && TPW % 2 == 0, "B copies: whole token rows per wave");
 };
-using ShapeWide = MmShape<128, 128, 2, 4, 2, 2>;
+using ShapeWide = MmShape<128, 128, 2, 4, 2, 2, 2>;
 using ShapeTall = MmShape<256, 64, 2>;
 
 struct MmArgs {
@@ -99,7 +100,7 @@ struct MmArgs {
     int T, H, I, E, K;
     int Kdim;           // reduction length (H for mode 0, I for modes 1/2)
     int nrb;            // row blocks of the weight matrix
-    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD (sizes the grid)
+    int tiles_pad;      // tile bound rounded up to a multiple of MM_XCD x the shape's GROUP (sizes the grid)
     int8_t* hq;         // mode 0 outputs
     float* hd;
     int* hs;
@@ -187,14 +188,19 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 
     // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
     // all row blocks of a tile the same id mod MM_XCD (they share the tile's
-    // activation rows in that XCD's L2).  (Ordering whole experts onto one XCD, so
-    // that tiles sharing a weight block reuse it in L2, cut fetched bytes but ran
-    // 2-4 % slower: this kernel is not bound by HBM traffic.)
+    // activation rows in that XCD's L2).  The wide shape takes GROUP = 2 consecutive
+    // tiles (mostly one expert's) together on one XCD with their work groups
+    // interleaved by row block, so one weight row block serves both from L2 (Zipf
+    // T=4096 Q4_0 ffn_up 2.578-2.617 -> 2.498-2.504 ms, the uniform T=4096 stack within
+    // 0.5 %; on the tall shape's T=512 tiles, of two experts as often as of one, 2 %
+    // slower).  (Ordering whole experts onto one XCD cut fetched bytes but ran 2-4 %
+    // slower: this kernel is not bound by HBM traffic.)
+    constexpr int MM_G = SH::GROUP;
     const int id = (int)blockIdx.x;
     const int xcd = id % MM_XCD, local = id / MM_XCD;
-    const int tile_rel = xcd + MM_XCD * (local / a.nrb);
-    const int rb = local % a.nrb;
-    const int tile = tile_rel;
+    const int q = local / (MM_G * a.nrb), within = local % (MM_G * a.nrb);
+    const int rb = within / MM_G;
+    const int tile = (q * MM_XCD + xcd) * MM_G + within % MM_G;
     if (tile >= a.R.meta[1]) return;
     const int e = a.R.tile_e[tile];
     const int start = a.R.tile_start[tile], n = a.R.tile_n[tile];
@@ -578,7 +584,7 @@ hipError_t launch_block_dots_mfma(int wtype, const uint8_t* w, const uint8_t* x,
 template <int MODE, class SH>
 static hipError_t launch_mode(int wtype, MmArgs a, int n_tiles_bound, int rows, hipStream_t s) {
     a.nrb = rows / SH::ROWS;
-    a.tiles_pad = (n_tiles_bound + MM_XCD - 1) / MM_XCD * MM_XCD;
+    a.tiles_pad = (n_tiles_bound + MM_XCD * SH::GROUP - 1) / (MM_XCD * SH::GROUP) * (MM_XCD * SH::GROUP);
     const dim3 grid(a.tiles_pad * a.nrb);
     if (wtype == HY_TYPE_Q4_0)
         hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE, SH>), grid, dim3(SH::THREADS), 0, s, a);
