@@ -493,20 +493,25 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 // expert-sorted pair order (the shared expert's token t at slot T*K + t) receives its
 // token's quantized row, block-major -- plane b holds every slot's block b (32 bytes)
 // and its scale -- so that the grouped GEMM's copies of a tile's consecutive slots read
-// contiguous memory.  One thread per 16-byte piece, consecutive threads writing
-// consecutive pieces of one plane; the token rows are read from L2.
+// contiguous memory.  A wave copies 16 slots x 4 blocks, one 32-byte block per thread
+// (thread = 4 slot + block): each slot's 4 blocks are one 128-byte run of its token's
+// row, each block's 16 slots one 512-byte run of its plane.
 __global__ __launch_bounds__(256) void gather_act_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                          const int* __restrict__ srt_tok, int T, int TK, int n_slots,
                                                          int nb, int8_t* __restrict__ gq, float* __restrict__ gd) {
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;  // piece: ((b * n_slots) + r) * 2 + half
-    if (idx >= (size_t)nb * n_slots * 2) return;
-    const size_t br = idx >> 1;
-    const int r = (int)(br % (size_t)n_slots), b = (int)(br / (size_t)n_slots);
+    const size_t wt = ((size_t)blockIdx.x * 256 + threadIdx.x) >> 6;  // the wave's (16 slots x 4 blocks) tile
+    const int lane = threadIdx.x & 63;
+    const size_t n_sg = ((size_t)n_slots + 15) / 16;
+    const int r = (int)(wt % n_sg) * 16 + (lane >> 2), b = (int)(wt / n_sg) * 4 + (lane & 3);
+    if (r >= n_slots || b >= nb) return;
     int tok = r < TK ? srt_tok[r] : r - TK;
     tok = tok < 0 ? 0 : (tok >= T ? T - 1 : tok);
-    const v4i_t v = *reinterpret_cast<const v4i_t*>(xq + ((size_t)tok * nb + b) * QK + (idx & 1) * 16);
-    *reinterpret_cast<v4i_t*>(gq + idx * 16) = v;
-    if ((idx & 1) == 0) gd[br] = xd[(size_t)tok * nb + b];
+    const v4i_t* src = reinterpret_cast<const v4i_t*>(xq + ((size_t)tok * nb + b) * QK);
+    v4i_t* dst = reinterpret_cast<v4i_t*>(gq + ((size_t)b * n_slots + r) * QK);
+    const v4i_t lo = src[0], hi = src[1];
+    dst[0] = lo;
+    dst[1] = hi;
+    gd[(size_t)b * n_slots + r] = xd[(size_t)tok * nb + b];
 }
 
 // Per-block int32 dots through the grouped GEMM's own operand path (hy_block_dots
@@ -623,9 +628,9 @@ int mfma_shape_tokens(int shape) {
 hipError_t launch_gather_act(const ActQ& X, const Routing& R, int T, int K, int H, int8_t* gq, float* gd,
                              hipStream_t s) {
     const int n_slots = T * K + T, nb = H / QK;
-    const size_t pieces = (size_t)nb * n_slots * 2;
-    hipLaunchKernelGGL(gather_act_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, X.q, X.d, R.srt_tok, T,
-                       T * K, n_slots, nb, gq, gd);
+    const size_t wave_tiles = (((size_t)n_slots + 15) / 16) * (((size_t)nb + 3) / 4);
+    hipLaunchKernelGGL(gather_act_kernel, dim3((unsigned)((wave_tiles * 64 + 255) / 256)), dim3(256), 0, s, X.q, X.d,
+                       R.srt_tok, T, T * K, n_slots, nb, gq, gd);
     return hipGetLastError();
 }
 
