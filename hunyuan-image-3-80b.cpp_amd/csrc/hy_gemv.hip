@@ -268,8 +268,8 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 // Quantized weights (Q8_0 / Q4_0): the same per-row block-sequential accumulation as
 // gemv_kernel, with the operand streams decoupled from the arithmetic.  Each work
 // group is one wave owning one 64-row group of one tile (<= NT tokens).  A private LDS
-// ring holds NSTEP steps; a step is U (8, or 4 when a launch's waves outnumber the LDS
-// slots) consecutive blocks:
+// ring holds NSTEP steps; a step is U consecutive blocks (8, or 4 or 2 when a launch's
+// waves outnumber the LDS slots of the larger steps):
 //   weights  U x (64 rows x 16 B / 32 B)      one DMA per block (two for Q8_0)
 //   scales   U x 64 fp16                      one DMA (contiguous in the plane)
 //   x        NT tokens x U x 32 B int8        one DMA (token = lane / (2 U))
@@ -282,9 +282,9 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 // first copies; the first activation copies follow, and one full wait joins both.
 // The last NSTEP steps are consumed by an unrolled tail whose waits count down to
 // zero: the wave leaves no copy in flight.
-constexpr int GQ_U = 8;       // blocks per step (GQ_U_SMALL when waves outnumber the LDS slots)
-constexpr int GQ_U_SMALL = 4;
-constexpr int GQ_U_TINY = 2;
+constexpr int GQ_U = 8;       // blocks per step
+constexpr int GQ_U_SMALL = 4;  // ... for launches whose waves only 4-block steps keep resident
+constexpr int GQ_U_TINY = 2;   // ... only 2-block steps
 constexpr int GQ_WAVES = 1;   // one wave per work group: work groups spread over every CU
 constexpr int GQ_THREADS = GQ_WAVES * WAVE;
 
