@@ -5,7 +5,9 @@
 // expert (or TOK consecutive tokens for the shared expert), a row block is ROWS weight
 // rows (ROWS/64 row groups of the row-group-interleaved weights).  Each K step copies
 // KB GGUF blocks of the ROWS weight rows and of the tile's TOK activation rows
-// straight from global memory into an LDS ring of stages.  Two shapes, picked per call
+// straight from global memory into an LDS ring of stages; the activations (the gathered
+// x, and h) are block-major in pair-slot order, so a tile's rows of one block are one
+// contiguous run.  Two shapes, picked per call
 // from the mean pairs per expert:
 //   wide  (ROWS 128, TOK 128, KB 2): four waves, 2 row slabs x 2 token halves, each
 //         wave 2 x 2 output tiles (64 rows x 64 tokens: one LDS read of each A and B
