@@ -231,7 +231,6 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GvArgs a) {
 
     if (MODE == 0) {
         // lanes 0..31: gate rows 32G+lane, lanes 32..63: the matching up rows
-        const int nb_i = a.I / QK;
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (i >= n) break;
@@ -574,7 +573,6 @@ __global__ __launch_bounds__(GQ_THREADS) void gemv_q_kernel(GvArgs a) {
 
     if (MODE == 0) {
         // lanes 0..31: gate rows 32G+lane, lanes 32..63: the matching up rows
-        const int nb_i = a.I / QK;
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (i >= n) break;
