@@ -104,6 +104,7 @@ struct hy_moe_ctx {
     int* hs = nullptr;
     int8_t* xg = nullptr;  // the grouped GEMM's gathered x, block-major in slot order [H/32][T*K+T][32]
     float* xgd = nullptr;
+    int* mm_ctr = nullptr;  // the grouped GEMM's work counters (zeroed by the gather before each use)
     float* hf = nullptr;
     float* y = nullptr;
     float* xn = nullptr;
@@ -352,17 +353,17 @@ int forward_impl(hy_moe_ctx* c, uint32_t layer, const float* x, uint32_t T, floa
     const int shared_tiles = has_shared ? (iT + NT - 1) / NT : 0;
     if (mfma) {
         // the dispatched activations: x's Q8_0 rows copied into slot order, block-major
-        HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] { return hy::launch_gather_act(X, R, iT, K, H, c->xg, c->xgd, s); }));
+        HY_TRY(timed(c, hy::KID_DISPATCH, s, [&] { return hy::launch_gather_act(X, R, iT, K, H, c->xg, c->xgd, c->mm_ctr, s); }));
         const hy::ActQ XG{c->xg, c->xgd, nullptr, H};
         HY_TRY(timed(c, hy::KID_UP, s, [&] {
             return hy::launch_ffn_up_mfma(wt, shape, routed_bound + shared_tiles, gu_view(c, L), R, XG, iT, H, I, E, K,
-                                          c->hq, c->hd, c->hs, s);
+                                          c->hq, c->hd, c->hs, c->mm_ctr, s);
         }));
         // routed and shared down products in one launch (y rows for every slot), then
         // the combine
         HY_TRY(timed(c, hy::KID_DOWN, s, [&] {
             return hy::launch_ffn_down_mfma(wt, shape, routed_bound + shared_tiles, dn_view(c, L), R, c->hq, c->hd, iT, H,
-                                            I, E, K, c->y, s);
+                                            I, E, K, c->y, c->mm_ctr, s);
         }));
         HY_TRY(timed(c, hy::KID_COMBINE, s, [&] {
             return hy::launch_combine(R, c->y, iT, H, K, has_shared, resid, out, s);
@@ -529,6 +530,7 @@ int hy_moe_create(const hy_moe_config* cfg, hy_moe_ctx** out) {
         {(void**)&c->hq, slots * I},       {(void**)&c->hd, slots * (I / 32) * 4},
         {(void**)&c->hs, slots * (I / 32) * 4},
         {(void**)&c->xg, wt == HY_TYPE_F32 ? 16 : slots * H}, {(void**)&c->xgd, wt == HY_TYPE_F32 ? 16 : slots * (H / 32) * 4},
+        {(void**)&c->mm_ctr, (size_t)hy::mfma_counter_ints() * 4},
         {(void**)&c->hf, wt == HY_TYPE_F32 ? slots * I * 4 : 16},
         {(void**)&c->y, slots * H * 4},    {(void**)&c->xn, Tm * H * 4},
         {(void**)&c->cur, Tm * H * 4},

@@ -99,16 +99,19 @@ bool mfma_path_ok(int wtype, int H, int I);
 enum MfmaShape { MM_SHAPE_WIDE = 0, MM_SHAPE_TALL = 1 };
 int mfma_shape(int T, int K, int E, int H, int I);
 int mfma_shape_tokens(int shape);
+// the grouped GEMM's work counters (ints of device memory a caller keeps per context);
+// launch_gather_act zeroes them for the gate/up and down launches that follow it
+int mfma_counter_ints();
 // the gate/up products' activations in expert-sorted slot order, block-major
 // ([H/32][T*K+T][32 B] and [H/32][T*K+T] scales), from x's Q8_0 rows and the sorted pairs
 hipError_t launch_gather_act(const ActQ& X, const Routing& R, int T, int K, int H, int8_t* gq, float* gd,
-                             hipStream_t s);
+                             int* mm_ctr, hipStream_t s);
 hipError_t launch_ffn_up_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                               const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
-                              hipStream_t s);
+                              int* mm_ctr, hipStream_t s);
 hipError_t launch_ffn_down_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                                 const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
-                                hipStream_t s);
+                                int* mm_ctr, hipStream_t s);
 
 // residency (hy_data.hip)
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);

@@ -48,6 +48,9 @@ typedef float v16f_t __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 
 constexpr int MM_XCD = 8;                  // XCDs of the device (work-group round robin)
+constexpr int MM_CU_PER_XCD = 32;          // CUs per XCD (256 in all)
+constexpr int MM_CTR_STRIDE = 32;          // ints between two work counters (one 128-byte line each)
+constexpr int MM_CTR_INTS = 2 * MM_XCD * MM_CTR_STRIDE;  // [mode][XCD] counters of the grouped GEMM
 
 // Tile shape.  LDS stage layout (bytes): A = CHUNKS (row group x block) chunks of
 // 64 rows x 32 B int8 (Q4_0: 64 rows x 16 B raw nibbles); B = KB blocks of TOK tokens
@@ -107,6 +110,7 @@ struct MmArgs {
     float* hd;
     int* hs;
     float* y;           // mode 1 output
+    int* ctr;           // MM_CTR_INTS work counters, zeroed by gather_act_kernel before the gate/up launch
 };
 
 // Byte offset, inside a 32-byte operand row, of the row's 16-byte half h: the halves
@@ -197,13 +201,87 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     // 0.5 %; on the tall shape's T=512 tiles, of two experts as often as of one, 2 %
     // slower).  (Ordering whole experts onto one XCD cut fetched bytes but ran 2-4 %
     // slower: this kernel is not bound by HBM traffic.)
+    //
+    // The XCDs do not run equally fast (per-work-group stamps: the same full tile takes
+    // 110-119 us on different XCDs of one launch), and with a fixed id -> item map the
+    // launch waits for the slowest (4096-token Q8_0 gate/up launch: XCDs ending at
+    // 2263-2457 us, the work groups' busy time 93 % of the launch's).  So only the first part of each XCD's item list is fixed:
+    // its last RESERVE items (two rounds of its work groups) are claimed through the
+    // XCD's work counter, and a work group that finds its own XCD's list exhausted
+    // claims from the XCD with the most items left.  Every item runs exactly once: a
+    // fixed item by the one work group whose id maps to it, a reserved item by the
+    // claim that drew it; the RESERVE work groups of an XCD whose ids follow its fixed
+    // part each claim from their own counter first, so their claims alone cover that
+    // XCD's reserve.  Work groups past an XCD's items (the tile bound's padding and
+    // MM_XCD * SLACK extra ones) only steal, and exit as soon as nothing is left.
     constexpr int MM_G = SH::GROUP;
+    constexpr int RESERVE = 2 * MM_CU_PER_XCD * SH::WG_PER_CU;
     const int id = (int)blockIdx.x;
     const int xcd = id % MM_XCD, local = id / MM_XCD;
-    const int q = local / (MM_G * a.nrb), within = local % (MM_G * a.nrb);
+    const int ntiles = a.R.meta[1];
+    const int per_group = MM_G * a.nrb;                 // items of one tile group
+    const int ngroups = (ntiles + MM_G - 1) / MM_G;     // group g belongs to XCD g % MM_XCD
+    auto items_of = [&](int x) { return ngroups > x ? (ngroups - x + MM_XCD - 1) / MM_XCD * per_group : 0; };
+    auto fixed_of = [&](int n_items) { return n_items > RESERVE ? n_items - RESERVE : 0; };
+    const int own = items_of(xcd), fixed = fixed_of(own);
+    int ix = xcd, ik = local;  // the item: XCD ix's ik-th
+    if (local >= fixed) {
+        __shared__ int claim_s[2];
+        int* ctr = a.ctr + MODE * MM_XCD * MM_CTR_STRIDE;
+        if (threadIdx.x < WAVE) {
+            const int ln = threadIdx.x;
+            int k = 0x3fffffff;
+            if (ln == 0 && local < own) k = atomicAdd(ctr + xcd * MM_CTR_STRIDE, 1);
+            k = __shfl(k, 0);
+            int cx = -1, ck = 0;
+            if (fixed + k < own) {
+                cx = xcd;
+                ck = fixed + k;
+            } else {
+                // steal: lanes 0..MM_XCD-1 read the counters, the XCD with the most reserved
+                // items left (the lowest on ties) is drawn from; a lost race reads again
+                for (int tries = 0; tries < 64 && cx < 0; tries++) {
+                    int left = 0;
+                    if (ln < MM_XCD) {
+                        const int n_items = items_of(ln);
+                        left = n_items - fixed_of(n_items) -
+                               __hip_atomic_load(ctr + ln * MM_CTR_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    int best = left, bx = ln;
+                    for (int m = 1; m < MM_XCD; m <<= 1) {
+                        const int ob = __shfl_xor(best, m), ox = __shfl_xor(bx, m);
+                        if (ob > best || (ob == best && ox < bx)) {
+                            best = ob;
+                            bx = ox;
+                        }
+                    }
+                    best = __shfl(best, 0);
+                    bx = __shfl(bx, 0);
+                    if (best <= 0) break;
+                    int k2 = 0;
+                    if (ln == 0) k2 = atomicAdd(ctr + bx * MM_CTR_STRIDE, 1);
+                    k2 = __shfl(k2, 0);
+                    const int n_items = items_of(bx), f = fixed_of(n_items);
+                    if (f + k2 < n_items) {
+                        cx = bx;
+                        ck = f + k2;
+                    }
+                }
+            }
+            if (ln == 0) {
+                claim_s[0] = cx;
+                claim_s[1] = ck;
+            }
+        }
+        __syncthreads();
+        ix = claim_s[0];
+        ik = claim_s[1];
+        if (ix < 0) return;
+    }
+    const int q = ik / per_group, within = ik % per_group;
     const int rb = within / MM_G;
-    const int tile = (q * MM_XCD + xcd) * MM_G + within % MM_G;
-    if (tile >= a.R.meta[1]) return;
+    const int tile = (q * MM_XCD + ix) * MM_G + within % MM_G;
+    if (tile >= ntiles) return;
     const int e = a.R.tile_e[tile];
     const int start = a.R.tile_start[tile], n = a.R.tile_n[tile];
     const bool shared = e == a.E;
@@ -352,8 +430,9 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
             lds_wait(A0, A1, B, dw0, dw1, dxb);
         }
         // the block's MFMAs issue at raised wave priority, so a wave whose operands are
-        // ready reaches the matrix unit ahead of the other waves' rescale (c5 ffn_up
-        // -2 %, c4 -3 %, c2 -4 %; ffn_down -2 % with the 2 x 2 tiles, nothing with 2 x 1)
+        // ready reaches the matrix unit ahead of the other waves' rescale (gate/up -2 %
+        // at 4096 Q8_0 tokens, -3 % at 4096 Q4_0, -4 % at 512 Q8_0; down -2 % with the
+        // 2 x 2 tiles, nothing with 2 x 1)
         __builtin_amdgcn_s_setprio(1);
         const v16i_t S0 = block_dot_tile(A0, B);
         const v16i_t S1 = block_dot_tile(A1, B);
@@ -500,8 +579,11 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 // row, each block's 16 slots one 512-byte run of its plane.
 __global__ __launch_bounds__(256) void gather_act_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                          const int* __restrict__ srt_tok, int T, int TK, int n_slots,
-                                                         int nb, int8_t* __restrict__ gq, float* __restrict__ gd) {
+                                                         int nb, int8_t* __restrict__ gq, float* __restrict__ gd,
+                                                         int* __restrict__ ctr) {
     const size_t wt = ((size_t)blockIdx.x * 256 + threadIdx.x) >> 6;  // the wave's (16 slots x 4 blocks) tile
+    // the grouped GEMM's work counters start at zero for the two launches that follow
+    if (blockIdx.x == 0 && threadIdx.x < 2 * MM_XCD) ctr[threadIdx.x * MM_CTR_STRIDE] = 0;
     const int lane = threadIdx.x & 63;
     const size_t n_sg = ((size_t)n_slots + 15) / 16;
     const int r = (int)(wt % n_sg) * 16 + (lane >> 2), b = (int)(wt / n_sg) * 4 + (lane & 3);
@@ -592,7 +674,10 @@ template <int MODE, class SH>
 static hipError_t launch_mode(int wtype, MmArgs a, int n_tiles_bound, int rows, hipStream_t s) {
     a.nrb = rows / SH::ROWS;
     a.tiles_pad = (n_tiles_bound + MM_XCD * SH::GROUP - 1) / (MM_XCD * SH::GROUP) * (MM_XCD * SH::GROUP);
-    const dim3 grid(a.tiles_pad * a.nrb);
+    // every item of the tile bound has its work group, plus half a round per XCD that
+    // only steals (a fast XCD's reserve claims beyond its own items)
+    constexpr int SLACK = MM_CU_PER_XCD * SH::WG_PER_CU / 2;
+    const dim3 grid(a.tiles_pad * a.nrb + MM_XCD * SLACK);
     if (wtype == HY_TYPE_Q4_0)
         hipLaunchKernelGGL((moe_mfma_kernel<HY_TYPE_Q4_0, MODE, SH>), grid, dim3(SH::THREADS), 0, s, a);
     else
@@ -628,26 +713,28 @@ int mfma_shape_tokens(int shape) {
 }
 
 hipError_t launch_gather_act(const ActQ& X, const Routing& R, int T, int K, int H, int8_t* gq, float* gd,
-                             hipStream_t s) {
+                             int* mm_ctr, hipStream_t s) {
     const int n_slots = T * K + T, nb = H / QK;
     const size_t wave_tiles = (((size_t)n_slots + 15) / 16) * (((size_t)nb + 3) / 4);
     hipLaunchKernelGGL(gather_act_kernel, dim3((unsigned)((wave_tiles * 64 + 255) / 256)), dim3(256), 0, s, X.q, X.d,
-                       R.srt_tok, T, T * K, n_slots, nb, gq, gd);
+                       R.srt_tok, T, T * K, n_slots, nb, gq, gd, mm_ctr);
     return hipGetLastError();
 }
 
 hipError_t launch_ffn_up_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                               const ActQ& X, int T, int H, int I, int E, int K, int8_t* hq, float* hd, int* hs,
-                              hipStream_t s) {
-    MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr};
+                              int* mm_ctr, hipStream_t s) {
+    MmArgs a{W, R, X.q, X.d, T, H, I, E, K, H, 0, 0, hq, hd, hs, nullptr, mm_ctr};
     return launch_shape<0>(wtype, shape, a, n_tiles_bound, 2 * I, s);
 }
 
 hipError_t launch_ffn_down_mfma(int wtype, int shape, int n_tiles_bound, const MatView& W, const Routing& R,
                                 const int8_t* hq, const float* hd, int T, int H, int I, int E, int K, float* y,
-                                hipStream_t s) {
-    MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y};
+                                int* mm_ctr, hipStream_t s) {
+    MmArgs a{W, R, hq, hd, T, H, I, E, K, I, 0, 0, nullptr, nullptr, nullptr, y, mm_ctr};
     return launch_shape<1>(wtype, shape, a, n_tiles_bound, H, s);
 }
+
+int mfma_counter_ints() { return MM_CTR_INTS; }
 
 }  // namespace hy

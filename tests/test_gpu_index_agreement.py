@@ -46,11 +46,11 @@ def test_stack_layers(layer_inputs, first):
         h = layer_inputs[l]
         wr = O.synth(SEED, l, O.T_ROUTER, 0, (E, H), 0.02)
         r = compare(rms_norm_seq(h), rms_norm_blocked(h), wr, K, with_norm=True)
-        print(f"c5 layer {l}: set_differs {r['set_differs']} {r['set_differs_tokens']} order_differs "
+        print(f"stack T=4096 layer {l}: set_differs {r['set_differs']} {r['set_differs_tokens']} order_differs "
               f"{r['order_differs']} near_ties(64uA) {r['near_ties_8_9_64uA']} prob_ties "
               f"{r['selected_prob_ties_with_distinct_logits']}/{r['boundary_prob_ties_with_distinct_logits']} "
               f"min_gap {r['min_gap_8_9']:.3e} max|dl|/uA {r['max_logit_diff_over_uA']:.1f} "
               f"worst/bound {r['worst_disagreement_over_bound']:.2e}", flush=True)
         for k in tot:
             tot[k] += r[k]
-    print(f"c5 layers {first}-{first + 7} total: {tot}", flush=True)
+    print(f"stack T=4096 layers {first}-{first + 7} total: {tot}", flush=True)

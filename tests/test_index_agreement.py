@@ -41,12 +41,12 @@ def report(name, r):
 @pytest.mark.parametrize("layer", [0, 1])
 def test_q8_0_t512(layer):
     x = bench_x(512)
-    report(f"c2 T=512 layer {layer}", compare(x, x, router(layer), K))
+    report(f"Q8_0 T=512 layer {layer}", compare(x, x, router(layer), K))
 
 
 def test_f32_t16():
     x = bench_x(16)
-    report("c1 T=16", compare(x, x, router(0), K))
+    report("F32 T=16", compare(x, x, router(0), K))
 
 
 def test_decode_t8_every_weight_set():
@@ -54,20 +54,20 @@ def test_decode_t8_every_weight_set():
     x = bench_x(8)
     for layer in range(8):
         r = compare(x, x, router(layer), K)
-        report(f"c3 T=8 layer {layer}", r)
+        report(f"decode T=8 layer {layer}", r)
 
 
 def test_q4_0_t4096_zipf():
     x = bench_x(4096)
     x[:, 0] = 1.0
-    report("c4 T=4096 Zipf", compare(x, x, router(0, bench.zipf_bias(SEED)), K))
+    report("Q4_0 T=4096 Zipf", compare(x, x, router(0, bench.zipf_bias(SEED)), K))
 
 
 def test_stack_layer0_t4096():
     """Layer 0 of the stack: the router reads RMSNorm(x), the reference's sequential
     norm on one side and the blocked norm on the other."""
     x = bench_x(4096)
-    report("c5 layer 0", compare(rms_norm_seq(x), rms_norm_blocked(x), router(0), K, with_norm=True))
+    report("stack T=4096 layer 0", compare(rms_norm_seq(x), rms_norm_blocked(x), router(0), K, with_norm=True))
 
 
 def test_bound_is_tight_enough_to_fail():
