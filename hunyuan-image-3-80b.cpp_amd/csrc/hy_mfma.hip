@@ -34,6 +34,11 @@
 // matching linear rows; epilogue h = silu(g) * u and Q8_0 quantization of h per token and
 // slab); 1 = down for every tile, routed and shared (writes y[slot][row]; the combine
 // kernel then forms out = resid + (y_shared + sum_{e ascending} w_e y_e)).
+//
+// Scheduling: work items are dealt to the 8 XCDs in tile groups (work-group ids go
+// round robin over the XCDs); each XCD's last two rounds of items are claimed at run
+// time through per-XCD counters, so an XCD that runs ahead takes over the others'
+// tail (moe_mfma_kernel).
 #include <utility>
 
 #include "hy_device.hpp"
