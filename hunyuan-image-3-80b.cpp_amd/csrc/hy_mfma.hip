@@ -98,7 +98,7 @@ struct MmShape {
     static_assert(KB == 2 || KB == 1, "B-scale copy: one 4-byte piece per (token, block)");
     static_assert(WAVES % KB == 0 && TPW % 2 == 0, "B copies: whole token rows per wave");
 };
-using ShapeWide = MmShape<128, 128, 2, 4, 2, 2, 2>;
+using ShapeWide = MmShape<128, 128, 2, 4, 2, 2, 4>;
 using ShapeTall = MmShape<256, 64, 2>;
 
 struct MmArgs {
@@ -199,13 +199,15 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
 
     // XCD-aware work mapping: work-group ids go round robin over the XCDs, so give
     // all row blocks of a tile the same id mod MM_XCD (they share the tile's
-    // activation rows in that XCD's L2).  The wide shape takes GROUP = 2 consecutive
+    // activation rows in that XCD's L2).  The wide shape takes GROUP = 4 consecutive
     // tiles (mostly one expert's) together on one XCD with their work groups
-    // interleaved by row block, so one weight row block serves both from L2 (Zipf
-    // T=4096 Q4_0 ffn_up 2.578-2.617 -> 2.498-2.504 ms, the uniform T=4096 stack within
-    // 0.5 %; on the tall shape's T=512 tiles, of two experts as often as of one, 2 %
-    // slower).  (Ordering whole experts onto one XCD cut fetched bytes but ran 2-4 %
-    // slower: this kernel is not bound by HBM traffic.)
+    // interleaved by row block, so one weight row block serves all four from L2 (two
+    // against one: Zipf T=4096 Q4_0 ffn_up 2.578-2.617 -> 2.498-2.504 ms; four against
+    // two, with the claimed tail below: the 4096-token Q8_0 stack -0.7 %, the Zipf
+    // layer unchanged; eight: the Zipf layer 5 % slower.  On the tall shape's T=512
+    // tiles, of two experts as often as of one, groups of two change nothing.)
+    // (Ordering whole experts onto one XCD cut fetched bytes but ran 2-4 % slower: this
+    // kernel is not bound by HBM traffic.)
     //
     // The XCDs do not run equally fast (per-work-group stamps: the same full tile takes
     // 110-119 us on different XCDs of one launch), and with a fixed id -> item map the
