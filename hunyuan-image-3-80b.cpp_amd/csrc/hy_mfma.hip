@@ -205,17 +205,17 @@ __global__ __launch_bounds__(SH::THREADS, SH::WG_PER_CU) void moe_mfma_kernel(Mm
     // against one: Zipf T=4096 Q4_0 ffn_up 2.578-2.617 -> 2.498-2.504 ms; four against
     // two, with the claimed tail below: the 4096-token Q8_0 stack -0.7 %, the Zipf
     // layer unchanged; eight: the Zipf layer 5 % slower.  On the tall shape's T=512
-    // tiles, of two experts as often as of one, groups of two change nothing.)
-    // (Ordering whole experts onto one XCD cut fetched bytes but ran 2-4 % slower: this
-    // kernel is not bound by HBM traffic.)
+    // tiles, of two experts as often as of one, groups of two change nothing.  Before
+    // the claimed tail, coarser groups ran slower: they unbalanced the XCDs.)
     //
     // The XCDs do not run equally fast (per-work-group stamps: the same full tile takes
     // 110-119 us on different XCDs of one launch), and with a fixed id -> item map the
     // launch waits for the slowest (4096-token Q8_0 gate/up launch: XCDs ending at
-    // 2263-2457 us, the work groups' busy time 93 % of the launch's).  So only the first part of each XCD's item list is fixed:
-    // its last RESERVE items (two rounds of its work groups) are claimed through the
-    // XCD's work counter, and a work group that finds its own XCD's list exhausted
-    // claims from the XCD with the most items left.  Every item runs exactly once: a
+    // 2263-2457 us, the work groups' busy time 93 % of the launch's).  So only the
+    // first part of each XCD's item list is fixed: its last RESERVE items (two rounds
+    // of its work groups) are claimed through the XCD's work counter, and a work group
+    // that finds its own XCD's list exhausted claims from the XCD with the most items
+    // left.  Every item runs exactly once: a
     // fixed item by the one work group whose id maps to it, a reserved item by the
     // claim that drew it; the RESERVE work groups of an XCD whose ids follow its fixed
     // part each claim from their own counter first, so their claims alone cover that
